@@ -1,0 +1,186 @@
+/*
+ * saga_amd.h -- C ABI of the MI355X (gfx950) SAGA + Atop-N decode-attention
+ * library (libsaga_amd.so).
+ *
+ * The reference (noamelata/SAGA) is Python: its decode path is the module
+ * attention/attention.py (torch ops) plus the Triton kernel in
+ * attention/triton_atopn.py.  Each entry point below replaces one function of
+ * that module; the comment above it names the function and file:line.  A
+ * Python caller binds them with ctypes (saga_amd/_lib.py); the same
+ * signatures are what a cffi/ctypes stub in the reference would bind.
+ *
+ * Conventions
+ *   - All tensor data live in device memory (HBM) and are owned by the
+ *     caller.  No entry point allocates, frees or synchronises; every one
+ *     enqueues work on `stream` and returns.  Calls are capturable into a
+ *     HIP graph.
+ *   - Strides are in elements.  The innermost (head_dim / position) stride
+ *     must be 1.  16-bit tensors need 16-byte aligned rows for the vector
+ *     loads (head_dim * 2 bytes, i.e. any d in {64, 128} with aligned base).
+ *   - query [b, q_h, 1, d]; key [b, k_h, L, d]; value [b, v_h, L, d];
+ *     q_h % k_h == 0 and q_h % v_h == 0; query head h reads key head
+ *     h / (q_h / k_h) and value head h / (q_h / v_h)
+ *     (attention/attention.py:70, 81, 119, 163).
+ *   - mask (optional) is an additive mask [b or 1, 1 or q_h, 1, L' >= L];
+ *     only its first L columns are used (attention/attention.py:125).  A
+ *     SAGA_DTYPE_BOOL mask adds 1.0 where true and 0.0 where false, which is
+ *     what `logits + bool_mask` does in torch.
+ *   - kv_len (optional, device int32 [b]) truncates batch row i to its first
+ *     kv_len[i] positions: results equal the reference applied to
+ *     key[i, :, :kv_len[i]] and value[i, :, :kv_len[i]].  No counterpart in
+ *     the reference; it lets a static KV cache skip its unfilled slots.
+ *   - Return value: SAGA_OK or a negative SAGA_ERR_* code; the message of
+ *     the last error on the calling thread is in saga_last_error().  Nothing
+ *     aborts and no C++ exception crosses this boundary.
+ *   - Workspace buffers must be zero-filled once when allocated; the kernels
+ *     leave the counters they use at zero after every call.  Two calls that
+ *     share a workspace must be ordered (same stream).
+ */
+#ifndef SAGA_AMD_H
+#define SAGA_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SAGA_DTYPE_F32 0
+#define SAGA_DTYPE_BF16 1
+#define SAGA_DTYPE_F16 2
+#define SAGA_DTYPE_BOOL 3 /* one byte, 0 or 1; masks only */
+#define SAGA_DTYPE_I32 4
+#define SAGA_DTYPE_I64 5
+
+#define SAGA_OK 0
+#define SAGA_ERR_INVALID (-1)     /* null pointer, bad shape/stride/dtype */
+#define SAGA_ERR_UNSUPPORTED (-2) /* valid but not built (head_dim, group size) */
+#define SAGA_ERR_WORKSPACE (-3)   /* workspace missing or too small */
+#define SAGA_ERR_HIP (-4)         /* a HIP runtime call failed */
+
+/* Score partials are kept per chunk of this many key positions. */
+#define SAGA_CHUNK 128
+
+typedef struct saga_tensor {
+  void* data;
+  int32_t dtype;
+  int32_t ndim; /* 1..4 */
+  int64_t shape[4];
+  int64_t stride[4]; /* elements */
+} saga_tensor;
+
+/* hipStream_t; NULL selects the null stream. */
+typedef void* saga_stream_t;
+
+/* Byte offsets of the fused decode workspace (for tests and inspection). */
+typedef struct saga_atopn_layout {
+  int64_t scores;    /* f32 [b*q_h, scores_ld] */
+  int64_t scores_ld; /* elements */
+  int64_t part_max;  /* f32 [b*q_h, nchunk] */
+  int64_t part_sum;  /* f32 [b*q_h, nchunk] */
+  int64_t nchunk;
+  int64_t thresh;    /* f32 [b*q_h] logit threshold (fast step) */
+  int64_t sel_idx;   /* i32 [b*q_h, buf_k] ascending positions */
+  int64_t sel_val;   /* f32 [b*q_h, buf_k] their logits */
+  int64_t sel_cnt;   /* i32 [b*q_h] kept (<= buf_k) */
+  int64_t sel_total; /* i32 [b*q_h] passing before the cap */
+  int64_t part_out;  /* f32 [b*q_h, npiece, 2 + d] softmax.V partials */
+  int64_t npiece;
+  int64_t counters;  /* i32 [b*q_h] arrival counters (self-resetting) */
+  int64_t total_bytes;
+} saga_atopn_layout;
+
+/* Library version (major*10000 + minor*100 + patch). */
+int saga_version(void);
+
+/* Message of the last error returned on this thread ("" if none). */
+const char* saga_last_error(void);
+
+/* Scaled, masked QK logits of one decode step.
+ * Replaces _compute_attn_weights, attention/attention.py:113-128
+ * (bmm of the grouped queries with K^T, * scaling, + mask).
+ * scores: f32 [b, q_h, 1, >=L] (last stride 1), written for positions < L
+ * (positions >= kv_len[i] are -inf).  part_max/part_sum (optional, f32
+ * [b*q_h, ceil(L/SAGA_CHUNK)]): per-chunk max and sum of exp(x - max). */
+int saga_qk_scores(const saga_tensor* query, const saga_tensor* key, const saga_tensor* mask,
+                   const int32_t* kv_len, float scale, saga_tensor* scores, float* part_max,
+                   float* part_sum, saga_stream_t stream);
+
+/* Softmax-space -> logit-space threshold per row.
+ * Replaces _transform_softmax_threshold, attention/attention.py:136-149:
+ * t = m + log(max(p*, 1e-30) * sum_j exp(x_j - m)), m = max of the last
+ * min(256, L) logits.  scores f32 [b, q_h, 1, L]; softmax_threshold f32
+ * [b*q_h]; logit_threshold f32 [b*q_h] (output). */
+int saga_logit_threshold(const saga_tensor* scores, const int32_t* kv_len,
+                         const float* softmax_threshold, float* logit_threshold,
+                         saga_stream_t stream);
+
+/* Threshold stream compaction.
+ * Replaces threshold_topk_fast + threshold_select_fast_kernel,
+ * attention/triton_atopn.py:59-113 and :6-53.  x [..., D] (f32/bf16/f16,
+ * rows contiguous in D); threshold f32 with threshold_numel == rows (per
+ * row), 1 (broadcast) or any other count (repeated, row r uses
+ * threshold[r % threshold_numel], :87-96).  Selects x > t (strict, fp32
+ * compare), at most k per row, in ascending index order (the reference's
+ * order is atomic-race order; on overflow it keeps a race-dependent subset,
+ * this keeps the first k).  out_values [..., k] (x's dtype) and out_indices
+ * int64 [..., k] are fully written, unfilled slots as (-inf, 0).
+ * out_counts (optional, int32 [rows]): passing elements before the cap. */
+int saga_threshold_select(const saga_tensor* x, const float* threshold, int64_t threshold_numel,
+                          int64_t k, saga_tensor* out_values, int64_t* out_indices,
+                          int32_t* out_counts, saga_stream_t stream);
+
+/* Softmax (or renormalisation) over K selected entries per row, then . V.
+ * Replaces _atopn_gather_and_output, attention/attention.py:152-170.
+ * weights [b, q_h, 1, K] (f32/bf16/f16; logits if input_is_logits, else
+ * probabilities), indices int64 [b, q_h, 1, K], value [b, v_h, L, d],
+ * out [b, q_h, 1, d] (f32/bf16/f16).  An all -inf logit row gives NaN, as
+ * torch's softmax does.  workspace: saga_sparse_pv_workspace_bytes(). */
+size_t saga_sparse_pv_workspace_bytes(int64_t b, int64_t q_h, int64_t d, int64_t K);
+int saga_sparse_softmax_pv(const saga_tensor* weights, const saga_tensor* indices,
+                           const saga_tensor* value, int32_t input_is_logits, saga_tensor* out,
+                           void* workspace, size_t workspace_bytes, saga_stream_t stream);
+
+/* Workspace of the fused decode entry points; buf_k = min(2*top_n, L) for
+ * saga_atopn_decode, min(top_n, L) for saga_atopn_calibrate. */
+size_t saga_atopn_workspace_bytes(int64_t b, int64_t q_h, int64_t L, int64_t d, int64_t buf_k);
+int saga_atopn_workspace_layout(int64_t b, int64_t q_h, int64_t L, int64_t d, int64_t buf_k,
+                                saga_atopn_layout* layout);
+
+/* Atop-N fast decode step: scores, logit threshold from the stored
+ * softmax-space thresholds, ordered compaction capped at
+ * buf_k = min(2*top_n, L), sparse softmax . V.
+ * Replaces approx_top_n_attention_amortized, attention/attention.py:192-209.
+ * softmax_threshold: f32 [b*q_h] (the reference reads
+ * AMORTIZED_THRESHOLD_TENSOR[layer_idx, :b*q_h], :200-201).
+ * out [b, q_h, 1, d] (f32/bf16/f16). */
+int saga_atopn_decode(const saga_tensor* query, const saga_tensor* key, const saga_tensor* value,
+                      const saga_tensor* mask, const int32_t* kv_len, float scale, int64_t top_n,
+                      const float* softmax_threshold, saga_tensor* out, void* workspace,
+                      size_t workspace_bytes, saga_stream_t stream);
+
+/* Atop-N calibration step: full softmax statistics, exact top-k
+ * (k = min(top_n, L), radix select; equal values: lower index first),
+ * stores the k-th largest probability per row into softmax_threshold_out
+ * f32 [b*q_h], output = renormalised top-k . V.
+ * Replaces approx_top_n_attention_amortized_cal, attention/attention.py:173-189. */
+int saga_atopn_calibrate(const saga_tensor* query, const saga_tensor* key,
+                         const saga_tensor* value, const saga_tensor* mask, const int32_t* kv_len,
+                         float scale, int64_t top_n, float* softmax_threshold_out,
+                         saga_tensor* out, void* workspace, size_t workspace_bytes,
+                         saga_stream_t stream);
+
+/* Dense decode attention (split-L, one pass over K and V).
+ * Replaces full_einsum_forward, attention/attention.py:64-85, for l_q == 1. */
+size_t saga_dense_workspace_bytes(int64_t b, int64_t q_h, int64_t L, int64_t d);
+int saga_dense_decode(const saga_tensor* query, const saga_tensor* key, const saga_tensor* value,
+                      const saga_tensor* mask, const int32_t* kv_len, float scale,
+                      saga_tensor* out, void* workspace, size_t workspace_bytes,
+                      saga_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SAGA_AMD_H */

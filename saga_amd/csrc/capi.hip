@@ -1,0 +1,560 @@
+// C ABI of libsaga_amd.so: argument validation, workspace layout and the
+// launch sequences of the fused decode entry points.  Declarations and the
+// reference function each entry point replaces: include/saga_amd.h.
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+
+#include "../../include/saga_amd.h"
+#include "kernels.h"
+
+using namespace saga;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = 0;
+  return SAGA_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(SAGA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return SAGA_OK;
+}
+
+int64_t elt_size(int dt) {
+  switch (dt) {
+    case SAGA_DTYPE_F32: return 4;
+    case SAGA_DTYPE_BF16: return 2;
+    case SAGA_DTYPE_F16: return 2;
+    case SAGA_DTYPE_BOOL: return 1;
+    case SAGA_DTYPE_I32: return 4;
+    case SAGA_DTYPE_I64: return 8;
+    default: return 0;
+  }
+}
+
+bool is_float(int dt) {
+  return dt == SAGA_DTYPE_F32 || dt == SAGA_DTYPE_BF16 || dt == SAGA_DTYPE_F16;
+}
+
+constexpr int64_t kMaxLen = (1LL << 30);  // positions are int32 inside kernels
+constexpr int kMaxGroup = 16;             // query heads per key head (one MFMA column tile)
+constexpr int kPiece = 128;               // selection entries per sparse-PV block
+
+int64_t align256(int64_t x) { return (x + 255) & ~static_cast<int64_t>(255); }
+
+int check_tensor(const saga_tensor* t, const char* name, int ndim) {
+  if (!t) return fail(SAGA_ERR_INVALID, "%s: null tensor descriptor", name);
+  if (!t->data) return fail(SAGA_ERR_INVALID, "%s: null data pointer", name);
+  if (t->ndim != ndim) return fail(SAGA_ERR_INVALID, "%s: expected %d dims, got %d", name, ndim, t->ndim);
+  for (int i = 0; i < ndim; ++i)
+    if (t->shape[i] < 1) return fail(SAGA_ERR_INVALID, "%s: dim %d has size %lld", name, i, (long long)t->shape[i]);
+  if (elt_size(t->dtype) == 0) return fail(SAGA_ERR_INVALID, "%s: unknown dtype %d", name, t->dtype);
+  return SAGA_OK;
+}
+
+// 16-byte vector loads of rows: aligned base and strides.
+int check_vec_rows(const saga_tensor* t, const char* name) {
+  const int64_t es = elt_size(t->dtype);
+  if (t->stride[t->ndim - 1] != 1) return fail(SAGA_ERR_INVALID, "%s: innermost stride must be 1", name);
+  if (reinterpret_cast<uintptr_t>(t->data) % 16)
+    return fail(SAGA_ERR_INVALID, "%s: data pointer must be 16-byte aligned", name);
+  for (int i = 0; i + 1 < t->ndim; ++i)
+    if (t->shape[i] > 1 && (t->stride[i] * es) % 16)
+      return fail(SAGA_ERR_INVALID, "%s: stride of dim %d must be a multiple of 16 bytes", name, i);
+  return SAGA_OK;
+}
+
+struct Shape {
+  int64_t b, q_h, k_h, v_h, d, L;
+  int dt;
+};
+
+int check_qk(const saga_tensor* q, const saga_tensor* k, const saga_tensor* mask, Shape* s) {
+  int rc;
+  if ((rc = check_tensor(q, "query", 4)) || (rc = check_tensor(k, "key", 4))) return rc;
+  s->b = q->shape[0];
+  s->q_h = q->shape[1];
+  s->d = q->shape[3];
+  s->k_h = k->shape[1];
+  s->L = k->shape[2];
+  s->dt = q->dtype;
+  if (q->shape[2] != 1) return fail(SAGA_ERR_UNSUPPORTED, "query: decode path needs l_q == 1, got %lld", (long long)q->shape[2]);
+  if (!is_float(q->dtype)) return fail(SAGA_ERR_INVALID, "query: dtype must be f32, bf16 or f16");
+  if (k->dtype != q->dtype) return fail(SAGA_ERR_INVALID, "key: dtype differs from query");
+  if (k->shape[0] != s->b || k->shape[3] != s->d)
+    return fail(SAGA_ERR_INVALID, "key: shape [%lld,%lld,%lld,%lld] does not match query [b=%lld, d=%lld]",
+                (long long)k->shape[0], (long long)k->shape[1], (long long)k->shape[2], (long long)k->shape[3],
+                (long long)s->b, (long long)s->d);
+  if (s->d != 64 && s->d != 128) return fail(SAGA_ERR_UNSUPPORTED, "head_dim %lld not built (64, 128)", (long long)s->d);
+  if (s->q_h % s->k_h) return fail(SAGA_ERR_INVALID, "q_h (%lld) not a multiple of k_h (%lld)", (long long)s->q_h, (long long)s->k_h);
+  if (s->q_h / s->k_h > kMaxGroup)
+    return fail(SAGA_ERR_UNSUPPORTED, "q_h / k_h = %lld > %d not built", (long long)(s->q_h / s->k_h), kMaxGroup);
+  if (s->L >= kMaxLen) return fail(SAGA_ERR_UNSUPPORTED, "key length %lld too large", (long long)s->L);
+  if (s->b * s->q_h >= (1LL << 31)) return fail(SAGA_ERR_UNSUPPORTED, "b * q_h too large");
+  if ((rc = check_vec_rows(q, "query")) || (rc = check_vec_rows(k, "key"))) return rc;
+  if (mask) {
+    if ((rc = check_tensor(mask, "mask", 4))) return rc;
+    if (!is_float(mask->dtype) && mask->dtype != SAGA_DTYPE_BOOL)
+      return fail(SAGA_ERR_INVALID, "mask: dtype must be f32, bf16, f16 or bool");
+    if ((mask->shape[0] != 1 && mask->shape[0] != s->b) || (mask->shape[1] != 1 && mask->shape[1] != s->q_h) ||
+        mask->shape[2] != 1 || mask->shape[3] < s->L)
+      return fail(SAGA_ERR_INVALID, "mask: shape [%lld,%lld,%lld,%lld] does not broadcast to [b, q_h, 1, L=%lld]",
+                  (long long)mask->shape[0], (long long)mask->shape[1], (long long)mask->shape[2],
+                  (long long)mask->shape[3], (long long)s->L);
+  }
+  return SAGA_OK;
+}
+
+int check_v(const saga_tensor* v, Shape* s) {
+  int rc;
+  if ((rc = check_tensor(v, "value", 4))) return rc;
+  s->v_h = v->shape[1];
+  if (v->dtype != s->dt) return fail(SAGA_ERR_INVALID, "value: dtype differs from query");
+  if (v->shape[0] != s->b || v->shape[2] != s->L || v->shape[3] != s->d)
+    return fail(SAGA_ERR_INVALID, "value: shape [%lld,%lld,%lld,%lld] does not match [b, v_h, L=%lld, d=%lld]",
+                (long long)v->shape[0], (long long)v->shape[1], (long long)v->shape[2], (long long)v->shape[3],
+                (long long)s->L, (long long)s->d);
+  if (s->q_h % s->v_h) return fail(SAGA_ERR_INVALID, "q_h (%lld) not a multiple of v_h (%lld)", (long long)s->q_h, (long long)s->v_h);
+  return check_vec_rows(v, "value");
+}
+
+int check_out(const saga_tensor* out, const Shape& s) {
+  int rc;
+  if ((rc = check_tensor(out, "out", 4))) return rc;
+  if (!is_float(out->dtype)) return fail(SAGA_ERR_INVALID, "out: dtype must be f32, bf16 or f16");
+  if (out->shape[0] != s.b || out->shape[1] != s.q_h || out->shape[2] != 1 || out->shape[3] != s.d)
+    return fail(SAGA_ERR_INVALID, "out: shape must be [b, q_h, 1, d]");
+  if (out->stride[3] != 1) return fail(SAGA_ERR_INVALID, "out: innermost stride must be 1");
+  return SAGA_OK;
+}
+
+QKParams make_qk(const saga_tensor* q, const saga_tensor* k, const saga_tensor* mask, const int32_t* kv_len,
+                 float scale, const Shape& s) {
+  QKParams p{};
+  p.q = static_cast<const char*>(q->data);
+  p.q_sb = q->stride[0];
+  p.q_sh = q->stride[1];
+  p.k = static_cast<const char*>(k->data);
+  p.k_sb = k->stride[0];
+  p.k_sh = k->stride[1];
+  p.k_sl = k->stride[2];
+  if (mask) {
+    p.mask = mask->data;
+    p.mask_dt = mask->dtype;
+    p.m_sb = mask->shape[0] == 1 ? 0 : mask->stride[0];
+    p.m_sh = mask->shape[1] == 1 ? 0 : mask->stride[1];
+    p.m_sl = mask->stride[3];
+  }
+  p.kv_len = kv_len;
+  p.b = static_cast<int32_t>(s.b);
+  p.q_h = static_cast<int32_t>(s.q_h);
+  p.k_h = static_cast<int32_t>(s.k_h);
+  p.g = static_cast<int32_t>(s.q_h / s.k_h);
+  p.L = static_cast<int32_t>(s.L);
+  p.nchunk = static_cast<int32_t>((s.L + SAGA_CHUNK - 1) / SAGA_CHUNK);
+  p.scale = scale;
+  return p;
+}
+
+void atopn_layout(int64_t b, int64_t q_h, int64_t L, int64_t d, int64_t buf_k, saga_atopn_layout* o) {
+  const int64_t nr = b * q_h;
+  const int64_t ld = (L + 15) / 16 * 16;
+  const int64_t nchunk = (L + SAGA_CHUNK - 1) / SAGA_CHUNK;
+  const int64_t npiece = buf_k <= kPiece ? 1 : (buf_k + kPiece - 1) / kPiece;
+  int64_t off = 0;
+  auto take = [&](int64_t bytes) {
+    const int64_t at = off;
+    off = align256(off + bytes);
+    return at;
+  };
+  o->scores_ld = ld;
+  o->nchunk = nchunk;
+  o->npiece = npiece;
+  o->scores = take(nr * ld * 4);
+  o->part_max = take(nr * nchunk * 4);
+  o->part_sum = take(nr * nchunk * 4);
+  o->thresh = take(nr * 4);
+  o->sel_idx = take(nr * buf_k * 4);
+  o->sel_val = take(nr * buf_k * 4);
+  o->sel_cnt = take(nr * 4);
+  o->sel_total = take(nr * 4);
+  o->part_out = take(nr * npiece * (2 + d) * 4);
+  o->counters = take(nr * 4);
+  o->total_bytes = off;
+}
+
+PVParams make_pv(const saga_tensor* v, const saga_tensor* out, const Shape& s) {
+  PVParams p{};
+  p.v = static_cast<const char*>(v->data);
+  p.v_dt = v->dtype;
+  p.v_sb = v->stride[0];
+  p.v_sh = v->stride[1];
+  p.v_sl = v->stride[2];
+  p.b = static_cast<int32_t>(s.b);
+  p.q_h = static_cast<int32_t>(s.q_h);
+  p.v_h = static_cast<int32_t>(s.v_h);
+  p.d = static_cast<int32_t>(s.d);
+  p.L = static_cast<int32_t>(s.L);
+  p.out = out->data;
+  p.out_dt = out->dtype;
+  p.o_sb = out->stride[0];
+  p.o_sh = out->stride[1];
+  return p;
+}
+
+// Shared body of the two fused Atop-N entry points.
+int atopn_run(bool calibrate, const saga_tensor* query, const saga_tensor* key, const saga_tensor* value,
+              const saga_tensor* mask, const int32_t* kv_len, float scale, int64_t top_n,
+              const float* pstar_in, float* pstar_out, saga_tensor* out, void* workspace,
+              size_t workspace_bytes, saga_stream_t stream) {
+  Shape s{};
+  int rc;
+  if ((rc = check_qk(query, key, mask, &s)) || (rc = check_v(value, &s)) || (rc = check_out(out, s))) return rc;
+  if (top_n < 1) return fail(SAGA_ERR_INVALID, "top_n must be >= 1, got %lld", (long long)top_n);
+  if (calibrate ? !pstar_out : !pstar_in) return fail(SAGA_ERR_INVALID, "threshold table row is null");
+  const int64_t buf_k = calibrate ? (top_n < s.L ? top_n : s.L) : (2 * top_n < s.L ? 2 * top_n : s.L);
+  saga_atopn_layout lay;
+  atopn_layout(s.b, s.q_h, s.L, s.d, buf_k, &lay);
+  if (!workspace || workspace_bytes < static_cast<size_t>(lay.total_bytes))
+    return fail(SAGA_ERR_WORKSPACE, "workspace of %zu bytes, need %lld", workspace_bytes, (long long)lay.total_bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(SAGA_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  char* ws = static_cast<char*>(workspace);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t nr = s.b * s.q_h;
+
+  QKParams qp = make_qk(query, key, mask, kv_len, scale, s);
+  qp.scores = reinterpret_cast<float*>(ws + lay.scores);
+  qp.s_sb = s.q_h * lay.scores_ld;
+  qp.s_sh = lay.scores_ld;
+  qp.vec_store = 1;
+  qp.pmax = reinterpret_cast<float*>(ws + lay.part_max);
+  qp.psum = reinterpret_cast<float*>(ws + lay.part_sum);
+  if ((rc = hip_status(launch_qk_scores(s.dt, static_cast<int>(s.d), qp, st), "qk_scores launch"))) return rc;
+
+  FusedSelParams sp{};
+  sp.scores = qp.scores;
+  sp.ld = lay.scores_ld;
+  sp.pmax = qp.pmax;
+  sp.psum = qp.psum;
+  sp.nchunk = static_cast<int32_t>(lay.nchunk);
+  sp.kv_len = kv_len;
+  sp.q_h = static_cast<int32_t>(s.q_h);
+  sp.nrows = static_cast<int32_t>(nr);
+  sp.L = static_cast<int32_t>(s.L);
+  sp.pstar = pstar_in;
+  sp.pstar_out = pstar_out;
+  sp.t_out = reinterpret_cast<float*>(ws + lay.thresh);
+  sp.cap = static_cast<int32_t>(buf_k);
+  sp.sel_idx = reinterpret_cast<int32_t*>(ws + lay.sel_idx);
+  sp.sel_val = reinterpret_cast<float*>(ws + lay.sel_val);
+  sp.sel_cnt = reinterpret_cast<int32_t*>(ws + lay.sel_cnt);
+  sp.sel_total = reinterpret_cast<int32_t*>(ws + lay.sel_total);
+  rc = calibrate ? hip_status(launch_select_calibrate(sp, st), "select_calibrate launch")
+                 : hip_status(launch_select_fast(sp, st), "select_fast launch");
+  if (rc) return rc;
+
+  PVParams pp = make_pv(value, out, s);
+  pp.w = sp.sel_val;
+  pp.w_dt = SAGA_DTYPE_F32;
+  pp.w_ld = buf_k;
+  pp.idx = sp.sel_idx;
+  pp.idx_i64 = 0;
+  pp.i_ld = buf_k;
+  pp.cnt = sp.sel_cnt;
+  pp.K = static_cast<int32_t>(buf_k);
+  pp.probs_mode = 0;  // calibration: softmax over the top-k logits == renormalised top-k probabilities
+  pp.part = reinterpret_cast<float*>(ws + lay.part_out);
+  pp.npiece = static_cast<int32_t>(lay.npiece);
+  pp.piece = lay.npiece == 1 ? static_cast<int32_t>(buf_k) : kPiece;
+  pp.counters = reinterpret_cast<int32_t*>(ws + lay.counters);
+  if ((rc = hip_status(launch_sparse_pv(pp, st), "sparse_pv launch"))) return rc;
+  return ok();
+}
+
+// Dense split plan: about 512 blocks in flight, splits of >= 512 positions,
+// split length a multiple of the 32-position wave step.
+void dense_plan(int64_t b, int64_t L, int64_t* nsplit, int64_t* split_len) {
+  int64_t ns = (512 + b - 1) / b;
+  const int64_t by_len = (L + 511) / 512;
+  if (ns > by_len) ns = by_len;
+  if (ns < 1) ns = 1;
+  int64_t sl = (L + ns - 1) / ns;
+  sl = (sl + 31) / 32 * 32;
+  *nsplit = (L + sl - 1) / sl;
+  *split_len = sl;
+}
+
+// Rows of a [..., D] tensor must be uniformly strided (collapsible leading dims).
+int rows_of(const saga_tensor* t, const char* name, int64_t* rows, int64_t* ld) {
+  if (!t) return fail(SAGA_ERR_INVALID, "%s: null tensor descriptor", name);
+  if (!t->data) return fail(SAGA_ERR_INVALID, "%s: null data pointer", name);
+  if (t->ndim < 1 || t->ndim > 4) return fail(SAGA_ERR_INVALID, "%s: 1 to 4 dims expected", name);
+  if (t->stride[t->ndim - 1] != 1) return fail(SAGA_ERR_INVALID, "%s: innermost stride must be 1", name);
+  int64_t r = 1;
+  for (int i = 0; i + 1 < t->ndim; ++i) r *= t->shape[i];
+  *rows = r;
+  *ld = t->ndim >= 2 ? t->stride[t->ndim - 2] : t->shape[0];
+  for (int i = 0; i + 2 < t->ndim; ++i)
+    if (t->shape[i] > 1 && t->stride[i] != t->stride[i + 1] * t->shape[i + 1])
+      return fail(SAGA_ERR_INVALID, "%s: leading dims must be collapsible into rows", name);
+  return SAGA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int saga_version(void) { return 100; }
+
+const char* saga_last_error(void) { return g_err; }
+
+int saga_qk_scores(const saga_tensor* query, const saga_tensor* key, const saga_tensor* mask,
+                   const int32_t* kv_len, float scale, saga_tensor* scores, float* part_max,
+                   float* part_sum, saga_stream_t stream) {
+  Shape s{};
+  int rc;
+  if ((rc = check_qk(query, key, mask, &s))) return rc;
+  if ((rc = check_tensor(scores, "scores", 4))) return rc;
+  if (scores->dtype != SAGA_DTYPE_F32) return fail(SAGA_ERR_INVALID, "scores: dtype must be f32");
+  if (scores->shape[0] != s.b || scores->shape[1] != s.q_h || scores->shape[2] != 1 || scores->shape[3] < s.L)
+    return fail(SAGA_ERR_INVALID, "scores: shape must be [b, q_h, 1, >=L]");
+  if (scores->stride[3] != 1) return fail(SAGA_ERR_INVALID, "scores: innermost stride must be 1");
+  if ((part_max == nullptr) != (part_sum == nullptr))
+    return fail(SAGA_ERR_INVALID, "part_max and part_sum must both be given or both be null");
+  QKParams p = make_qk(query, key, mask, kv_len, scale, s);
+  p.scores = static_cast<float*>(scores->data);
+  p.s_sb = scores->stride[0];
+  p.s_sh = scores->stride[1];
+  p.vec_store = (reinterpret_cast<uintptr_t>(scores->data) % 16 == 0) && (p.s_sb % 4 == 0) && (p.s_sh % 4 == 0);
+  p.pmax = part_max;
+  p.psum = part_sum;
+  if ((rc = hip_status(launch_qk_scores(s.dt, static_cast<int>(s.d), p, static_cast<hipStream_t>(stream)),
+                       "qk_scores launch")))
+    return rc;
+  return ok();
+}
+
+int saga_logit_threshold(const saga_tensor* scores, const int32_t* kv_len, const float* softmax_threshold,
+                         float* logit_threshold, saga_stream_t stream) {
+  int rc;
+  if ((rc = check_tensor(scores, "scores", 4))) return rc;
+  if (scores->dtype != SAGA_DTYPE_F32) return fail(SAGA_ERR_INVALID, "scores: dtype must be f32");
+  if (scores->shape[2] != 1 || scores->stride[3] != 1) return fail(SAGA_ERR_INVALID, "scores: [b, q_h, 1, L], innermost stride 1");
+  if (!softmax_threshold || !logit_threshold) return fail(SAGA_ERR_INVALID, "threshold pointers must not be null");
+  if (scores->shape[3] >= kMaxLen) return fail(SAGA_ERR_UNSUPPORTED, "length too large");
+  ThreshParams p{};
+  p.scores = static_cast<const float*>(scores->data);
+  p.s_sb = scores->stride[0];
+  p.s_sh = scores->stride[1];
+  p.q_h = static_cast<int32_t>(scores->shape[1]);
+  p.nrows = static_cast<int32_t>(scores->shape[0] * scores->shape[1]);
+  p.L = static_cast<int32_t>(scores->shape[3]);
+  p.kv_len = kv_len;
+  p.pstar = softmax_threshold;
+  p.t_out = logit_threshold;
+  if ((rc = hip_status(launch_logit_threshold(p, static_cast<hipStream_t>(stream)), "logit_threshold launch"))) return rc;
+  return ok();
+}
+
+int saga_threshold_select(const saga_tensor* x, const float* threshold, int64_t threshold_numel, int64_t k,
+                          saga_tensor* out_values, int64_t* out_indices, int32_t* out_counts,
+                          saga_stream_t stream) {
+  int rc;
+  int64_t rows, ld, orows, old;
+  if ((rc = rows_of(x, "x", &rows, &ld))) return rc;
+  if (!is_float(x->dtype)) return fail(SAGA_ERR_INVALID, "x: dtype must be f32, bf16 or f16");
+  const int64_t D = x->shape[x->ndim - 1];
+  if (D < 1 || D >= kMaxLen) return fail(SAGA_ERR_UNSUPPORTED, "row length %lld unsupported", (long long)D);
+  if (rows < 1 || rows >= (1LL << 31)) return fail(SAGA_ERR_UNSUPPORTED, "row count %lld unsupported", (long long)rows);
+  if (!threshold || threshold_numel < 1) return fail(SAGA_ERR_INVALID, "threshold: null or empty");
+  if (k < 0 || k >= kMaxLen) return fail(SAGA_ERR_INVALID, "k = %lld out of range", (long long)k);
+  if ((rc = rows_of(out_values, "out_values", &orows, &old))) return rc;
+  if (out_values->dtype != x->dtype) return fail(SAGA_ERR_INVALID, "out_values: dtype must match x");
+  if (orows != rows || out_values->shape[out_values->ndim - 1] != k)
+    return fail(SAGA_ERR_INVALID, "out_values: shape must be x.shape[:-1] + (k,)");
+  if (!out_indices) return fail(SAGA_ERR_INVALID, "out_indices: null");
+  if (k == 0) return ok();
+  ApiSelParams p{};
+  p.x = x->data;
+  p.x_dt = x->dtype;
+  p.x_ld = ld;
+  p.nrows = static_cast<int32_t>(rows);
+  p.D = D;
+  p.thresh = threshold;
+  p.thresh_numel = threshold_numel;
+  p.k = static_cast<int32_t>(k);
+  p.out_val = out_values->data;
+  p.ov_ld = old;
+  p.out_idx = out_indices;
+  p.oi_ld = k;
+  p.out_counts = out_counts;
+  if ((rc = hip_status(launch_select_api(p, static_cast<hipStream_t>(stream)), "threshold_select launch"))) return rc;
+  return ok();
+}
+
+size_t saga_sparse_pv_workspace_bytes(int64_t b, int64_t q_h, int64_t d, int64_t K) {
+  const int64_t nr = b * q_h;
+  const int64_t npiece = K <= kPiece ? 1 : (K + kPiece - 1) / kPiece;
+  return static_cast<size_t>(align256(nr * npiece * (2 + d) * 4) + align256(nr * 4));
+}
+
+int saga_sparse_softmax_pv(const saga_tensor* weights, const saga_tensor* indices, const saga_tensor* value,
+                           int32_t input_is_logits, saga_tensor* out, void* workspace, size_t workspace_bytes,
+                           saga_stream_t stream) {
+  int rc;
+  if ((rc = check_tensor(weights, "weights", 4)) || (rc = check_tensor(indices, "indices", 4))) return rc;
+  Shape s{};
+  s.b = weights->shape[0];
+  s.q_h = weights->shape[1];
+  s.L = value ? value->shape[2] : 0;
+  s.d = value ? value->shape[3] : 0;
+  s.dt = value ? value->dtype : -1;
+  if ((rc = check_v(value, &s)) || (rc = check_out(out, s))) return rc;
+  if (!is_float(s.dt)) return fail(SAGA_ERR_INVALID, "value: dtype must be f32, bf16 or f16");
+  if (s.d != 64 && s.d != 128) return fail(SAGA_ERR_UNSUPPORTED, "head_dim %lld not built (64, 128)", (long long)s.d);
+  if (s.L >= kMaxLen) return fail(SAGA_ERR_UNSUPPORTED, "value length too large");
+  const int64_t K = weights->shape[3];
+  if (weights->shape[2] != 1 || indices->shape[0] != s.b || indices->shape[1] != s.q_h || indices->shape[2] != 1 ||
+      indices->shape[3] != K)
+    return fail(SAGA_ERR_INVALID, "weights/indices: shapes must both be [b, q_h, 1, K]");
+  if (!is_float(weights->dtype)) return fail(SAGA_ERR_INVALID, "weights: dtype must be f32, bf16 or f16");
+  if (indices->dtype != SAGA_DTYPE_I64 && indices->dtype != SAGA_DTYPE_I32)
+    return fail(SAGA_ERR_INVALID, "indices: dtype must be int64 or int32");
+  if (weights->stride[3] != 1 || indices->stride[3] != 1 || (s.b > 1 && weights->stride[0] != s.q_h * weights->stride[1]) ||
+      (s.b > 1 && indices->stride[0] != s.q_h * indices->stride[1]))
+    return fail(SAGA_ERR_INVALID, "weights/indices: rows must be uniformly strided with unit innermost stride");
+  if (K >= kMaxLen) return fail(SAGA_ERR_UNSUPPORTED, "K too large");
+  const int64_t nr = s.b * s.q_h;
+  const int64_t npiece = K <= kPiece ? 1 : (K + kPiece - 1) / kPiece;
+  const size_t need = saga_sparse_pv_workspace_bytes(s.b, s.q_h, s.d, K);
+  if (npiece > 1 && (!workspace || workspace_bytes < need))
+    return fail(SAGA_ERR_WORKSPACE, "workspace of %zu bytes, need %zu", workspace_bytes, need);
+  if (npiece > 1 && reinterpret_cast<uintptr_t>(workspace) % 256)
+    return fail(SAGA_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  PVParams p = make_pv(value, out, s);
+  p.w = weights->data;
+  p.w_dt = weights->dtype;
+  p.w_ld = weights->stride[1];
+  p.idx = indices->data;
+  p.idx_i64 = indices->dtype == SAGA_DTYPE_I64;
+  p.i_ld = indices->stride[1];
+  p.cnt = nullptr;
+  p.K = static_cast<int32_t>(K);
+  p.probs_mode = input_is_logits ? 0 : 1;
+  p.npiece = static_cast<int32_t>(npiece);
+  p.piece = npiece == 1 ? static_cast<int32_t>(K) : kPiece;
+  if (npiece > 1) {
+    char* ws = static_cast<char*>(workspace);
+    p.part = reinterpret_cast<float*>(ws);
+    p.counters = reinterpret_cast<int32_t*>(ws + align256(nr * npiece * (2 + s.d) * 4));
+  }
+  if (p.piece > 256) return fail(SAGA_ERR_UNSUPPORTED, "internal: piece size");
+  if ((rc = hip_status(launch_sparse_pv(p, static_cast<hipStream_t>(stream)), "sparse_pv launch"))) return rc;
+  return ok();
+}
+
+size_t saga_atopn_workspace_bytes(int64_t b, int64_t q_h, int64_t L, int64_t d, int64_t buf_k) {
+  saga_atopn_layout lay;
+  atopn_layout(b, q_h, L, d, buf_k, &lay);
+  return static_cast<size_t>(lay.total_bytes);
+}
+
+int saga_atopn_workspace_layout(int64_t b, int64_t q_h, int64_t L, int64_t d, int64_t buf_k,
+                                saga_atopn_layout* layout) {
+  if (!layout) return fail(SAGA_ERR_INVALID, "layout: null");
+  if (b < 1 || q_h < 1 || L < 1 || d < 1 || buf_k < 1) return fail(SAGA_ERR_INVALID, "sizes must be >= 1");
+  atopn_layout(b, q_h, L, d, buf_k, layout);
+  return ok();
+}
+
+int saga_atopn_decode(const saga_tensor* query, const saga_tensor* key, const saga_tensor* value,
+                      const saga_tensor* mask, const int32_t* kv_len, float scale, int64_t top_n,
+                      const float* softmax_threshold, saga_tensor* out, void* workspace, size_t workspace_bytes,
+                      saga_stream_t stream) {
+  return atopn_run(false, query, key, value, mask, kv_len, scale, top_n, softmax_threshold, nullptr, out,
+                   workspace, workspace_bytes, stream);
+}
+
+int saga_atopn_calibrate(const saga_tensor* query, const saga_tensor* key, const saga_tensor* value,
+                         const saga_tensor* mask, const int32_t* kv_len, float scale, int64_t top_n,
+                         float* softmax_threshold_out, saga_tensor* out, void* workspace, size_t workspace_bytes,
+                         saga_stream_t stream) {
+  return atopn_run(true, query, key, value, mask, kv_len, scale, top_n, nullptr, softmax_threshold_out, out,
+                   workspace, workspace_bytes, stream);
+}
+
+size_t saga_dense_workspace_bytes(int64_t b, int64_t q_h, int64_t L, int64_t d) {
+  int64_t ns, sl;
+  dense_plan(b, L, &ns, &sl);
+  return static_cast<size_t>(align256(b * q_h * ns * (2 + d) * 4) + align256(b * q_h * 4));
+}
+
+int saga_dense_decode(const saga_tensor* query, const saga_tensor* key, const saga_tensor* value,
+                      const saga_tensor* mask, const int32_t* kv_len, float scale, saga_tensor* out, void* workspace,
+                      size_t workspace_bytes, saga_stream_t stream) {
+  Shape s{};
+  int rc;
+  if ((rc = check_qk(query, key, mask, &s)) || (rc = check_v(value, &s)) || (rc = check_out(out, s))) return rc;
+  int64_t ns, sl;
+  dense_plan(s.b, s.L, &ns, &sl);
+  const size_t need = saga_dense_workspace_bytes(s.b, s.q_h, s.L, s.d);
+  if (ns > 1 && (!workspace || workspace_bytes < need))
+    return fail(SAGA_ERR_WORKSPACE, "workspace of %zu bytes, need %zu", workspace_bytes, need);
+  if (ns > 1 && reinterpret_cast<uintptr_t>(workspace) % 256)
+    return fail(SAGA_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  QKParams qp = make_qk(query, key, mask, kv_len, scale, s);
+  DenseParams p{};
+  p.q = qp.q;
+  p.q_sb = qp.q_sb;
+  p.q_sh = qp.q_sh;
+  p.k = qp.k;
+  p.k_sb = qp.k_sb;
+  p.k_sh = qp.k_sh;
+  p.k_sl = qp.k_sl;
+  p.v = static_cast<const char*>(value->data);
+  p.v_sb = value->stride[0];
+  p.v_sh = value->stride[1];
+  p.v_sl = value->stride[2];
+  p.mask = qp.mask;
+  p.mask_dt = qp.mask_dt;
+  p.m_sb = qp.m_sb;
+  p.m_sh = qp.m_sh;
+  p.m_sl = qp.m_sl;
+  p.kv_len = kv_len;
+  p.b = qp.b;
+  p.q_h = qp.q_h;
+  p.k_h = qp.k_h;
+  p.v_h = static_cast<int32_t>(s.v_h);
+  p.g = qp.g;
+  p.L = qp.L;
+  p.scale = scale;
+  p.out = out->data;
+  p.out_dt = out->dtype;
+  p.o_sb = out->stride[0];
+  p.o_sh = out->stride[1];
+  p.nsplit = static_cast<int32_t>(ns);
+  p.split_len = static_cast<int32_t>(sl);
+  if (ns > 1) {
+    char* ws = static_cast<char*>(workspace);
+    p.part = reinterpret_cast<float*>(ws);
+    p.counters = reinterpret_cast<int32_t*>(ws + align256(s.b * s.q_h * ns * (2 + s.d) * 4));
+  }
+  if ((rc = hip_status(launch_dense_decode(s.dt, static_cast<int>(s.d), p, static_cast<hipStream_t>(stream)),
+                       "dense_decode launch")))
+    return rc;
+  return ok();
+}
+
+}  // extern "C"

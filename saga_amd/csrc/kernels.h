@@ -1,0 +1,129 @@
+// Launch parameter blocks and host launchers of the SAGA decode kernels.
+// Shapes follow the reference's decode tensors (l_q == 1):
+//   query [b, q_h, 1, d], key [b, k_h, L, d], value [b, v_h, L, d];
+// score / selection rows are r = batch * q_h + head.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace saga {
+
+// K1: scores = (Q_group . K^T) * scale (+ mask), per-chunk (max, sumexp).
+struct QKParams {
+  const char* q;
+  int64_t q_sb, q_sh;  // element strides of batch / head
+  const char* k;
+  int64_t k_sb, k_sh, k_sl;
+  const void* mask;  // nullable additive mask
+  int32_t mask_dt;
+  int64_t m_sb, m_sh, m_sl;
+  const int32_t* kv_len;  // nullable
+  int32_t b, q_h, k_h, g, L, nchunk;
+  float scale;
+  float* scores;  // nullable: skip storing scores
+  int64_t s_sb, s_sh;
+  int32_t vec_store;  // rows 16-byte aligned: store 4 scores at once
+  float* pmax;        // nullable: [row * nchunk + chunk]
+  float* psum;
+};
+hipError_t launch_qk_scores(int dtype, int d, const QKParams& p, hipStream_t st);
+
+// Standalone logit threshold from a scores tensor.
+struct ThreshParams {
+  const float* scores;
+  int64_t s_sb, s_sh;
+  int32_t q_h, nrows, L;
+  const int32_t* kv_len;
+  const float* pstar;
+  float* t_out;
+};
+hipError_t launch_logit_threshold(const ThreshParams& p, hipStream_t st);
+
+// K2: selection over fp32 score rows of the fused workspace.
+struct FusedSelParams {
+  const float* scores;
+  int64_t ld;
+  const float* pmax;
+  const float* psum;
+  int32_t nchunk;
+  const int32_t* kv_len;
+  int32_t q_h, nrows, L;
+  const float* pstar;  // fast step: softmax-space thresholds in
+  float* pstar_out;    // calibration: k-th largest probability out
+  float* t_out;        // fast step: logit thresholds out
+  int32_t cap;         // buf_k (fast) ; top_n (calibration)
+  int32_t* sel_idx;
+  float* sel_val;
+  int32_t* sel_cnt;
+  int32_t* sel_total;
+};
+hipError_t launch_select_fast(const FusedSelParams& p, hipStream_t st);
+hipError_t launch_select_calibrate(const FusedSelParams& p, hipStream_t st);
+
+// API selection (threshold_topk_fast): typed rows, typed values out.
+struct ApiSelParams {
+  const void* x;
+  int32_t x_dt;
+  int64_t x_ld;
+  int32_t nrows;
+  int64_t D;
+  const float* thresh;
+  int64_t thresh_numel;
+  int32_t k;
+  void* out_val;
+  int64_t ov_ld;
+  int64_t* out_idx;
+  int64_t oi_ld;
+  int32_t* out_counts;  // nullable
+};
+hipError_t launch_select_api(const ApiSelParams& p, hipStream_t st);
+
+// K3: softmax (or renormalisation) over selected entries . V.
+struct PVParams {
+  const void* w;
+  int32_t w_dt;
+  int64_t w_ld;
+  const void* idx;
+  int32_t idx_i64;
+  int64_t i_ld;
+  const int32_t* cnt;  // nullable: all K entries
+  int32_t K;
+  const char* v;
+  int32_t v_dt;
+  int64_t v_sb, v_sh, v_sl;
+  int32_t b, q_h, v_h, d, L;
+  int32_t probs_mode;
+  void* out;
+  int32_t out_dt;
+  int64_t o_sb, o_sh;
+  float* part;  // [row][npiece][2 + d]
+  int32_t npiece, piece;
+  int32_t* counters;  // [row], zero between calls
+};
+hipError_t launch_sparse_pv(const PVParams& p, hipStream_t st);
+
+// Dense split-L decode (flash-decoding): one pass over K and V.
+struct DenseParams {
+  const char* q;
+  int64_t q_sb, q_sh;
+  const char* k;
+  int64_t k_sb, k_sh, k_sl;
+  const char* v;
+  int64_t v_sb, v_sh, v_sl;
+  const void* mask;
+  int32_t mask_dt;
+  int64_t m_sb, m_sh, m_sl;
+  const int32_t* kv_len;
+  int32_t b, q_h, k_h, v_h, g, L;
+  float scale;
+  void* out;
+  int32_t out_dt;
+  int64_t o_sb, o_sh;
+  float* part;  // [unit][nsplit][g][2 + d]
+  int32_t nsplit, split_len;
+  int32_t* counters;  // [unit]
+};
+hipError_t launch_dense_decode(int dtype, int d, const DenseParams& p, hipStream_t st);
+
+}  // namespace saga

@@ -1,0 +1,250 @@
+"""Tensor-level operations of the SAGA + Atop-N decode path on MI355X.
+
+Each function validates torch tensors, makes sure they live on a ROCm device,
+and calls one C-ABI entry point of libsaga_amd.so on the current stream.
+Nothing here computes on the CPU.  Workspaces are allocated once per
+(device, kind), zero-filled, grown when needed and reused (the counterpart of
+the reference's _BUFFER_CACHE, attention/triton_atopn.py:56, 73-84), so calls
+are capturable in a HIP graph after a warm-up call.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+
+_WORKSPACES: dict = {}
+
+
+def _need_gpu(*ts: Optional[torch.Tensor]) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                f"saga_amd: tensors must be on a ROCm GPU (got {t.device}); the decode path has no CPU fallback")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"saga_amd: tensors on different devices ({dev}, {t.device})")
+    return dev
+
+
+def workspace(device: torch.device, kind: str, nbytes: int) -> torch.Tensor:
+    """Zero-filled uint8 workspace of at least nbytes, cached per (device, kind)."""
+    key = (device, kind)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def clear_workspaces() -> None:
+    _WORKSPACES.clear()
+
+
+def _scale(query: torch.Tensor, scaling: Optional[float]) -> float:
+    # attention/attention.py:117
+    return 1 / math.sqrt(query.size(-1)) if scaling is None else float(scaling)
+
+
+def _vec_ready(t: torch.Tensor) -> torch.Tensor:
+    """Rows must have a unit innermost stride and 16-byte aligned strides."""
+    es = t.element_size()
+    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all(
+        (s * es) % 16 == 0 for s, n in zip(t.stride()[:-1], t.shape[:-1]) if n > 1)
+    return t if ok else t.contiguous()
+
+
+def _mask_view(mask: Optional[torch.Tensor], L: int) -> Optional[torch.Tensor]:
+    if mask is None:
+        return None
+    if mask.dim() != 4:
+        raise ValueError(f"saga_amd: attention mask must be 4-D [b, 1|q_h, 1, L'], got {tuple(mask.shape)}")
+    return mask[:, :, :, :L]
+
+
+def _kv_len(kv_len: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+    if kv_len is None:
+        return None
+    if kv_len.dtype != torch.int32 or not kv_len.is_contiguous():
+        raise ValueError("saga_amd: kv_len must be a contiguous int32 tensor [b]")
+    return kv_len
+
+
+def qk_scores(query, key, attention_mask=None, scaling=None, kv_len=None, with_partials=False):
+    """Scaled, masked logits [b, q_h, 1, L] in fp32 (attention/attention.py:113-128).
+
+    with_partials: also return the per-128-position-chunk max and sum of
+    exp(x - max) [b*q_h, ceil(L/128)].
+    """
+    dev = _need_gpu(query, key, attention_mask, kv_len)
+    lib = _lib.load()
+    query, key = _vec_ready(query), _vec_ready(key)
+    b, q_h, _, _ = query.shape
+    L = key.shape[2]
+    mask = _mask_view(attention_mask, L)
+    scores = torch.empty(b, q_h, 1, L, dtype=torch.float32, device=dev)
+    pm = ps = None
+    if with_partials:
+        nch = (L + _lib.CHUNK - 1) // _lib.CHUNK
+        pm = torch.empty(b * q_h, nch, dtype=torch.float32, device=dev)
+        ps = torch.empty_like(pm)
+    _lib.check(lib.saga_qk_scores(_lib.tensor(query), _lib.tensor(key), _lib.tensor(mask), _lib.ptr(_kv_len(kv_len)),
+                                  _scale(query, scaling), _lib.tensor(scores), _lib.ptr(pm), _lib.ptr(ps),
+                                  _lib.stream_of(query)), "qk_scores")
+    return (scores, pm, ps) if with_partials else scores
+
+
+def logit_threshold(scores, softmax_threshold, kv_len=None):
+    """Logit-space threshold per row (attention/attention.py:136-149)."""
+    dev = _need_gpu(scores, softmax_threshold, kv_len)
+    b, q_h = scores.shape[0], scores.shape[1]
+    pstar = softmax_threshold.reshape(-1).to(torch.float32).contiguous()
+    if pstar.numel() != b * q_h:
+        raise ValueError("saga_amd: softmax_threshold must have b*q_h entries")
+    out = torch.empty(b * q_h, dtype=torch.float32, device=dev)
+    _lib.check(_lib.load().saga_logit_threshold(_lib.tensor(scores), _lib.ptr(_kv_len(kv_len)), _lib.ptr(pstar),
+                                                _lib.ptr(out), _lib.stream_of(scores)), "logit_threshold")
+    return out
+
+
+def threshold_select(x, k, threshold, out_values=None, out_indices=None, with_counts=False):
+    """Ordered threshold compaction (attention/triton_atopn.py:59-113).
+
+    Returns (values [..., k] in x's dtype, int64 indices [..., k]) and, with
+    with_counts, the per-row number of passing elements before the cap.
+    """
+    dev = _need_gpu(x, threshold)
+    D = x.shape[-1]
+    xf = x.reshape(-1, D).contiguous()
+    rows = xf.shape[0]
+    thr = threshold.reshape(-1).to(torch.float32).contiguous()
+    if out_values is None:
+        out_values = torch.empty(rows, k, dtype=x.dtype, device=dev)
+    if out_indices is None:
+        out_indices = torch.empty(rows, k, dtype=torch.int64, device=dev)
+    counts = torch.empty(rows, dtype=torch.int32, device=dev) if with_counts else None
+    _lib.check(_lib.load().saga_threshold_select(_lib.tensor(xf), _lib.ptr(thr), thr.numel(), k,
+                                                 _lib.tensor(out_values), _lib.ptr(out_indices), _lib.ptr(counts),
+                                                 _lib.stream_of(x)), "threshold_select")
+    shape = tuple(x.shape[:-1]) + (k,)
+    vals, idx = out_values.reshape(shape), out_indices.reshape(shape)
+    return (vals, idx, counts) if with_counts else (vals, idx)
+
+
+def sparse_softmax_pv(weights, indices, value, query_shape, input_is_logits=False, out_dtype=None):
+    """Softmax / renormalisation over K selected entries, then . V
+    (attention/attention.py:152-170).  Returns [b, q_h, 1, d]."""
+    dev = _need_gpu(weights, indices, value)
+    b, q_h, l_q, d = query_shape
+    if l_q != 1:
+        raise NotImplementedError("saga_amd: sparse softmax.V is the decode path (l_q == 1)")
+    K = weights.shape[-1]
+    w = weights.reshape(b, q_h, 1, K).contiguous()
+    idx = indices.reshape(b, q_h, 1, K).contiguous()
+    value = _vec_ready(value)
+    out = torch.empty(b, q_h, 1, d, dtype=out_dtype or value.dtype, device=dev)
+    lib = _lib.load()
+    nbytes = lib.saga_sparse_pv_workspace_bytes(b, q_h, d, K)
+    ws = workspace(dev, "sparse_pv", nbytes)
+    _lib.check(lib.saga_sparse_softmax_pv(_lib.tensor(w), _lib.tensor(idx), _lib.tensor(value),
+                                          1 if input_is_logits else 0, _lib.tensor(out), _lib.ptr(ws), ws.numel(),
+                                          _lib.stream_of(value)), "sparse_softmax_pv")
+    return out
+
+
+def _decode_prep(query, key, value, attention_mask, kv_len):
+    dev = _need_gpu(query, key, value, attention_mask, kv_len)
+    query, key, value = _vec_ready(query), _vec_ready(key), _vec_ready(value)
+    if query.shape[2] != 1:
+        raise NotImplementedError("saga_amd: the HIP decode kernels take l_q == 1")
+    return dev, query, key, value, _mask_view(attention_mask, key.shape[2])
+
+
+def atopn_decode(query, key, value, softmax_threshold, top_n, attention_mask=None, scaling=None, kv_len=None,
+                 out=None, out_dtype=None):
+    """Atop-N fast step (attention/attention.py:192-209).
+
+    softmax_threshold: fp32 [b*q_h] (a row of the threshold table).
+    """
+    dev, query, key, value, mask = _decode_prep(query, key, value, attention_mask, kv_len)
+    b, q_h, _, d = query.shape
+    L = key.shape[2]
+    if softmax_threshold.dtype != torch.float32 or not softmax_threshold.is_contiguous() \
+            or softmax_threshold.numel() < b * q_h:
+        raise ValueError("saga_amd: softmax_threshold must be contiguous fp32 with b*q_h entries")
+    if out is None:
+        out = torch.empty(b, q_h, 1, d, dtype=out_dtype or query.dtype, device=dev)
+    lib = _lib.load()
+    buf_k = min(2 * top_n, L)
+    ws = workspace(dev, "atopn", lib.saga_atopn_workspace_bytes(b, q_h, L, d, buf_k))
+    _lib.check(lib.saga_atopn_decode(_lib.tensor(query), _lib.tensor(key), _lib.tensor(value), _lib.tensor(mask),
+                                     _lib.ptr(_kv_len(kv_len)), _scale(query, scaling), int(top_n),
+                                     _lib.ptr(softmax_threshold), _lib.tensor(out), _lib.ptr(ws), ws.numel(),
+                                     _lib.stream_of(query)), "atopn_decode")
+    return out
+
+
+def atopn_calibrate(query, key, value, top_n, threshold_out, attention_mask=None, scaling=None, kv_len=None,
+                    out=None, out_dtype=None):
+    """Atop-N calibration step (attention/attention.py:173-189).
+
+    threshold_out: fp32 [b*q_h], receives the k-th largest probability per row.
+    """
+    dev, query, key, value, mask = _decode_prep(query, key, value, attention_mask, kv_len)
+    b, q_h, _, d = query.shape
+    L = key.shape[2]
+    if threshold_out.dtype != torch.float32 or not threshold_out.is_contiguous() or threshold_out.numel() < b * q_h:
+        raise ValueError("saga_amd: threshold_out must be contiguous fp32 with b*q_h entries")
+    if out is None:
+        out = torch.empty(b, q_h, 1, d, dtype=out_dtype or query.dtype, device=dev)
+    lib = _lib.load()
+    buf_k = min(top_n, L)
+    ws = workspace(dev, "atopn", lib.saga_atopn_workspace_bytes(b, q_h, L, d, buf_k))
+    _lib.check(lib.saga_atopn_calibrate(_lib.tensor(query), _lib.tensor(key), _lib.tensor(value), _lib.tensor(mask),
+                                        _lib.ptr(_kv_len(kv_len)), _scale(query, scaling), int(top_n),
+                                        _lib.ptr(threshold_out), _lib.tensor(out), _lib.ptr(ws), ws.numel(),
+                                        _lib.stream_of(query)), "atopn_calibrate")
+    return out
+
+
+def dense_decode(query, key, value, attention_mask=None, scaling=None, kv_len=None, out=None, out_dtype=None):
+    """Dense decode attention (attention/attention.py:64-85, l_q == 1)."""
+    dev, query, key, value, mask = _decode_prep(query, key, value, attention_mask, kv_len)
+    b, q_h, _, d = query.shape
+    L = key.shape[2]
+    if out is None:
+        out = torch.empty(b, q_h, 1, d, dtype=out_dtype or query.dtype, device=dev)
+    lib = _lib.load()
+    ws = workspace(dev, "dense", lib.saga_dense_workspace_bytes(b, q_h, L, d))
+    _lib.check(lib.saga_dense_decode(_lib.tensor(query), _lib.tensor(key), _lib.tensor(value), _lib.tensor(mask),
+                                     _lib.ptr(_kv_len(kv_len)), _scale(query, scaling), _lib.tensor(out),
+                                     _lib.ptr(ws), ws.numel(), _lib.stream_of(query)), "dense_decode")
+    return out
+
+
+def atopn_workspace_views(b: int, q_h: int, L: int, d: int, buf_k: int, device) -> dict:
+    """Views into the cached fused-decode workspace (thresholds, counts,
+    selected indices) for inspection after a call; valid until the next call."""
+    lay = _lib.atopn_layout(b, q_h, L, d, buf_k)
+    ws = _WORKSPACES[(torch.device(device), "atopn")]
+    nr = b * q_h
+
+    def view(off, n, dt):
+        es = torch.tensor([], dtype=dt).element_size()
+        return ws[off:off + n * es].view(dt)
+
+    return {
+        "thresh": view(lay.thresh, nr, torch.float32),
+        "sel_cnt": view(lay.sel_cnt, nr, torch.int32),
+        "sel_total": view(lay.sel_total, nr, torch.int32),
+        "sel_idx": view(lay.sel_idx, nr * buf_k, torch.int32).reshape(nr, buf_k),
+        "sel_val": view(lay.sel_val, nr * buf_k, torch.float32).reshape(nr, buf_k),
+        "scores": view(lay.scores, nr * lay.scores_ld, torch.float32).reshape(nr, lay.scores_ld)[:, :L],
+    }

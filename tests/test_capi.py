@@ -1,0 +1,152 @@
+"""C ABI of libsaga_amd.so on the CPU: it loads, exports every symbol the
+header declares, sizes workspaces, and rejects bad arguments with an error
+code and message before anything is launched (no GPU needed)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from saga_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "saga_amd.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(saga_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_symbols()
+    assert len(names) >= 13
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(_lib._SIGS), "ctypes signatures and header declarations differ"
+    assert lib.saga_version() == 100
+
+
+def _t(shape, dtype=_lib.DTYPE_BF16, data=0x100000, strides=None):
+    d = _lib.SagaTensor()
+    d.data = data
+    d.dtype = dtype
+    d.ndim = len(shape)
+    if strides is None:
+        strides, acc = [], 1
+        for n in reversed(shape):
+            strides.insert(0, acc)
+            acc *= n
+    for i, (n, s) in enumerate(zip(shape, strides)):
+        d.shape[i] = n
+        d.stride[i] = s
+    return d
+
+
+def _call_decode(q, k, v, out, mask=None, top_n=8, ws=0x200000, nbytes=1 << 30, fn="saga_atopn_decode"):
+    lib = _lib.load()
+    return getattr(lib, fn)(ctypes.byref(q), ctypes.byref(k), ctypes.byref(v),
+                            ctypes.byref(mask) if mask is not None else None, None, 0.125, top_n,
+                            ctypes.c_void_p(0x300000), ctypes.byref(out), ctypes.c_void_p(ws), nbytes, None)
+
+
+def _err():
+    return _lib.load().saga_last_error().decode()
+
+
+GOOD = dict(q=(2, 12, 1, 128), k=(2, 1, 64, 128), v=(2, 2, 64, 128), out=(2, 12, 1, 128))
+
+
+def _good():
+    return {n: _t(s) for n, s in GOOD.items()}
+
+
+@pytest.mark.parametrize("mutate,code,needle", [
+    (lambda a: a.__setitem__("q", _t((2, 12, 2, 128))), -2, "l_q == 1"),
+    (lambda a: a.__setitem__("k", _t((2, 5, 64, 128))), -1, "multiple of k_h"),
+    (lambda a: a.__setitem__("v", _t((2, 5, 64, 128))), -1, "multiple of v_h"),
+    (lambda a: a.__setitem__("v", _t((2, 2, 63, 128))), -1, "value: shape"),
+    (lambda a: a.update(q=_t((2, 12, 1, 96)), k=_t((2, 1, 64, 96)), v=_t((2, 2, 64, 96)),
+                        out=_t((2, 12, 1, 96))), -2, "head_dim"),
+    (lambda a: a.update(q=_t((2, 32, 1, 128)), out=_t((2, 32, 1, 128))), -2, "q_h / k_h"),
+    (lambda a: a.__setitem__("k", _t((2, 1, 64, 128), dtype=_lib.DTYPE_F32)), -1, "dtype differs"),
+    (lambda a: a.__setitem__("q", _t((2, 12, 1, 128), data=0x100002)), -1, "16-byte aligned"),
+    (lambda a: a.__setitem__("k", _t((2, 1, 64, 128), strides=(64 * 130, 64 * 130, 130, 1))), -1, "multiple of 16"),
+    (lambda a: a.__setitem__("out", _t((2, 12, 1, 64))), -1, "out: shape"),
+    (lambda a: a.__setitem__("q", _t((2, 12, 1, 128), data=0)), -1, "null data"),
+])
+def test_decode_argument_errors(mutate, code, needle):
+    a = _good()
+    mutate(a)
+    rc = _call_decode(a["q"], a["k"], a["v"], a["out"])
+    assert rc == code, _err()
+    assert needle in _err()
+
+
+def test_decode_rejects_bad_mask_and_topn_and_workspace():
+    a = _good()
+    rc = _call_decode(a["q"], a["k"], a["v"], a["out"], mask=_t((2, 1, 1, 63), dtype=_lib.DTYPE_BOOL))
+    assert rc == -1 and "mask" in _err()
+    rc = _call_decode(a["q"], a["k"], a["v"], a["out"], mask=_t((2, 1, 1, 64), dtype=_lib.DTYPE_I32))
+    assert rc == -1 and "mask: dtype" in _err()
+    rc = _call_decode(a["q"], a["k"], a["v"], a["out"], top_n=0)
+    assert rc == -1 and "top_n" in _err()
+    rc = _call_decode(a["q"], a["k"], a["v"], a["out"], nbytes=100)
+    assert rc == -3 and "workspace" in _err()
+    rc = _call_decode(a["q"], a["k"], a["v"], a["out"], ws=0x200010)
+    assert rc == -3 and "aligned" in _err()
+
+
+def test_null_descriptor_is_an_error_not_a_crash():
+    lib = _lib.load()
+    rc = lib.saga_atopn_decode(None, None, None, None, None, 1.0, 8, None, None, None, 0, None)
+    assert rc == -1 and "null" in _err()
+    rc = lib.saga_threshold_select(None, None, 0, 4, None, None, None, None)
+    assert rc == -1
+
+
+def test_threshold_select_argument_errors():
+    lib = _lib.load()
+    x = _t((4, 100), dtype=_lib.DTYPE_F32)
+    vals = _t((4, 8), dtype=_lib.DTYPE_F32)
+    bad_vals = _t((4, 8), dtype=_lib.DTYPE_BF16)
+    thr = ctypes.c_void_p(0x400000)
+    idx = ctypes.c_void_p(0x500000)
+    assert lib.saga_threshold_select(ctypes.byref(x), thr, 0, 8, ctypes.byref(vals), idx, None, None) == -1
+    assert lib.saga_threshold_select(ctypes.byref(x), thr, 4, 8, ctypes.byref(bad_vals), idx, None, None) == -1
+    assert "dtype must match" in _err()
+    assert lib.saga_threshold_select(ctypes.byref(x), thr, 4, 9, ctypes.byref(vals), idx, None, None) == -1
+    strided = _t((2, 2, 100), dtype=_lib.DTYPE_F32, strides=(1000, 100, 1))
+    assert lib.saga_threshold_select(ctypes.byref(strided), thr, 4, 8, ctypes.byref(vals), idx, None, None) == -1
+    assert "collapsible" in _err()
+
+
+def test_workspace_sizes_and_layout():
+    lib = _lib.load()
+    lay = _lib.atopn_layout(8, 12, 33024, 128, 1024)
+    offs = [lay.scores, lay.part_max, lay.part_sum, lay.thresh, lay.sel_idx, lay.sel_val, lay.sel_cnt,
+            lay.sel_total, lay.part_out, lay.counters]
+    assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
+    assert lay.scores_ld % 16 == 0 and lay.scores_ld >= 33024
+    assert lay.nchunk == (33024 + 127) // 128
+    assert lay.total_bytes == lib.saga_atopn_workspace_bytes(8, 12, 33024, 128, 1024)
+    assert lay.part_max - lay.scores >= 96 * 33024 * 4
+    assert lib.saga_dense_workspace_bytes(8, 12, 33024, 128) > 0
+    assert lib.saga_sparse_pv_workspace_bytes(8, 12, 128, 1024) >= 96 * 8 * 130 * 4
+    bad = _lib.AtopnLayout()
+    assert lib.saga_atopn_workspace_layout(0, 12, 10, 128, 4, ctypes.byref(bad)) == -1
+
+
+def test_ops_refuse_cpu_tensors():
+    import torch
+    from saga_amd import ops
+    q = torch.zeros(1, 2, 1, 64)
+    k = torch.zeros(1, 1, 8, 64)
+    v = torch.zeros(1, 2, 8, 64)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.dense_decode(q, k, v)
+    import attention.attention as A
+    A.init_amortized_threshold_tensor("cpu", A.MAX_LAYERS, 2)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        A.approx_top_n_attention_amortized(q, k, v, top_n_attention=4)
