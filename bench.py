@@ -1,0 +1,253 @@
+#!/usr/bin/env python
+"""Decode throughput of the SAGA + Atop-N path on one MI355X.
+
+Workload (the headline configuration): a Qwen2.5-1.5B-shaped SAGA decoder
+(28 layers, hidden 1536, 12 query / 1 key / 2 value heads, head_dim 128,
+vocab 151936), random-init bf16 weights, batch 8, a 32768-token random-id
+prompt prefilled at batch 1 and replicated (as speedup.py:146-161), then
+`--steps` decode steps with Atop-N N=512 (the first step calibrates),
+replayed as HIP graphs.  value = batch * steps / decode wall time.
+
+Also reported on the same line:
+  roofline      the dominant kernel (K1, QK scores streaming the K cache):
+                algorithmic bytes per launch / its average duration, timed
+                with HIP events over a graph of launches on the stream they
+                run on, against the 8 TB/s HBM peak;
+  cpu_baseline  the CPU oracle (the reference's fp32 path restated in numpy)
+                on a bounded sample: one decode step of attention over the
+                28 layers at the same shapes, as attention tokens/s;
+  dense_gqa     the same harness with 2 key / 2 value heads and the dense
+                split-L decode kernel (the in-house dense-GQA comparator).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "decode tokens/sec @1.5B-shape 32k ctx; attn kernel HBM GB/s vs peak"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def timed_graph(fn, n_launch, repeats=3):
+    """Average time (us) of one of `n_launch` fn(i) calls captured in a graph."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(2):
+            fn(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n_launch):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    best = None
+    for _ in range(repeats):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1000.0 / n_launch
+        best = us if best is None else min(best, us)
+    return best
+
+
+def decode_rate(model, steps, warmup):
+    """Warm-up replays, then exactly `steps` timed replays bracketed by syncs."""
+    model.reset()
+    for i in range(warmup):
+        model.replay(i)
+    torch.cuda.synchronize()
+    model.reset()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for i in range(steps):
+        model.replay(i)
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1)
+    return ms / steps, model.batch * steps / (ms / 1000.0), wall
+
+
+def cpu_baseline(batch, ctx, shape, top_n, layers):
+    """The oracle (reference fp32 path) on one decode step of attention."""
+    from oracle import saga_oracle as O
+    try:
+        from threadpoolctl import threadpool_limits
+    except ImportError:  # pragma: no cover
+        threadpool_limits = None
+    cores = min(16, os.cpu_count() or 1)
+    rng = np.random.default_rng(0)
+    L = ctx + 1
+    q = rng.standard_normal((batch, shape.n_q, 1, shape.head_dim), dtype=np.float32)
+    k = rng.standard_normal((batch, shape.n_k, L, shape.head_dim), dtype=np.float32)
+    v = rng.standard_normal((batch, shape.n_v, L, shape.head_dim), dtype=np.float32)
+    q2 = q + np.float32(0.3) * rng.standard_normal(q.shape, dtype=np.float32)
+
+    def run():
+        t0 = time.perf_counter()
+        _, thr, _ = O.calibrate(q, k, v, None, top_n, None)
+        for _ in range(layers - 1):
+            O.fast(q2, k, v, thr, None, top_n, None)
+        return time.perf_counter() - t0
+
+    if threadpool_limits is not None:
+        with threadpool_limits(limits=cores):
+            secs = run()
+    else:
+        secs = run()
+    return {
+        "value": round(batch / secs, 3),
+        "unit": "tokens/s (attention only, 28 layers)",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"one decode step: {layers} layers of Atop-N attention (1 calibration + {layers - 1} fast), "
+                   f"b{batch} q{shape.n_q}/k{shape.n_k}/v{shape.n_v} d{shape.head_dim} ctx {L}, fp32, "
+                   f"numpy oracle, {secs:.1f} s"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=8)
+    ap.add_argument("--ctx", type=int, default=32768)
+    ap.add_argument("--top-n", type=int, default=512)
+    ap.add_argument("--no-dense", action="store_true", help="skip the dense-GQA comparator")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--synthetic-kv", action="store_true", help="fill the caches with N(0,1) instead of a prefill")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(sharding is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+
+    from saga_amd import ops
+    from saga_amd.decoder import QWEN25_15B_GQA, QWEN25_15B_SAGA, SagaDecoder
+
+    B, ctx, K, W = args.batch, args.ctx, args.steps, args.warmup
+    max_len = ctx + K
+    torch.manual_seed(0)
+    prompt = torch.randint(0, QWEN25_15B_SAGA.vocab, (ctx,), dtype=torch.int64)
+
+    def build(shape, mode):
+        m = SagaDecoder(shape, B, max_len, mode=mode, top_n=args.top_n)
+        t0 = time.perf_counter()
+        if args.synthetic_kv:
+            m.fill_synthetic(ctx)
+        else:
+            m.prefill(prompt)
+        torch.cuda.synchronize()
+        log(f"{mode} model: prefill {time.perf_counter() - t0:.2f}s")
+        m.capture()
+        return m
+
+    log("SAGA model (12Q/1K/2V, Atop-N)")
+    saga = build(QWEN25_15B_SAGA, "atopn")
+    ms, tps, wall = decode_rate(saga, K, W)
+    log(f"SAGA decode: {ms:.3f} ms/step, {tps:.0f} tokens/s (host wall {wall:.3f}s)")
+
+    # dominant kernel: K1 over the 28 layers' K caches, at the decode shape
+    s = saga.shape
+    q4 = saga._q.view(B, s.n_q, 1, s.head_dim)
+    kvl = torch.full((B,), ctx + 1, dtype=torch.int32, device="cuda")
+    nlaunch = 2 * s.layers
+    k1_us = timed_graph(lambda i: ops.qk_scores(q4, saga.k_cache[i % s.layers], kv_len=kvl, with_partials=True),
+                        nlaunch)
+    k1_bytes = B * s.n_k * (ctx + 1) * s.head_dim * 2 + B * s.n_q * s.head_dim * 2
+    k1_gbs = k1_bytes / (k1_us * 1e-6) / 1e9
+    attn_us = timed_graph(lambda i: ops.atopn_decode(q4, saga.k_cache[i % s.layers], saga.v_cache[i % s.layers],
+                                                     saga.table[i % s.layers], args.top_n, kv_len=kvl,
+                                                     out=saga._attn), nlaunch)
+    log(f"K1 qk_scores: {k1_us:.2f} us/launch, {k1_gbs:.0f} GB/s; Atop-N fast attention {attn_us:.2f} us/layer")
+    saga_cache = saga.k_cache.shape, saga.v_cache.shape
+    del saga
+    torch.cuda.empty_cache()
+
+    dense = None
+    if not args.no_dense:
+        log("dense-GQA comparator (12Q/2K/2V, dense decode)")
+        gqa = build(QWEN25_15B_GQA, "dense")
+        d_ms, d_tps, _ = decode_rate(gqa, K, W)
+        gs = gqa.shape
+        dq = gqa._q.view(B, gs.n_q, 1, gs.head_dim)
+        d_attn_us = timed_graph(lambda i: ops.dense_decode(dq, gqa.k_cache[i % gs.layers], gqa.v_cache[i % gs.layers],
+                                                           kv_len=kvl, out=gqa._attn), nlaunch)
+        dense = {"tokens_per_s": round(d_tps, 1), "ms_per_step": round(d_ms, 4),
+                 "attention_us_per_layer": round(d_attn_us, 2), "speedup_saga_vs_dense": round(tps / d_tps, 3)}
+        log(f"dense GQA decode: {d_ms:.3f} ms/step, {d_tps:.0f} tokens/s, attention {d_attn_us:.2f} us/layer; "
+            f"SAGA speedup {tps / d_tps:.2f}x")
+        del gqa
+        torch.cuda.empty_cache()
+
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baseline (oracle, fp32)")
+        cpu = cpu_baseline(B, ctx, QWEN25_15B_SAGA, args.top_n, QWEN25_15B_SAGA.layers)
+        log(f"CPU: {cpu['value']} attention tokens/s on {cpu['cores']} cores")
+
+    out = {
+        "metric": METRIC,
+        "value": round(tps, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: random-init weights, random prompt ids" + (", N(0,1) KV cache" if args.synthetic_kv else ""),
+        "config": {
+            "workload": (f"Qwen2.5-1.5B-shaped SAGA decoder (28 layers, hidden 1536, 12Q/1K/2V heads, d128, "
+                         f"vocab 151936), batch {B}, {ctx}-token context, {K} decode steps, Atop-N N={args.top_n}"),
+            "global_batch": B,
+            "seq_len": ctx,
+            "parallelism": "single GPU",
+            "kv_cache": {"k": list(saga_cache[0]), "v": list(saga_cache[1]), "dtype": "bf16"},
+        },
+        "roofline": {
+            "kernel": "saga::qk_scores_kernel<bf16,128,8> (K1)",
+            "bound": "hbm",
+            "achieved": round(k1_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(k1_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "us_per_launch": round(k1_us, 3),
+            "algorithmic_bytes_per_launch": k1_bytes,
+        },
+        "attention_us_per_layer": round(attn_us, 2),
+        "attention_tokens_per_s_gpu": round(B / (attn_us * 1e-6 * QWEN25_15B_SAGA.layers), 1),
+        "dense_gqa": dense,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

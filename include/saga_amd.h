@@ -32,9 +32,9 @@
  *   - Return value: SAGA_OK or a negative SAGA_ERR_* code; the message of
  *     the last error on the calling thread is in saga_last_error().  Nothing
  *     aborts and no C++ exception crosses this boundary.
- *   - Workspace buffers must be zero-filled once when allocated; the kernels
- *     leave the counters they use at zero after every call.  Two calls that
- *     share a workspace must be ordered (same stream).
+ *   - Workspaces are caller-allocated device buffers of the size the
+ *     matching *_workspace_bytes() returns; no initial contents are needed.
+ *     Calls that share a workspace must be ordered (same stream).
  */
 #ifndef SAGA_AMD_H
 #define SAGA_AMD_H
@@ -85,9 +85,6 @@ typedef struct saga_atopn_layout {
   int64_t sel_val;   /* f32 [b*q_h, buf_k] their logits */
   int64_t sel_cnt;   /* i32 [b*q_h] kept (<= buf_k) */
   int64_t sel_total; /* i32 [b*q_h] passing before the cap */
-  int64_t part_out;  /* f32 [b*q_h, npiece, 2 + d] softmax.V partials */
-  int64_t npiece;
-  int64_t counters;  /* i32 [b*q_h] arrival counters (self-resetting) */
   int64_t total_bytes;
 } saga_atopn_layout;
 
@@ -134,13 +131,13 @@ int saga_threshold_select(const saga_tensor* x, const float* threshold, int64_t 
 /* Softmax (or renormalisation) over K selected entries per row, then . V.
  * Replaces _atopn_gather_and_output, attention/attention.py:152-170.
  * weights [b, q_h, 1, K] (f32/bf16/f16; logits if input_is_logits, else
- * probabilities), indices int64 [b, q_h, 1, K], value [b, v_h, L, d],
- * out [b, q_h, 1, d] (f32/bf16/f16).  An all -inf logit row gives NaN, as
- * torch's softmax does.  workspace: saga_sparse_pv_workspace_bytes(). */
-size_t saga_sparse_pv_workspace_bytes(int64_t b, int64_t q_h, int64_t d, int64_t K);
+ * probabilities), indices int64 or int32 [b, q_h, 1, K], value
+ * [b, v_h, L, d], out [b, q_h, 1, d] (f32/bf16/f16).  An all -inf logit row
+ * gives NaN, as torch's softmax does; an index outside [0, L) makes its row
+ * NaN (the reference's gather raises). */
 int saga_sparse_softmax_pv(const saga_tensor* weights, const saga_tensor* indices,
                            const saga_tensor* value, int32_t input_is_logits, saga_tensor* out,
-                           void* workspace, size_t workspace_bytes, saga_stream_t stream);
+                           saga_stream_t stream);
 
 /* Workspace of the fused decode entry points; buf_k = min(2*top_n, L) for
  * saga_atopn_decode, min(top_n, L) for saga_atopn_calibrate. */
@@ -178,6 +175,30 @@ int saga_dense_decode(const saga_tensor* query, const saga_tensor* key, const sa
                       const saga_tensor* mask, const int32_t* kv_len, float scale,
                       saga_tensor* out, void* workspace, size_t workspace_bytes,
                       saga_stream_t stream);
+
+/* ---- decode-step kernels around the attention path ---- */
+
+/* RoPE + KV-cache append for N new tokens.
+ * Replaces apply_rotary_pos_emb + the cache update of the reference's model
+ * (transformers models/qwen2/modeling_qwen2.py:211-214, cache_utils.py:455-487)
+ * with the separate key / value caches of speedup.py:119-139.
+ * qkv [N, >= (n_q + n_k + n_v) * d]: the fused projection output (bias
+ * included), heads in the order q, k, v.  Rotation (rotate-half form, fp32):
+ * angle_i = pos * theta^(-2i/d).  q_out [N, n_q, d] receives the rotated
+ * queries; k_cache [B, n_k, Lmax, d] / v_cache [B, n_v, Lmax, d] receive the
+ * rotated key and the value at [batch[n], :, pos[n]] (batch == NULL: token n
+ * is batch row n).  A pos or batch index out of range writes no cache row and
+ * NaN queries. */
+int saga_rope_kv_append(const saga_tensor* qkv, int64_t n_q, int64_t n_k, int64_t n_v, float theta,
+                        const int32_t* pos, const int32_t* batch, saga_tensor* q_out,
+                        saga_tensor* k_cache, saga_tensor* v_cache, saga_stream_t stream);
+
+/* y = weight * x / sqrt(mean(x^2) + eps) per row, x and y [N, H] (Qwen2RMSNorm). */
+int saga_rmsnorm(const saga_tensor* x, const saga_tensor* weight, float eps, saga_tensor* y,
+                 saga_stream_t stream);
+
+/* y[n, i] = silu(x[n, i]) * x[n, H + i]; x [N, 2H] = [gate | up], y [N, H]. */
+int saga_silu_mul(const saga_tensor* gate_up, saga_tensor* y, saga_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -237,3 +237,40 @@ def truncate_kv(key, value, kv_len):
     is "the reference applied to the key/value truncated to that length".
     """
     return [(key[i:i + 1, :, :int(n)], value[i:i + 1, :, :int(n)]) for i, n in enumerate(kv_len)]
+
+
+# --------------------------------------------------------------------------
+# Decode-step ops around the attention path.  Their reference is the model
+# the reference benchmarks (transformers Qwen2, installed version 5.15.0; the
+# reference pins 5.3.0, which is not in this container):
+#   TF = transformers/models/qwen2/modeling_qwen2.py
+# Pinned in tests/test_oracle.py by brute-force loops and identities.
+
+def rope_inv_freq(d, theta):
+    """TF:86 inv_freq = 1 / theta^(arange(0, d, 2) / d), computed in fp32."""
+    return (1.0 / (np.float32(theta) ** (np.arange(0, d, 2, dtype=np.float32) / np.float32(d)))).astype(np.float32)
+
+
+def rope(x, pos, theta):
+    """TF:97-120 rotate-half RoPE of x [..., d] at integer positions pos
+    (broadcast over the leading dims): x*cos + rotate_half(x)*sin with
+    cos/sin of cat(freqs, freqs), freqs = pos * inv_freq (fp32)."""
+    d = x.shape[-1]
+    ang = np.asarray(pos, dtype=np.float32)[..., None] * rope_inv_freq(d, theta)
+    c, s = np.cos(ang.astype(np.float64)), np.sin(ang.astype(np.float64))
+    x1, x2 = x[..., : d // 2].astype(np.float64), x[..., d // 2:].astype(np.float64)
+    return np.concatenate([x1 * c - x2 * s, x2 * c + x1 * s], axis=-1)
+
+
+def rmsnorm(x, w, eps):
+    """TF:247-253 w * x / sqrt(mean(x^2) + eps) over the last axis (float64)."""
+    x = np.asarray(x, dtype=np.float64)
+    return np.asarray(w, dtype=np.float64) * (x / np.sqrt((x * x).mean(axis=-1, keepdims=True) + eps))
+
+
+def silu_mul(gate_up):
+    """TF:46-47 act_fn(gate) * up with act = silu, gate_up = [gate | up]."""
+    g = np.asarray(gate_up, dtype=np.float64)
+    h = g.shape[-1] // 2
+    gate, up = g[..., :h], g[..., h:]
+    return gate / (1.0 + np.exp(-gate)) * up

@@ -43,7 +43,7 @@ class SagaTensor(ctypes.Structure):
 class AtopnLayout(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int64) for n in (
         "scores", "scores_ld", "part_max", "part_sum", "nchunk", "thresh", "sel_idx", "sel_val",
-        "sel_cnt", "sel_total", "part_out", "npiece", "counters", "total_bytes")]
+        "sel_cnt", "sel_total", "total_bytes")]
 
 
 # Every symbol include/saga_amd.h declares, with its ctypes signature.
@@ -56,14 +56,16 @@ _SIGS = {
     "saga_qk_scores": (ctypes.c_int, [_T, _T, _T, _P, ctypes.c_float, _T, _P, _P, _P]),
     "saga_logit_threshold": (ctypes.c_int, [_T, _P, _P, _P, _P]),
     "saga_threshold_select": (ctypes.c_int, [_T, _P, _I64, _I64, _T, _P, _P, _P]),
-    "saga_sparse_pv_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I64]),
-    "saga_sparse_softmax_pv": (ctypes.c_int, [_T, _T, _T, ctypes.c_int32, _T, _P, ctypes.c_size_t, _P]),
+    "saga_sparse_softmax_pv": (ctypes.c_int, [_T, _T, _T, ctypes.c_int32, _T, _P]),
     "saga_atopn_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I64, _I64]),
     "saga_atopn_workspace_layout": (ctypes.c_int, [_I64, _I64, _I64, _I64, _I64, ctypes.POINTER(AtopnLayout)]),
     "saga_atopn_decode": (ctypes.c_int, [_T, _T, _T, _T, _P, ctypes.c_float, _I64, _P, _T, _P, ctypes.c_size_t, _P]),
     "saga_atopn_calibrate": (ctypes.c_int, [_T, _T, _T, _T, _P, ctypes.c_float, _I64, _P, _T, _P, ctypes.c_size_t, _P]),
     "saga_dense_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I64]),
     "saga_dense_decode": (ctypes.c_int, [_T, _T, _T, _T, _P, ctypes.c_float, _T, _P, ctypes.c_size_t, _P]),
+    "saga_rope_kv_append": (ctypes.c_int, [_T, _I64, _I64, _I64, ctypes.c_float, _P, _P, _T, _T, _T, _P]),
+    "saga_rmsnorm": (ctypes.c_int, [_T, _T, ctypes.c_float, _T, _P]),
+    "saga_silu_mul": (ctypes.c_int, [_T, _T, _P]),
 }
 
 _lock = threading.Lock()

@@ -50,7 +50,6 @@ bool is_float(int dt) {
 
 constexpr int64_t kMaxLen = (1LL << 30);  // positions are int32 inside kernels
 constexpr int kMaxGroup = 16;             // query heads per key head (one MFMA column tile)
-constexpr int kPiece = 128;               // selection entries per sparse-PV block
 
 int64_t align256(int64_t x) { return (x + 255) & ~static_cast<int64_t>(255); }
 
@@ -169,10 +168,10 @@ QKParams make_qk(const saga_tensor* q, const saga_tensor* k, const saga_tensor* 
 }
 
 void atopn_layout(int64_t b, int64_t q_h, int64_t L, int64_t d, int64_t buf_k, saga_atopn_layout* o) {
+  (void)d;
   const int64_t nr = b * q_h;
   const int64_t ld = (L + 15) / 16 * 16;
   const int64_t nchunk = (L + SAGA_CHUNK - 1) / SAGA_CHUNK;
-  const int64_t npiece = buf_k <= kPiece ? 1 : (buf_k + kPiece - 1) / kPiece;
   int64_t off = 0;
   auto take = [&](int64_t bytes) {
     const int64_t at = off;
@@ -181,7 +180,6 @@ void atopn_layout(int64_t b, int64_t q_h, int64_t L, int64_t d, int64_t buf_k, s
   };
   o->scores_ld = ld;
   o->nchunk = nchunk;
-  o->npiece = npiece;
   o->scores = take(nr * ld * 4);
   o->part_max = take(nr * nchunk * 4);
   o->part_sum = take(nr * nchunk * 4);
@@ -190,8 +188,6 @@ void atopn_layout(int64_t b, int64_t q_h, int64_t L, int64_t d, int64_t buf_k, s
   o->sel_val = take(nr * buf_k * 4);
   o->sel_cnt = take(nr * 4);
   o->sel_total = take(nr * 4);
-  o->part_out = take(nr * npiece * (2 + d) * 4);
-  o->counters = take(nr * 4);
   o->total_bytes = off;
 }
 
@@ -261,32 +257,18 @@ int atopn_run(bool calibrate, const saga_tensor* query, const saga_tensor* key, 
   sp.sel_val = reinterpret_cast<float*>(ws + lay.sel_val);
   sp.sel_cnt = reinterpret_cast<int32_t*>(ws + lay.sel_cnt);
   sp.sel_total = reinterpret_cast<int32_t*>(ws + lay.sel_total);
-  rc = calibrate ? hip_status(launch_select_calibrate(sp, st), "select_calibrate launch")
-                 : hip_status(launch_select_fast(sp, st), "select_fast launch");
-  if (rc) return rc;
-
-  PVParams pp = make_pv(value, out, s);
-  pp.w = sp.sel_val;
-  pp.w_dt = SAGA_DTYPE_F32;
-  pp.w_ld = buf_k;
-  pp.idx = sp.sel_idx;
-  pp.idx_i64 = 0;
-  pp.i_ld = buf_k;
-  pp.cnt = sp.sel_cnt;
-  pp.K = static_cast<int32_t>(buf_k);
-  pp.probs_mode = 0;  // calibration: softmax over the top-k logits == renormalised top-k probabilities
-  pp.part = reinterpret_cast<float*>(ws + lay.part_out);
-  pp.npiece = static_cast<int32_t>(lay.npiece);
-  pp.piece = lay.npiece == 1 ? static_cast<int32_t>(buf_k) : kPiece;
-  pp.counters = reinterpret_cast<int32_t*>(ws + lay.counters);
-  if ((rc = hip_status(launch_sparse_pv(pp, st), "sparse_pv launch"))) return rc;
+  // calibration: softmax over the top-k logits == renormalised top-k probabilities
+  const PVParams pp = make_pv(value, out, s);
+  if ((rc = hip_status(launch_atopn_select_pv(calibrate, sp, pp, st), "atopn select/pv launch"))) return rc;
   return ok();
 }
 
-// Dense split plan: about 512 blocks in flight, splits of >= 512 positions,
-// split length a multiple of the 32-position wave step.
-void dense_plan(int64_t b, int64_t L, int64_t* nsplit, int64_t* split_len) {
-  int64_t ns = (512 + b - 1) / b;
+// Dense split plan: about 512 blocks over the (batch, key head) units,
+// splits of >= 512 positions, split length a multiple of the 32-position wave
+// step.  The split count never grows with the number of units, so the
+// workspace bound computed for k_h = 1 covers every k_h.
+void dense_plan(int64_t units, int64_t L, int64_t* nsplit, int64_t* split_len) {
+  int64_t ns = (512 + units - 1) / units;
   const int64_t by_len = (L + 511) / 512;
   if (ns > by_len) ns = by_len;
   if (ns < 1) ns = 1;
@@ -404,15 +386,8 @@ int saga_threshold_select(const saga_tensor* x, const float* threshold, int64_t 
   return ok();
 }
 
-size_t saga_sparse_pv_workspace_bytes(int64_t b, int64_t q_h, int64_t d, int64_t K) {
-  const int64_t nr = b * q_h;
-  const int64_t npiece = K <= kPiece ? 1 : (K + kPiece - 1) / kPiece;
-  return static_cast<size_t>(align256(nr * npiece * (2 + d) * 4) + align256(nr * 4));
-}
-
 int saga_sparse_softmax_pv(const saga_tensor* weights, const saga_tensor* indices, const saga_tensor* value,
-                           int32_t input_is_logits, saga_tensor* out, void* workspace, size_t workspace_bytes,
-                           saga_stream_t stream) {
+                           int32_t input_is_logits, saga_tensor* out, saga_stream_t stream) {
   int rc;
   if ((rc = check_tensor(weights, "weights", 4)) || (rc = check_tensor(indices, "indices", 4))) return rc;
   Shape s{};
@@ -436,13 +411,6 @@ int saga_sparse_softmax_pv(const saga_tensor* weights, const saga_tensor* indice
       (s.b > 1 && indices->stride[0] != s.q_h * indices->stride[1]))
     return fail(SAGA_ERR_INVALID, "weights/indices: rows must be uniformly strided with unit innermost stride");
   if (K >= kMaxLen) return fail(SAGA_ERR_UNSUPPORTED, "K too large");
-  const int64_t nr = s.b * s.q_h;
-  const int64_t npiece = K <= kPiece ? 1 : (K + kPiece - 1) / kPiece;
-  const size_t need = saga_sparse_pv_workspace_bytes(s.b, s.q_h, s.d, K);
-  if (npiece > 1 && (!workspace || workspace_bytes < need))
-    return fail(SAGA_ERR_WORKSPACE, "workspace of %zu bytes, need %zu", workspace_bytes, need);
-  if (npiece > 1 && reinterpret_cast<uintptr_t>(workspace) % 256)
-    return fail(SAGA_ERR_WORKSPACE, "workspace must be 256-byte aligned");
   PVParams p = make_pv(value, out, s);
   p.w = weights->data;
   p.w_dt = weights->dtype;
@@ -450,17 +418,8 @@ int saga_sparse_softmax_pv(const saga_tensor* weights, const saga_tensor* indice
   p.idx = indices->data;
   p.idx_i64 = indices->dtype == SAGA_DTYPE_I64;
   p.i_ld = indices->stride[1];
-  p.cnt = nullptr;
   p.K = static_cast<int32_t>(K);
   p.probs_mode = input_is_logits ? 0 : 1;
-  p.npiece = static_cast<int32_t>(npiece);
-  p.piece = npiece == 1 ? static_cast<int32_t>(K) : kPiece;
-  if (npiece > 1) {
-    char* ws = static_cast<char*>(workspace);
-    p.part = reinterpret_cast<float*>(ws);
-    p.counters = reinterpret_cast<int32_t*>(ws + align256(nr * npiece * (2 + s.d) * 4));
-  }
-  if (p.piece > 256) return fail(SAGA_ERR_UNSUPPORTED, "internal: piece size");
   if ((rc = hip_status(launch_sparse_pv(p, static_cast<hipStream_t>(stream)), "sparse_pv launch"))) return rc;
   return ok();
 }
@@ -498,7 +457,7 @@ int saga_atopn_calibrate(const saga_tensor* query, const saga_tensor* key, const
 size_t saga_dense_workspace_bytes(int64_t b, int64_t q_h, int64_t L, int64_t d) {
   int64_t ns, sl;
   dense_plan(b, L, &ns, &sl);
-  return static_cast<size_t>(align256(b * q_h * ns * (2 + d) * 4) + align256(b * q_h * 4));
+  return static_cast<size_t>(align256(b * q_h * ns * (2 + d) * 4));
 }
 
 int saga_dense_decode(const saga_tensor* query, const saga_tensor* key, const saga_tensor* value,
@@ -508,8 +467,8 @@ int saga_dense_decode(const saga_tensor* query, const saga_tensor* key, const sa
   int rc;
   if ((rc = check_qk(query, key, mask, &s)) || (rc = check_v(value, &s)) || (rc = check_out(out, s))) return rc;
   int64_t ns, sl;
-  dense_plan(s.b, s.L, &ns, &sl);
-  const size_t need = saga_dense_workspace_bytes(s.b, s.q_h, s.L, s.d);
+  dense_plan(s.b * s.k_h, s.L, &ns, &sl);
+  const size_t need = static_cast<size_t>(s.b * s.q_h * ns * (2 + s.d) * 4);
   if (ns > 1 && (!workspace || workspace_bytes < need))
     return fail(SAGA_ERR_WORKSPACE, "workspace of %zu bytes, need %zu", workspace_bytes, need);
   if (ns > 1 && reinterpret_cast<uintptr_t>(workspace) % 256)
@@ -546,15 +505,98 @@ int saga_dense_decode(const saga_tensor* query, const saga_tensor* key, const sa
   p.o_sh = out->stride[1];
   p.nsplit = static_cast<int32_t>(ns);
   p.split_len = static_cast<int32_t>(sl);
-  if (ns > 1) {
-    char* ws = static_cast<char*>(workspace);
-    p.part = reinterpret_cast<float*>(ws);
-    p.counters = reinterpret_cast<int32_t*>(ws + align256(s.b * s.q_h * ns * (2 + s.d) * 4));
-  }
+  p.part = static_cast<float*>(workspace);
   if ((rc = hip_status(launch_dense_decode(s.dt, static_cast<int>(s.d), p, static_cast<hipStream_t>(stream)),
                        "dense_decode launch")))
     return rc;
   return ok();
+}
+
+int saga_rope_kv_append(const saga_tensor* qkv, int64_t n_q, int64_t n_k, int64_t n_v, float theta,
+                        const int32_t* pos, const int32_t* batch, saga_tensor* q_out, saga_tensor* k_cache,
+                        saga_tensor* v_cache, saga_stream_t stream) {
+  int rc;
+  if ((rc = check_tensor(qkv, "qkv", 2)) || (rc = check_tensor(q_out, "q_out", 3)) ||
+      (rc = check_tensor(k_cache, "k_cache", 4)) || (rc = check_tensor(v_cache, "v_cache", 4)))
+    return rc;
+  if (!pos) return fail(SAGA_ERR_INVALID, "pos: null");
+  if (n_q < 1 || n_k < 1 || n_v < 1) return fail(SAGA_ERR_INVALID, "head counts must be >= 1");
+  const int64_t N = qkv->shape[0];
+  const int64_t d = q_out->shape[2];
+  if (d % 2 || d < 2) return fail(SAGA_ERR_INVALID, "head_dim must be even");
+  if (!is_float(qkv->dtype) || q_out->dtype != qkv->dtype || k_cache->dtype != qkv->dtype || v_cache->dtype != qkv->dtype)
+    return fail(SAGA_ERR_INVALID, "qkv, q_out and the caches must share one float dtype");
+  if (qkv->shape[1] < (n_q + n_k + n_v) * d) return fail(SAGA_ERR_INVALID, "qkv: row shorter than (n_q + n_k + n_v) * d");
+  if (q_out->shape[0] != N || q_out->shape[1] != n_q) return fail(SAGA_ERR_INVALID, "q_out: shape must be [N, n_q, d]");
+  if (k_cache->shape[1] != n_k || k_cache->shape[3] != d || v_cache->shape[1] != n_v || v_cache->shape[3] != d ||
+      v_cache->shape[0] != k_cache->shape[0] || v_cache->shape[2] != k_cache->shape[2])
+    return fail(SAGA_ERR_INVALID, "caches: shapes must be [B, n_k, Lmax, d] and [B, n_v, Lmax, d]");
+  if (qkv->stride[1] != 1 || q_out->stride[2] != 1 || k_cache->stride[3] != 1 || v_cache->stride[3] != 1)
+    return fail(SAGA_ERR_INVALID, "innermost strides must be 1");
+  if (!batch && N > k_cache->shape[0]) return fail(SAGA_ERR_INVALID, "without batch indices N must be <= B");
+  if (N >= (1LL << 31) || k_cache->shape[2] >= kMaxLen) return fail(SAGA_ERR_UNSUPPORTED, "sizes too large");
+  RopeParams p{};
+  p.qkv = qkv->data;
+  p.qkv_ld = qkv->stride[0];
+  p.dt = qkv->dtype;
+  p.N = static_cast<int32_t>(N);
+  p.n_q = static_cast<int32_t>(n_q);
+  p.n_k = static_cast<int32_t>(n_k);
+  p.n_v = static_cast<int32_t>(n_v);
+  p.d = static_cast<int32_t>(d);
+  p.theta = theta;
+  p.pos = pos;
+  p.batch = batch;
+  p.q_out = q_out->data;
+  p.q_sn = q_out->stride[0];
+  p.q_sh = q_out->stride[1];
+  p.k_cache = k_cache->data;
+  p.k_sb = k_cache->stride[0];
+  p.k_sh = k_cache->stride[1];
+  p.k_sl = k_cache->stride[2];
+  p.v_cache = v_cache->data;
+  p.v_sb = v_cache->stride[0];
+  p.v_sh = v_cache->stride[1];
+  p.v_sl = v_cache->stride[2];
+  p.B = static_cast<int32_t>(k_cache->shape[0]);
+  p.Lmax = static_cast<int32_t>(k_cache->shape[2]);
+  if ((rc = hip_status(launch_rope_kv_append(p, static_cast<hipStream_t>(stream)), "rope_kv_append launch"))) return rc;
+  return ok();
+}
+
+static int row_op(bool silu, const saga_tensor* x, const saga_tensor* w, float eps, saga_tensor* y, saga_stream_t stream) {
+  int rc;
+  if ((rc = check_tensor(x, "x", 2)) || (rc = check_tensor(y, "y", 2))) return rc;
+  if (!is_float(x->dtype) || y->dtype != x->dtype) return fail(SAGA_ERR_INVALID, "x and y must share one float dtype");
+  const int64_t H = y->shape[1];
+  if (x->shape[0] != y->shape[0] || x->shape[1] != (silu ? 2 * H : H))
+    return fail(SAGA_ERR_INVALID, silu ? "x must be [N, 2H] for y [N, H]" : "x and y must have the same shape");
+  if (x->stride[1] != 1 || y->stride[1] != 1) return fail(SAGA_ERR_INVALID, "innermost strides must be 1");
+  if (!silu) {
+    if ((rc = check_tensor(w, "weight", 1))) return rc;
+    if (w->dtype != x->dtype || w->shape[0] != H || w->stride[0] != 1) return fail(SAGA_ERR_INVALID, "weight must be [H], same dtype");
+  }
+  RowParams p{};
+  p.x = x->data;
+  p.x_ld = x->stride[0];
+  p.w = silu ? nullptr : w->data;
+  p.y = y->data;
+  p.y_ld = y->stride[0];
+  p.dt = x->dtype;
+  p.N = static_cast<int32_t>(x->shape[0]);
+  p.H = static_cast<int32_t>(H);
+  p.eps = eps;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if ((rc = hip_status(silu ? launch_silu_mul(p, st) : launch_rmsnorm(p, st), "row op launch"))) return rc;
+  return ok();
+}
+
+int saga_rmsnorm(const saga_tensor* x, const saga_tensor* weight, float eps, saga_tensor* y, saga_stream_t stream) {
+  return row_op(false, x, weight, eps, y, stream);
+}
+
+int saga_silu_mul(const saga_tensor* gate_up, saga_tensor* y, saga_stream_t stream) {
+  return row_op(true, gate_up, nullptr, 0.f, y, stream);
 }
 
 }  // extern "C"

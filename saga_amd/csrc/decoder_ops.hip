@@ -1,0 +1,101 @@
+// Decode-step kernels around the attention path (one launch each):
+//   * rope_kv_append: the new tokens' q/k/v from the fused projection, RoPE on
+//     q and k, k/v written into the separate key-head / value-head caches
+//     (replaces apply_rotary_pos_emb + StaticLayer.update's index_copy_,
+//     transformers models/qwen2/modeling_qwen2.py:211-214 and
+//     cache_utils.py:455-487, with the caches laid out as speedup.py:119-139);
+//   * rmsnorm: y = w * x / sqrt(mean(x^2) + eps) per row (Qwen2RMSNorm);
+//   * silu_mul: act = silu(gate) * up over a fused [gate | up] projection.
+// All arithmetic in fp32, one rounding to the storage dtype.
+#include "common.cuh"
+#include "kernels.h"
+
+namespace saga {
+
+__global__ void __launch_bounds__(256) rope_kv_append_kernel(RopeParams p) {
+  const int n = blockIdx.x;
+  const int half = p.d / 2;
+  const int pos = p.pos[n];
+  const int b = p.batch ? p.batch[n] : n;
+  const bool ok = pos >= 0 && pos < p.Lmax && b >= 0 && b < p.B;
+  const int64_t row = static_cast<int64_t>(n) * p.qkv_ld;
+  // q heads, then k heads (rotated), then v heads (copied)
+  const int nrot = (p.n_q + p.n_k) * half;
+  for (int e = threadIdx.x; e < nrot + p.n_v * p.d; e += blockDim.x) {
+    if (e < nrot) {
+      const int hh = e / half, i = e - hh * half;
+      // inv_freq_i = theta^(-2i/d); angle = pos * inv_freq_i (fp32, as HF)
+      const float inv_freq = 1.0f / powf(p.theta, static_cast<float>(2 * i) / static_cast<float>(p.d));
+      const float ang = static_cast<float>(pos) * inv_freq;
+      float sn, cs;
+      sincosf(ang, &sn, &cs);
+      const int64_t base = row + static_cast<int64_t>(hh) * p.d;
+      const float x1 = load_as_f32(p.qkv, p.dt, base + i);
+      const float x2 = load_as_f32(p.qkv, p.dt, base + i + half);
+      const float y1 = x1 * cs - x2 * sn;
+      const float y2 = x2 * cs + x1 * sn;
+      if (hh < p.n_q) {
+        const int64_t qo = static_cast<int64_t>(n) * p.q_sn + static_cast<int64_t>(hh) * p.q_sh;
+        store_from_f32(p.q_out, p.dt, qo + i, ok ? y1 : __builtin_nanf(""));
+        store_from_f32(p.q_out, p.dt, qo + i + half, ok ? y2 : __builtin_nanf(""));
+      } else if (ok) {
+        const int kh = hh - p.n_q;
+        const int64_t ko = b * p.k_sb + static_cast<int64_t>(kh) * p.k_sh + static_cast<int64_t>(pos) * p.k_sl;
+        store_from_f32(p.k_cache, p.dt, ko + i, y1);
+        store_from_f32(p.k_cache, p.dt, ko + i + half, y2);
+      }
+    } else if (ok) {
+      const int f = e - nrot;
+      const int vh = f / p.d, i = f - vh * p.d;
+      const float v = load_as_f32(p.qkv, p.dt, row + static_cast<int64_t>(p.n_q + p.n_k + vh) * p.d + i);
+      const int64_t vo = b * p.v_sb + static_cast<int64_t>(vh) * p.v_sh + static_cast<int64_t>(pos) * p.v_sl;
+      store_from_f32(p.v_cache, p.dt, vo + i, v);
+    }
+  }
+}
+
+hipError_t launch_rope_kv_append(const RopeParams& p, hipStream_t st) {
+  hipLaunchKernelGGL(rope_kv_append_kernel, dim3(p.N), dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
+__global__ void __launch_bounds__(256) rmsnorm_kernel(RowParams p) {
+  __shared__ float red[4];
+  const int n = blockIdx.x;
+  const int64_t xi = static_cast<int64_t>(n) * p.x_ld;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < p.H; i += 256) {
+    const float v = load_as_f32(p.x, p.dt, xi + i);
+    ss += v * v;
+  }
+  ss = block_sum<4>(ss, red);
+  const float r = rsqrtf(ss / static_cast<float>(p.H) + p.eps);
+  const int64_t yi = static_cast<int64_t>(n) * p.y_ld;
+  for (int i = threadIdx.x; i < p.H; i += 256) {
+    const float v = load_as_f32(p.x, p.dt, xi + i);
+    store_from_f32(p.y, p.dt, yi + i, load_as_f32(p.w, p.dt, i) * (v * r));
+  }
+}
+
+hipError_t launch_rmsnorm(const RowParams& p, hipStream_t st) {
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(p.N), dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
+// y[n, i] = silu(x[n, i]) * x[n, H + i]; H = width of the output row.
+__global__ void __launch_bounds__(256) silu_mul_kernel(RowParams p) {
+  const int n = blockIdx.y;
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= p.H) return;
+  const int64_t xi = static_cast<int64_t>(n) * p.x_ld;
+  const float g = load_as_f32(p.x, p.dt, xi + i);
+  const float u = load_as_f32(p.x, p.dt, xi + p.H + i);
+  store_from_f32(p.y, p.dt, static_cast<int64_t>(n) * p.y_ld + i, g / (1.0f + expf(-g)) * u);
+}
+
+hipError_t launch_silu_mul(const RowParams& p, hipStream_t st) {
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((p.H + 255) / 256, p.N), dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
+}  // namespace saga

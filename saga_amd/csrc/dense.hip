@@ -2,51 +2,62 @@
 //
 // Replaces full_einsum_forward (attention/attention.py:64-85) for l_q == 1:
 // it serves the layers exempt from Atop-N, SAGA with full attention and the
-// dense-GQA comparator.  A block owns one (batch, key head) unit and one
-// split of the positions; its four waves step through 32-position
-// sub-chunks in lockstep:
+// dense-GQA comparator.  Kernel 1 gives a block one (batch, key head) unit
+// and one split of the positions; its four waves step through
+// sub-chunks of 16 positions, each with one burst of loads (the K rows and
+// the V rows of up to two value heads):
 //   * QK on MFMA exactly as the score kernel (K rows -> A fragments, the
 //     g <= 16 query heads of the unit -> B fragment),
 //   * online softmax per head (running max / sum, rescale factor alpha),
-//   * P (fp32) through LDS, then P . V on the VALU in fp32: one V row per
-//     wave instruction, two dims per lane, accumulators for every head of
-//     the unit; heads read value head h / (q_h / v_h), so a unit may touch
-//     several value heads (SAGA: 1 key head, 2 value heads).
-// Waves merge in LDS, splits write (max, sum, o[d]) partials, and the last
-// block of a unit to arrive merges them and writes the output.
+//   * P (fp32) through wave-private LDS, then P . V on the VALU in fp32, one
+//     V row per wave load (d / 64 dims per lane); heads read value head
+//     h / (q_h / v_h), so a unit may touch several value heads (SAGA: 1 key
+//     head, 2 value heads).
+// Waves merge in LDS; with several splits each writes a (max, sum, o[d])
+// partial per head and kernel 2 (one block per head) merges them.
+#include <type_traits>
+
 #include "common.cuh"
 #include "kernels.h"
 
 namespace saga {
 
-constexpr int kDenseSub = 32;  // positions per wave step (2 MFMA tiles)
+constexpr int kDenseSub = 16;  // positions per wave step (one MFMA tile)
 
-template <int DT>
-__device__ __forceinline__ void load_v2(const char* p, float& a, float& b) {
-  if constexpr (DT == SAGA_DTYPE_F32) {
-    const u32x2 v = *reinterpret_cast<const u32x2*>(p);
-    a = __uint_as_float(v.x);
-    b = __uint_as_float(v.y);
-  } else {
-    const uint32_t v = *reinterpret_cast<const uint32_t*>(p);
-    a = Elt<DT>::to_f32(v & 0xffffu);
-    b = Elt<DT>::to_f32(v >> 16);
+// One V row per wave load: lane l holds dims [l*DL, l*DL + DL), DL = D / 64.
+template <int DT, int DL>
+struct VLane {
+  static constexpr int BYTES = DL * Elt<DT>::kBytes;  // 2, 4 or 8
+  using Raw = typename std::conditional<BYTES == 8, u32x2, typename std::conditional<BYTES == 4, uint32_t, uint16_t>::type>::type;
+  __device__ static Raw load(const char* p) { return *reinterpret_cast<const Raw*>(p); }
+  __device__ static void unpack(const Raw& r, float* f) {
+    if constexpr (DT == SAGA_DTYPE_F32) {
+      if constexpr (DL == 2) {
+        f[0] = __uint_as_float(r.x);
+        f[1] = __uint_as_float(r.y);
+      } else {
+        f[0] = __uint_as_float(r);
+      }
+    } else if constexpr (DL == 2) {
+      f[0] = Elt<DT>::to_f32(r & 0xffffu);
+      f[1] = Elt<DT>::to_f32(r >> 16);
+    } else {
+      f[0] = Elt<DT>::to_f32(r);
+    }
   }
-}
+};
 
 template <int DT, int D>
-__global__ void __launch_bounds__(256) dense_decode_kernel(DenseParams p) {
+__global__ void __launch_bounds__(256) dense_split_kernel(DenseParams p) {
   using E = Elt<DT>;
   constexpr int E16 = E::kPer16B;
   constexpr int NLOAD = D / (4 * E16);
-  constexpr int LPR = D / 2;            // lanes per V row, 2 dims each
-  constexpr int RPI = kWave / LPR;      // V rows per wave load (1 or 2)
-  constexpr int NVL = kDenseSub / RPI;  // V loads per value head per sub-chunk
-  __shared__ float Ps[4][kDenseSub][16];
+  constexpr int DL = D / kWave;  // dims per lane in the P . V phase
+  using VL = VLane<DT, DL>;
+  __shared__ float Ps[4][16][kDenseSub];  // per wave: P[head][position]
   __shared__ float Al[4][16];
   __shared__ float Wm[4][16], Wl[4][16];
   __shared__ float Wo[4][16][D];
-  __shared__ int is_last;
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int col = lane & 15, s = lane >> 4;
@@ -69,12 +80,14 @@ __global__ void __launch_bounds__(256) dense_decode_kernel(DenseParams p) {
   const char* kbase = p.k + (bi * p.k_sb + static_cast<int64_t>(kh) * p.k_sh) * E::kBytes;
 
   const int vh_first = h0 / g_v, vh_last = (h0 + g - 1) / g_v;
-  const int dim = 2 * (lane % LPR);  // this lane's two dims of a V row
-  const int rpar = lane / LPR;       // row parity for D = 64
+  const int64_t vrow = p.v_sl * E::kBytes;
+  const char* vlane = p.v + (bi * p.v_sb + static_cast<int64_t>(lane) * DL) * E::kBytes;
 
-  float acc[16][2];
+  float acc[16][DL];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) acc[i][0] = acc[i][1] = 0.f;
+  for (int i = 0; i < 16; ++i)
+#pragma unroll
+    for (int d = 0; d < DL; ++d) acc[i][d] = 0.f;
   float m_run = kNegInf, l_run = 0.f;  // for head `col` (replicated over s)
 
   const int beg = split * p.split_len;
@@ -83,19 +96,31 @@ __global__ void __launch_bounds__(256) dense_decode_kernel(DenseParams p) {
   for (int it = 0; it < n_iter; ++it) {
     const int c0 = beg + (it * 4 + w) * kDenseSub;
     const bool active = c0 < end;
-    float x[2][4];
+    // V rows of the unit's first two value heads ride in the K load burst
+    typename VL::Raw v0[kDenseSub], v1[kDenseSub];
     if (active) {
-      u32x4 kf[2][NLOAD];
+      constexpr int NT = kDenseSub / 16;
+      u32x4 kf[NT][NLOAD];
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < NT; ++t) {
         const int pos = min(c0 + 16 * t + col, p.L - 1);
         const char* krow = kbase + static_cast<int64_t>(pos) * p.k_sl * E::kBytes;
 #pragma unroll
         for (int j = 0; j < NLOAD; ++j) kf[t][j] = ld16(krow + (j * 4 * E16 + s * E16) * E::kBytes);
       }
+      const char* vb0 = vlane + static_cast<int64_t>(vh_first) * p.v_sh * E::kBytes;
+#pragma unroll
+      for (int i = 0; i < kDenseSub; ++i) v0[i] = VL::load(vb0 + static_cast<int64_t>(min(c0 + i, p.L - 1)) * vrow);
+      if (vh_last > vh_first) {
+        const char* vb1 = vlane + static_cast<int64_t>(vh_first + 1) * p.v_sh * E::kBytes;
+#pragma unroll
+        for (int i = 0; i < kDenseSub; ++i) v1[i] = VL::load(vb1 + static_cast<int64_t>(min(c0 + i, p.L - 1)) * vrow);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // the K and V burst stays in flight together
+      float x[NT][4];
       float mt = kNegInf;
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < NT; ++t) {
         f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < NLOAD; ++j) a = mfma_16b<DT>(kf[t][j], qf[j], a);
@@ -119,13 +144,16 @@ __global__ void __launch_bounds__(256) dense_decode_kernel(DenseParams p) {
       const float alpha = (m_run == kNegInf) ? (m_new == kNegInf ? 1.f : 0.f) : __expf(m_run - m_new);
       float ps = 0.f;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < NT; ++t) {
+        f32x4 e4;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float e = m_new == kNegInf ? 0.f : __expf(x[t][r] - m_new);
           ps += e;
-          Ps[w][16 * t + 4 * s + r][col] = e;
+          e4[r] = e;
         }
+        *reinterpret_cast<f32x4*>(&Ps[w][col][16 * t + 4 * s]) = e4;
+      }
       ps += __shfl_xor(ps, 16);
       ps += __shfl_xor(ps, 32);
       l_run = l_run * alpha + ps;
@@ -134,30 +162,44 @@ __global__ void __launch_bounds__(256) dense_decode_kernel(DenseParams p) {
     }
     __syncthreads();
     if (active) {
+      {
+        const f32x4* a4 = reinterpret_cast<const f32x4*>(&Al[w][0]);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float a = Al[w][i];
-        acc[i][0] *= a;
-        acc[i][1] *= a;
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 a = a4[q];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int d = 0; d < DL; ++d) acc[4 * q + e][d] *= a[e];
+        }
       }
       for (int vh = vh_first; vh <= vh_last; ++vh) {
-        const int hb = max(vh * g_v, h0) - h0, he = min((vh + 1) * g_v, h0 + g) - h0;  // unit-local heads
-        const char* vbase = p.v + (bi * p.v_sb + static_cast<int64_t>(vh) * p.v_sh + dim) * E::kBytes;
-        float va[NVL], vb[NVL];
+        const int u = vh - vh_first;
+        float vf[kDenseSub][DL];
+        if (u == 1) {
 #pragma unroll
-        for (int i = 0; i < NVL; ++i) {
-          const int pos = min(c0 + i * RPI + rpar, p.L - 1);
-          load_v2<DT>(vbase + static_cast<int64_t>(pos) * p.v_sl * E::kBytes, va[i], vb[i]);
+          for (int i = 0; i < kDenseSub; ++i) VL::unpack(v1[i], vf[i]);
+        } else {
+          if (u >= 2) {  // further value heads: a load burst of their own
+            const char* vb = vlane + static_cast<int64_t>(vh) * p.v_sh * E::kBytes;
+#pragma unroll
+            for (int i = 0; i < kDenseSub; ++i) v0[i] = VL::load(vb + static_cast<int64_t>(min(c0 + i, p.L - 1)) * vrow);
+          }
+#pragma unroll
+          for (int i = 0; i < kDenseSub; ++i) VL::unpack(v0[i], vf[i]);
         }
+        const int hb = max(vh * g_v, h0) - h0, he = min((vh + 1) * g_v, h0 + g) - h0;  // unit-local heads
 #pragma unroll
-        for (int i = 0; i < NVL; ++i) {
-          const int prow = i * RPI + rpar;
+        for (int hh = 0; hh < 16; ++hh) {
+          if (hh >= hb && hh < he) {
+            const f32x4* p4 = reinterpret_cast<const f32x4*>(&Ps[w][hh][0]);
 #pragma unroll
-          for (int hh = 0; hh < 16; ++hh) {
-            if (hh >= hb && hh < he) {
-              const float pw = Ps[w][prow][hh];
-              acc[hh][0] += pw * va[i];
-              acc[hh][1] += pw * vb[i];
+            for (int i4 = 0; i4 < kDenseSub / 4; ++i4) {
+              const f32x4 pw = p4[i4];
+#pragma unroll
+              for (int k = 0; k < 4; ++k)
+#pragma unroll
+                for (int d = 0; d < DL; ++d) acc[hh][d] += pw[k] * vf[4 * i4 + k][d];
             }
           }
         }
@@ -166,28 +208,17 @@ __global__ void __launch_bounds__(256) dense_decode_kernel(DenseParams p) {
     __syncthreads();
   }
 
-  // rows of the other parity (D = 64) hold the same dims
-  if constexpr (RPI == 2) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      acc[i][0] += __shfl_xor(acc[i][0], 32);
-      acc[i][1] += __shfl_xor(acc[i][1], 32);
-    }
-  }
   if (s == 0) {
     Wm[w][col] = m_run;
     Wl[w][col] = l_run;
   }
-  if (lane < LPR) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      Wo[w][i][dim] = acc[i][0];
-      Wo[w][i][dim + 1] = acc[i][1];
-    }
-  }
+  for (int i = 0; i < 16; ++i)
+#pragma unroll
+    for (int d = 0; d < DL; ++d) Wo[w][i][lane * DL + d] = acc[i][d];
   __syncthreads();
 
-  // merge the four waves; split partial (or the output when nsplit == 1)
+  // merge the four waves: the split's partial, or the output when nsplit == 1
   float* part = p.part + (static_cast<int64_t>(unit) * p.nsplit + split) * g * (2 + D);
   for (int e = tid; e < g * D; e += 256) {
     const int hh = e / D, dd = e - hh * D;
@@ -211,38 +242,57 @@ __global__ void __launch_bounds__(256) dense_decode_kernel(DenseParams p) {
       }
     }
   }
-  if (p.nsplit == 1) return;
+}
 
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) is_last = atomicAdd(p.counters + unit, 1) == p.nsplit - 1;
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  const float* pu = p.part + static_cast<int64_t>(unit) * p.nsplit * g * (2 + D);
-  for (int e = tid; e < g * D; e += 256) {
-    const int hh = e / D, dd = e - hh * D;
-    float M = kNegInf;
-    for (int q = 0; q < p.nsplit; ++q) M = fmaxf(M, pu[(q * g + hh) * (2 + D)]);
-    float l = 0.f, o = 0.f;
-    for (int q = 0; q < p.nsplit; ++q) {
-      const float* pp = pu + (q * g + hh) * (2 + D);
-      const float f = pp[0] == kNegInf ? 0.f : __expf(pp[0] - M);
-      l += pp[1] * f;
-      o += pp[2 + dd] * f;
-    }
-    store_from_f32(p.out, p.out_dt, bi * p.o_sb + static_cast<int64_t>(h0 + hh) * p.o_sh + dd, o / l);
+// Merge the split partials of one (batch, head): block of D threads.
+template <int D>
+__global__ void __launch_bounds__(D) dense_merge_kernel(DenseParams p) {
+  __shared__ float fm[1024];
+  __shared__ float red[D / kWave];
+  const int unit = blockIdx.x / p.g, hh = blockIdx.x - unit * p.g;
+  const int bi = unit / p.k_h, kh = unit - bi * p.k_h;
+  const int tid = threadIdx.x;
+  const int64_t stride = static_cast<int64_t>(p.g) * (2 + D);  // between splits
+  const float* base = p.part + static_cast<int64_t>(unit) * p.nsplit * stride + hh * (2 + D);
+  // (max, sum) of every split, then the common max
+  float mloc = kNegInf;
+  for (int q = tid; q < p.nsplit; q += D) {
+    const float m = base[q * stride];
+    fm[q] = m;
+    mloc = fmaxf(mloc, m);
   }
-  if (tid == 0) p.counters[unit] = 0;
+  const float M = block_max<D / kWave>(mloc, red);
+  float lloc = 0.f;
+  for (int q = tid; q < p.nsplit; q += D) {
+    const float f = fm[q] == kNegInf ? 0.f : __expf(fm[q] - M);
+    lloc += base[q * stride + 1] * f;
+    fm[q] = f;
+  }
+  const float l = block_sum<D / kWave>(lloc, red);  // orders the fm writes too
+  // o[tid]: independent loads, eight splits in flight
+  float o = 0.f;
+  for (int q0 = 0; q0 < p.nsplit; q0 += 8) {
+    float ov[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) ov[u] = q0 + u < p.nsplit ? base[(q0 + u) * stride + 2 + tid] : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (q0 + u < p.nsplit) o += ov[u] * fm[q0 + u];
+  }
+  store_from_f32(p.out, p.out_dt, bi * p.o_sb + static_cast<int64_t>(kh * p.g + hh) * p.o_sh + tid, o / l);
 }
 
 template <int DT>
 static hipError_t launch_dense_typed(int d, const DenseParams& p, hipStream_t st) {
   const unsigned blocks = static_cast<unsigned>(p.b * p.k_h * p.nsplit);
-  if (d == 128)
-    hipLaunchKernelGGL((dense_decode_kernel<DT, 128>), dim3(blocks), dim3(256), 0, st, p);
-  else
-    hipLaunchKernelGGL((dense_decode_kernel<DT, 64>), dim3(blocks), dim3(256), 0, st, p);
+  const unsigned heads = static_cast<unsigned>(p.b * p.k_h * p.g);
+  if (d == 128) {
+    hipLaunchKernelGGL((dense_split_kernel<DT, 128>), dim3(blocks), dim3(256), 0, st, p);
+    if (p.nsplit > 1) hipLaunchKernelGGL((dense_merge_kernel<128>), dim3(heads), dim3(128), 0, st, p);
+  } else {
+    hipLaunchKernelGGL((dense_split_kernel<DT, 64>), dim3(blocks), dim3(256), 0, st, p);
+    if (p.nsplit > 1) hipLaunchKernelGGL((dense_merge_kernel<64>), dim3(heads), dim3(64), 0, st, p);
+  }
   return hipGetLastError();
 }
 

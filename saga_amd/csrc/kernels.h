@@ -40,7 +40,29 @@ struct ThreshParams {
 };
 hipError_t launch_logit_threshold(const ThreshParams& p, hipStream_t st);
 
-// K2: selection over fp32 score rows of the fused workspace.
+// Selection-list softmax . V parameters (value tensor, output, row mapping).
+struct PVParams {
+  const void* w;  // API path: weights per row [nrows][K]
+  int32_t w_dt;
+  int64_t w_ld;
+  const void* idx;  // API path: indices per row
+  int32_t idx_i64;
+  int64_t i_ld;
+  int32_t K;
+  const char* v;
+  int32_t v_dt;
+  int64_t v_sb, v_sh, v_sl;
+  int32_t b, q_h, v_h, d, L;
+  int32_t probs_mode;
+  void* out;
+  int32_t out_dt;
+  int64_t o_sb, o_sh;
+};
+// API path of _atopn_gather_and_output: one block per row.
+hipError_t launch_sparse_pv(const PVParams& p, hipStream_t st);
+
+// K2: per score row of the fused workspace, threshold (fast step) or exact
+// top-k (calibration), ordered compaction, then softmax . V of the list.
 struct FusedSelParams {
   const float* scores;
   int64_t ld;
@@ -52,14 +74,13 @@ struct FusedSelParams {
   const float* pstar;  // fast step: softmax-space thresholds in
   float* pstar_out;    // calibration: k-th largest probability out
   float* t_out;        // fast step: logit thresholds out
-  int32_t cap;         // buf_k (fast) ; top_n (calibration)
+  int32_t cap;         // buf_k (fast) ; top_n capped at L (calibration)
   int32_t* sel_idx;
   float* sel_val;
   int32_t* sel_cnt;
   int32_t* sel_total;
 };
-hipError_t launch_select_fast(const FusedSelParams& p, hipStream_t st);
-hipError_t launch_select_calibrate(const FusedSelParams& p, hipStream_t st);
+hipError_t launch_atopn_select_pv(bool calibrate, const FusedSelParams& p, const PVParams& v, hipStream_t st);
 
 // API selection (threshold_topk_fast): typed rows, typed values out.
 struct ApiSelParams {
@@ -78,30 +99,6 @@ struct ApiSelParams {
   int32_t* out_counts;  // nullable
 };
 hipError_t launch_select_api(const ApiSelParams& p, hipStream_t st);
-
-// K3: softmax (or renormalisation) over selected entries . V.
-struct PVParams {
-  const void* w;
-  int32_t w_dt;
-  int64_t w_ld;
-  const void* idx;
-  int32_t idx_i64;
-  int64_t i_ld;
-  const int32_t* cnt;  // nullable: all K entries
-  int32_t K;
-  const char* v;
-  int32_t v_dt;
-  int64_t v_sb, v_sh, v_sl;
-  int32_t b, q_h, v_h, d, L;
-  int32_t probs_mode;
-  void* out;
-  int32_t out_dt;
-  int64_t o_sb, o_sh;
-  float* part;  // [row][npiece][2 + d]
-  int32_t npiece, piece;
-  int32_t* counters;  // [row], zero between calls
-};
-hipError_t launch_sparse_pv(const PVParams& p, hipStream_t st);
 
 // Dense split-L decode (flash-decoding): one pass over K and V.
 struct DenseParams {
@@ -122,8 +119,40 @@ struct DenseParams {
   int64_t o_sb, o_sh;
   float* part;  // [unit][nsplit][g][2 + d]
   int32_t nsplit, split_len;
-  int32_t* counters;  // [unit]
 };
 hipError_t launch_dense_decode(int dtype, int d, const DenseParams& p, hipStream_t st);
+
+// RoPE on q/k of new tokens + k/v append into the separate caches.
+struct RopeParams {
+  const void* qkv;  // [N, qkv_ld]: n_q, n_k, n_v heads of d, in that order
+  int64_t qkv_ld;
+  int32_t dt;
+  int32_t N, n_q, n_k, n_v, d;
+  float theta;
+  const int32_t* pos;    // [N]
+  const int32_t* batch;  // [N] or null (token n -> batch row n)
+  void* q_out;           // [N, n_q, d]
+  int64_t q_sn, q_sh;
+  void* k_cache;  // [B, n_k, Lmax, d]
+  int64_t k_sb, k_sh, k_sl;
+  void* v_cache;  // [B, n_v, Lmax, d]
+  int64_t v_sb, v_sh, v_sl;
+  int32_t B, Lmax;
+};
+hipError_t launch_rope_kv_append(const RopeParams& p, hipStream_t st);
+
+// Row-wise ops: rmsnorm (y = w * x * rsqrt(mean(x^2) + eps)) and silu_mul.
+struct RowParams {
+  const void* x;
+  int64_t x_ld;
+  const void* w;
+  void* y;
+  int64_t y_ld;
+  int32_t dt;
+  int32_t N, H;
+  float eps;
+};
+hipError_t launch_rmsnorm(const RowParams& p, hipStream_t st);
+hipError_t launch_silu_mul(const RowParams& p, hipStream_t st);
 
 }  // namespace saga

@@ -32,8 +32,6 @@ __global__ void __launch_bounds__(256) qk_scores_kernel(QKParams p) {
   const int unit = static_cast<int>(item / p.nchunk);
   const int bi = unit / p.k_h;
   const int kh = unit - bi * p.k_h;
-  int Leff = p.L;
-  if (p.kv_len) Leff = min(Leff, max(p.kv_len[bi], 0));
   const bool hvalid = col < p.g;
   const int h = kh * p.g + (hvalid ? col : 0);
 
@@ -60,6 +58,8 @@ __global__ void __launch_bounds__(256) qk_scores_kernel(QKParams p) {
 #pragma unroll
       for (int j = 0; j < NLOAD; ++j) kf[t][j] = ld16(krow + (j * 4 * E16 + s * E16) * E::kBytes);
     }
+    // keep the whole burst in flight: no MFMA may be hoisted between the loads
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t < TPL; ++t) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -70,6 +70,8 @@ __global__ void __launch_bounds__(256) qk_scores_kernel(QKParams p) {
     }
   }
 
+  int Leff = p.L;
+  if (p.kv_len) Leff = min(Leff, max(p.kv_len[bi], 0));
   // Lane holds head `col`, positions p0 + 16*t + 4*s + r.
   float m = kNegInf;
 #pragma unroll

@@ -1,30 +1,37 @@
-// K2: Atop-N selection kernels (one 1024-thread block per score row).
+// K2: Atop-N selection + sparse softmax . V, one 1024-thread block per score row.
 //
 // Replaces the Triton stream compaction threshold_select_fast_kernel
-// (attention/triton_atopn.py:6-53) and, for calibration, torch.topk over the
-// softmax (attention/attention.py:179-187).  The compaction is ordered and
-// deterministic: a row is processed in super-tiles of 1024 x 16 elements;
-// each wave turns its pass flags into 64-bit ballots, wave counts are
-// prefix-summed in LDS in (element-slot, wave) order -- which is ascending
-// index order -- and every passing element is written to
-// base + prefix + popcount(ballot & lanes_below).  The result is the list of
-// passing positions in ascending order; past `cap` entries nothing is
-// written (the reference's atomic-order output keeps a race-dependent
-// subset there).
-#include "common.cuh"
+// (attention/triton_atopn.py:6-53), the threshold transform
+// (attention/attention.py:136-149), torch.topk for calibration (:179-187) and
+// _atopn_gather_and_output (:152-170).  Per row, in one block and with no
+// cross-block communication:
+//   1. loads of the tail, the chunk partials and the first row tile are
+//      issued together; the logit threshold t follows from the partials;
+//   2. ordered, deterministic compaction: a row is read in tiles of
+//      1024 x 16 elements (the next tile prefetched); each wave turns its pass
+//      flags into 64-bit ballots, the per-(slot, wave) counts are
+//      prefix-summed in LDS in ascending index order, and every passing
+//      element goes to base + prefix + popcount(ballot & lanes_below).  The
+//      list (position, logit) lands in LDS and in the workspace; past `cap`
+//      entries nothing is kept (the reference keeps a race-dependent subset
+//      there);
+//   3. softmax over the list and the gather of only those V rows
+//      (BlockPV), written as the row's output.
+#include <type_traits>
+
+#include "block_pv.cuh"
 #include "kernels.h"
 
 namespace saga {
 
-constexpr int kSelThreads = 1024;
-constexpr int kSelWaves = kSelThreads / kWave;      // 16
-constexpr int kSelEPT = 16;                         // elements per thread per super-tile
-constexpr int kSelSlots = kSelEPT * kSelWaves;      // 256 (slot, wave) counters
-constexpr int kSelTile = kSelThreads * kSelEPT;     // 16384 elements
+constexpr int kSelEPT = 16;                       // elements per thread per tile
+constexpr int kSelSlots = kSelEPT * kBlkWaves;    // 256 (slot, wave) counters
+constexpr int kSelTile = kBlkThreads * kSelEPT;   // 16384 elements
+constexpr int kListLDS = 4096;                    // selection entries kept in LDS
 
 static_assert(kSelSlots == 4 * kWave, "wave-0 scan handles 4 counters per lane");
 
-// Exclusive scan of cnt[0..256) into pre[0..256], pre[256] = total (wave 0).
+// Exclusive scan of cnt[0..256) into pre[0..256], pre[256] = total (one wave).
 __device__ __forceinline__ void scan_slots(const int* cnt, int* pre, int lane) {
   const int c0 = cnt[4 * lane], c1 = cnt[4 * lane + 1], c2 = cnt[4 * lane + 2], c3 = cnt[4 * lane + 3];
   const int tot = c0 + c1 + c2 + c3;
@@ -41,176 +48,183 @@ __device__ __forceinline__ unsigned long long lanes_below(int lane) {
   return lane == 0 ? 0ull : (~0ull >> (kWave - lane));
 }
 
-// Ordered compaction of {i < n : v(i) > t}; emit(pos, i, v) for pos < cap.
-// Returns the number of passing elements (before the cap).
-template <class LoadF, class EmitF>
-__device__ int ordered_compact(int n, float t, int cap, LoadF load, EmitF emit, int* cnt, int* pre) {
+struct SelShared {
+  float red[kBlkWaves];
+  int cnt[kSelSlots];
+  int pre[kSelSlots + 1];
+  int cntE[kSelSlots];
+  int preE[kSelSlots + 1];
+  int hist[2048];
+  int sel_bin, sel_above;
+  int sidx[kListLDS];
+  float sval[kListLDS];
+};
+
+// Run the PV phase over a row's list: from LDS when it fits, otherwise in
+// LDS-sized batches re-read from the workspace copy.
+template <int DT, int D>
+__device__ void row_pv(SelShared& sh, float* accs, int n, const int32_t* gidx, const float* gval, const PVParams& v,
+                       int bi, int h, bool probs) {
+  const int vh = h / (v.q_h / v.v_h);
+  const char* vbase = v.v + (bi * v.v_sb + static_cast<int64_t>(vh) * v.v_sh) * Elt<DT>::kBytes;
+  const int64_t vrow = v.v_sl * Elt<DT>::kBytes;
+  BlockPV<DT, D> pv;
+  pv.init();
+  if (n <= kListLDS) {
+    pv.add(n, sh.sidx, sh.sval, vbase, vrow, probs, sh.red);
+  } else {
+    for (int b0 = 0; b0 < n; b0 += kListLDS) {
+      const int nb = min(kListLDS, n - b0);
+      __syncthreads();
+      for (int i = threadIdx.x; i < nb; i += kBlkThreads) {
+        sh.sidx[i] = gidx[b0 + i];
+        sh.sval[i] = gval[b0 + i];
+      }
+      __syncthreads();
+      pv.add(nb, sh.sidx, sh.sval, vbase, vrow, probs, sh.red);
+    }
+  }
+  pv.finish(accs, v.out, v.out_dt, bi * v.o_sb + static_cast<int64_t>(h) * v.o_sh, probs);
+}
+
+template <int DT, int D>
+__global__ void __launch_bounds__(kBlkThreads) atopn_fast_kernel(FusedSelParams p, PVParams v) {
+  __shared__ SelShared sh;
+  __shared__ float accs[kBlkWaves * D];
+  const int r = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int bi = r / p.q_h, h = r - bi * p.q_h;
+  int Leff = p.L;
+  if (p.kv_len) Leff = min(Leff, max(p.kv_len[bi], 0));
+  const float* x = p.scores + static_cast<int64_t>(r) * p.ld;
+  const float* prow_m = p.pmax + static_cast<int64_t>(r) * p.nchunk;
+  const float* prow_s = p.psum + static_cast<int64_t>(r) * p.nchunk;
+
+  // 1. tail, partials and the first tile in flight together
+  const int tail = min(256, Leff);
+  const float tv = tid < tail ? x[Leff - tail + tid] : kNegInf;
+  const int nch = (Leff + SAGA_CHUNK - 1) / SAGA_CHUNK;
+  const float pm0 = tid < nch ? prow_m[tid] : kNegInf;
+  const float ps0 = tid < nch ? prow_s[tid] : 0.f;
+  float xa[kSelEPT];
+#pragma unroll
+  for (int k = 0; k < kSelEPT; ++k) {
+    const int i = k * kBlkThreads + tid;
+    xa[k] = i < Leff ? x[i] : kNegInf;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // attention/attention.py:142-147
+  const float mt = block_max<kBlkWaves>(tv, sh.red);
+  float acc = pm0 != kNegInf ? ps0 * __expf(pm0 - mt) : 0.f;
+  for (int c = tid + kBlkThreads; c < nch; c += kBlkThreads) {
+    const float pm = prow_m[c];
+    if (pm != kNegInf) acc += prow_s[c] * __expf(pm - mt);
+  }
+  const float ssum = block_sum<kBlkWaves>(acc, sh.red);
+  const float t = mt + logf(fmaxf(p.pstar[r], 1e-30f) * ssum);
+
+  // 2. ordered compaction (attention/triton_atopn.py:42: strict x > t)
+  int32_t* gidx = p.sel_idx + static_cast<int64_t>(r) * p.cap;
+  float* gval = p.sel_val + static_cast<int64_t>(r) * p.cap;
   int base = 0;
-  for (int st = 0; st < n; st += kSelTile) {
-    float xv[kSelEPT];
+  for (int st = 0; st < Leff; st += kSelTile) {
+    float xn[kSelEPT];
+    const bool more = st + kSelTile < Leff;
+    if (more) {
+#pragma unroll
+      for (int k = 0; k < kSelEPT; ++k) {
+        const int i = st + kSelTile + k * kBlkThreads + tid;
+        xn[k] = i < Leff ? x[i] : kNegInf;
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // next tile in flight during this one's compaction
     unsigned long long bal[kSelEPT];
 #pragma unroll
     for (int k = 0; k < kSelEPT; ++k) {
-      const int i = st + k * kSelThreads + tid;
-      xv[k] = i < n ? load(i) : kNegInf;
-    }
-#pragma unroll
-    for (int k = 0; k < kSelEPT; ++k) {
-      const int i = st + k * kSelThreads + tid;
-      bal[k] = __ballot(i < n && xv[k] > t);
-      if (lane == 0) cnt[k * kSelWaves + w] = __popcll(bal[k]);
+      const int i = st + k * kBlkThreads + tid;
+      bal[k] = __ballot(i < Leff && xa[k] > t);
+      if (lane == 0) sh.cnt[k * kBlkWaves + w] = __popcll(bal[k]);
     }
     __syncthreads();
-    if (w == 0) scan_slots(cnt, pre, lane);
+    if (w == 0) scan_slots(sh.cnt, sh.pre, lane);
     __syncthreads();
-    if (base < cap) {
+    if (base < p.cap) {
 #pragma unroll
       for (int k = 0; k < kSelEPT; ++k) {
         if ((bal[k] >> lane) & 1ull) {
-          const int pos = base + pre[k * kSelWaves + w] + __popcll(bal[k] & lanes_below(lane));
-          if (pos < cap) emit(pos, st + k * kSelThreads + tid, xv[k]);
+          const int pos = base + sh.pre[k * kBlkWaves + w] + __popcll(bal[k] & lanes_below(lane));
+          if (pos < p.cap) {
+            const int i = st + k * kBlkThreads + tid;
+            gidx[pos] = i;
+            gval[pos] = xa[k];
+            if (pos < kListLDS) {
+              sh.sidx[pos] = i;
+              sh.sval[pos] = xa[k];
+            }
+          }
         }
       }
     }
-    base += pre[kSelSlots];
+    base += sh.pre[kSelSlots];
     __syncthreads();
+    if (more) {
+#pragma unroll
+      for (int k = 0; k < kSelEPT; ++k) xa[k] = xn[k];
+    }
   }
-  return base;
-}
-
-// Fast step: logit threshold from the K1 chunk partials (no extra pass over
-// the scores), then ordered compaction capped at buf_k.
-__global__ void __launch_bounds__(kSelThreads) select_fast_kernel(FusedSelParams p) {
-  __shared__ float red[kSelWaves];
-  __shared__ int cnt[kSelSlots];
-  __shared__ int pre[kSelSlots + 1];
-  const int r = blockIdx.x;
-  const int tid = threadIdx.x;
-  const int bi = r / p.q_h;
-  int Leff = p.L;
-  if (p.kv_len) Leff = min(Leff, max(p.kv_len[bi], 0));
-  const float* x = p.scores + static_cast<int64_t>(r) * p.ld;
-
-  // attention/attention.py:142-143: approximate max over the last 256 logits.
-  const int tail = min(256, Leff);
-  const float mt = block_max<kSelWaves>(tid < tail ? x[Leff - tail + tid] : kNegInf, red);
-  // :145 sum_j exp(x_j - m) = sum_c s_c * exp(m_c - m)
-  const int nch = (Leff + SAGA_CHUNK - 1) / SAGA_CHUNK;
-  float acc = 0.f;
-  for (int c = tid; c < nch; c += kSelThreads) {
-    const float pm = p.pmax[static_cast<int64_t>(r) * p.nchunk + c];
-    if (pm != kNegInf) acc += p.psum[static_cast<int64_t>(r) * p.nchunk + c] * __expf(pm - mt);
-  }
-  const float ssum = block_sum<kSelWaves>(acc, red);
-  // :147 t = m + log(clamp(p*, 1e-30) * s)
-  const float t = mt + logf(fmaxf(p.pstar[r], 1e-30f) * ssum);
-  if (tid == 0 && p.t_out) p.t_out[r] = t;
-
-  int32_t* oi = p.sel_idx + static_cast<int64_t>(r) * p.cap;
-  float* ov = p.sel_val + static_cast<int64_t>(r) * p.cap;
-  const int total = ordered_compact(
-      Leff, t, p.cap, [&](int i) { return x[i]; },
-      [&](int pos, int i, float v) { oi[pos] = i; ov[pos] = v; }, cnt, pre);
+  const int n = min(base, p.cap);
   if (tid == 0) {
-    p.sel_cnt[r] = min(total, p.cap);
-    if (p.sel_total) p.sel_total[r] = total;
+    p.sel_cnt[r] = n;
+    if (p.sel_total) p.sel_total[r] = base;
+    if (p.t_out) p.t_out[r] = t;
   }
+  // 3. softmax over the selected logits . V (attention/attention.py:158-168)
+  row_pv<DT, D>(sh, accs, n, gidx, gval, v, bi, h, false);
 }
 
-hipError_t launch_select_fast(const FusedSelParams& p, hipStream_t st) {
-  hipLaunchKernelGGL(select_fast_kernel, dim3(p.nrows), dim3(kSelThreads), 0, st, p);
-  return hipGetLastError();
-}
-
-// threshold_topk_fast API (attention/triton_atopn.py:59-113): typed rows,
-// per-row / broadcast / repeated thresholds (:87-96), values kept in the
-// input dtype, int64 indices, every slot of the k-wide outputs written
-// (unfilled: -inf, 0 as the reference pre-fills them, :82-84).
-template <int DT>
-__global__ void __launch_bounds__(kSelThreads) select_api_kernel(ApiSelParams p) {
-  __shared__ int cnt[kSelSlots];
-  __shared__ int pre[kSelSlots + 1];
-  const int r = blockIdx.x;
-  const int tid = threadIdx.x;
-  const float t = p.thresh[r % p.thresh_numel];
-  const int n = static_cast<int>(p.D);
-  int64_t* oi = p.out_idx + static_cast<int64_t>(r) * p.oi_ld;
-  int total;
-  if constexpr (DT == SAGA_DTYPE_F32) {
-    const float* x = static_cast<const float*>(p.x) + static_cast<int64_t>(r) * p.x_ld;
-    float* ov = static_cast<float*>(p.out_val) + static_cast<int64_t>(r) * p.ov_ld;
-    total = ordered_compact(
-        n, t, p.k, [&](int i) { return x[i]; },
-        [&](int pos, int i, float v) { oi[pos] = i; ov[pos] = v; }, cnt, pre);
-    for (int j = min(total, p.k) + tid; j < p.k; j += kSelThreads) { oi[j] = 0; ov[j] = kNegInf; }
-  } else {
-    const uint16_t* x = static_cast<const uint16_t*>(p.x) + static_cast<int64_t>(r) * p.x_ld;
-    uint16_t* ov = static_cast<uint16_t*>(p.out_val) + static_cast<int64_t>(r) * p.ov_ld;
-    total = ordered_compact(
-        n, t, p.k, [&](int i) { return Elt<DT>::to_f32(x[i]); },
-        [&](int pos, int i, float) { oi[pos] = i; ov[pos] = x[i]; }, cnt, pre);
-    const uint16_t ninf = DT == SAGA_DTYPE_BF16 ? 0xff80u : 0xfc00u;
-    for (int j = min(total, p.k) + tid; j < p.k; j += kSelThreads) { oi[j] = 0; ov[j] = ninf; }
-  }
-  if (tid == 0 && p.out_counts) p.out_counts[r] = total;
-}
-
-hipError_t launch_select_api(const ApiSelParams& p, hipStream_t st) {
-  switch (p.x_dt) {
-    case SAGA_DTYPE_F32:
-      hipLaunchKernelGGL(select_api_kernel<SAGA_DTYPE_F32>, dim3(p.nrows), dim3(kSelThreads), 0, st, p);
-      break;
-    case SAGA_DTYPE_BF16:
-      hipLaunchKernelGGL(select_api_kernel<SAGA_DTYPE_BF16>, dim3(p.nrows), dim3(kSelThreads), 0, st, p);
-      break;
-    default:
-      hipLaunchKernelGGL(select_api_kernel<SAGA_DTYPE_F16>, dim3(p.nrows), dim3(kSelThreads), 0, st, p);
-      break;
-  }
-  return hipGetLastError();
-}
-
-// Calibration: exact top-k of each score row (k = min(top_n, L)).
+// Calibration: exact top-k of the row (k = min(top_n, L)).
 //   1. full-row max M and sum S of exp(x - M) from the K1 partials;
 //   2. the k-th largest value by a 3-pass radix select (11/11/10 bits of the
-//      order-preserving uint32 key) with 2048-bin LDS histograms;
+//      order-preserving uint32 key) over 2048-bin LDS histograms;
 //   3. ordered compaction of the elements above it plus the first (by index)
-//      elements equal to it, to exactly k;
+//      elements equal to it, exactly k;
 //   4. p* = exp(x_k - M) / S, the k-th largest probability, into the
-//      threshold table (attention/attention.py:185-187).
-__global__ void __launch_bounds__(kSelThreads) select_calibrate_kernel(FusedSelParams p) {
-  __shared__ float red[kSelWaves];
-  __shared__ int hist[2048];
-  __shared__ int wsum[kSelWaves];
-  __shared__ int sel_bin, sel_above;
-  __shared__ int cntG[kSelSlots], cntE[kSelSlots];
-  __shared__ int preG[kSelSlots + 1], preE[kSelSlots + 1];
+//      threshold table (attention/attention.py:185-187);
+//   5. softmax over the k logits . V == renormalised top-k probabilities . V.
+template <int DT, int D>
+__global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_kernel(FusedSelParams p, PVParams v) {
+  __shared__ SelShared sh;
+  __shared__ float accs[kBlkWaves * D];
   const int r = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int bi = r / p.q_h;
+  const int bi = r / p.q_h, h = r - bi * p.q_h;
   int Leff = p.L;
   if (p.kv_len) Leff = min(Leff, max(p.kv_len[bi], 0));
   const float* x = p.scores + static_cast<int64_t>(r) * p.ld;
+  const float* prow_m = p.pmax + static_cast<int64_t>(r) * p.nchunk;
+  const float* prow_s = p.psum + static_cast<int64_t>(r) * p.nchunk;
 
   const int nch = (Leff + SAGA_CHUNK - 1) / SAGA_CHUNK;
   float mloc = kNegInf;
-  for (int c = tid; c < nch; c += kSelThreads) mloc = fmaxf(mloc, p.pmax[static_cast<int64_t>(r) * p.nchunk + c]);
-  const float M = block_max<kSelWaves>(mloc, red);
+  for (int c = tid; c < nch; c += kBlkThreads) mloc = fmaxf(mloc, prow_m[c]);
+  const float M = block_max<kBlkWaves>(mloc, sh.red);
   float sloc = 0.f;
-  for (int c = tid; c < nch; c += kSelThreads) {
-    const float pm = p.pmax[static_cast<int64_t>(r) * p.nchunk + c];
-    if (pm != kNegInf) sloc += p.psum[static_cast<int64_t>(r) * p.nchunk + c] * __expf(pm - M);
+  for (int c = tid; c < nch; c += kBlkThreads) {
+    const float pm = prow_m[c];
+    if (pm != kNegInf) sloc += prow_s[c] * __expf(pm - M);
   }
-  const float S = block_sum<kSelWaves>(sloc, red);
+  const float S = block_sum<kBlkWaves>(sloc, sh.red);
 
   const int k = min(p.cap, Leff);
+  int32_t* gidx = p.sel_idx + static_cast<int64_t>(r) * p.cap;
+  float* gval = p.sel_val + static_cast<int64_t>(r) * p.cap;
   if (k <= 0) {
     if (tid == 0) {
       p.sel_cnt[r] = 0;
       if (p.sel_total) p.sel_total[r] = 0;
       p.pstar_out[r] = 0.f;
     }
+    row_pv<DT, D>(sh, accs, 0, gidx, gval, v, bi, h, false);
     return;
   }
 
@@ -222,83 +236,83 @@ __global__ void __launch_bounds__(kSelThreads) select_calibrate_kernel(FusedSelP
   for (int pass = 0; pass < 3; ++pass) {
     const int nb = 1 << nbits[pass];
     const uint32_t hmask = pass == 0 ? 0u : (0xffffffffu << (shifts[pass] + nbits[pass]));
-    for (int i = tid; i < 2048; i += kSelThreads) hist[i] = 0;
+    for (int i = tid; i < 2048; i += kBlkThreads) sh.hist[i] = 0;
     __syncthreads();
-    for (int i = tid; i < Leff; i += kSelThreads) {
+    for (int i = tid; i < Leff; i += kBlkThreads) {
       const uint32_t key = f32_to_key(x[i]);
-      if ((key & hmask) == prefix) atomicAdd(&hist[(key >> shifts[pass]) & (nb - 1)], 1);
+      if ((key & hmask) == prefix) atomicAdd(&sh.hist[(key >> shifts[pass]) & (nb - 1)], 1);
     }
     __syncthreads();
     // bins scanned from the top: thread t owns bins nb-1-2t and nb-2-2t
     const int b0 = nb - 1 - 2 * tid, b1 = b0 - 1;
-    const int c0 = b0 >= 0 ? hist[b0] : 0;
-    const int c1 = b1 >= 0 ? hist[b1] : 0;
+    const int c0 = b0 >= 0 ? sh.hist[b0] : 0;
+    const int c1 = b1 >= 0 ? sh.hist[b1] : 0;
     const int tsum = c0 + c1;
     const int incl = wave_incl_scan(tsum, lane);
-    if (lane == kWave - 1) wsum[w] = incl;
+    if (lane == kWave - 1) sh.cnt[w] = incl;
     __syncthreads();
     int woff = 0;
-    for (int i = 0; i < w; ++i) woff += wsum[i];
+    for (int i = 0; i < w; ++i) woff += sh.cnt[i];
     const int ex = woff + incl - tsum;
     if (c0 > 0 && ex < krem && krem <= ex + c0) {
-      sel_bin = b0;
-      sel_above = ex;
+      sh.sel_bin = b0;
+      sh.sel_above = ex;
     } else if (c1 > 0 && ex + c0 < krem && krem <= ex + tsum) {
-      sel_bin = b1;
-      sel_above = ex + c0;
+      sh.sel_bin = b1;
+      sh.sel_above = ex + c0;
     }
     __syncthreads();
-    prefix |= static_cast<uint32_t>(sel_bin) << shifts[pass];
-    krem -= sel_above;
+    prefix |= static_cast<uint32_t>(sh.sel_bin) << shifts[pass];
+    krem -= sh.sel_above;
     __syncthreads();
   }
   const uint32_t kth = prefix;
   const int need = krem;  // elements equal to the k-th value that are taken
 
-  int32_t* oi = p.sel_idx + static_cast<int64_t>(r) * p.cap;
-  float* ov = p.sel_val + static_cast<int64_t>(r) * p.cap;
   int baseG = 0, baseE = 0;
   for (int st = 0; st < Leff; st += kSelTile) {
     float xv[kSelEPT];
     unsigned long long bg[kSelEPT], be[kSelEPT];
 #pragma unroll
     for (int kk = 0; kk < kSelEPT; ++kk) {
-      const int i = st + kk * kSelThreads + tid;
+      const int i = st + kk * kBlkThreads + tid;
       xv[kk] = i < Leff ? x[i] : kNegInf;
     }
 #pragma unroll
     for (int kk = 0; kk < kSelEPT; ++kk) {
-      const int i = st + kk * kSelThreads + tid;
+      const int i = st + kk * kBlkThreads + tid;
       const uint32_t key = f32_to_key(xv[kk]);
       bg[kk] = __ballot(i < Leff && key > kth);
       be[kk] = __ballot(i < Leff && key == kth);
       if (lane == 0) {
-        cntG[kk * kSelWaves + w] = __popcll(bg[kk]);
-        cntE[kk * kSelWaves + w] = __popcll(be[kk]);
+        sh.cnt[kk * kBlkWaves + w] = __popcll(bg[kk]);
+        sh.cntE[kk * kBlkWaves + w] = __popcll(be[kk]);
       }
     }
     __syncthreads();
-    if (w == 0) scan_slots(cntG, preG, lane);
-    if (w == 1) scan_slots(cntE, preE, lane);
+    if (w == 0) scan_slots(sh.cnt, sh.pre, lane);
+    if (w == 1) scan_slots(sh.cntE, sh.preE, lane);
     __syncthreads();
 #pragma unroll
     for (int kk = 0; kk < kSelEPT; ++kk) {
-      const int slot = kk * kSelWaves + w;
-      const int i = st + kk * kSelThreads + tid;
-      const int g_before = baseG + preG[slot] + __popcll(bg[kk] & lanes_below(lane));
-      const int e_before = baseE + preE[slot] + __popcll(be[kk] & lanes_below(lane));
-      if ((bg[kk] >> lane) & 1ull) {
-        const int pos = g_before + min(e_before, need);
-        oi[pos] = i;
-        ov[pos] = xv[kk];
-      } else if (((be[kk] >> lane) & 1ull) && e_before < need) {
-        const int pos = g_before + e_before;
-        oi[pos] = i;
-        ov[pos] = xv[kk];
+      const int slot = kk * kBlkWaves + w;
+      const int i = st + kk * kBlkThreads + tid;
+      const int g_before = baseG + sh.pre[slot] + __popcll(bg[kk] & lanes_below(lane));
+      const int e_before = baseE + sh.preE[slot] + __popcll(be[kk] & lanes_below(lane));
+      int pos = -1;
+      if ((bg[kk] >> lane) & 1ull) pos = g_before + min(e_before, need);
+      else if (((be[kk] >> lane) & 1ull) && e_before < need) pos = g_before + e_before;
+      if (pos >= 0) {
+        gidx[pos] = i;
+        gval[pos] = xv[kk];
+        if (pos < kListLDS) {
+          sh.sidx[pos] = i;
+          sh.sval[pos] = xv[kk];
+        }
       }
     }
-    baseG += preG[kSelSlots];
-    baseE += preE[kSelSlots];
+    baseG += sh.pre[kSelSlots];
+    baseE += sh.preE[kSelSlots];
     __syncthreads();
   }
   if (tid == 0) {
@@ -306,10 +320,98 @@ __global__ void __launch_bounds__(kSelThreads) select_calibrate_kernel(FusedSelP
     if (p.sel_total) p.sel_total[r] = k;
     p.pstar_out[r] = expf(key_to_f32(kth) - M) / S;
   }
+  row_pv<DT, D>(sh, accs, k, gidx, gval, v, bi, h, false);
 }
 
-hipError_t launch_select_calibrate(const FusedSelParams& p, hipStream_t st) {
-  hipLaunchKernelGGL(select_calibrate_kernel, dim3(p.nrows), dim3(kSelThreads), 0, st, p);
+template <int DT, int D>
+static hipError_t launch_fused(bool calibrate, const FusedSelParams& p, const PVParams& v, hipStream_t st) {
+  if (calibrate)
+    hipLaunchKernelGGL((atopn_calibrate_kernel<DT, D>), dim3(p.nrows), dim3(kBlkThreads), 0, st, p, v);
+  else
+    hipLaunchKernelGGL((atopn_fast_kernel<DT, D>), dim3(p.nrows), dim3(kBlkThreads), 0, st, p, v);
+  return hipGetLastError();
+}
+
+template <int DT>
+static hipError_t launch_fused_d(bool calibrate, const FusedSelParams& p, const PVParams& v, hipStream_t st) {
+  return v.d == 128 ? launch_fused<DT, 128>(calibrate, p, v, st) : launch_fused<DT, 64>(calibrate, p, v, st);
+}
+
+hipError_t launch_atopn_select_pv(bool calibrate, const FusedSelParams& p, const PVParams& v, hipStream_t st) {
+  if (v.v_dt == SAGA_DTYPE_BF16) return launch_fused_d<SAGA_DTYPE_BF16>(calibrate, p, v, st);
+  if (v.v_dt == SAGA_DTYPE_F16) return launch_fused_d<SAGA_DTYPE_F16>(calibrate, p, v, st);
+  return launch_fused_d<SAGA_DTYPE_F32>(calibrate, p, v, st);
+}
+
+// threshold_topk_fast API (attention/triton_atopn.py:59-113): typed rows,
+// per-row / broadcast / repeated thresholds (:87-96), values kept in the
+// input dtype, int64 indices, every slot of the k-wide outputs written
+// (unfilled: -inf, 0 as the reference pre-fills them, :82-84).
+template <int DT>
+__global__ void __launch_bounds__(kBlkThreads) select_api_kernel(ApiSelParams p) {
+  __shared__ int cnt[kSelSlots];
+  __shared__ int pre[kSelSlots + 1];
+  using Raw = typename std::conditional<DT == SAGA_DTYPE_F32, uint32_t, uint16_t>::type;
+  const int r = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const float t = p.thresh[r % p.thresh_numel];
+  const int n = static_cast<int>(p.D);
+  const Raw* x = static_cast<const Raw*>(p.x) + static_cast<int64_t>(r) * p.x_ld;
+  Raw* ov = static_cast<Raw*>(p.out_val) + static_cast<int64_t>(r) * p.ov_ld;
+  int64_t* oi = p.out_idx + static_cast<int64_t>(r) * p.oi_ld;
+  int base = 0;
+  for (int st = 0; st < n; st += kSelTile) {
+    Raw xr[kSelEPT];
+    unsigned long long bal[kSelEPT];
+#pragma unroll
+    for (int k = 0; k < kSelEPT; ++k) {
+      const int i = st + k * kBlkThreads + tid;
+      xr[k] = i < n ? x[i] : Raw(0);
+    }
+#pragma unroll
+    for (int k = 0; k < kSelEPT; ++k) {
+      const int i = st + k * kBlkThreads + tid;
+      bal[k] = __ballot(i < n && Elt<DT>::to_f32(xr[k]) > t);
+      if (lane == 0) cnt[k * kBlkWaves + w] = __popcll(bal[k]);
+    }
+    __syncthreads();
+    if (w == 0) scan_slots(cnt, pre, lane);
+    __syncthreads();
+    if (base < p.k) {
+#pragma unroll
+      for (int k = 0; k < kSelEPT; ++k) {
+        if ((bal[k] >> lane) & 1ull) {
+          const int pos = base + pre[k * kBlkWaves + w] + __popcll(bal[k] & lanes_below(lane));
+          if (pos < p.k) {
+            oi[pos] = st + k * kBlkThreads + tid;
+            ov[pos] = xr[k];
+          }
+        }
+      }
+    }
+    base += pre[kSelSlots];
+    __syncthreads();
+  }
+  const Raw ninf = DT == SAGA_DTYPE_F32 ? Raw(0xff800000u) : (DT == SAGA_DTYPE_BF16 ? Raw(0xff80u) : Raw(0xfc00u));
+  for (int j = min(base, p.k) + tid; j < p.k; j += kBlkThreads) {
+    oi[j] = 0;
+    ov[j] = ninf;
+  }
+  if (tid == 0 && p.out_counts) p.out_counts[r] = base;
+}
+
+hipError_t launch_select_api(const ApiSelParams& p, hipStream_t st) {
+  switch (p.x_dt) {
+    case SAGA_DTYPE_F32:
+      hipLaunchKernelGGL(select_api_kernel<SAGA_DTYPE_F32>, dim3(p.nrows), dim3(kBlkThreads), 0, st, p);
+      break;
+    case SAGA_DTYPE_BF16:
+      hipLaunchKernelGGL(select_api_kernel<SAGA_DTYPE_BF16>, dim3(p.nrows), dim3(kBlkThreads), 0, st, p);
+      break;
+    default:
+      hipLaunchKernelGGL(select_api_kernel<SAGA_DTYPE_F16>, dim3(p.nrows), dim3(kBlkThreads), 0, st, p);
+      break;
+  }
   return hipGetLastError();
 }
 

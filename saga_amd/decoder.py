@@ -1,0 +1,237 @@
+"""Decode harness: a Qwen2/Llama-shaped decoder on the SAGA decode path.
+
+The counterpart of the reference's benchmark machinery (speedup.py:119-440):
+separate key-head / value-head KV caches (initialize_kv_cache, :119-139), a
+batch-1 prefill replicated to the whole batch (prefill, :146-161), and decode
+steps captured as two HIP graphs -- one for the Atop-N calibration step and
+one for the fast steps -- replayed once per token (capture_cuda_graphs /
+decode_with_graph, :179-291).  Weights are random (no checkpoints here); the
+shapes are the benchmarked models'.
+
+Per layer and step: rmsnorm -> fused q/k/v projection (+bias) -> RoPE + cache
+append -> attention (Atop-N fast step, calibration step or dense) -> o_proj
+with the residual folded in -> rmsnorm -> [gate | up] projection -> silu*up ->
+down projection with the residual folded in.  The attention and the
+row-wise ops are saga_amd HIP kernels; the projections are hipBLASLt GEMMs.
+Positions advance on the device, so one captured graph serves every step.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, replace
+from typing import Optional
+
+import torch
+
+from . import ops
+from .attention.attention import sdpa_attention_forward
+
+
+@dataclass(frozen=True)
+class DecoderShape:
+    """Transformer shape; n_k / n_v are SAGA's separate key / value head counts."""
+    layers: int
+    hidden: int
+    n_q: int
+    n_k: int
+    n_v: int
+    head_dim: int
+    intermediate: int
+    vocab: int
+    rope_theta: float
+    eps: float
+    qkv_bias: bool = True
+
+    @property
+    def qkv_width(self) -> int:
+        return (self.n_q + self.n_k + self.n_v) * self.head_dim
+
+
+# Qwen2.5-1.5B with one key head and two value heads (SAGA); the dense-GQA
+# comparator keeps the original two key/value heads.
+QWEN25_15B_SAGA = DecoderShape(28, 1536, 12, 1, 2, 128, 8960, 151936, 1e6, 1e-6, True)
+QWEN25_15B_GQA = replace(QWEN25_15B_SAGA, n_k=2)
+# SmolLM2-360M with 1 key head / 5 value heads (Llama: no q/k/v bias).
+SMOLLM2_360M_SAGA = DecoderShape(32, 960, 15, 1, 5, 64, 2560, 49152, 1e5, 1e-5, False)
+
+
+def kv_cache_bytes(shape: DecoderShape, batch: int, max_len: int, dtype=torch.bfloat16) -> int:
+    es = torch.tensor([], dtype=dtype).element_size()
+    return shape.layers * batch * (shape.n_k + shape.n_v) * max_len * shape.head_dim * es
+
+
+class _HeadGroups(torch.nn.Module):
+    """Stand-in for the HF attention module passed to sdpa_attention_forward."""
+    num_key_value_groups = 1
+
+
+class SagaDecoder:
+    """Random-init decoder with SAGA attention on MI355X.
+
+    mode: "atopn" (calibration + fast Atop-N steps) or "dense" (every layer
+    dense; with n_k == n_v this is plain GQA).  exempt_layers run dense in
+    "atopn" mode (attention/attention.py:94, speedup.py:65-66).
+    """
+
+    def __init__(self, shape: DecoderShape, batch: int, max_len: int, mode: str = "atopn", top_n: int = 512,
+                 exempt_layers=(), device="cuda", dtype=torch.bfloat16, seed: int = 0):
+        if mode not in ("atopn", "dense"):
+            raise ValueError(f"mode must be 'atopn' or 'dense', got {mode!r}")
+        self.shape, self.batch, self.max_len, self.mode, self.top_n = shape, batch, max_len, mode, top_n
+        self.exempt = set(exempt_layers)
+        self.device, self.dtype = torch.device(device), dtype
+        free, _ = torch.cuda.mem_get_info(self.device)
+        need = kv_cache_bytes(shape, batch, max_len, dtype)
+        if need > 0.8 * free:
+            raise MemoryError(f"KV cache of {need / 2**30:.1f} GiB does not fit in {free / 2**30:.1f} GiB free HBM")
+        g = torch.Generator(device=self.device).manual_seed(seed)
+        s, d = shape, shape.head_dim
+
+        def w(*size, std=0.02):
+            return (torch.randn(*size, generator=g, device=self.device, dtype=torch.float32) * std).to(dtype)
+
+        self.embed = w(s.vocab, s.hidden)  # tied with the LM head
+        self.ln1 = [torch.ones(s.hidden, device=self.device, dtype=dtype) for _ in range(s.layers)]
+        self.ln2 = [torch.ones(s.hidden, device=self.device, dtype=dtype) for _ in range(s.layers)]
+        self.w_qkv = [w(s.qkv_width, s.hidden) for _ in range(s.layers)]
+        self.b_qkv = [w(s.qkv_width) if s.qkv_bias else torch.zeros(s.qkv_width, device=self.device, dtype=dtype)
+                      for _ in range(s.layers)]
+        self.w_o = [w(s.hidden, s.n_q * d) for _ in range(s.layers)]
+        self.w_gu = [w(2 * s.intermediate, s.hidden) for _ in range(s.layers)]
+        self.w_d = [w(s.hidden, s.intermediate) for _ in range(s.layers)]
+        self.ln_f = torch.ones(s.hidden, device=self.device, dtype=dtype)
+        # separate key-head and value-head caches [layer][batch, heads, max_len, d]
+        self.k_cache = torch.zeros(s.layers, batch, s.n_k, max_len, d, device=self.device, dtype=dtype)
+        self.v_cache = torch.zeros(s.layers, batch, s.n_v, max_len, d, device=self.device, dtype=dtype)
+        # Atop-N threshold table, rows = batch * n_q (attention/attention.py:92-99)
+        self.table = torch.zeros(max(s.layers, 1), batch * s.n_q, device=self.device, dtype=torch.float32)
+        # static decode-step state (fixed addresses for graph replay)
+        self.tokens = torch.zeros(batch, dtype=torch.int64, device=self.device)
+        self.pos = torch.zeros(batch, dtype=torch.int32, device=self.device)
+        self.kv_len = torch.zeros(batch, dtype=torch.int32, device=self.device)
+        self._x = torch.empty(batch, s.hidden, device=self.device, dtype=dtype)
+        self._h = torch.empty(batch, s.hidden, device=self.device, dtype=dtype)
+        self._qkv = torch.empty(batch, s.qkv_width, device=self.device, dtype=dtype)
+        self._q = torch.empty(batch, s.n_q, d, device=self.device, dtype=dtype)
+        self._attn = torch.empty(batch, s.n_q, 1, d, device=self.device, dtype=dtype)
+        self._gu = torch.empty(batch, 2 * s.intermediate, device=self.device, dtype=dtype)
+        self._act = torch.empty(batch, s.intermediate, device=self.device, dtype=dtype)
+        self._logits = torch.empty(batch, s.vocab, device=self.device, dtype=dtype)
+        self.graph_cal: Optional[torch.cuda.CUDAGraph] = None
+        self.graph_fast: Optional[torch.cuda.CUDAGraph] = None
+        self.prompt_len = 0
+
+    # ------------------------------------------------------------------ prefill
+    @torch.no_grad()
+    def prefill(self, prompt: torch.Tensor, chunk: int = 8192) -> None:
+        """Run a batch-1 prompt through the model, fill cache row 0 and copy it
+        to every batch row (speedup.py:146-161); the next token (argmax of the
+        last position) is the first decode input of every row."""
+        s, d = self.shape, self.shape.head_dim
+        T = int(prompt.numel())
+        if T + 1 > self.max_len:
+            raise ValueError("prompt does not fit the cache")
+        x = self.embed.index_select(0, prompt.to(self.device).reshape(-1))
+        pos = torch.arange(T, device=self.device, dtype=torch.int32)
+        zeros = torch.zeros(T, device=self.device, dtype=torch.int32)
+        mod = _HeadGroups()
+        for l in range(s.layers):
+            h = ops.rmsnorm(x, self.ln1[l], s.eps)
+            qkv = torch.addmm(self.b_qkv[l], h, self.w_qkv[l].t())
+            q = ops.rope_kv_append(qkv, s.n_q, s.n_k, s.n_v, s.rope_theta, pos, self.k_cache[l], self.v_cache[l],
+                                   batch=zeros)
+            k = self.k_cache[l, 0:1, :, :T]
+            v = self.v_cache[l, 0:1, :, :T]
+            # prefill attention stays on torch SDPA (attention/attention.py:13-53)
+            o, _ = sdpa_attention_forward(mod, q.transpose(0, 1).unsqueeze(0), k, v, None, is_causal=True)
+            x = torch.addmm(x, o.reshape(T, s.n_q * d), self.w_o[l].t())
+            for c0 in range(0, T, chunk):
+                xc = x[c0:c0 + chunk]
+                gu = torch.mm(ops.rmsnorm(xc, self.ln2[l], s.eps), self.w_gu[l].t())
+                xc.addmm_(ops.silu_mul(gu), self.w_d[l].t())
+        last = ops.rmsnorm(x[-1:], self.ln_f, s.eps)
+        first = torch.mm(last, self.embed.t()).argmax(dim=-1)
+        self.k_cache[:, 1:, :, :T] = self.k_cache[:, 0:1, :, :T]
+        self.v_cache[:, 1:, :, :T] = self.v_cache[:, 0:1, :, :T]
+        self.prompt_len = T
+        self.reset()
+        self._first_token = first
+        self.tokens.fill_(0)
+        self.tokens.copy_(first.expand(self.batch))
+
+    def fill_synthetic(self, prompt_len: int, seed: int = 1) -> None:
+        """Fill the cache with N(0,1) keys/values of prompt_len positions
+        instead of a prefill (tests and kernel-level runs)."""
+        g = torch.Generator(device=self.device).manual_seed(seed)
+        for c in (self.k_cache, self.v_cache):
+            c[..., :prompt_len, :] = torch.randn(c[..., :prompt_len, :].shape, generator=g, device=self.device,
+                                                 dtype=torch.float32).to(self.dtype)
+        self.prompt_len = prompt_len
+        self._first_token = torch.zeros(1, dtype=torch.int64, device=self.device)
+        self.reset()
+
+    def reset(self) -> None:
+        """Rewind the decode state to just after the prompt."""
+        self.pos.fill_(self.prompt_len)
+        self.kv_len.fill_(self.prompt_len + 1)
+        if hasattr(self, "_first_token"):
+            self.tokens.copy_(self._first_token.expand(self.batch))
+
+    # ------------------------------------------------------------------- decode
+    @torch.no_grad()
+    def step(self, calibrate: bool) -> None:
+        """One decode step for every batch row (static buffers only)."""
+        s, d, B = self.shape, self.shape.head_dim, self.batch
+        x = self._x
+        torch.index_select(self.embed, 0, self.tokens, out=x)
+        q4 = self._q.view(B, s.n_q, 1, d)
+        for l in range(s.layers):
+            ops.rmsnorm(x, self.ln1[l], s.eps, out=self._h)
+            torch.addmm(self.b_qkv[l], self._h, self.w_qkv[l].t(), out=self._qkv)
+            ops.rope_kv_append(self._qkv, s.n_q, s.n_k, s.n_v, s.rope_theta, self.pos, self.k_cache[l],
+                               self.v_cache[l], q_out=self._q)
+            K, V = self.k_cache[l], self.v_cache[l]
+            if self.mode == "dense" or l in self.exempt:
+                ops.dense_decode(q4, K, V, kv_len=self.kv_len, out=self._attn)
+            elif calibrate:
+                ops.atopn_calibrate(q4, K, V, self.top_n, self.table[l], kv_len=self.kv_len, out=self._attn)
+            else:
+                ops.atopn_decode(q4, K, V, self.table[l], self.top_n, kv_len=self.kv_len, out=self._attn)
+            x.addmm_(self._attn.view(B, s.n_q * d), self.w_o[l].t())
+            ops.rmsnorm(x, self.ln2[l], s.eps, out=self._h)
+            torch.mm(self._h, self.w_gu[l].t(), out=self._gu)
+            ops.silu_mul(self._gu, out=self._act)
+            x.addmm_(self._act, self.w_d[l].t())
+        ops.rmsnorm(x, self.ln_f, s.eps, out=self._h)
+        torch.mm(self._h, self.embed.t(), out=self._logits)
+        torch.argmax(self._logits, dim=-1, out=self.tokens)
+        self.pos.add_(1)
+        self.kv_len.add_(1)
+
+    def capture(self) -> None:
+        """Capture the calibration and fast steps as HIP graphs (after an eager
+        warm-up that allocates every workspace)."""
+        side = torch.cuda.Stream(self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            for cal in (True, False):
+                self.reset()
+                self.step(cal)
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        self.reset()
+        graphs = []
+        for cal in (True, False):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self.step(cal)
+            graphs.append(g)
+        self.graph_cal, self.graph_fast = graphs
+        torch.cuda.synchronize(self.device)
+
+    def replay(self, i: int) -> None:
+        """Step i of a generation: the calibration graph first (Atop-N), then fast steps."""
+        if self.mode == "atopn" and i == 0:
+            self.graph_cal.replay()
+        else:
+            self.graph_fast.replay()

@@ -150,12 +150,9 @@ def sparse_softmax_pv(weights, indices, value, query_shape, input_is_logits=Fals
     idx = indices.reshape(b, q_h, 1, K).contiguous()
     value = _vec_ready(value)
     out = torch.empty(b, q_h, 1, d, dtype=out_dtype or value.dtype, device=dev)
-    lib = _lib.load()
-    nbytes = lib.saga_sparse_pv_workspace_bytes(b, q_h, d, K)
-    ws = workspace(dev, "sparse_pv", nbytes)
-    _lib.check(lib.saga_sparse_softmax_pv(_lib.tensor(w), _lib.tensor(idx), _lib.tensor(value),
-                                          1 if input_is_logits else 0, _lib.tensor(out), _lib.ptr(ws), ws.numel(),
-                                          _lib.stream_of(value)), "sparse_softmax_pv")
+    _lib.check(_lib.load().saga_sparse_softmax_pv(_lib.tensor(w), _lib.tensor(idx), _lib.tensor(value),
+                                                  1 if input_is_logits else 0, _lib.tensor(out),
+                                                  _lib.stream_of(value)), "sparse_softmax_pv")
     return out
 
 
@@ -248,3 +245,41 @@ def atopn_workspace_views(b: int, q_h: int, L: int, d: int, buf_k: int, device) 
         "sel_val": view(lay.sel_val, nr * buf_k, torch.float32).reshape(nr, buf_k),
         "scores": view(lay.scores, nr * lay.scores_ld, torch.float32).reshape(nr, lay.scores_ld)[:, :L],
     }
+
+
+# ----------------------------------------------------------- decode-step ops
+
+def rope_kv_append(qkv, n_q, n_k, n_v, theta, pos, k_cache, v_cache, batch=None, q_out=None):
+    """RoPE on the new tokens' q and k, k/v appended into the separate caches
+    (transformers models/qwen2/modeling_qwen2.py:211-214 + cache update).
+    qkv [N, (n_q+n_k+n_v)*d]; pos int32 [N]; batch int32 [N] or None.
+    Returns q_out [N, n_q, d]."""
+    dev = _need_gpu(qkv, pos, k_cache, v_cache, batch)
+    d = k_cache.shape[-1]
+    if q_out is None:
+        q_out = torch.empty(qkv.shape[0], n_q, d, dtype=qkv.dtype, device=dev)
+    for t, name in ((pos, "pos"), (batch, "batch")):
+        if t is not None and (t.dtype != torch.int32 or not t.is_contiguous()):
+            raise ValueError(f"saga_amd: {name} must be a contiguous int32 tensor")
+    _lib.check(_lib.load().saga_rope_kv_append(_lib.tensor(qkv), n_q, n_k, n_v, float(theta), _lib.ptr(pos),
+                                               _lib.ptr(batch), _lib.tensor(q_out), _lib.tensor(k_cache),
+                                               _lib.tensor(v_cache), _lib.stream_of(qkv)), "rope_kv_append")
+    return q_out
+
+
+def rmsnorm(x, weight, eps, out=None):
+    """weight * x / sqrt(mean(x^2) + eps) over the last dim of x [N, H]."""
+    _need_gpu(x, weight)
+    out = torch.empty_like(x) if out is None else out
+    _lib.check(_lib.load().saga_rmsnorm(_lib.tensor(x), _lib.tensor(weight), float(eps), _lib.tensor(out),
+                                        _lib.stream_of(x)), "rmsnorm")
+    return out
+
+
+def silu_mul(gate_up, out=None):
+    """silu(gate) * up for gate_up = [gate | up] of shape [N, 2H] -> [N, H]."""
+    _need_gpu(gate_up)
+    n, h2 = gate_up.shape
+    out = torch.empty(n, h2 // 2, dtype=gate_up.dtype, device=gate_up.device) if out is None else out
+    _lib.check(_lib.load().saga_silu_mul(_lib.tensor(gate_up), _lib.tensor(out), _lib.stream_of(gate_up)), "silu_mul")
+    return out

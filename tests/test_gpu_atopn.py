@@ -180,9 +180,12 @@ def test_kv_len_equals_truncated_reference():
     (q, k, v), (qd, kd, vd) = qkv(rng, b, q_h, k_h, v_h, d, L, "bf16")
     lens = np.array([3000, 1777, 200], dtype=np.int32)
     kvl = torch.from_numpy(lens).cuda()
+    # the fast step uses a perturbed query: with the calibration query itself
+    # t equals the k-th logit exactly and that element's inclusion is a tie
+    q2 = O.round_bf16(q + np.float32(0.3) * rng.standard_normal(q.shape, dtype=np.float32))
     table = torch.zeros(b * q_h, device="cuda")
     cal = host(ops.atopn_calibrate(qd, kd, vd, N, table, kv_len=kvl, out_dtype=torch.float32))
-    fast = host(_run_fast(qd, kd, vd, table, N, kv_len=kvl))
+    fast = host(_run_fast(dev(q2, "bf16"), kd, vd, table, N, kv_len=kvl))
     dense = host(ops.dense_decode(qd, kd, vd, kv_len=kvl, out_dtype=torch.float32))
     views = _views(b, q_h, L, d, min(2 * N, L))
     _check_selection_rule(views, b * q_h, L, min(2 * N, L), kv_len=lens, q_h=q_h)
@@ -195,7 +198,7 @@ def test_kv_len_equals_truncated_reference():
         assert rel_l2(dense[i:i + 1], O.dense(qi, ki, vi)) < 1e-4
         # fast step over the truncated row uses the truncated row's own buf_k
         # only through L; here min(2N, n) == 2N for every n.
-        rf, _, _, _ = O.fast(qi, ki, vi, thr[i * q_h:(i + 1) * q_h], None, N, None)
+        rf, _, _, _ = O.fast(q2[i:i + 1], ki, vi, thr[i * q_h:(i + 1) * q_h], None, N, None)
         assert rel_l2(fast[i:i + 1], rf) < 1e-3
 
 

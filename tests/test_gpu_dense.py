@@ -46,3 +46,20 @@ def test_dense_with_masks():
         out = host(ops.dense_decode(qd, kd, vd, torch.from_numpy(m).cuda(), 0.1, out_dtype=torch.float32))
         ref = O.dense(q, k, v, m, 0.1)
         assert rel_l2(out, ref) < 1e-4
+
+
+def test_workspace_reuse_across_shapes():
+    """Calls of different shapes share one cached workspace; the arrival
+    counters live in a fixed region, so a later call never sees stale data
+    of an earlier layout (regression test)."""
+    rng = np.random.default_rng(6)
+    shapes = [(8, 12, 2, 2, 128, 20000), (2, 12, 1, 2, 128, 1000), (1, 15, 1, 5, 64, 4096), (2, 12, 1, 2, 128, 1000)]
+    for shape in shapes:
+        b, q_h, k_h, v_h, d, L = shape
+        (q, k, v), (qd, kd, vd) = qkv(rng, b, q_h, k_h, v_h, d, L, "bf16")
+        out = host(ops.dense_decode(qd, kd, vd, out_dtype=torch.float32))
+        assert rel_l2(out, O.dense(q, k, v)) < 1e-4, shape
+        table = torch.full((b * q_h,), 2e-4, device="cuda")
+        fast = host(ops.atopn_decode(qd, kd, vd, table, 128, out_dtype=torch.float32))
+        ref, _, _, _ = O.fast(q, k, v, host(table), None, 128, None)
+        assert rel_l2(fast, ref) < 1e-3, shape

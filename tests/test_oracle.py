@@ -330,3 +330,38 @@ def test_planted_unrenormalised_probs_is_caught(golden):
     rows = O._value_rows(inp["value"], 15, ik.reshape(1, 15, -1))
     raw = np.matmul(pk.reshape(1, 15, 1, -1), rows).reshape(g["cal_out"].shape)
     assert rel_l2(raw, g["cal_out"]) > 1e-2
+
+
+# ------------------------------------------------------- decode-step op pins
+
+def test_rope_is_a_rotation_with_the_hf_frequencies():
+    rng = np.random.default_rng(30)
+    d, theta = 8, 1e4
+    x = rng.standard_normal((3, d))
+    pos = np.array([0, 1, 37])
+    y = O.rope(x, pos, theta)
+    np.testing.assert_allclose(y[0], x[0])                      # position 0: identity
+    np.testing.assert_allclose(np.linalg.norm(y, axis=-1), np.linalg.norm(x, axis=-1))  # rotation
+    inv = 1.0 / theta ** (np.arange(0, d, 2) / d)
+    for n, p in enumerate(pos):                                 # brute force per pair (i, i + d/2)
+        for i in range(d // 2):
+            a = p * inv[i]
+            assert abs(y[n, i] - (x[n, i] * math.cos(a) - x[n, i + d // 2] * math.sin(a))) < 1e-5
+            assert abs(y[n, i + d // 2] - (x[n, i + d // 2] * math.cos(a) + x[n, i] * math.sin(a))) < 1e-5
+    # relative-position property of rotate-half RoPE: <R(p)q, R(p+k)k'> depends only on k
+    q, k = rng.standard_normal(d), rng.standard_normal(d)
+    dots = [float(O.rope(q, p, theta) @ O.rope(k, p + 5, theta)) for p in (0, 3, 11)]
+    np.testing.assert_allclose(dots, dots[0], rtol=1e-5)
+
+
+def test_rmsnorm_and_silu_mul_closed_forms():
+    rng = np.random.default_rng(31)
+    x = rng.standard_normal((2, 6))
+    w = rng.standard_normal(6)
+    y = O.rmsnorm(x, w, 1e-6)
+    np.testing.assert_allclose(((y / w) ** 2).mean(axis=-1), 1.0, rtol=1e-5)
+    gu = rng.standard_normal((2, 8))
+    ref = [[gu[n, i] * (1 / (1 + math.exp(-gu[n, i]))) * gu[n, 4 + i] for i in range(4)] for n in range(2)]
+    np.testing.assert_allclose(O.silu_mul(gu), ref)
+    t = torch.from_numpy(gu[:, :4])
+    np.testing.assert_allclose(O.silu_mul(gu), (torch.nn.functional.silu(t) * torch.from_numpy(gu[:, 4:])).numpy())
