@@ -200,6 +200,26 @@ int saga_rmsnorm(const saga_tensor* x, const saga_tensor* weight, float eps, sag
 /* y[n, i] = silu(x[n, i]) * x[n, H + i]; x [N, 2H] = [gate | up], y [N, H]. */
 int saga_silu_mul(const saga_tensor* gate_up, saga_tensor* y, saga_stream_t stream);
 
+/* Skinny GEMM for decode projections (M <= 16 token rows, bf16):
+ *   y[m, n] (op)= s[m] * sum_k x[m, k] * w[n, k]  (+ bias[n])
+ * s[m] = 1 / sqrt(mean_k x[m, k]^2 + eps) when rms_eps >= 0 (RMSNorm of x
+ * fused; its weight is expected folded into w), else 1.  epilogue:
+ *   SAGA_GEMV_STORE       y = result
+ *   SAGA_GEMV_ADD         y += result (residual stream, in place)
+ *   SAGA_GEMV_SILU_PAIRS  w rows are interleaved (gate_i, up_i); y[m, i] =
+ *                         silu(gate_i) * up_i, y is [M, N / 2]
+ * Replaces the hipBLASLt calls of the decode step (no reference counterpart:
+ * the reference's projections are torch nn.Linear).  N % 16 == 0, K % 32 == 0. */
+#define SAGA_GEMV_STORE 0
+#define SAGA_GEMV_ADD 1
+#define SAGA_GEMV_SILU_PAIRS 2
+int saga_gemv(const saga_tensor* x, const saga_tensor* w, const saga_tensor* bias, float rms_eps,
+              int32_t epilogue, saga_tensor* y, saga_stream_t stream);
+
+/* out[r] = first index of the maximum of row r of x [rows, N] (bf16); the
+ * greedy next token of speedup.py:169/193 (logits.argmax(dim=-1)). */
+int saga_argmax(const saga_tensor* x, int64_t* out, saga_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

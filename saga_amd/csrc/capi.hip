@@ -599,4 +599,58 @@ int saga_silu_mul(const saga_tensor* gate_up, saga_tensor* y, saga_stream_t stre
   return row_op(true, gate_up, nullptr, 0.f, y, stream);
 }
 
+int saga_gemv(const saga_tensor* x, const saga_tensor* w, const saga_tensor* bias, float rms_eps, int32_t epilogue,
+              saga_tensor* y, saga_stream_t stream) {
+  int rc;
+  if ((rc = check_tensor(x, "x", 2)) || (rc = check_tensor(w, "w", 2)) || (rc = check_tensor(y, "y", 2))) return rc;
+  if (x->dtype != SAGA_DTYPE_BF16 || w->dtype != SAGA_DTYPE_BF16 || y->dtype != SAGA_DTYPE_BF16)
+    return fail(SAGA_ERR_UNSUPPORTED, "gemv: bf16 only");
+  const int64_t M = x->shape[0], K = x->shape[1], N = w->shape[0];
+  if (w->shape[1] != K) return fail(SAGA_ERR_INVALID, "gemv: w must be [N, K] with K = x.shape[1]");
+  if (M > 16) return fail(SAGA_ERR_UNSUPPORTED, "gemv: at most 16 rows");
+  if (N % 16 || K % 32 || K >= (1LL << 30) || N >= (1LL << 30))
+    return fail(SAGA_ERR_UNSUPPORTED, "gemv: N %% 16 == 0 and K %% 32 == 0 required");
+  if (epilogue != SAGA_GEMV_STORE && epilogue != SAGA_GEMV_ADD && epilogue != SAGA_GEMV_SILU_PAIRS)
+    return fail(SAGA_ERR_INVALID, "gemv: unknown epilogue %d", epilogue);
+  const int64_t ny = epilogue == SAGA_GEMV_SILU_PAIRS ? N / 2 : N;
+  if (y->shape[0] != M || y->shape[1] != ny) return fail(SAGA_ERR_INVALID, "gemv: y must be [M, %lld]", (long long)ny);
+  if ((rc = check_vec_rows(x, "x")) || (rc = check_vec_rows(w, "w"))) return rc;
+  if (y->stride[1] != 1) return fail(SAGA_ERR_INVALID, "y: innermost stride must be 1");
+  if (bias) {
+    if ((rc = check_tensor(bias, "bias", 1))) return rc;
+    if (bias->dtype != SAGA_DTYPE_BF16 || bias->shape[0] != N || bias->stride[0] != 1)
+      return fail(SAGA_ERR_INVALID, "bias must be bf16 [N]");
+    if (epilogue == SAGA_GEMV_SILU_PAIRS) return fail(SAGA_ERR_UNSUPPORTED, "bias with SILU_PAIRS");
+  }
+  GemvParams p{};
+  p.x = x->data;
+  p.x_ld = x->stride[0];
+  p.w = w->data;
+  p.w_ld = w->stride[0];
+  p.bias = bias ? bias->data : nullptr;
+  p.y = y->data;
+  p.y_ld = y->stride[0];
+  p.M = static_cast<int32_t>(M);
+  p.N = static_cast<int32_t>(N);
+  p.K = static_cast<int32_t>(K);
+  p.rms = rms_eps >= 0.f;
+  p.eps = rms_eps;
+  p.epilogue = epilogue;
+  if ((rc = hip_status(launch_gemv(p, static_cast<hipStream_t>(stream)), "gemv launch"))) return rc;
+  return ok();
+}
+
+int saga_argmax(const saga_tensor* x, int64_t* out, saga_stream_t stream) {
+  int rc;
+  if ((rc = check_tensor(x, "x", 2))) return rc;
+  if (x->dtype != SAGA_DTYPE_BF16 || x->stride[1] != 1) return fail(SAGA_ERR_UNSUPPORTED, "argmax: bf16 rows with unit stride");
+  if (!out) return fail(SAGA_ERR_INVALID, "out: null");
+  if (x->shape[0] >= (1LL << 31) || x->shape[1] >= (1LL << 31)) return fail(SAGA_ERR_UNSUPPORTED, "argmax: too large");
+  if ((rc = hip_status(launch_argmax(x->data, x->stride[0], static_cast<int>(x->shape[0]), static_cast<int>(x->shape[1]),
+                                     out, static_cast<hipStream_t>(stream)),
+                       "argmax launch")))
+    return rc;
+  return ok();
+}
+
 }  // extern "C"

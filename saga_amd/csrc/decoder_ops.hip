@@ -24,11 +24,14 @@ __global__ void __launch_bounds__(256) rope_kv_append_kernel(RopeParams p) {
   for (int e = threadIdx.x; e < nrot + p.n_v * p.d; e += blockDim.x) {
     if (e < nrot) {
       const int hh = e / half, i = e - hh * half;
-      // inv_freq_i = theta^(-2i/d); angle = pos * inv_freq_i (fp32, as HF)
+      // inv_freq_i = theta^(-2i/d) and angle = pos * inv_freq_i in fp32, as
+      // HF computes them; cos/sin of that fp32 angle evaluated in fp64 (the
+      // angle reaches ~3e4 rad, where an fp32 sincos reduces slowly)
       const float inv_freq = 1.0f / powf(p.theta, static_cast<float>(2 * i) / static_cast<float>(p.d));
       const float ang = static_cast<float>(pos) * inv_freq;
-      float sn, cs;
-      sincosf(ang, &sn, &cs);
+      double sd, cd;
+      sincos(static_cast<double>(ang), &sd, &cd);
+      const float sn = static_cast<float>(sd), cs = static_cast<float>(cd);
       const int64_t base = row + static_cast<int64_t>(hh) * p.d;
       const float x1 = load_as_f32(p.qkv, p.dt, base + i);
       const float x2 = load_as_f32(p.qkv, p.dt, base + i + half);

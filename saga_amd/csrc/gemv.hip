@@ -1,0 +1,169 @@
+// Skinny GEMM for decode projections: y[m, n] = sum_k x[m, k] * W[n, k], m < 16.
+//
+// Decode steps multiply a handful of token rows (the batch) by every weight
+// matrix once, so the kernel is a weight stream: 16 rows of W per MFMA tile,
+// loaded 16 bytes per lane straight into the A fragment of
+// v_mfma_f32_16x16x32_bf16 (as K1 streams K rows), with the token rows as
+// the B fragment.  A workgroup owns 16 output columns n; its waves split K
+// and meet in LDS.  Fused pieces:
+//   * RMSNorm of x (Qwen2RMSNorm): the norm weight is folded into W when the
+//     model is built, and the per-row 1/sqrt(mean(x^2) + eps) is a scalar of
+//     the output row, accumulated from the x fragments the waves load anyway;
+//   * epilogues: + bias, += into y (residual stream), or silu(gate) * up for
+//     W rows interleaved as [gate_0, up_0, gate_1, up_1, ...].
+#include "common.cuh"
+#include "kernels.h"
+
+namespace saga {
+
+constexpr int kGemvUnroll = 8;  // 32-wide k steps in flight per wave
+
+template <int WAVES, int EPI>
+__global__ void __launch_bounds__(WAVES * 64) gemv_kernel(GemvParams p) {
+  __shared__ float red[WAVES][64][5];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int col = lane & 15, s = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const bool mvalid = col < p.M;
+  const char* wrow = static_cast<const char*>(p.w) + (static_cast<int64_t>(n0 + col) * p.w_ld + 8 * s) * 2;
+  const char* xrow = static_cast<const char*>(p.x) + (static_cast<int64_t>(mvalid ? col : 0) * p.x_ld + 8 * s) * 2;
+  const int steps = p.K / 32;
+  const int j0 = w * steps / WAVES, j1 = (w + 1) * steps / WAVES;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  float ssq = 0.f;
+  for (int j = j0; j < j1; j += kGemvUnroll) {
+    u32x4 a[kGemvUnroll], b[kGemvUnroll];
+#pragma unroll
+    for (int u = 0; u < kGemvUnroll; ++u) {
+      const int jj = min(j + u, j1 - 1);
+      a[u] = ld16(wrow + static_cast<int64_t>(jj) * 64);
+      b[u] = mvalid ? ld16(xrow + static_cast<int64_t>(jj) * 64) : u32x4{0u, 0u, 0u, 0u};
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kGemvUnroll; ++u) {
+      if (j + u < j1) {
+        acc = mfma_16b<SAGA_DTYPE_BF16>(a[u], b[u], acc);
+        if (p.rms) {
+          float f[8];
+          unpack16<SAGA_DTYPE_BF16>(b[u], f);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) ssq += f[i] * f[i];
+        }
+      }
+    }
+  }
+  // lane (col, s): rows n0 + 4s + r of the tile for token row m = col
+#pragma unroll
+  for (int r = 0; r < 4; ++r) red[w][lane][r] = acc[r];
+  red[w][lane][4] = ssq;
+  __syncthreads();
+  if (w != 0) return;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  float sq = 0.f;
+#pragma unroll
+  for (int q = 0; q < WAVES; ++q) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] += red[q][lane][r];
+    if (p.rms) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) sq += red[q][col + 16 * g][4];  // all k-slot groups of row m
+    }
+  }
+  if (!mvalid) return;
+  const float scale = p.rms ? rsqrtf(sq / static_cast<float>(p.K) + p.eps) : 1.f;
+  const int n = n0 + 4 * s;
+  uint16_t* y = static_cast<uint16_t*>(p.y) + static_cast<int64_t>(col) * p.y_ld;
+  if constexpr (EPI == SAGA_GEMV_SILU_PAIRS) {
+    // rows (n, n+1) and (n+2, n+3) are (gate, up) pairs -> outputs n/2, n/2 + 1
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const float g = v[2 * q] * scale, u = v[2 * q + 1] * scale;
+      y[n / 2 + q] = f32_to_bf16_bits(g / (1.0f + expf(-g)) * u);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float o = v[r] * scale;
+      if (p.bias) o += bf16_bits_to_f32(static_cast<const uint16_t*>(p.bias)[n + r]);
+      if constexpr (EPI == SAGA_GEMV_ADD) o += bf16_bits_to_f32(y[n + r]);
+      y[n + r] = f32_to_bf16_bits(o);
+    }
+  }
+}
+
+template <int EPI>
+static hipError_t launch_gemv_epi(const GemvParams& p, hipStream_t st) {
+  const unsigned blocks = static_cast<unsigned>(p.N / 16);
+  // long rows of W: more waves per workgroup split K
+  if (p.K >= 4096)
+    hipLaunchKernelGGL((gemv_kernel<16, EPI>), dim3(blocks), dim3(1024), 0, st, p);
+  else
+    hipLaunchKernelGGL((gemv_kernel<4, EPI>), dim3(blocks), dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemv(const GemvParams& p, hipStream_t st) {
+  switch (p.epilogue) {
+    case SAGA_GEMV_ADD: return launch_gemv_epi<SAGA_GEMV_ADD>(p, st);
+    case SAGA_GEMV_SILU_PAIRS: return launch_gemv_epi<SAGA_GEMV_SILU_PAIRS>(p, st);
+    default: return launch_gemv_epi<SAGA_GEMV_STORE>(p, st);
+  }
+}
+
+// Row-wise argmax (first index of the maximum), one block per row; rows are
+// read 8 bf16 per lane (16-byte loads), four loads in flight per lane.
+__device__ __forceinline__ void argmax_take(float v, int i, float& best, int& idx) {
+  if (v > best || (v == best && i < idx)) {
+    best = v;
+    idx = i;
+  }
+}
+
+__global__ void __launch_bounds__(1024) argmax_kernel(const uint16_t* x, int64_t ld, int N, int64_t* out) {
+  __shared__ float bv[16];
+  __shared__ int bi[16];
+  const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const uint16_t* row = x + static_cast<int64_t>(r) * ld;
+  float best = kNegInf;
+  int idx = 0x7fffffff;
+  const bool vec = (reinterpret_cast<uintptr_t>(row) % 16) == 0;
+  const int nv = vec ? N / 8 : 0;  // full 8-element groups
+  for (int g0 = tid; g0 < nv; g0 += 4 * 1024) {
+    u32x4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int g = g0 + u * 1024;
+      v[u] = g < nv ? ld16(row + 8 * static_cast<int64_t>(g)) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int g = g0 + u * 1024;
+      if (g < nv) {
+        float f[8];
+        unpack16<SAGA_DTYPE_BF16>(v[u], f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) argmax_take(f[e], 8 * g + e, best, idx);
+      }
+    }
+  }
+  for (int i = 8 * nv + tid; i < N; i += 1024) argmax_take(bf16_bits_to_f32(row[i]), i, best, idx);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) argmax_take(__shfl_xor(best, o), __shfl_xor(idx, o), best, idx);
+  if (lane == 0) {
+    bv[w] = best;
+    bi[w] = idx;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int q = 1; q < 16; ++q) argmax_take(bv[q], bi[q], best, idx);
+    out[r] = idx == 0x7fffffff ? 0 : idx;
+  }
+}
+
+hipError_t launch_argmax(const void* x, int64_t ld, int rows, int N, int64_t* out, hipStream_t st) {
+  hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(1024), 0, st, static_cast<const uint16_t*>(x), ld, N, out);
+  return hipGetLastError();
+}
+
+}  // namespace saga

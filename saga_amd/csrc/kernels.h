@@ -155,4 +155,21 @@ struct RowParams {
 hipError_t launch_rmsnorm(const RowParams& p, hipStream_t st);
 hipError_t launch_silu_mul(const RowParams& p, hipStream_t st);
 
+// Skinny GEMM y[m, n] = rms(x)[m] * sum_k x[m, k] W[n, k] (+ epilogue), m < 16.
+struct GemvParams {
+  const void* x;  // bf16 [M, K]
+  int64_t x_ld;
+  const void* w;  // bf16 [N, K]
+  int64_t w_ld;
+  const void* bias;  // bf16 [N] or null
+  void* y;           // bf16 [M, N] (SILU_PAIRS: [M, N / 2])
+  int64_t y_ld;
+  int32_t M, N, K;
+  int32_t rms;  // scale by 1/sqrt(mean(x^2) + eps)
+  float eps;
+  int32_t epilogue;
+};
+hipError_t launch_gemv(const GemvParams& p, hipStream_t st);
+hipError_t launch_argmax(const void* x, int64_t ld, int rows, int N, int64_t* out, hipStream_t st);
+
 }  // namespace saga

@@ -8,12 +8,14 @@ one for the fast steps -- replayed once per token (capture_cuda_graphs /
 decode_with_graph, :179-291).  Weights are random (no checkpoints here); the
 shapes are the benchmarked models'.
 
-Per layer and step: rmsnorm -> fused q/k/v projection (+bias) -> RoPE + cache
-append -> attention (Atop-N fast step, calibration step or dense) -> o_proj
-with the residual folded in -> rmsnorm -> [gate | up] projection -> silu*up ->
-down projection with the residual folded in.  The attention and the
-row-wise ops are saga_amd HIP kernels; the projections are hipBLASLt GEMMs.
-Positions advance on the device, so one captured graph serves every step.
+Per layer and step (7 launches): q/k/v projection with the RMSNorm and bias
+fused -> RoPE + cache append -> attention (Atop-N: scores, then
+select + softmax.V; or dense) -> o_proj accumulated into the residual stream
+-> [gate, up] projection with the RMSNorm and silu(gate)*up fused -> down
+projection accumulated into the residual stream.  Projections use the
+saga_amd skinny GEMM (batch <= 16; hipBLASLt otherwise), the LM head is
+followed by a row argmax kernel.  Positions advance on the device, so one
+captured graph serves every step.
 """
 from __future__ import annotations
 
@@ -117,9 +119,30 @@ class SagaDecoder:
         self._gu = torch.empty(batch, 2 * s.intermediate, device=self.device, dtype=dtype)
         self._act = torch.empty(batch, s.intermediate, device=self.device, dtype=dtype)
         self._logits = torch.empty(batch, s.vocab, device=self.device, dtype=dtype)
+        # decode projections: the skinny-GEMM kernel for up to 16 token rows
+        self.use_gemv = (batch <= 16 and dtype == torch.bfloat16 and s.hidden % 32 == 0 and s.intermediate % 32 == 0
+                         and (s.n_q * d) % 32 == 0 and s.qkv_width % 16 == 0 and s.vocab % 16 == 0)
+        self.prepare_kernel_weights()
         self.graph_cal: Optional[torch.cuda.CUDAGraph] = None
         self.graph_fast: Optional[torch.cuda.CUDAGraph] = None
         self.prompt_len = 0
+
+    def prepare_kernel_weights(self) -> None:
+        """Decode-layout copies of the weights for the skinny GEMM: RMSNorm
+        weights folded into the following projection (w * diag(norm)), gate
+        and up rows interleaved (gate_0, up_0, gate_1, ...) so one output tile
+        holds both halves of silu(gate) * up, and a normed LM head."""
+        if not self.use_gemv:
+            return
+        s = self.shape
+        with torch.no_grad():
+            self.kw_qkv = [(self.w_qkv[l].float() * self.ln1[l].float()).to(self.dtype) for l in range(s.layers)]
+            self.kw_gu = []
+            for l in range(s.layers):
+                w = (self.w_gu[l].float() * self.ln2[l].float()).to(self.dtype)
+                self.kw_gu.append(torch.stack([w[:s.intermediate], w[s.intermediate:]], dim=1)
+                                  .reshape(2 * s.intermediate, s.hidden).contiguous())
+            self.kw_lm = (self.embed.float() * self.ln_f.float()).to(self.dtype)
 
     # ------------------------------------------------------------------ prefill
     @torch.no_grad()
@@ -186,8 +209,11 @@ class SagaDecoder:
         torch.index_select(self.embed, 0, self.tokens, out=x)
         q4 = self._q.view(B, s.n_q, 1, d)
         for l in range(s.layers):
-            ops.rmsnorm(x, self.ln1[l], s.eps, out=self._h)
-            torch.addmm(self.b_qkv[l], self._h, self.w_qkv[l].t(), out=self._qkv)
+            if self.use_gemv:
+                ops.gemv(x, self.kw_qkv[l], bias=self.b_qkv[l], rms_eps=s.eps, out=self._qkv)
+            else:
+                ops.rmsnorm(x, self.ln1[l], s.eps, out=self._h)
+                torch.addmm(self.b_qkv[l], self._h, self.w_qkv[l].t(), out=self._qkv)
             ops.rope_kv_append(self._qkv, s.n_q, s.n_k, s.n_v, s.rope_theta, self.pos, self.k_cache[l],
                                self.v_cache[l], q_out=self._q)
             K, V = self.k_cache[l], self.v_cache[l]
@@ -197,14 +223,23 @@ class SagaDecoder:
                 ops.atopn_calibrate(q4, K, V, self.top_n, self.table[l], kv_len=self.kv_len, out=self._attn)
             else:
                 ops.atopn_decode(q4, K, V, self.table[l], self.top_n, kv_len=self.kv_len, out=self._attn)
-            x.addmm_(self._attn.view(B, s.n_q * d), self.w_o[l].t())
-            ops.rmsnorm(x, self.ln2[l], s.eps, out=self._h)
-            torch.mm(self._h, self.w_gu[l].t(), out=self._gu)
-            ops.silu_mul(self._gu, out=self._act)
-            x.addmm_(self._act, self.w_d[l].t())
-        ops.rmsnorm(x, self.ln_f, s.eps, out=self._h)
-        torch.mm(self._h, self.embed.t(), out=self._logits)
-        torch.argmax(self._logits, dim=-1, out=self.tokens)
+            if self.use_gemv:
+                ops.gemv(self._attn.view(B, s.n_q * d), self.w_o[l], epilogue="add", out=x)
+                ops.gemv(x, self.kw_gu[l], rms_eps=s.eps, epilogue="silu_pairs", out=self._act)
+                ops.gemv(self._act, self.w_d[l], epilogue="add", out=x)
+            else:
+                x.addmm_(self._attn.view(B, s.n_q * d), self.w_o[l].t())
+                ops.rmsnorm(x, self.ln2[l], s.eps, out=self._h)
+                torch.mm(self._h, self.w_gu[l].t(), out=self._gu)
+                ops.silu_mul(self._gu, out=self._act)
+                x.addmm_(self._act, self.w_d[l].t())
+        if self.use_gemv:
+            ops.gemv(x, self.kw_lm, rms_eps=s.eps, out=self._logits)
+            ops.argmax_rows(self._logits, out=self.tokens)
+        else:
+            ops.rmsnorm(x, self.ln_f, s.eps, out=self._h)
+            torch.mm(self._h, self.embed.t(), out=self._logits)
+            torch.argmax(self._logits, dim=-1, out=self.tokens)
         self.pos.add_(1)
         self.kv_len.add_(1)
 

@@ -283,3 +283,31 @@ def silu_mul(gate_up, out=None):
     out = torch.empty(n, h2 // 2, dtype=gate_up.dtype, device=gate_up.device) if out is None else out
     _lib.check(_lib.load().saga_silu_mul(_lib.tensor(gate_up), _lib.tensor(out), _lib.stream_of(gate_up)), "silu_mul")
     return out
+
+
+def gemv(x, w, bias=None, rms_eps=None, epilogue="store", out=None):
+    """Skinny projection for decode (x [M <= 16, K] bf16, w [N, K] bf16):
+    y = s * x @ w.T (+ bias), s = 1/sqrt(mean(x^2) + rms_eps) per row when
+    rms_eps is given (RMSNorm fused, norm weight folded into w).
+    epilogue: "store", "add" (out += result, in place) or "silu_pairs" (w rows
+    interleaved gate/up; out = silu(gate) * up, [M, N/2])."""
+    _need_gpu(x, w, bias, out)
+    codes = {"store": _lib.GEMV_STORE, "add": _lib.GEMV_ADD, "silu_pairs": _lib.GEMV_SILU_PAIRS}
+    code = codes[epilogue]
+    M, N = x.shape[0], w.shape[0]
+    if out is None:
+        if code == _lib.GEMV_ADD:
+            raise ValueError("saga_amd: epilogue 'add' needs out")
+        out = torch.empty(M, N // 2 if code == _lib.GEMV_SILU_PAIRS else N, dtype=x.dtype, device=x.device)
+    eps = -1.0 if rms_eps is None else float(rms_eps)
+    _lib.check(_lib.load().saga_gemv(_lib.tensor(x), _lib.tensor(w), _lib.tensor(bias), eps, code, _lib.tensor(out),
+                                     _lib.stream_of(x)), "gemv")
+    return out
+
+
+def argmax_rows(x, out=None):
+    """First index of each row's maximum (bf16 [rows, N]) -> int64 [rows]."""
+    _need_gpu(x, out)
+    out = torch.empty(x.shape[0], dtype=torch.int64, device=x.device) if out is None else out
+    _lib.check(_lib.load().saga_argmax(_lib.tensor(x), _lib.ptr(out), _lib.stream_of(x)), "argmax")
+    return out

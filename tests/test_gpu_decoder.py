@@ -60,7 +60,7 @@ def test_rmsnorm_and_silu_mul_match_oracle():
 
 def _tiny_model(mode, top_n=16):
     from saga_amd.decoder import DecoderShape, SagaDecoder
-    shape = DecoderShape(layers=3, hidden=256, n_q=4, n_k=1, n_v=2, head_dim=64, intermediate=512, vocab=1000,
+    shape = DecoderShape(layers=3, hidden=256, n_q=4, n_k=1, n_v=2, head_dim=64, intermediate=512, vocab=1024,
                          rope_theta=1e4, eps=1e-6, qkv_bias=True)
     m = SagaDecoder(shape, batch=2, max_len=600, mode=mode, top_n=top_n, exempt_layers=(0,) if mode == "atopn" else ())
     return m
@@ -69,7 +69,7 @@ def _tiny_model(mode, top_n=16):
 @pytest.mark.parametrize("mode", ["atopn", "dense"])
 def test_graph_replay_equals_eager_steps(mode):
     m = _tiny_model(mode)
-    m.prefill(torch.randint(0, 1000, (500,)))
+    m.prefill(torch.randint(0, 1024, (500,)))
     m.capture()
     m.reset()
     for i in range(4):
@@ -92,15 +92,20 @@ def test_one_decode_step_vs_float64_reference():
     (Dense attention: an Atop-N top-k boundary could flip under the bf16
     rounding of the intermediates; selection is checked by its own tests.)"""
     m = _tiny_model("dense")
+    g = torch.Generator(device="cuda").manual_seed(5)
+    for t in m.ln1 + m.ln2 + [m.ln_f]:  # non-trivial norm weights: exercises their folding
+        t.copy_((1 + 0.3 * torch.randn(t.shape, generator=g, device="cuda")).to(t.dtype))
+    m.prepare_kernel_weights()
+    assert m.use_gemv
     prompt_len = 400
     m.fill_synthetic(prompt_len)
-    m.tokens.copy_(torch.tensor([3, 999], device="cuda"))
+    m.tokens.copy_(torch.tensor([3, 1023], device="cuda"))
     s = m.shape
     f = lambda t: t.detach().to(torch.float64).cpu().numpy()
     kc0, vc0 = f(m.k_cache), f(m.v_cache)
     m.step(calibrate=True)
     torch.cuda.synchronize()
-    x = f(m.embed)[[3, 999]]
+    x = f(m.embed)[[3, 1023]]
     for l in range(s.layers):
         h = O.rmsnorm(x, f(m.ln1[l]), s.eps)
         qkv = h @ f(m.w_qkv[l]).T + f(m.b_qkv[l])
