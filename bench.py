@@ -66,6 +66,21 @@ def timed_graph(fn, n_launch, repeats=3):
     return best
 
 
+def k1_traffic(batch, ctx, shape):
+    """HBM bytes per K1 launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes (profiles/k1_qk_scores_*_traffic.json), when they were
+    taken at this workload; else None."""
+    import glob
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "k1_qk_scores_*_traffic.json"))):
+        with open(path) as f:
+            d = json.load(f)
+        w = d.get("workload", {})
+        if (w.get("batch"), w.get("ctx"), w.get("n_q"), w.get("n_k"), w.get("head_dim")) == \
+                (batch, ctx, shape.n_q, shape.n_k, shape.head_dim):
+            return int(d["traffic_bytes_per_launch"]), os.path.relpath(path, ROOT)
+    return None, None
+
+
 def decode_rate(model, steps, warmup):
     """Warm-up replays, then exactly `steps` timed replays bracketed by syncs."""
     model.reset()
@@ -86,7 +101,7 @@ def decode_rate(model, steps, warmup):
     return ms / steps, model.batch * steps / (ms / 1000.0), wall
 
 
-def cpu_baseline(batch, ctx, shape, top_n, layers):
+def cpu_baseline(batch, ctx, shape, top_n, layers, min_secs=10.0, max_steps=30):
     """The oracle (reference fp32 path) on one decode step of attention."""
     from oracle import saga_oracle as O
     try:
@@ -102,26 +117,57 @@ def cpu_baseline(batch, ctx, shape, top_n, layers):
     q2 = q + np.float32(0.3) * rng.standard_normal(q.shape, dtype=np.float32)
 
     def run():
-        t0 = time.perf_counter()
-        _, thr, _ = O.calibrate(q, k, v, None, top_n, None)
-        for _ in range(layers - 1):
-            O.fast(q2, k, v, thr, None, top_n, None)
-        return time.perf_counter() - t0
+        # whole decode steps (a calibration layer + fast layers) until about
+        # min_secs of CPU work, at most max_steps
+        steps, t0 = 0, time.perf_counter()
+        while True:
+            _, thr, _ = O.calibrate(q, k, v, None, top_n, None)
+            for _ in range(layers - 1):
+                O.fast(q2, k, v, thr, None, top_n, None)
+            steps += 1
+            secs = time.perf_counter() - t0
+            if secs >= min_secs or steps >= max_steps:
+                return steps, secs
 
     if threadpool_limits is not None:
         with threadpool_limits(limits=cores):
-            secs = run()
+            steps, secs = run()
     else:
-        secs = run()
+        steps, secs = run()
     return {
-        "value": round(batch / secs, 3),
-        "unit": "tokens/s (attention only, 28 layers)",
+        "value": round(batch * steps / secs, 3),
+        "unit": f"tokens/s (attention only, {layers} layers)",
         "cores": cores,
         "kind": "port",
-        "sample": (f"one decode step: {layers} layers of Atop-N attention (1 calibration + {layers - 1} fast), "
-                   f"b{batch} q{shape.n_q}/k{shape.n_k}/v{shape.n_v} d{shape.head_dim} ctx {L}, fp32, "
+        "sample": (f"{steps} decode steps of attention, each {layers} layers (1 calibration + {layers - 1} fast), "
+                   f"b{batch} q{shape.n_q}/k{shape.n_k}/v{shape.n_v} d{shape.head_dim} ctx {L}, N={top_n}, fp32, "
                    f"numpy oracle, {secs:.1f} s"),
     }
+
+
+def profile_kernels(batch, ctx, shape, launches=8):
+    """K1 alone at the decode shape (K cache of ctx + 1 positions), then a
+    plain 1 GiB device-to-device copy: per-dispatch hardware counters of the
+    copy (2 GiB of known traffic) scale those of K1."""
+    from saga_amd import ops
+    L = ctx + 1
+    g = torch.Generator(device="cuda").manual_seed(0)
+    q = torch.randn(batch, shape.n_q, 1, shape.head_dim, device="cuda", generator=g).to(torch.bfloat16)
+    k = torch.randn(batch, shape.n_k, L, shape.head_dim, device="cuda", generator=g).to(torch.bfloat16)
+    kvl = torch.full((batch,), L, dtype=torch.int32, device="cuda")
+    for _ in range(launches):
+        ops.qk_scores(q, k, kv_len=kvl, with_partials=True)
+    src = torch.empty(1 << 29, dtype=torch.int16, device="cuda")
+    src.fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    k1_bytes = batch * shape.n_k * L * shape.head_dim * 2 + batch * shape.n_q * shape.head_dim * 2
+    print(json.dumps({"k1_launches": launches, "k1_algorithmic_bytes": k1_bytes,
+                      "copy_launches": 3, "copy_bytes_read": src.numel() * 2, "copy_bytes_written": dst.numel() * 2}),
+          flush=True)
+    return 0
 
 
 def main():
@@ -135,6 +181,9 @@ def main():
     ap.add_argument("--no-dense", action="store_true", help="skip the dense-GQA comparator")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--synthetic-kv", action="store_true", help="fill the caches with N(0,1) instead of a prefill")
+    ap.add_argument("--profile-kernels", action="store_true",
+                    help="only launch K1 (qk_scores) at the workload shape and a 1 GiB device copy, "
+                         "for hardware-counter runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -148,6 +197,8 @@ def main():
     from saga_amd.decoder import QWEN25_15B_GQA, QWEN25_15B_SAGA, SagaDecoder
 
     B, ctx, K, W = args.batch, args.ctx, args.steps, args.warmup
+    if args.profile_kernels:
+        return profile_kernels(B, ctx, QWEN25_15B_SAGA)
     max_len = ctx + K
     torch.manual_seed(0)
     prompt = torch.randint(0, QWEN25_15B_SAGA.vocab, (ctx,), dtype=torch.int64)
@@ -208,6 +259,7 @@ def main():
         cpu = cpu_baseline(B, ctx, QWEN25_15B_SAGA, args.top_n, QWEN25_15B_SAGA.layers)
         log(f"CPU: {cpu['value']} attention tokens/s on {cpu['cores']} cores")
 
+    traffic, traffic_src = k1_traffic(B, ctx, QWEN25_15B_SAGA)
     out = {
         "metric": METRIC,
         "value": round(tps, 1),
@@ -236,7 +288,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(k1_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_src,
             "us_per_launch": round(k1_us, 3),
             "algorithmic_bytes_per_launch": k1_bytes,
         },

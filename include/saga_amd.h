@@ -59,9 +59,6 @@ extern "C" {
 #define SAGA_ERR_WORKSPACE (-3)   /* workspace missing or too small */
 #define SAGA_ERR_HIP (-4)         /* a HIP runtime call failed */
 
-/* Score partials are kept per chunk of this many key positions. */
-#define SAGA_CHUNK 128
-
 typedef struct saga_tensor {
   void* data;
   int32_t dtype;
@@ -77,9 +74,9 @@ typedef void* saga_stream_t;
 typedef struct saga_atopn_layout {
   int64_t scores;    /* f32 [b*q_h, scores_ld] */
   int64_t scores_ld; /* elements */
-  int64_t part_max;  /* f32 [b*q_h, nchunk] */
-  int64_t part_sum;  /* f32 [b*q_h, nchunk] */
-  int64_t nchunk;
+  int64_t part_max;  /* f32 [b*q_h, nparts] */
+  int64_t part_sum;  /* f32 [b*q_h, nparts] */
+  int64_t nparts;    /* saga_qk_nparts(b, k_h, L) */
   int64_t thresh;    /* f32 [b*q_h] logit threshold (fast step) */
   int64_t sel_idx;   /* i32 [b*q_h, buf_k] ascending positions */
   int64_t sel_val;   /* f32 [b*q_h, buf_k] their logits */
@@ -99,7 +96,11 @@ const char* saga_last_error(void);
  * (bmm of the grouped queries with K^T, * scaling, + mask).
  * scores: f32 [b, q_h, 1, >=L] (last stride 1), written for positions < L
  * (positions >= kv_len[i] are -inf).  part_max/part_sum (optional, f32
- * [b*q_h, ceil(L/SAGA_CHUNK)]): per-chunk max and sum of exp(x - max). */
+ * [b*q_h, saga_qk_nparts(b, k_h, L)]): max and sum of exp(x - max) of each
+ * part of the row (contiguous ranges of positions; a part wholly past kv_len
+ * holds (-inf, 0)).  Their log-sum-exp merge is the row's softmax
+ * normaliser, so the logit threshold needs no second pass over the scores. */
+int64_t saga_qk_nparts(int64_t b, int64_t k_h, int64_t L);
 int saga_qk_scores(const saga_tensor* query, const saga_tensor* key, const saga_tensor* mask,
                    const int32_t* kv_len, float scale, saga_tensor* scores, float* part_max,
                    float* part_sum, saga_stream_t stream);
@@ -141,8 +142,8 @@ int saga_sparse_softmax_pv(const saga_tensor* weights, const saga_tensor* indice
 
 /* Workspace of the fused decode entry points; buf_k = min(2*top_n, L) for
  * saga_atopn_decode, min(top_n, L) for saga_atopn_calibrate. */
-size_t saga_atopn_workspace_bytes(int64_t b, int64_t q_h, int64_t L, int64_t d, int64_t buf_k);
-int saga_atopn_workspace_layout(int64_t b, int64_t q_h, int64_t L, int64_t d, int64_t buf_k,
+size_t saga_atopn_workspace_bytes(int64_t b, int64_t q_h, int64_t k_h, int64_t L, int64_t d, int64_t buf_k);
+int saga_atopn_workspace_layout(int64_t b, int64_t q_h, int64_t k_h, int64_t L, int64_t d, int64_t buf_k,
                                 saga_atopn_layout* layout);
 
 /* Atop-N fast decode step: scores, logit threshold from the stored
@@ -215,6 +216,22 @@ int saga_silu_mul(const saga_tensor* gate_up, saga_tensor* y, saga_stream_t stre
 #define SAGA_GEMV_SILU_PAIRS 2
 int saga_gemv(const saga_tensor* x, const saga_tensor* w, const saga_tensor* bias, float rms_eps,
               int32_t epilogue, saga_tensor* y, saga_stream_t stream);
+
+/* saga_gemv (STORE, bias, fused RMSNorm) of the fused q/k/v projection with
+ * saga_rope_kv_append applied in its epilogue: one launch per layer for
+ * projection + RoPE + cache append.  x [M, K] (M <= 16 new tokens), w bf16
+ * [(n_q + n_k + n_v) * d, K] and bias [(n_q + n_k + n_v) * d] hold the q, k
+ * and v heads in that order, with the rows of every q and k head permuted to
+ * rotary-pair order [0, d/2, 1, d/2 + 1, ..., d/2 - 1, d - 1] (v heads
+ * unpermuted).  The projection output is rounded to bf16 before the rotation,
+ * so results equal saga_gemv into an unpermuted qkv followed by
+ * saga_rope_kv_append.  Replaces q/k/v_proj + apply_rotary_pos_emb + the
+ * cache update (transformers models/qwen2/modeling_qwen2.py:205-214,
+ * cache_utils.py:455-487).  d % 16 == 0. */
+int saga_gemv_rope_kv(const saga_tensor* x, const saga_tensor* w, const saga_tensor* bias, float rms_eps,
+                      int64_t n_q, int64_t n_k, int64_t n_v, float theta, const int32_t* pos,
+                      const int32_t* batch, saga_tensor* q_out, saga_tensor* k_cache,
+                      saga_tensor* v_cache, saga_stream_t stream);
 
 /* out[r] = first index of the maximum of row r of x [rows, N] (bf16); the
  * greedy next token of speedup.py:169/193 (logits.argmax(dim=-1)). */

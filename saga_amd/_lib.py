@@ -27,7 +27,6 @@ _TORCH_DTYPES = {
 
 SAGA_OK = 0
 ERRORS = {-1: "invalid argument", -2: "unsupported", -3: "workspace", -4: "HIP runtime"}
-CHUNK = 128  # SAGA_CHUNK
 
 
 class SagaTensor(ctypes.Structure):
@@ -42,7 +41,7 @@ class SagaTensor(ctypes.Structure):
 
 class AtopnLayout(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int64) for n in (
-        "scores", "scores_ld", "part_max", "part_sum", "nchunk", "thresh", "sel_idx", "sel_val",
+        "scores", "scores_ld", "part_max", "part_sum", "nparts", "thresh", "sel_idx", "sel_val",
         "sel_cnt", "sel_total", "total_bytes")]
 
 
@@ -57,8 +56,10 @@ _SIGS = {
     "saga_logit_threshold": (ctypes.c_int, [_T, _P, _P, _P, _P]),
     "saga_threshold_select": (ctypes.c_int, [_T, _P, _I64, _I64, _T, _P, _P, _P]),
     "saga_sparse_softmax_pv": (ctypes.c_int, [_T, _T, _T, ctypes.c_int32, _T, _P]),
-    "saga_atopn_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I64, _I64]),
-    "saga_atopn_workspace_layout": (ctypes.c_int, [_I64, _I64, _I64, _I64, _I64, ctypes.POINTER(AtopnLayout)]),
+    "saga_qk_nparts": (ctypes.c_int64, [_I64, _I64, _I64]),
+    "saga_atopn_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I64, _I64, _I64]),
+    "saga_atopn_workspace_layout": (ctypes.c_int, [_I64, _I64, _I64, _I64, _I64, _I64,
+                                                   ctypes.POINTER(AtopnLayout)]),
     "saga_atopn_decode": (ctypes.c_int, [_T, _T, _T, _T, _P, ctypes.c_float, _I64, _P, _T, _P, ctypes.c_size_t, _P]),
     "saga_atopn_calibrate": (ctypes.c_int, [_T, _T, _T, _T, _P, ctypes.c_float, _I64, _P, _T, _P, ctypes.c_size_t, _P]),
     "saga_dense_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I64]),
@@ -67,6 +68,8 @@ _SIGS = {
     "saga_rmsnorm": (ctypes.c_int, [_T, _T, ctypes.c_float, _T, _P]),
     "saga_silu_mul": (ctypes.c_int, [_T, _T, _P]),
     "saga_gemv": (ctypes.c_int, [_T, _T, _T, ctypes.c_float, ctypes.c_int32, _T, _P]),
+    "saga_gemv_rope_kv": (ctypes.c_int, [_T, _T, _T, ctypes.c_float, _I64, _I64, _I64, ctypes.c_float, _P, _P,
+                                         _T, _T, _T, _P]),
     "saga_argmax": (ctypes.c_int, [_T, _P, _P]),
 }
 GEMV_STORE, GEMV_ADD, GEMV_SILU_PAIRS = 0, 1, 2
@@ -134,7 +137,7 @@ def stream_of(t: torch.Tensor):
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
-def atopn_layout(b: int, q_h: int, L: int, d: int, buf_k: int) -> AtopnLayout:
+def atopn_layout(b: int, q_h: int, k_h: int, L: int, d: int, buf_k: int) -> AtopnLayout:
     lay = AtopnLayout()
-    check(load().saga_atopn_workspace_layout(b, q_h, L, d, buf_k, ctypes.byref(lay)), "workspace_layout")
+    check(load().saga_atopn_workspace_layout(b, q_h, k_h, L, d, buf_k, ctypes.byref(lay)), "workspace_layout")
     return lay

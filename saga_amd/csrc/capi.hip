@@ -162,16 +162,17 @@ QKParams make_qk(const saga_tensor* q, const saga_tensor* k, const saga_tensor* 
   p.k_h = static_cast<int32_t>(s.k_h);
   p.g = static_cast<int32_t>(s.q_h / s.k_h);
   p.L = static_cast<int32_t>(s.L);
-  p.nchunk = static_cast<int32_t>((s.L + SAGA_CHUNK - 1) / SAGA_CHUNK);
+  p.ntiles = static_cast<int32_t>((s.L + 15) / 16);
+  p.nparts = static_cast<int32_t>(qk_plan(s.b, s.k_h, s.L));
   p.scale = scale;
   return p;
 }
 
-void atopn_layout(int64_t b, int64_t q_h, int64_t L, int64_t d, int64_t buf_k, saga_atopn_layout* o) {
+void atopn_layout(int64_t b, int64_t q_h, int64_t k_h, int64_t L, int64_t d, int64_t buf_k, saga_atopn_layout* o) {
   (void)d;
   const int64_t nr = b * q_h;
   const int64_t ld = (L + 15) / 16 * 16;
-  const int64_t nchunk = (L + SAGA_CHUNK - 1) / SAGA_CHUNK;
+  const int64_t nparts = qk_plan(b, k_h, L);
   int64_t off = 0;
   auto take = [&](int64_t bytes) {
     const int64_t at = off;
@@ -179,10 +180,10 @@ void atopn_layout(int64_t b, int64_t q_h, int64_t L, int64_t d, int64_t buf_k, s
     return at;
   };
   o->scores_ld = ld;
-  o->nchunk = nchunk;
+  o->nparts = nparts;
   o->scores = take(nr * ld * 4);
-  o->part_max = take(nr * nchunk * 4);
-  o->part_sum = take(nr * nchunk * 4);
+  o->part_max = take(nr * nparts * 4);
+  o->part_sum = take(nr * nparts * 4);
   o->thresh = take(nr * 4);
   o->sel_idx = take(nr * buf_k * 4);
   o->sel_val = take(nr * buf_k * 4);
@@ -222,7 +223,7 @@ int atopn_run(bool calibrate, const saga_tensor* query, const saga_tensor* key, 
   if (calibrate ? !pstar_out : !pstar_in) return fail(SAGA_ERR_INVALID, "threshold table row is null");
   const int64_t buf_k = calibrate ? (top_n < s.L ? top_n : s.L) : (2 * top_n < s.L ? 2 * top_n : s.L);
   saga_atopn_layout lay;
-  atopn_layout(s.b, s.q_h, s.L, s.d, buf_k, &lay);
+  atopn_layout(s.b, s.q_h, s.k_h, s.L, s.d, buf_k, &lay);
   if (!workspace || workspace_bytes < static_cast<size_t>(lay.total_bytes))
     return fail(SAGA_ERR_WORKSPACE, "workspace of %zu bytes, need %lld", workspace_bytes, (long long)lay.total_bytes);
   if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(SAGA_ERR_WORKSPACE, "workspace must be 256-byte aligned");
@@ -244,7 +245,7 @@ int atopn_run(bool calibrate, const saga_tensor* query, const saga_tensor* key, 
   sp.ld = lay.scores_ld;
   sp.pmax = qp.pmax;
   sp.psum = qp.psum;
-  sp.nchunk = static_cast<int32_t>(lay.nchunk);
+  sp.nparts = static_cast<int32_t>(lay.nparts);
   sp.kv_len = kv_len;
   sp.q_h = static_cast<int32_t>(s.q_h);
   sp.nrows = static_cast<int32_t>(nr);
@@ -424,17 +425,23 @@ int saga_sparse_softmax_pv(const saga_tensor* weights, const saga_tensor* indice
   return ok();
 }
 
-size_t saga_atopn_workspace_bytes(int64_t b, int64_t q_h, int64_t L, int64_t d, int64_t buf_k) {
+int64_t saga_qk_nparts(int64_t b, int64_t k_h, int64_t L) {
+  if (b < 1 || k_h < 1 || L < 1) return 0;
+  return qk_plan(b, k_h, L);
+}
+
+size_t saga_atopn_workspace_bytes(int64_t b, int64_t q_h, int64_t k_h, int64_t L, int64_t d, int64_t buf_k) {
+  if (b < 1 || q_h < 1 || k_h < 1 || L < 1 || d < 1 || buf_k < 1) return 0;
   saga_atopn_layout lay;
-  atopn_layout(b, q_h, L, d, buf_k, &lay);
+  atopn_layout(b, q_h, k_h, L, d, buf_k, &lay);
   return static_cast<size_t>(lay.total_bytes);
 }
 
-int saga_atopn_workspace_layout(int64_t b, int64_t q_h, int64_t L, int64_t d, int64_t buf_k,
+int saga_atopn_workspace_layout(int64_t b, int64_t q_h, int64_t k_h, int64_t L, int64_t d, int64_t buf_k,
                                 saga_atopn_layout* layout) {
   if (!layout) return fail(SAGA_ERR_INVALID, "layout: null");
-  if (b < 1 || q_h < 1 || L < 1 || d < 1 || buf_k < 1) return fail(SAGA_ERR_INVALID, "sizes must be >= 1");
-  atopn_layout(b, q_h, L, d, buf_k, layout);
+  if (b < 1 || q_h < 1 || k_h < 1 || L < 1 || d < 1 || buf_k < 1) return fail(SAGA_ERR_INVALID, "sizes must be >= 1");
+  atopn_layout(b, q_h, k_h, L, d, buf_k, layout);
   return ok();
 }
 
@@ -512,33 +519,36 @@ int saga_dense_decode(const saga_tensor* query, const saga_tensor* key, const sa
   return ok();
 }
 
-int saga_rope_kv_append(const saga_tensor* qkv, int64_t n_q, int64_t n_k, int64_t n_v, float theta,
-                        const int32_t* pos, const int32_t* batch, saga_tensor* q_out, saga_tensor* k_cache,
-                        saga_tensor* v_cache, saga_stream_t stream) {
+}  // extern "C"
+
+namespace {
+
+// Validates the RoPE / cache-append operands shared by saga_rope_kv_append and
+// saga_gemv_rope_kv: N token rows of dtype dt, q_out [N, n_q, d], caches
+// [B, n_k, Lmax, d] / [B, n_v, Lmax, d].
+int make_rope(int64_t N, int32_t dt, int64_t n_q, int64_t n_k, int64_t n_v, float theta, const int32_t* pos,
+              const int32_t* batch, saga_tensor* q_out, saga_tensor* k_cache, saga_tensor* v_cache, RopeParams& p) {
   int rc;
-  if ((rc = check_tensor(qkv, "qkv", 2)) || (rc = check_tensor(q_out, "q_out", 3)) ||
-      (rc = check_tensor(k_cache, "k_cache", 4)) || (rc = check_tensor(v_cache, "v_cache", 4)))
+  if ((rc = check_tensor(q_out, "q_out", 3)) || (rc = check_tensor(k_cache, "k_cache", 4)) ||
+      (rc = check_tensor(v_cache, "v_cache", 4)))
     return rc;
   if (!pos) return fail(SAGA_ERR_INVALID, "pos: null");
   if (n_q < 1 || n_k < 1 || n_v < 1) return fail(SAGA_ERR_INVALID, "head counts must be >= 1");
-  const int64_t N = qkv->shape[0];
   const int64_t d = q_out->shape[2];
   if (d % 2 || d < 2) return fail(SAGA_ERR_INVALID, "head_dim must be even");
-  if (!is_float(qkv->dtype) || q_out->dtype != qkv->dtype || k_cache->dtype != qkv->dtype || v_cache->dtype != qkv->dtype)
-    return fail(SAGA_ERR_INVALID, "qkv, q_out and the caches must share one float dtype");
-  if (qkv->shape[1] < (n_q + n_k + n_v) * d) return fail(SAGA_ERR_INVALID, "qkv: row shorter than (n_q + n_k + n_v) * d");
+  if (q_out->dtype != dt || k_cache->dtype != dt || v_cache->dtype != dt)
+    return fail(SAGA_ERR_INVALID, "q_out and the caches must have the dtype of the projection");
   if (q_out->shape[0] != N || q_out->shape[1] != n_q) return fail(SAGA_ERR_INVALID, "q_out: shape must be [N, n_q, d]");
   if (k_cache->shape[1] != n_k || k_cache->shape[3] != d || v_cache->shape[1] != n_v || v_cache->shape[3] != d ||
       v_cache->shape[0] != k_cache->shape[0] || v_cache->shape[2] != k_cache->shape[2])
     return fail(SAGA_ERR_INVALID, "caches: shapes must be [B, n_k, Lmax, d] and [B, n_v, Lmax, d]");
-  if (qkv->stride[1] != 1 || q_out->stride[2] != 1 || k_cache->stride[3] != 1 || v_cache->stride[3] != 1)
+  if (q_out->stride[2] != 1 || k_cache->stride[3] != 1 || v_cache->stride[3] != 1)
     return fail(SAGA_ERR_INVALID, "innermost strides must be 1");
   if (!batch && N > k_cache->shape[0]) return fail(SAGA_ERR_INVALID, "without batch indices N must be <= B");
-  if (N >= (1LL << 31) || k_cache->shape[2] >= kMaxLen) return fail(SAGA_ERR_UNSUPPORTED, "sizes too large");
-  RopeParams p{};
-  p.qkv = qkv->data;
-  p.qkv_ld = qkv->stride[0];
-  p.dt = qkv->dtype;
+  if (N >= (1LL << 31) || k_cache->shape[2] >= kMaxLen || n_q + n_k + n_v > 65535)
+    return fail(SAGA_ERR_UNSUPPORTED, "sizes too large");
+  p = RopeParams{};
+  p.dt = dt;
   p.N = static_cast<int32_t>(N);
   p.n_q = static_cast<int32_t>(n_q);
   p.n_k = static_cast<int32_t>(n_k);
@@ -560,7 +570,75 @@ int saga_rope_kv_append(const saga_tensor* qkv, int64_t n_q, int64_t n_k, int64_
   p.v_sl = v_cache->stride[2];
   p.B = static_cast<int32_t>(k_cache->shape[0]);
   p.Lmax = static_cast<int32_t>(k_cache->shape[2]);
+  return SAGA_OK;
+}
+
+// Validates x [M, K] and w [N, K] (bf16, 16-byte aligned rows) and an optional
+// bias [N] of a skinny GEMM and fills the shared fields of p.
+int make_gemv(const saga_tensor* x, const saga_tensor* w, const saga_tensor* bias, float rms_eps, GemvParams& p) {
+  int rc;
+  if ((rc = check_tensor(x, "x", 2)) || (rc = check_tensor(w, "w", 2))) return rc;
+  if (x->dtype != SAGA_DTYPE_BF16 || w->dtype != SAGA_DTYPE_BF16) return fail(SAGA_ERR_UNSUPPORTED, "gemv: bf16 only");
+  const int64_t M = x->shape[0], K = x->shape[1], N = w->shape[0];
+  if (w->shape[1] != K) return fail(SAGA_ERR_INVALID, "gemv: w must be [N, K] with K = x.shape[1]");
+  if (M > 16) return fail(SAGA_ERR_UNSUPPORTED, "gemv: at most 16 rows");
+  if (N % 16 || K % 32 || K >= (1LL << 30) || N >= (1LL << 30))
+    return fail(SAGA_ERR_UNSUPPORTED, "gemv: N %% 16 == 0 and K %% 32 == 0 required");
+  if ((rc = check_vec_rows(x, "x")) || (rc = check_vec_rows(w, "w"))) return rc;
+  if (bias) {
+    if ((rc = check_tensor(bias, "bias", 1))) return rc;
+    if (bias->dtype != SAGA_DTYPE_BF16 || bias->shape[0] != N || bias->stride[0] != 1)
+      return fail(SAGA_ERR_INVALID, "bias must be bf16 [N]");
+  }
+  p = GemvParams{};
+  p.x = x->data;
+  p.x_ld = x->stride[0];
+  p.w = w->data;
+  p.w_ld = w->stride[0];
+  p.bias = bias ? bias->data : nullptr;
+  p.M = static_cast<int32_t>(M);
+  p.N = static_cast<int32_t>(N);
+  p.K = static_cast<int32_t>(K);
+  p.rms = rms_eps >= 0.f;
+  p.eps = rms_eps;
+  return SAGA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int saga_rope_kv_append(const saga_tensor* qkv, int64_t n_q, int64_t n_k, int64_t n_v, float theta,
+                        const int32_t* pos, const int32_t* batch, saga_tensor* q_out, saga_tensor* k_cache,
+                        saga_tensor* v_cache, saga_stream_t stream) {
+  int rc;
+  if ((rc = check_tensor(qkv, "qkv", 2))) return rc;
+  if (!is_float(qkv->dtype)) return fail(SAGA_ERR_INVALID, "qkv: float dtype required");
+  const int64_t N = qkv->shape[0];
+  RopeParams p;
+  if ((rc = make_rope(N, qkv->dtype, n_q, n_k, n_v, theta, pos, batch, q_out, k_cache, v_cache, p))) return rc;
+  if (qkv->shape[1] < (n_q + n_k + n_v) * p.d) return fail(SAGA_ERR_INVALID, "qkv: row shorter than (n_q + n_k + n_v) * d");
+  if (qkv->stride[1] != 1) return fail(SAGA_ERR_INVALID, "innermost strides must be 1");
+  if (N == 0) return ok();
+  p.qkv = qkv->data;
+  p.qkv_ld = qkv->stride[0];
   if ((rc = hip_status(launch_rope_kv_append(p, static_cast<hipStream_t>(stream)), "rope_kv_append launch"))) return rc;
+  return ok();
+}
+
+int saga_gemv_rope_kv(const saga_tensor* x, const saga_tensor* w, const saga_tensor* bias, float rms_eps,
+                      int64_t n_q, int64_t n_k, int64_t n_v, float theta, const int32_t* pos, const int32_t* batch,
+                      saga_tensor* q_out, saga_tensor* k_cache, saga_tensor* v_cache, saga_stream_t stream) {
+  int rc;
+  GemvParams p;
+  if ((rc = make_gemv(x, w, bias, rms_eps, p))) return rc;
+  if ((rc = make_rope(p.M, SAGA_DTYPE_BF16, n_q, n_k, n_v, theta, pos, batch, q_out, k_cache, v_cache, p.rope)))
+    return rc;
+  if (p.rope.d % 16) return fail(SAGA_ERR_UNSUPPORTED, "gemv_rope_kv: head_dim %% 16 == 0 required");
+  if (p.N != (n_q + n_k + n_v) * p.rope.d) return fail(SAGA_ERR_INVALID, "gemv_rope_kv: w must have (n_q + n_k + n_v) * d rows");
+  if (p.M == 0) return ok();
+  p.epilogue = kGemvRopeKV;
+  if ((rc = hip_status(launch_gemv(p, static_cast<hipStream_t>(stream)), "gemv_rope_kv launch"))) return rc;
   return ok();
 }
 
@@ -576,6 +654,7 @@ static int row_op(bool silu, const saga_tensor* x, const saga_tensor* w, float e
     if ((rc = check_tensor(w, "weight", 1))) return rc;
     if (w->dtype != x->dtype || w->shape[0] != H || w->stride[0] != 1) return fail(SAGA_ERR_INVALID, "weight must be [H], same dtype");
   }
+  if (x->shape[0] == 0 || H == 0) return ok();
   RowParams p{};
   p.x = x->data;
   p.x_ld = x->stride[0];
@@ -602,39 +681,19 @@ int saga_silu_mul(const saga_tensor* gate_up, saga_tensor* y, saga_stream_t stre
 int saga_gemv(const saga_tensor* x, const saga_tensor* w, const saga_tensor* bias, float rms_eps, int32_t epilogue,
               saga_tensor* y, saga_stream_t stream) {
   int rc;
-  if ((rc = check_tensor(x, "x", 2)) || (rc = check_tensor(w, "w", 2)) || (rc = check_tensor(y, "y", 2))) return rc;
-  if (x->dtype != SAGA_DTYPE_BF16 || w->dtype != SAGA_DTYPE_BF16 || y->dtype != SAGA_DTYPE_BF16)
-    return fail(SAGA_ERR_UNSUPPORTED, "gemv: bf16 only");
-  const int64_t M = x->shape[0], K = x->shape[1], N = w->shape[0];
-  if (w->shape[1] != K) return fail(SAGA_ERR_INVALID, "gemv: w must be [N, K] with K = x.shape[1]");
-  if (M > 16) return fail(SAGA_ERR_UNSUPPORTED, "gemv: at most 16 rows");
-  if (N % 16 || K % 32 || K >= (1LL << 30) || N >= (1LL << 30))
-    return fail(SAGA_ERR_UNSUPPORTED, "gemv: N %% 16 == 0 and K %% 32 == 0 required");
+  GemvParams p;
+  if ((rc = make_gemv(x, w, bias, rms_eps, p))) return rc;
+  if ((rc = check_tensor(y, "y", 2))) return rc;
+  if (y->dtype != SAGA_DTYPE_BF16) return fail(SAGA_ERR_UNSUPPORTED, "gemv: bf16 only");
   if (epilogue != SAGA_GEMV_STORE && epilogue != SAGA_GEMV_ADD && epilogue != SAGA_GEMV_SILU_PAIRS)
     return fail(SAGA_ERR_INVALID, "gemv: unknown epilogue %d", epilogue);
-  const int64_t ny = epilogue == SAGA_GEMV_SILU_PAIRS ? N / 2 : N;
-  if (y->shape[0] != M || y->shape[1] != ny) return fail(SAGA_ERR_INVALID, "gemv: y must be [M, %lld]", (long long)ny);
-  if ((rc = check_vec_rows(x, "x")) || (rc = check_vec_rows(w, "w"))) return rc;
+  const int64_t ny = epilogue == SAGA_GEMV_SILU_PAIRS ? p.N / 2 : p.N;
+  if (y->shape[0] != p.M || y->shape[1] != ny) return fail(SAGA_ERR_INVALID, "gemv: y must be [M, %lld]", (long long)ny);
   if (y->stride[1] != 1) return fail(SAGA_ERR_INVALID, "y: innermost stride must be 1");
-  if (bias) {
-    if ((rc = check_tensor(bias, "bias", 1))) return rc;
-    if (bias->dtype != SAGA_DTYPE_BF16 || bias->shape[0] != N || bias->stride[0] != 1)
-      return fail(SAGA_ERR_INVALID, "bias must be bf16 [N]");
-    if (epilogue == SAGA_GEMV_SILU_PAIRS) return fail(SAGA_ERR_UNSUPPORTED, "bias with SILU_PAIRS");
-  }
-  GemvParams p{};
-  p.x = x->data;
-  p.x_ld = x->stride[0];
-  p.w = w->data;
-  p.w_ld = w->stride[0];
-  p.bias = bias ? bias->data : nullptr;
+  if (bias && epilogue == SAGA_GEMV_SILU_PAIRS) return fail(SAGA_ERR_UNSUPPORTED, "bias with SILU_PAIRS");
+  if (p.M == 0 || p.N == 0) return ok();
   p.y = y->data;
   p.y_ld = y->stride[0];
-  p.M = static_cast<int32_t>(M);
-  p.N = static_cast<int32_t>(N);
-  p.K = static_cast<int32_t>(K);
-  p.rms = rms_eps >= 0.f;
-  p.eps = rms_eps;
   p.epilogue = epilogue;
   if ((rc = hip_status(launch_gemv(p, static_cast<hipStream_t>(stream)), "gemv launch"))) return rc;
   return ok();
@@ -646,6 +705,7 @@ int saga_argmax(const saga_tensor* x, int64_t* out, saga_stream_t stream) {
   if (x->dtype != SAGA_DTYPE_BF16 || x->stride[1] != 1) return fail(SAGA_ERR_UNSUPPORTED, "argmax: bf16 rows with unit stride");
   if (!out) return fail(SAGA_ERR_INVALID, "out: null");
   if (x->shape[0] >= (1LL << 31) || x->shape[1] >= (1LL << 31)) return fail(SAGA_ERR_UNSUPPORTED, "argmax: too large");
+  if (x->shape[0] == 0) return ok();
   if ((rc = hip_status(launch_argmax(x->data, x->stride[0], static_cast<int>(x->shape[0]), static_cast<int>(x->shape[1]),
                                      out, static_cast<hipStream_t>(stream)),
                        "argmax launch")))

@@ -196,4 +196,12 @@ __device__ __forceinline__ float key_to_f32(uint32_t k) {
   return __uint_as_float(u);
 }
 
+// RoPE angle of rotary pair i at position pos (Qwen2RotaryEmbedding,
+// transformers models/qwen2/modeling_qwen2.py:86-120): inv_freq_i =
+// 1 / theta^(2i/d) and angle = pos * inv_freq_i, both in fp32.
+__device__ __forceinline__ void rope_cos_sin(int pos, int i, int d, float theta, float& c, float& s) {
+  const float inv_freq = 1.0f / powf(theta, static_cast<float>(2 * i) / static_cast<float>(d));
+  sincosf(static_cast<float>(pos) * inv_freq, &s, &c);
+}
+
 }  // namespace saga

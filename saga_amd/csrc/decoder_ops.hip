@@ -12,27 +12,20 @@
 
 namespace saga {
 
-__global__ void __launch_bounds__(256) rope_kv_append_kernel(RopeParams p) {
-  const int n = blockIdx.x;
+// One 64-lane block per (token n, head hh); heads are ordered q, k, v as in
+// the fused projection row.  q and k heads rotate pairs (i, i + d/2), v heads
+// are copied.
+__global__ void __launch_bounds__(64) rope_kv_append_kernel(RopeParams p) {
+  const int n = blockIdx.x, hh = blockIdx.y;
   const int half = p.d / 2;
   const int pos = p.pos[n];
   const int b = p.batch ? p.batch[n] : n;
   const bool ok = pos >= 0 && pos < p.Lmax && b >= 0 && b < p.B;
-  const int64_t row = static_cast<int64_t>(n) * p.qkv_ld;
-  // q heads, then k heads (rotated), then v heads (copied)
-  const int nrot = (p.n_q + p.n_k) * half;
-  for (int e = threadIdx.x; e < nrot + p.n_v * p.d; e += blockDim.x) {
-    if (e < nrot) {
-      const int hh = e / half, i = e - hh * half;
-      // inv_freq_i = theta^(-2i/d) and angle = pos * inv_freq_i in fp32, as
-      // HF computes them; cos/sin of that fp32 angle evaluated in fp64 (the
-      // angle reaches ~3e4 rad, where an fp32 sincos reduces slowly)
-      const float inv_freq = 1.0f / powf(p.theta, static_cast<float>(2 * i) / static_cast<float>(p.d));
-      const float ang = static_cast<float>(pos) * inv_freq;
-      double sd, cd;
-      sincos(static_cast<double>(ang), &sd, &cd);
-      const float sn = static_cast<float>(sd), cs = static_cast<float>(cd);
-      const int64_t base = row + static_cast<int64_t>(hh) * p.d;
+  const int64_t base = static_cast<int64_t>(n) * p.qkv_ld + static_cast<int64_t>(hh) * p.d;
+  if (hh < p.n_q + p.n_k) {
+    for (int i = threadIdx.x; i < half; i += 64) {
+      float cs, sn;
+      rope_cos_sin(pos, i, p.d, p.theta, cs, sn);
       const float x1 = load_as_f32(p.qkv, p.dt, base + i);
       const float x2 = load_as_f32(p.qkv, p.dt, base + i + half);
       const float y1 = x1 * cs - x2 * sn;
@@ -47,18 +40,16 @@ __global__ void __launch_bounds__(256) rope_kv_append_kernel(RopeParams p) {
         store_from_f32(p.k_cache, p.dt, ko + i, y1);
         store_from_f32(p.k_cache, p.dt, ko + i + half, y2);
       }
-    } else if (ok) {
-      const int f = e - nrot;
-      const int vh = f / p.d, i = f - vh * p.d;
-      const float v = load_as_f32(p.qkv, p.dt, row + static_cast<int64_t>(p.n_q + p.n_k + vh) * p.d + i);
-      const int64_t vo = b * p.v_sb + static_cast<int64_t>(vh) * p.v_sh + static_cast<int64_t>(pos) * p.v_sl;
-      store_from_f32(p.v_cache, p.dt, vo + i, v);
     }
+  } else if (ok) {
+    const int vh = hh - p.n_q - p.n_k;
+    const int64_t vo = b * p.v_sb + static_cast<int64_t>(vh) * p.v_sh + static_cast<int64_t>(pos) * p.v_sl;
+    for (int i = threadIdx.x; i < p.d; i += 64) store_from_f32(p.v_cache, p.dt, vo + i, load_as_f32(p.qkv, p.dt, base + i));
   }
 }
 
 hipError_t launch_rope_kv_append(const RopeParams& p, hipStream_t st) {
-  hipLaunchKernelGGL(rope_kv_append_kernel, dim3(p.N), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(rope_kv_append_kernel, dim3(p.N, p.n_q + p.n_k + p.n_v), dim3(64), 0, st, p);
   return hipGetLastError();
 }
 

@@ -73,6 +73,52 @@ __global__ void __launch_bounds__(WAVES * 64) gemv_kernel(GemvParams p) {
   if (!mvalid) return;
   const float scale = p.rms ? rsqrtf(sq / static_cast<float>(p.K) + p.eps) : 1.f;
   const int n = n0 + 4 * s;
+  if constexpr (EPI == kGemvRopeKV) {
+    // token row m = col; the 4 rows n..n+3 lie in one head (d % 16 == 0).  q/k
+    // heads are stored in rotary-pair order [0, d/2, 1, d/2 + 1, ...], so rows
+    // (n, n+1) and (n+2, n+3) are the pairs (i, i + d/2) of i = j/2, j/2 + 1.
+    const RopeParams& rp = p.rope;
+    const int pos = rp.pos[col];
+    const int b = rp.batch ? rp.batch[col] : col;
+    const bool ok = pos >= 0 && pos < rp.Lmax && b >= 0 && b < rp.B;
+    const int hh = n / rp.d, j = n - hh * rp.d;
+    float o[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float t = v[r] * scale;
+      if (p.bias) t += bf16_bits_to_f32(static_cast<const uint16_t*>(p.bias)[n + r]);
+      o[r] = bf16_bits_to_f32(f32_to_bf16_bits(t));  // the projection output, rounded as stored
+    }
+    if (hh < rp.n_q + rp.n_k) {
+      const int half = rp.d / 2;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int i = j / 2 + q;
+        float cs, sn;
+        rope_cos_sin(pos, i, rp.d, rp.theta, cs, sn);
+        const float x1 = o[2 * q], x2 = o[2 * q + 1];
+        const float y1 = x1 * cs - x2 * sn;
+        const float y2 = x2 * cs + x1 * sn;
+        if (hh < rp.n_q) {
+          uint16_t* qo = static_cast<uint16_t*>(rp.q_out) + static_cast<int64_t>(col) * rp.q_sn +
+                         static_cast<int64_t>(hh) * rp.q_sh;
+          qo[i] = f32_to_bf16_bits(ok ? y1 : __builtin_nanf(""));
+          qo[i + half] = f32_to_bf16_bits(ok ? y2 : __builtin_nanf(""));
+        } else if (ok) {
+          uint16_t* ko = static_cast<uint16_t*>(rp.k_cache) + b * rp.k_sb +
+                         static_cast<int64_t>(hh - rp.n_q) * rp.k_sh + static_cast<int64_t>(pos) * rp.k_sl;
+          ko[i] = f32_to_bf16_bits(y1);
+          ko[i + half] = f32_to_bf16_bits(y2);
+        }
+      }
+    } else if (ok) {
+      uint16_t* vo = static_cast<uint16_t*>(rp.v_cache) + b * rp.v_sb +
+                     static_cast<int64_t>(hh - rp.n_q - rp.n_k) * rp.v_sh + static_cast<int64_t>(pos) * rp.v_sl;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) vo[j + r] = f32_to_bf16_bits(o[r]);
+    }
+    return;
+  }
   uint16_t* y = static_cast<uint16_t*>(p.y) + static_cast<int64_t>(col) * p.y_ld;
   if constexpr (EPI == SAGA_GEMV_SILU_PAIRS) {
     // rows (n, n+1) and (n+2, n+3) are (gate, up) pairs -> outputs n/2, n/2 + 1
@@ -107,6 +153,7 @@ hipError_t launch_gemv(const GemvParams& p, hipStream_t st) {
   switch (p.epilogue) {
     case SAGA_GEMV_ADD: return launch_gemv_epi<SAGA_GEMV_ADD>(p, st);
     case SAGA_GEMV_SILU_PAIRS: return launch_gemv_epi<SAGA_GEMV_SILU_PAIRS>(p, st);
+    case kGemvRopeKV: return launch_gemv_epi<kGemvRopeKV>(p, st);
     default: return launch_gemv_epi<SAGA_GEMV_STORE>(p, st);
   }
 }

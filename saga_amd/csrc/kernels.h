@@ -19,15 +19,22 @@ struct QKParams {
   int32_t mask_dt;
   int64_t m_sb, m_sh, m_sl;
   const int32_t* kv_len;  // nullable
-  int32_t b, q_h, k_h, g, L, nchunk;
+  int32_t b, q_h, k_h, g, L;
+  int32_t ntiles, nparts;  // ceil(L / 16) tiles per row, split into nparts ranges
   float scale;
   float* scores;  // nullable: skip storing scores
   int64_t s_sb, s_sh;
   int32_t vec_store;  // rows 16-byte aligned: store 4 scores at once
-  float* pmax;        // nullable: [row * nchunk + chunk]
+  float* pmax;        // nullable: [row * nparts + part]
   float* psum;
 };
 hipError_t launch_qk_scores(int dtype, int d, const QKParams& p, hipStream_t st);
+// K1 tile ranges: at most kQKMaxTiles 16-position tiles per wave; launches are
+// planned in whole rounds of kQKResidentWaves (256 CUs x 4 SIMDs x 3 waves, the
+// occupancy the kernel is built for: at least 3).
+constexpr int kQKMaxTiles = 6;
+constexpr int64_t kQKResidentWaves = 256 * 4 * 3;
+int64_t qk_plan(int64_t b, int64_t k_h, int64_t L);  // nparts per (batch, key head)
 
 // Standalone logit threshold from a scores tensor.
 struct ThreshParams {
@@ -68,7 +75,7 @@ struct FusedSelParams {
   int64_t ld;
   const float* pmax;
   const float* psum;
-  int32_t nchunk;
+  int32_t nparts;
   const int32_t* kv_len;
   int32_t q_h, nrows, L;
   const float* pstar;  // fast step: softmax-space thresholds in
@@ -168,7 +175,11 @@ struct GemvParams {
   int32_t rms;  // scale by 1/sqrt(mean(x^2) + eps)
   float eps;
   int32_t epilogue;
+  // kGemvRopeKV: y is unused; rows of w are the fused q/k/v projection with
+  // the q and k heads in rotary-pair order, written through `rope` (qkv unused)
+  RopeParams rope;
 };
+constexpr int kGemvRopeKV = 3;
 hipError_t launch_gemv(const GemvParams& p, hipStream_t st);
 hipError_t launch_argmax(const void* x, int64_t ld, int rows, int N, int64_t* out, hipStream_t st);
 

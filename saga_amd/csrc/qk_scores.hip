@@ -1,39 +1,57 @@
 // K1: decode QK scores for every query head against its shared key head.
 //
 // Replaces the bmm + scale + mask of _compute_attn_weights
-// (attention/attention.py:113-128).  One wave owns one (batch, key head,
-// 128-position chunk) item: it streams the chunk's K rows once with 16-byte
-// loads straight into MFMA A fragments (16 positions x 32 dims per
-// v_mfma_f32_16x16x32_bf16), multiplies by the g = q_h / k_h query heads of
-// the group held as the B fragment (g <= 16, padded with zeros), and writes
+// (attention/attention.py:113-128).  The key rows of one (batch, key head)
+// are split into `nparts` contiguous ranges of 16-position MFMA tiles, with
+// the tile counts balanced (they differ by at most one, and are at most
+// kQKMaxTiles).  One wave owns one range: it issues every 16-byte load of the
+// range's K rows at once, straight into MFMA A fragments (16 positions x 32
+// dims per v_mfma_f32_16x16x32_bf16), multiplies by the g = q_h / k_h query
+// heads of the group held as the B fragment (g <= 16, padded with zeros), and
+// writes
 //   * fp32 scores  x = acc * scale (+ mask), -inf at positions >= kv_len,
-//   * the chunk's per-head max m_c and sum_c exp(x - m_c),
+//   * the range's per-head max m_c and sum_c exp(x - m_c),
 // so the logit threshold t = m + log(p* * sum_c s_c exp(m_c - m)) needs no
-// second pass over the scores.  The K stream is the only large read.
+// second pass over the scores.  The K stream is the only large read.  The
+// host planner (qk_plan) picks nparts so that all waves of a launch fit the
+// GPU in whole rounds: no round runs a handful of leftover waves.
+#include <algorithm>
+
 #include "common.cuh"
 #include "kernels.h"
 
 namespace saga {
 
-constexpr int kQKTiles = SAGA_CHUNK / 16;  // 16-position MFMA tiles per chunk item
+template <int DT, int D>
+struct QKShape {
+  static constexpr int E16 = Elt<DT>::kPer16B;  // elements per 16-byte fragment
+  static constexpr int NLOAD = D / (4 * E16);   // fragments per K row per lane
+  // tiles per load burst: at most 24 fragments (96 VGPRs) in flight per lane
+  static constexpr int BURST = (24 / NLOAD) < kQKMaxTiles ? (24 / NLOAD) : kQKMaxTiles;
+};
 
-template <int DT, int D, int TPL>
-__global__ void __launch_bounds__(256) qk_scores_kernel(QKParams p) {
+template <int DT, int D>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8)))
+qk_scores_kernel(QKParams p) {
   using E = Elt<DT>;
-  constexpr int E16 = E::kPer16B;           // elements per 16-byte fragment
-  constexpr int NLOAD = D / (4 * E16);      // fragments per K row per lane
+  using S = QKShape<DT, D>;
+  constexpr int E16 = S::E16, NLOAD = S::NLOAD, BURST = S::BURST;
   const int lane = threadIdx.x & 63;
   const int col = lane & 15;                // MFMA row (position) / column (head)
   const int s = lane >> 4;                  // k-slot group
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  const int64_t nitems = static_cast<int64_t>(p.b) * p.k_h * p.nchunk;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + wave;
+  const int64_t nitems = static_cast<int64_t>(p.b) * p.k_h * p.nparts;
   if (item >= nitems) return;
-  const int chunk = static_cast<int>(item % p.nchunk);
-  const int unit = static_cast<int>(item / p.nchunk);
+  const int part = static_cast<int>(item % p.nparts);
+  const int unit = static_cast<int>(item / p.nparts);
   const int bi = unit / p.k_h;
   const int kh = unit - bi * p.k_h;
   const bool hvalid = col < p.g;
   const int h = kh * p.g + (hvalid ? col : 0);
+  // this wave's tiles [t0, t0 + nt), nt <= kQKMaxTiles
+  const int t0 = static_cast<int>(static_cast<int64_t>(part) * p.ntiles / p.nparts);
+  const int nt = static_cast<int>(static_cast<int64_t>(part + 1) * p.ntiles / p.nparts) - t0;
 
   // B fragment: query head (kh*g + col), dims [j*4*E16 + s*E16, +E16).
   u32x4 qf[NLOAD];
@@ -44,24 +62,25 @@ __global__ void __launch_bounds__(256) qk_scores_kernel(QKParams p) {
   }
 
   const char* kbase = p.k + (bi * p.k_sb + static_cast<int64_t>(kh) * p.k_sh) * E::kBytes;
-  const int p0 = chunk * SAGA_CHUNK;
-  float x[kQKTiles][4];
+  float x[kQKMaxTiles][4];
 #pragma unroll
-  for (int tb = 0; tb < kQKTiles; tb += TPL) {
-    u32x4 kf[TPL][NLOAD];
+  for (int tb = 0; tb < kQKMaxTiles; tb += BURST) {
+    if (tb >= nt) break;
+    u32x4 kf[BURST][NLOAD];
 #pragma unroll
-    for (int t = 0; t < TPL; ++t) {
-      // A fragment: key row (p0 + 16*(tb+t) + col); rows past L are clamped
-      // (their scores are discarded below).
-      const int pos = min(p0 + 16 * (tb + t) + col, p.L - 1);
+    for (int t = 0; t < BURST; ++t) {
+      // A fragment: key row (16*(t0+tb+t) + col), rows past L clamped (their
+      // scores are discarded below); tiles past the range are not loaded
+      const int pos = min(16 * (t0 + tb + t) + col, p.L - 1);
       const char* krow = kbase + static_cast<int64_t>(pos) * p.k_sl * E::kBytes;
 #pragma unroll
-      for (int j = 0; j < NLOAD; ++j) kf[t][j] = ld16(krow + (j * 4 * E16 + s * E16) * E::kBytes);
+      for (int j = 0; j < NLOAD; ++j)
+        kf[t][j] = tb + t < nt ? ld16(krow + (j * 4 * E16 + s * E16) * E::kBytes) : u32x4{0u, 0u, 0u, 0u};
     }
     // keep the whole burst in flight: no MFMA may be hoisted between the loads
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int t = 0; t < TPL; ++t) {
+    for (int t = 0; t < BURST; ++t) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < NLOAD; ++j) acc = mfma_16b<DT>(kf[t][j], qf[j], acc);
@@ -72,20 +91,20 @@ __global__ void __launch_bounds__(256) qk_scores_kernel(QKParams p) {
 
   int Leff = p.L;
   if (p.kv_len) Leff = min(Leff, max(p.kv_len[bi], 0));
-  // Lane holds head `col`, positions p0 + 16*t + 4*s + r.
+  // Lane holds head `col`, positions 16*(t0+t) + 4*s + r.
   float m = kNegInf;
 #pragma unroll
-  for (int t = 0; t < kQKTiles; ++t) {
+  for (int t = 0; t < kQKMaxTiles; ++t) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int pos = p0 + 16 * t + 4 * s + r;
+      const int pos = 16 * (t0 + t) + 4 * s + r;
       float v = x[t][r] * p.scale;
       if (p.mask) {
         const int mp = min(pos, p.L - 1);
         v = v + load_as_f32(p.mask, p.mask_dt, bi * p.m_sb + static_cast<int64_t>(h) * p.m_sh +
                                                    static_cast<int64_t>(mp) * p.m_sl);
       }
-      if (pos >= Leff) v = kNegInf;
+      if (pos >= Leff || t >= nt) v = kNegInf;
       x[t][r] = v;
       m = fmaxf(m, v);
     }
@@ -94,8 +113,9 @@ __global__ void __launch_bounds__(256) qk_scores_kernel(QKParams p) {
   if (p.scores && hvalid) {
     float* srow = p.scores + bi * p.s_sb + static_cast<int64_t>(h) * p.s_sh;
 #pragma unroll
-    for (int t = 0; t < kQKTiles; ++t) {
-      const int pos0 = p0 + 16 * t + 4 * s;
+    for (int t = 0; t < kQKMaxTiles; ++t) {
+      if (t >= nt) break;
+      const int pos0 = 16 * (t0 + t) + 4 * s;
       if (p.vec_store && pos0 + 3 < p.L) {
         *reinterpret_cast<f32x4*>(srow + pos0) = f32x4{x[t][0], x[t][1], x[t][2], x[t][3]};
       } else {
@@ -110,7 +130,7 @@ __global__ void __launch_bounds__(256) qk_scores_kernel(QKParams p) {
     float sum = 0.f;
     if (m != kNegInf) {
 #pragma unroll
-      for (int t = 0; t < kQKTiles; ++t)
+      for (int t = 0; t < kQKMaxTiles; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r) sum += __expf(x[t][r] - m);
     }
@@ -118,20 +138,28 @@ __global__ void __launch_bounds__(256) qk_scores_kernel(QKParams p) {
     lse_merge(m, sum, __shfl_xor(m, 16), __shfl_xor(sum, 16));
     lse_merge(m, sum, __shfl_xor(m, 32), __shfl_xor(sum, 32));
     if (s == 0 && hvalid) {
-      const int64_t o = static_cast<int64_t>(bi * p.q_h + h) * p.nchunk + chunk;
+      const int64_t o = static_cast<int64_t>(bi * p.q_h + h) * p.nparts + part;
       p.pmax[o] = m;
       p.psum[o] = sum;
     }
   }
 }
 
+int64_t qk_plan(int64_t b, int64_t k_h, int64_t L) {
+  const int64_t tiles = (L + 15) / 16;
+  if (tiles == 0) return 1;
+  const int64_t units = b * k_h;
+  const int64_t minp = (tiles + kQKMaxTiles - 1) / kQKMaxTiles;
+  const int64_t rounds = (units * minp + kQKResidentWaves - 1) / kQKResidentWaves;
+  const int64_t fill = rounds * kQKResidentWaves / units;  // whole rounds of resident waves
+  return std::max(minp, std::min(tiles, fill));
+}
+
 template <int DT, int D>
 static hipError_t launch_qk_typed(const QKParams& p, hipStream_t st) {
-  constexpr int NLOAD = D / (4 * Elt<DT>::kPer16B);
-  constexpr int TPL = (NLOAD * kQKTiles <= 32) ? kQKTiles : (32 / NLOAD);
-  const int64_t nitems = static_cast<int64_t>(p.b) * p.k_h * p.nchunk;
+  const int64_t nitems = static_cast<int64_t>(p.b) * p.k_h * p.nparts;
   const int64_t blocks = (nitems + 3) / 4;
-  hipLaunchKernelGGL((qk_scores_kernel<DT, D, TPL>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((qk_scores_kernel<DT, D>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, p);
   return hipGetLastError();
 }
 

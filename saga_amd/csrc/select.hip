@@ -97,13 +97,13 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_fast_kernel(FusedSelParams 
   int Leff = p.L;
   if (p.kv_len) Leff = min(Leff, max(p.kv_len[bi], 0));
   const float* x = p.scores + static_cast<int64_t>(r) * p.ld;
-  const float* prow_m = p.pmax + static_cast<int64_t>(r) * p.nchunk;
-  const float* prow_s = p.psum + static_cast<int64_t>(r) * p.nchunk;
+  const float* prow_m = p.pmax + static_cast<int64_t>(r) * p.nparts;
+  const float* prow_s = p.psum + static_cast<int64_t>(r) * p.nparts;
 
   // 1. tail, partials and the first tile in flight together
   const int tail = min(256, Leff);
   const float tv = tid < tail ? x[Leff - tail + tid] : kNegInf;
-  const int nch = (Leff + SAGA_CHUNK - 1) / SAGA_CHUNK;
+  const int nch = p.nparts;  // parts past kv_len hold (-inf, 0)
   const float pm0 = tid < nch ? prow_m[tid] : kNegInf;
   const float ps0 = tid < nch ? prow_s[tid] : 0.f;
   float xa[kSelEPT];
@@ -201,10 +201,10 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_kernel(FusedSelPa
   int Leff = p.L;
   if (p.kv_len) Leff = min(Leff, max(p.kv_len[bi], 0));
   const float* x = p.scores + static_cast<int64_t>(r) * p.ld;
-  const float* prow_m = p.pmax + static_cast<int64_t>(r) * p.nchunk;
-  const float* prow_s = p.psum + static_cast<int64_t>(r) * p.nchunk;
+  const float* prow_m = p.pmax + static_cast<int64_t>(r) * p.nparts;
+  const float* prow_s = p.psum + static_cast<int64_t>(r) * p.nparts;
 
-  const int nch = (Leff + SAGA_CHUNK - 1) / SAGA_CHUNK;
+  const int nch = p.nparts;  // parts past kv_len hold (-inf, 0)
   float mloc = kNegInf;
   for (int c = tid; c < nch; c += kBlkThreads) mloc = fmaxf(mloc, prow_m[c]);
   const float M = block_max<kBlkWaves>(mloc, sh.red);

@@ -76,7 +76,7 @@ class SagaDecoder:
     """
 
     def __init__(self, shape: DecoderShape, batch: int, max_len: int, mode: str = "atopn", top_n: int = 512,
-                 exempt_layers=(), device="cuda", dtype=torch.bfloat16, seed: int = 0):
+                 exempt_layers=(), device="cuda", dtype=torch.bfloat16, seed: int = 0, fuse_rope: bool = True):
         if mode not in ("atopn", "dense"):
             raise ValueError(f"mode must be 'atopn' or 'dense', got {mode!r}")
         self.shape, self.batch, self.max_len, self.mode, self.top_n = shape, batch, max_len, mode, top_n
@@ -122,6 +122,8 @@ class SagaDecoder:
         # decode projections: the skinny-GEMM kernel for up to 16 token rows
         self.use_gemv = (batch <= 16 and dtype == torch.bfloat16 and s.hidden % 32 == 0 and s.intermediate % 32 == 0
                          and (s.n_q * d) % 32 == 0 and s.qkv_width % 16 == 0 and s.vocab % 16 == 0)
+        # q/k/v projection, RoPE and cache append in one launch (pair-ordered rows)
+        self.fuse_rope = fuse_rope and self.use_gemv and d % 16 == 0
         self.prepare_kernel_weights()
         self.graph_cal: Optional[torch.cuda.CUDAGraph] = None
         self.graph_fast: Optional[torch.cuda.CUDAGraph] = None
@@ -137,6 +139,11 @@ class SagaDecoder:
         s = self.shape
         with torch.no_grad():
             self.kw_qkv = [(self.w_qkv[l].float() * self.ln1[l].float()).to(self.dtype) for l in range(s.layers)]
+            self.kb_qkv = self.b_qkv
+            if self.fuse_rope:
+                order = ops.rope_pair_order(s.n_q, s.n_k, s.n_v, s.head_dim, device=self.device)
+                self.kw_qkv = [w.index_select(0, order).contiguous() for w in self.kw_qkv]
+                self.kb_qkv = [b.index_select(0, order).contiguous() for b in self.b_qkv]
             self.kw_gu = []
             for l in range(s.layers):
                 w = (self.w_gu[l].float() * self.ln2[l].float()).to(self.dtype)
@@ -209,13 +216,17 @@ class SagaDecoder:
         torch.index_select(self.embed, 0, self.tokens, out=x)
         q4 = self._q.view(B, s.n_q, 1, d)
         for l in range(s.layers):
-            if self.use_gemv:
-                ops.gemv(x, self.kw_qkv[l], bias=self.b_qkv[l], rms_eps=s.eps, out=self._qkv)
+            if self.fuse_rope:
+                ops.gemv_rope_kv(x, self.kw_qkv[l], self.kb_qkv[l], s.n_q, s.n_k, s.n_v, s.rope_theta, self.pos,
+                                 self.k_cache[l], self.v_cache[l], rms_eps=s.eps, q_out=self._q)
             else:
-                ops.rmsnorm(x, self.ln1[l], s.eps, out=self._h)
-                torch.addmm(self.b_qkv[l], self._h, self.w_qkv[l].t(), out=self._qkv)
-            ops.rope_kv_append(self._qkv, s.n_q, s.n_k, s.n_v, s.rope_theta, self.pos, self.k_cache[l],
-                               self.v_cache[l], q_out=self._q)
+                if self.use_gemv:
+                    ops.gemv(x, self.kw_qkv[l], bias=self.b_qkv[l], rms_eps=s.eps, out=self._qkv)
+                else:
+                    ops.rmsnorm(x, self.ln1[l], s.eps, out=self._h)
+                    torch.addmm(self.b_qkv[l], self._h, self.w_qkv[l].t(), out=self._qkv)
+                ops.rope_kv_append(self._qkv, s.n_q, s.n_k, s.n_v, s.rope_theta, self.pos, self.k_cache[l],
+                                   self.v_cache[l], q_out=self._q)
             K, V = self.k_cache[l], self.v_cache[l]
             if self.mode == "dense" or l in self.exempt:
                 ops.dense_decode(q4, K, V, kv_len=self.kv_len, out=self._attn)

@@ -92,8 +92,8 @@ def qk_scores(query, key, attention_mask=None, scaling=None, kv_len=None, with_p
     scores = torch.empty(b, q_h, 1, L, dtype=torch.float32, device=dev)
     pm = ps = None
     if with_partials:
-        nch = (L + _lib.CHUNK - 1) // _lib.CHUNK
-        pm = torch.empty(b * q_h, nch, dtype=torch.float32, device=dev)
+        nparts = lib.saga_qk_nparts(b, key.shape[1], L)
+        pm = torch.empty(b * q_h, nparts, dtype=torch.float32, device=dev)
         ps = torch.empty_like(pm)
     _lib.check(lib.saga_qk_scores(_lib.tensor(query), _lib.tensor(key), _lib.tensor(mask), _lib.ptr(_kv_len(kv_len)),
                                   _scale(query, scaling), _lib.tensor(scores), _lib.ptr(pm), _lib.ptr(ps),
@@ -180,7 +180,7 @@ def atopn_decode(query, key, value, softmax_threshold, top_n, attention_mask=Non
         out = torch.empty(b, q_h, 1, d, dtype=out_dtype or query.dtype, device=dev)
     lib = _lib.load()
     buf_k = min(2 * top_n, L)
-    ws = workspace(dev, "atopn", lib.saga_atopn_workspace_bytes(b, q_h, L, d, buf_k))
+    ws = workspace(dev, "atopn", lib.saga_atopn_workspace_bytes(b, q_h, key.shape[1], L, d, buf_k))
     _lib.check(lib.saga_atopn_decode(_lib.tensor(query), _lib.tensor(key), _lib.tensor(value), _lib.tensor(mask),
                                      _lib.ptr(_kv_len(kv_len)), _scale(query, scaling), int(top_n),
                                      _lib.ptr(softmax_threshold), _lib.tensor(out), _lib.ptr(ws), ws.numel(),
@@ -203,7 +203,7 @@ def atopn_calibrate(query, key, value, top_n, threshold_out, attention_mask=None
         out = torch.empty(b, q_h, 1, d, dtype=out_dtype or query.dtype, device=dev)
     lib = _lib.load()
     buf_k = min(top_n, L)
-    ws = workspace(dev, "atopn", lib.saga_atopn_workspace_bytes(b, q_h, L, d, buf_k))
+    ws = workspace(dev, "atopn", lib.saga_atopn_workspace_bytes(b, q_h, key.shape[1], L, d, buf_k))
     _lib.check(lib.saga_atopn_calibrate(_lib.tensor(query), _lib.tensor(key), _lib.tensor(value), _lib.tensor(mask),
                                         _lib.ptr(_kv_len(kv_len)), _scale(query, scaling), int(top_n),
                                         _lib.ptr(threshold_out), _lib.tensor(out), _lib.ptr(ws), ws.numel(),
@@ -226,10 +226,10 @@ def dense_decode(query, key, value, attention_mask=None, scaling=None, kv_len=No
     return out
 
 
-def atopn_workspace_views(b: int, q_h: int, L: int, d: int, buf_k: int, device) -> dict:
+def atopn_workspace_views(b: int, q_h: int, k_h: int, L: int, d: int, buf_k: int, device) -> dict:
     """Views into the cached fused-decode workspace (thresholds, counts,
     selected indices) for inspection after a call; valid until the next call."""
-    lay = _lib.atopn_layout(b, q_h, L, d, buf_k)
+    lay = _lib.atopn_layout(b, q_h, k_h, L, d, buf_k)
     ws = _WORKSPACES[(torch.device(device), "atopn")]
     nr = b * q_h
 
@@ -303,6 +303,38 @@ def gemv(x, w, bias=None, rms_eps=None, epilogue="store", out=None):
     _lib.check(_lib.load().saga_gemv(_lib.tensor(x), _lib.tensor(w), _lib.tensor(bias), eps, code, _lib.tensor(out),
                                      _lib.stream_of(x)), "gemv")
     return out
+
+
+def rope_pair_order(n_q, n_k, n_v, d, device=None):
+    """Row permutation of a fused [q | k | v] projection (heads of d rows)
+    that puts every q and k head in rotary-pair order [0, d/2, 1, d/2+1, ...]
+    and leaves the v heads in place: w_pairs = w[order], bias_pairs = bias[order]
+    (the layout gemv_rope_kv expects)."""
+    half = d // 2
+    pair = torch.stack([torch.arange(half), torch.arange(half) + half], dim=1).reshape(-1)
+    parts = [pair + h * d for h in range(n_q + n_k)]
+    parts += [torch.arange(d) + (n_q + n_k + h) * d for h in range(n_v)]
+    return torch.cat(parts).to(device=device)
+
+
+def gemv_rope_kv(x, w_pairs, bias_pairs, n_q, n_k, n_v, theta, pos, k_cache, v_cache, rms_eps=None, batch=None,
+                 q_out=None):
+    """Fused q/k/v projection + RoPE + KV-cache append for M <= 16 new tokens:
+    the same results as gemv(x, w, bias) followed by rope_kv_append, with w
+    and bias given in rope_pair_order.  Returns q_out [M, n_q, d]."""
+    dev = _need_gpu(x, w_pairs, bias_pairs, pos, k_cache, v_cache, batch, q_out)
+    d = k_cache.shape[-1]
+    if q_out is None:
+        q_out = torch.empty(x.shape[0], n_q, d, dtype=x.dtype, device=dev)
+    for t, name in ((pos, "pos"), (batch, "batch")):
+        if t is not None and (t.dtype != torch.int32 or not t.is_contiguous()):
+            raise ValueError(f"saga_amd: {name} must be a contiguous int32 tensor")
+    eps = -1.0 if rms_eps is None else float(rms_eps)
+    _lib.check(_lib.load().saga_gemv_rope_kv(_lib.tensor(x), _lib.tensor(w_pairs), _lib.tensor(bias_pairs), eps,
+                                             n_q, n_k, n_v, float(theta), _lib.ptr(pos), _lib.ptr(batch),
+                                             _lib.tensor(q_out), _lib.tensor(k_cache), _lib.tensor(v_cache),
+                                             _lib.stream_of(x)), "gemv_rope_kv")
+    return q_out
 
 
 def argmax_rows(x, out=None):

@@ -124,17 +124,34 @@ def test_threshold_select_argument_errors():
 
 def test_workspace_sizes_and_layout():
     lib = _lib.load()
-    lay = _lib.atopn_layout(8, 12, 33024, 128, 1024)
+    lay = _lib.atopn_layout(8, 12, 1, 33024, 128, 1024)
     offs = [lay.scores, lay.part_max, lay.part_sum, lay.thresh, lay.sel_idx, lay.sel_val, lay.sel_cnt,
             lay.sel_total]
     assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
     assert lay.scores_ld % 16 == 0 and lay.scores_ld >= 33024
-    assert lay.nchunk == (33024 + 127) // 128
-    assert lay.total_bytes == lib.saga_atopn_workspace_bytes(8, 12, 33024, 128, 1024)
+    assert lay.nparts == lib.saga_qk_nparts(8, 1, 33024)
+    assert lay.total_bytes == lib.saga_atopn_workspace_bytes(8, 12, 1, 33024, 128, 1024)
     assert lay.part_max - lay.scores >= 96 * 33024 * 4
     assert lib.saga_dense_workspace_bytes(8, 12, 33024, 128) > 0
     bad = _lib.AtopnLayout()
-    assert lib.saga_atopn_workspace_layout(0, 12, 10, 128, 4, ctypes.byref(bad)) == -1
+    assert lib.saga_atopn_workspace_layout(0, 12, 1, 10, 128, 4, ctypes.byref(bad)) == -1
+
+
+@pytest.mark.parametrize("b", [1, 4, 8, 32])
+@pytest.mark.parametrize("k_h", [1, 2])
+def test_qk_part_plan(b, k_h):
+    """K1 splits each (batch, key head) row into nparts balanced ranges of at
+    most 6 sixteen-position tiles, in whole rounds of 3072 resident waves."""
+    lib = _lib.load()
+    for L in (1, 15, 16, 17, 100, 4096, 32769, 33024, 131072, 131328):
+        n = lib.saga_qk_nparts(b, k_h, L)
+        T = (L + 15) // 16
+        assert 1 <= n <= T
+        assert -(-T // n) <= 6
+        rounds = -(-(b * k_h * -(-T // 6)) // 3072)
+        assert b * k_h * n <= rounds * 3072
+    assert lib.saga_qk_nparts(8, 1, 33024) == 384
+    assert lib.saga_qk_nparts(0, 1, 10) == 0
 
 
 def test_ops_refuse_cpu_tensors():

@@ -27,8 +27,8 @@ from saga_amd import ops
 pytestmark = pytest.mark.gpu
 
 
-def _views(b, q_h, L, d, buf_k):
-    return {k: v.cpu().numpy() for k, v in ops.atopn_workspace_views(b, q_h, L, d, buf_k, "cuda:0").items()}
+def _views(b, q_h, k_h, L, d, buf_k):
+    return {k: v.cpu().numpy() for k, v in ops.atopn_workspace_views(b, q_h, k_h, L, d, buf_k, "cuda:0").items()}
 
 
 def _run_fast(qd, kd, vd, table_row, N, mask=None, scale=None, out_dtype=torch.float32, kv_len=None):
@@ -75,7 +75,7 @@ def test_against_reference_golden(name, golden):
     cal = host(ops.atopn_calibrate(q1, k, v, N, table, mask, sc, out_dtype=torch.float32))
     np.testing.assert_allclose(host(table), g["cal_threshold" + sfx], rtol=1e-4)
     kk = min(N, L)
-    views = _views(b, q_h, L, d, kk)
+    views = _views(b, q_h, k.shape[1], L, d, kk)
     for r in range(nr):
         assert views["sel_cnt"][r] == kk
         got = np.sort(views["sel_idx"][r, :kk])
@@ -87,7 +87,7 @@ def test_against_reference_golden(name, golden):
     for tag, tab in (("fast", torch.from_numpy(g["cal_threshold" + sfx]).cuda()),
                      ("zero", torch.zeros(nr, device="cuda"))):
         out = host(_run_fast(q2, k, v, tab.contiguous(), N, mask, sc))
-        views = _views(b, q_h, L, d, buf_k)
+        views = _views(b, q_h, k.shape[1], L, d, buf_k)
         _check_selection_rule(views, nr, L, buf_k)
         t_ref = g[f"{tag}_t" + sfx]
         fin = np.isfinite(t_ref)
@@ -142,7 +142,7 @@ def test_bf16_benchmark_shapes_vs_fp32_path(name):
 
     out32 = host(_run_fast(q2d, kd, vd, table, N, out_dtype=torch.float32))
     buf_k = min(2 * N, L)
-    views = _views(b, q_h, L, d, buf_k)
+    views = _views(b, q_h, k_h, L, d, buf_k)
     _check_selection_rule(views, nr, L, buf_k)
     out16 = host(_run_fast(q2d, kd, vd, table, N, out_dtype=torch.bfloat16))
 
@@ -187,7 +187,7 @@ def test_kv_len_equals_truncated_reference():
     cal = host(ops.atopn_calibrate(qd, kd, vd, N, table, kv_len=kvl, out_dtype=torch.float32))
     fast = host(_run_fast(dev(q2, "bf16"), kd, vd, table, N, kv_len=kvl))
     dense = host(ops.dense_decode(qd, kd, vd, kv_len=kvl, out_dtype=torch.float32))
-    views = _views(b, q_h, L, d, min(2 * N, L))
+    views = _views(b, q_h, k_h, L, d, min(2 * N, L))
     _check_selection_rule(views, b * q_h, L, min(2 * N, L), kv_len=lens, q_h=q_h)
     thr = host(table)
     for i, n in enumerate(lens):
@@ -207,9 +207,9 @@ def test_fast_step_is_deterministic():
     (_, _, _), (qd, kd, vd) = qkv(rng, 4, 12, 1, 2, 128, 20000, "bf16")
     table = torch.full((48,), 1e-4, device="cuda")
     a = ops.atopn_decode(qd, kd, vd, table, 256)
-    idx_a = ops.atopn_workspace_views(4, 12, 20000, 128, 512, "cuda:0")["sel_idx"].clone()
+    idx_a = ops.atopn_workspace_views(4, 12, 1, 20000, 128, 512, "cuda:0")["sel_idx"].clone()
     bb = ops.atopn_decode(qd, kd, vd, table, 256)
-    idx_b = ops.atopn_workspace_views(4, 12, 20000, 128, 512, "cuda:0")["sel_idx"].clone()
+    idx_b = ops.atopn_workspace_views(4, 12, 1, 20000, 128, 512, "cuda:0")["sel_idx"].clone()
     assert torch.equal(a, bb) and torch.equal(idx_a, idx_b)
 
 

@@ -128,3 +128,20 @@ def test_one_decode_step_vs_float64_reference():
         top2 = np.sort(logits[r])[-2:]
         if top2[1] - top2[0] > 0.05:
             assert int(m.tokens[r]) == int(np.argmax(logits[r]))
+
+
+def test_fused_rope_projection_equals_unfused_step():
+    """The decode step with the q/k/v projection, RoPE and cache append fused
+    in one launch writes the caches and logits of the unfused step."""
+    from saga_amd.decoder import DecoderShape, SagaDecoder
+    shape = DecoderShape(layers=2, hidden=256, n_q=4, n_k=1, n_v=2, head_dim=64, intermediate=512, vocab=1024,
+                         rope_theta=1e4, eps=1e-6, qkv_bias=True)
+    ms = [SagaDecoder(shape, batch=3, max_len=300, mode="dense", fuse_rope=f) for f in (True, False)]
+    assert ms[0].fuse_rope and not ms[1].fuse_rope
+    for m in ms:
+        m.fill_synthetic(200)
+        m.tokens.copy_(torch.tensor([5, 77, 1000], device="cuda"))
+        m.step(calibrate=True)
+    torch.cuda.synchronize()
+    for a, b in ((ms[0].k_cache, ms[1].k_cache), (ms[0].v_cache, ms[1].v_cache), (ms[0]._logits, ms[1]._logits)):
+        assert torch.allclose(a.float(), b.float(), rtol=2 ** -7, atol=1e-3)

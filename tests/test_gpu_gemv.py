@@ -74,3 +74,43 @@ def test_argmax_rows_first_max(N):
         x[3, 5] = x[3, N - 2] = 100.0  # tie: first index wins
     got = ops.argmax_rows(dev(x, "bf16")).cpu().numpy()
     np.testing.assert_array_equal(got, np.argmax(x, axis=1))
+
+
+@pytest.mark.parametrize("M,K,n_q,n_k,n_v,d", [(8, 1536, 12, 1, 2, 128), (1, 960, 15, 1, 5, 64), (16, 512, 4, 2, 2, 64)])
+def test_gemv_rope_kv_matches_unfused(M, K, n_q, n_k, n_v, d):
+    """Projection + RoPE + cache append in one launch == gemv then
+    rope_kv_append (the projection is rounded to bf16 before the rotation in
+    both), and both match the oracle's RoPE of the float64 projection."""
+    rng = np.random.default_rng(M * 7 + K)
+    N = (n_q + n_k + n_v) * d
+    x, w, b = _data(rng, M, K, N)
+    B, Lmax = 16, 2048
+    pos = torch.from_numpy(rng.integers(0, Lmax, M).astype(np.int32)).cuda()
+    batch = torch.from_numpy(rng.permutation(B)[:M].astype(np.int32)).cuda()
+    xd, wd, bd = dev(x, "bf16"), dev(w, "bf16"), dev(b, "bf16")
+    caches = [torch.zeros(B, h, Lmax, d, device="cuda", dtype=torch.bfloat16) for h in (n_k, n_v, n_k, n_v)]
+    qkv = ops.gemv(xd, wd, bias=bd, rms_eps=1e-6)
+    q_ref = ops.rope_kv_append(qkv, n_q, n_k, n_v, 1e6, pos, caches[0], caches[1], batch=batch)
+    order = ops.rope_pair_order(n_q, n_k, n_v, d, device="cuda")
+    q = ops.gemv_rope_kv(xd, wd[order].contiguous(), bd[order].contiguous(), n_q, n_k, n_v, 1e6, pos,
+                         caches[2], caches[3], rms_eps=1e-6, batch=batch)
+    torch.cuda.synchronize()
+    for a, r in ((q, q_ref), (caches[2], caches[0]), (caches[3], caches[1])):
+        assert torch.allclose(a.float(), r.float(), rtol=2 ** -7, atol=1e-6)
+    # against the oracle: float64 projection, RoPE in float64
+    xs = x.astype(np.float64)
+    xs = xs / np.sqrt((xs ** 2).mean(-1, keepdims=True) + 1e-6)
+    proj = (xs @ w.astype(np.float64).T + b).reshape(M, n_q + n_k + n_v, d)
+    p = host(pos).astype(np.int64)
+    assert rel_l2(host(q), O.rope(proj[:, :n_q], p[:, None], 1e6)) < 4e-3
+    kh, vh, bt = host(caches[2]), host(caches[3]), host(batch).astype(np.int64)
+    k_ref = O.rope(proj[:, n_q:n_q + n_k], p[:, None], 1e6)
+    for m in range(M):
+        assert rel_l2(kh[bt[m], :, p[m]], k_ref[m]) < 4e-3
+        assert rel_l2(vh[bt[m], :, p[m]], proj[m, n_q + n_k:]) < 4e-3
+
+
+def test_rope_pair_order_is_a_permutation():
+    order = ops.rope_pair_order(3, 1, 2, 8)
+    assert sorted(order.tolist()) == list(range(6 * 8))
+    assert order[:8].tolist() == [0, 4, 1, 5, 2, 6, 3, 7] and order[32:].tolist() == list(range(32, 48))

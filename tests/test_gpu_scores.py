@@ -1,4 +1,4 @@
-"""QK scores, chunk partials and the logit threshold on the GPU vs the oracle.
+"""QK scores, per-part partials and the logit threshold on the GPU vs the oracle.
 
 saga_qk_scores replaces _compute_attn_weights (attention/attention.py:113-128),
 saga_logit_threshold replaces _transform_softmax_threshold (:136-149).
@@ -56,10 +56,13 @@ def test_scores_and_partials(dt, shape, mask_kind):
     assert np.max(np.abs(got[fin] - ref[fin])) <= tol
     # partials are exact functions of the kernel's own scores
     x = got.reshape(b * q_h, L)
-    nch = (L + 127) // 128
+    T, nparts = (L + 15) // 16, pm.shape[1]
     pm, ps = host(pm), host(ps)
-    for c in range(nch):
-        blk = x[:, c * 128:(c + 1) * 128].astype(np.float64)
+    for c in range(nparts):
+        # part c: tiles [c*T/nparts, (c+1)*T/nparts) of 16 positions
+        t0, t1 = c * T // nparts, (c + 1) * T // nparts
+        assert 1 <= t1 - t0 <= 6
+        blk = x[:, 16 * t0:min(16 * t1, L)].astype(np.float64)
         mx = blk.max(axis=1)
         np.testing.assert_array_equal(pm[:, c], mx.astype(np.float32))
         with np.errstate(invalid="ignore"):
