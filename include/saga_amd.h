@@ -76,12 +76,23 @@ typedef struct saga_atopn_layout {
   int64_t scores_ld; /* elements */
   int64_t part_max;  /* f32 [b*q_h, nparts] */
   int64_t part_sum;  /* f32 [b*q_h, nparts] */
+  int64_t part_tail; /* f32 [b*q_h, nparts] max over the last min(256, kv_len) positions */
   int64_t nparts;    /* saga_qk_nparts(b, k_h, L) */
   int64_t thresh;    /* f32 [b*q_h] logit threshold (fast step) */
-  int64_t sel_idx;   /* i32 [b*q_h, buf_k] ascending positions */
+  int64_t sel_idx;   /* i32 [b*q_h, buf_k] ascending positions (calibration; the fast step
+                        keeps its list in the slice lists, concatenated and cut at buf_k) */
   int64_t sel_val;   /* f32 [b*q_h, buf_k] their logits */
   int64_t sel_cnt;   /* i32 [b*q_h] kept (<= buf_k) */
   int64_t sel_total; /* i32 [b*q_h] passing before the cap */
+  /* fast step: rows cut into nslice slices of 1024 positions */
+  int64_t nslice;
+  int64_t slice_cap; /* min(1024, buf_k) */
+  int64_t slice_idx; /* i32 [b*q_h, nslice, slice_cap] passing positions per slice */
+  int64_t slice_val; /* f32 [b*q_h, nslice, slice_cap] their logits */
+  int64_t slice_cnt; /* i32 [b*q_h, nslice] passing per slice */
+  int64_t slice_pre; /* i32 [b*q_h, nslice + 1] prefix of slice_cnt */
+  int64_t slice_o;   /* f32 [b*q_h, nslice, d] partial sum_e exp(x_e - m) V[e] */
+  int64_t slice_ml;  /* f32 [b*q_h, nslice, 2] partial (m, sum_e exp(x_e - m)) */
   int64_t total_bytes;
 } saga_atopn_layout;
 

@@ -1,11 +1,11 @@
-// Block-level sparse softmax . V (1024 threads = 64 lane groups of 16 lanes).
+// Block-level sparse softmax . V (NT threads = NT / 16 lane groups of 16 lanes).
 //
 // The selected positions and their logits (or probabilities) sit in LDS.
 // Lane c of group G owns dims [c*DPL, c*DPL + DPL) of the head dim and walks
-// entries G, G+64, ...; eight V rows per group are in flight at a time (raw
-// 16-byte fragments), so one block keeps 512 rows (128 KiB of bf16 V) of
-// gathers outstanding.  Lists longer than one LDS batch are accumulated with
-// a running max and rescaled sums (online softmax).
+// entries G, G + NT/16, ...; eight V rows per group are in flight at a time
+// (raw 16-byte fragments), so a 1024-thread block keeps 512 rows (128 KiB of
+// bf16 V) of gathers outstanding.  Lists longer than one LDS batch are
+// accumulated with a running max and rescaled sums (online softmax).
 #pragma once
 
 #include "common.cuh"
@@ -17,8 +17,10 @@ constexpr int kBlkWaves = kBlkThreads / kWave;  // 16
 constexpr int kBlkGroups = kBlkThreads / 16;    // 64 lane groups
 constexpr int kPVUnroll = 8;
 
-template <int DT, int D>
+template <int DT, int D, int NT = kBlkThreads>
 struct BlockPV {
+  static constexpr int NW = NT / kWave;      // waves
+  static constexpr int NG = NT / 16;         // lane groups
   static constexpr int DPL = D / 16;                   // dims per lane
   static constexpr int BYTES = DPL * Elt<DT>::kBytes;  // bytes per lane per row (8, 16 or 32)
   static constexpr int NV = BYTES >= 16 ? BYTES / 16 : 1;
@@ -65,23 +67,23 @@ struct BlockPV {
     float scale_old = 1.f;
     if (!probs) {
       float cm = kNegInf;
-      for (int i = tid; i < n; i += kBlkThreads) cm = fmaxf(cm, sval[i]);
-      cm = block_max<kBlkWaves>(cm, red);
+      for (int i = tid; i < n; i += NT) cm = fmaxf(cm, sval[i]);
+      cm = block_max<NW>(cm, red);
       const float mn = fmaxf(m, cm);
       scale_old = (m == kNegInf) ? 0.f : __expf(m - mn);
       float ls = 0.f;
-      for (int i = tid; i < n; i += kBlkThreads) {
+      for (int i = tid; i < n; i += NT) {
         const float w = mn == kNegInf ? 0.f : __expf(sval[i] - mn);
         sval[i] = w;
         ls += w;
       }
-      ls = block_sum<kBlkWaves>(ls, red);  // also orders the weight writes
+      ls = block_sum<NW>(ls, red);  // also orders the weight writes
       l = l * scale_old + ls;
       m = mn;
     } else {
       float ls = 0.f;
-      for (int i = tid; i < n; i += kBlkThreads) ls += sval[i];
-      ls = block_sum<kBlkWaves>(ls, red);
+      for (int i = tid; i < n; i += NT) ls += sval[i];
+      ls = block_sum<NW>(ls, red);
       l += ls;
     }
 #pragma unroll
@@ -89,17 +91,17 @@ struct BlockPV {
 
     const int G = tid >> 4, c = tid & 15;
     const char* vb = vbase + static_cast<int64_t>(c) * BYTES;
-    for (int e0 = G; e0 < n; e0 += kBlkGroups * kPVUnroll) {
+    for (int e0 = G; e0 < n; e0 += NG * kPVUnroll) {
       u32x4 raw[kPVUnroll][NV];
 #pragma unroll
       for (int u = 0; u < kPVUnroll; ++u) {
-        const int e = e0 + u * kBlkGroups;
+        const int e = e0 + u * NG;
         if (e < n) load_raw(vb + static_cast<int64_t>(sidx[e]) * vrow, raw[u]);
       }
       __builtin_amdgcn_sched_barrier(0);  // all gathers in flight before the FMAs
 #pragma unroll
       for (int u = 0; u < kPVUnroll; ++u) {
-        const int e = e0 + u * kBlkGroups;
+        const int e = e0 + u * NG;
         if (e < n) {
           const float w = sval[e];
           float f[DPL];
@@ -111,9 +113,9 @@ struct BlockPV {
     }
   }
 
-  // Reduce the 64 lane groups and write out[off + i] = o_i / l (probs:
-  // / max(l, 1e-12)).  accs: LDS of kBlkWaves * D floats.
-  __device__ void finish(float* accs, void* out, int out_dt, int64_t off, bool probs) {
+  // Sum the lane groups: on return, thread i < D holds sum_e w_e * V[e, i]
+  // (unnormalised).  accs: LDS of NW * D floats.
+  __device__ float reduce(float* accs) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = tid & 15;
 #pragma unroll
     for (int i = 0; i < DPL; ++i) {
@@ -125,12 +127,20 @@ struct BlockPV {
       for (int i = 0; i < DPL; ++i) accs[w * D + c * DPL + i] = acc[i];
     }
     __syncthreads();
+    float o = 0.f;
     if (tid < D) {
-      float o = 0.f;
 #pragma unroll
-      for (int q = 0; q < kBlkWaves; ++q) o += accs[q * D + tid];
+      for (int q = 0; q < NW; ++q) o += accs[q * D + tid];
+    }
+    return o;
+  }
+
+  // Reduce and write out[off + i] = o_i / l (probs: / max(l, 1e-12)).
+  __device__ void finish(float* accs, void* out, int out_dt, int64_t off, bool probs) {
+    const float o = reduce(accs);
+    if (threadIdx.x < D) {
       const float den = probs ? fmaxf(l, 1e-12f) : l;
-      store_from_f32(out, out_dt, off + tid, o / den);
+      store_from_f32(out, out_dt, off + threadIdx.x, o / den);
     }
   }
 };

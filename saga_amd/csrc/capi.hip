@@ -1,6 +1,7 @@
 // C ABI of libsaga_amd.so: argument validation, workspace layout and the
 // launch sequences of the fused decode entry points.  Declarations and the
 // reference function each entry point replaces: include/saga_amd.h.
+#include <algorithm>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
@@ -169,10 +170,9 @@ QKParams make_qk(const saga_tensor* q, const saga_tensor* k, const saga_tensor* 
 }
 
 void atopn_layout(int64_t b, int64_t q_h, int64_t k_h, int64_t L, int64_t d, int64_t buf_k, saga_atopn_layout* o) {
-  (void)d;
   const int64_t nr = b * q_h;
   const int64_t ld = (L + 15) / 16 * 16;
-  const int64_t nparts = qk_plan(b, k_h, L);
+  const int64_t nparts = qk_plan(b, k_h, L) / 4;  // K1 partials: one per block of 4 waves
   int64_t off = 0;
   auto take = [&](int64_t bytes) {
     const int64_t at = off;
@@ -184,11 +184,20 @@ void atopn_layout(int64_t b, int64_t q_h, int64_t k_h, int64_t L, int64_t d, int
   o->scores = take(nr * ld * 4);
   o->part_max = take(nr * nparts * 4);
   o->part_sum = take(nr * nparts * 4);
+  o->part_tail = take(nr * nparts * 4);
   o->thresh = take(nr * 4);
   o->sel_idx = take(nr * buf_k * 4);
   o->sel_val = take(nr * buf_k * 4);
   o->sel_cnt = take(nr * 4);
   o->sel_total = take(nr * 4);
+  o->nslice = (L + kSliceLen - 1) / kSliceLen;
+  o->slice_cap = std::min<int64_t>(kSliceLen, buf_k);
+  o->slice_idx = take(nr * o->nslice * o->slice_cap * 4);
+  o->slice_val = take(nr * o->nslice * o->slice_cap * 4);
+  o->slice_cnt = take(nr * o->nslice * 4);
+  o->slice_pre = take(nr * (o->nslice + 1) * 4);
+  o->slice_o = take(nr * o->nslice * d * 4);
+  o->slice_ml = take(nr * o->nslice * 2 * 4);
   o->total_bytes = off;
 }
 
@@ -238,6 +247,7 @@ int atopn_run(bool calibrate, const saga_tensor* query, const saga_tensor* key, 
   qp.vec_store = 1;
   qp.pmax = reinterpret_cast<float*>(ws + lay.part_max);
   qp.psum = reinterpret_cast<float*>(ws + lay.part_sum);
+  qp.ptail = reinterpret_cast<float*>(ws + lay.part_tail);
   if ((rc = hip_status(launch_qk_scores(s.dt, static_cast<int>(s.d), qp, st), "qk_scores launch"))) return rc;
 
   FusedSelParams sp{};
@@ -245,6 +255,7 @@ int atopn_run(bool calibrate, const saga_tensor* query, const saga_tensor* key, 
   sp.ld = lay.scores_ld;
   sp.pmax = qp.pmax;
   sp.psum = qp.psum;
+  sp.ptail = qp.ptail;
   sp.nparts = static_cast<int32_t>(lay.nparts);
   sp.kv_len = kv_len;
   sp.q_h = static_cast<int32_t>(s.q_h);
@@ -258,6 +269,15 @@ int atopn_run(bool calibrate, const saga_tensor* query, const saga_tensor* key, 
   sp.sel_val = reinterpret_cast<float*>(ws + lay.sel_val);
   sp.sel_cnt = reinterpret_cast<int32_t*>(ws + lay.sel_cnt);
   sp.sel_total = reinterpret_cast<int32_t*>(ws + lay.sel_total);
+  sp.nslice = static_cast<int32_t>(lay.nslice);
+  sp.slice_cap = static_cast<int32_t>(lay.slice_cap);
+  sp.sl_idx = reinterpret_cast<int32_t*>(ws + lay.slice_idx);
+  sp.sl_val = reinterpret_cast<float*>(ws + lay.slice_val);
+  sp.sl_cnt = reinterpret_cast<int32_t*>(ws + lay.slice_cnt);
+  sp.sl_pre = reinterpret_cast<int32_t*>(ws + lay.slice_pre);
+  sp.sl_o = reinterpret_cast<float*>(ws + lay.slice_o);
+  sp.sl_ml = reinterpret_cast<float*>(ws + lay.slice_ml);
+  if (nr * lay.nslice >= (1LL << 31)) return fail(SAGA_ERR_UNSUPPORTED, "too many score rows x slices");
   // calibration: softmax over the top-k logits == renormalised top-k probabilities
   const PVParams pp = make_pv(value, out, s);
   if ((rc = hip_status(launch_atopn_select_pv(calibrate, sp, pp, st), "atopn select/pv launch"))) return rc;
@@ -427,7 +447,7 @@ int saga_sparse_softmax_pv(const saga_tensor* weights, const saga_tensor* indice
 
 int64_t saga_qk_nparts(int64_t b, int64_t k_h, int64_t L) {
   if (b < 1 || k_h < 1 || L < 1) return 0;
-  return qk_plan(b, k_h, L);
+  return qk_plan(b, k_h, L) / 4;
 }
 
 size_t saga_atopn_workspace_bytes(int64_t b, int64_t q_h, int64_t k_h, int64_t L, int64_t d, int64_t buf_k) {

@@ -125,25 +125,60 @@ __device__ __forceinline__ u32x4 ld16(const void* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
 
+// Cross-lane steps on the DPP path (no LDS round trip).  GFX9 DPP controls:
+// quad_perm [1,0,3,2] / [2,3,0,1], row_half_mirror, row_mirror, row_shr:n,
+// row_bcast:15 / :31.
+constexpr int kDppQuadXor1 = 0xB1;
+constexpr int kDppQuadXor2 = 0x4E;
+constexpr int kDppRowMirror = 0x140;
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowShr = 0x110;
+constexpr int kDppRowBcast15 = 0x142;
+constexpr int kDppRowBcast31 = 0x143;
+
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ int dpp_i(int old, int src) {
+  return __builtin_amdgcn_update_dpp(old, src, CTRL, ROW_MASK, 0xf, false);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(dpp_i<CTRL>(__float_as_int(v), __float_as_int(v)));
+}
+
+__device__ __forceinline__ float lane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// Max / sum over the 64 lanes, returned in every lane: the four 16-lane rows
+// reduce by quad and mirror permutes, then the row results are read out.
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
+  v = fmaxf(v, dpp_f<kDppQuadXor1>(v));
+  v = fmaxf(v, dpp_f<kDppQuadXor2>(v));
+  v = fmaxf(v, dpp_f<kDppRowHalfMirror>(v));
+  v = fmaxf(v, dpp_f<kDppRowMirror>(v));
+  return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+  v += dpp_f<kDppQuadXor1>(v);
+  v += dpp_f<kDppQuadXor2>(v);
+  v += dpp_f<kDppRowHalfMirror>(v);
+  v += dpp_f<kDppRowMirror>(v);
+  return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
 }
 
-// Inclusive prefix sum over the 64 lanes.
+// Inclusive prefix sum over the 64 lanes: row_shr 1, 2, 4, 8 scan each
+// 16-lane row (lanes without a source add 0), then row_bcast:15 adds row 0's
+// total to row 1 and row 2's to row 3, and row_bcast:31 adds rows 0-1 to 2-3.
 __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    int n = __shfl_up(v, o);
-    if (lane >= o) v += n;
-  }
+  (void)lane;
+  v += dpp_i<kDppRowShr | 1>(0, v);
+  v += dpp_i<kDppRowShr | 2>(0, v);
+  v += dpp_i<kDppRowShr | 4>(0, v);
+  v += dpp_i<kDppRowShr | 8>(0, v);
+  v += dpp_i<kDppRowBcast15, 0xa>(0, v);
+  v += dpp_i<kDppRowBcast31, 0xc>(0, v);
   return v;
 }
 

@@ -25,8 +25,10 @@ struct QKParams {
   float* scores;  // nullable: skip storing scores
   int64_t s_sb, s_sh;
   int32_t vec_store;  // rows 16-byte aligned: store 4 scores at once
-  float* pmax;        // nullable: [row * nparts + part]
+  float* pmax;        // nullable: [row * (nparts / 4) + part / 4], one per block of 4 parts
   float* psum;
+  float* ptail;       // nullable: max over the part's positions in the tail window
+                      // [Leff - min(256, Leff), Leff), -inf if none
 };
 hipError_t launch_qk_scores(int dtype, int d, const QKParams& p, hipStream_t st);
 // K1 tile ranges: at most kQKMaxTiles 16-position tiles per wave; launches are
@@ -34,7 +36,7 @@ hipError_t launch_qk_scores(int dtype, int d, const QKParams& p, hipStream_t st)
 // occupancy the kernel is built for: at least 3).
 constexpr int kQKMaxTiles = 6;
 constexpr int64_t kQKResidentWaves = 256 * 4 * 3;
-int64_t qk_plan(int64_t b, int64_t k_h, int64_t L);  // nparts per (batch, key head)
+int64_t qk_plan(int64_t b, int64_t k_h, int64_t L);  // waves (parts) per (batch, key head), % 4 == 0
 
 // Standalone logit threshold from a scores tensor.
 struct ThreshParams {
@@ -75,7 +77,8 @@ struct FusedSelParams {
   int64_t ld;
   const float* pmax;
   const float* psum;
-  int32_t nparts;
+  const float* ptail;  // [row * nparts + part] tail-window max of the part
+  int32_t nparts;      // K1 block partials per row
   const int32_t* kv_len;
   int32_t q_h, nrows, L;
   const float* pstar;  // fast step: softmax-space thresholds in
@@ -86,8 +89,19 @@ struct FusedSelParams {
   float* sel_val;
   int32_t* sel_cnt;
   int32_t* sel_total;
+  // fast step, split over slices of kSliceLen positions per row
+  int32_t nslice, slice_cap;  // slice_cap = min(kSliceLen, cap)
+  int32_t* sl_idx;            // [row][slice][slice_cap]
+  float* sl_val;
+  int32_t* sl_cnt;  // [row][slice] passing count in the slice
+  float* sl_o;      // [row][slice][d] unnormalised sum_e w_e V[e]
+  float* sl_ml;     // [row][slice][2] (max logit, sum of weights)
+  int32_t* sl_pre;  // [row][nslice + 1] exclusive prefix of sl_cnt (overflow merge scratch)
 };
+// calibrate: one block per row; fast step: slice kernel + merge kernel
 hipError_t launch_atopn_select_pv(bool calibrate, const FusedSelParams& p, const PVParams& v, hipStream_t st);
+constexpr int kSliceLen = 1024;  // score positions per slice wave of the fast step
+hipError_t launch_atopn_fast(const FusedSelParams& p, const PVParams& v, hipStream_t st);
 
 // API selection (threshold_topk_fast): typed rows, typed values out.
 struct ApiSelParams {

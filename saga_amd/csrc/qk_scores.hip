@@ -10,7 +10,9 @@
 // heads of the group held as the B fragment (g <= 16, padded with zeros), and
 // writes
 //   * fp32 scores  x = acc * scale (+ mask), -inf at positions >= kv_len,
-//   * the range's per-head max m_c and sum_c exp(x - m_c),
+//   * per block of 4 waves (4 consecutive ranges) and head: the max m_c, the
+//     sum_c exp(x - m_c) and the max over the tail window (the last
+//     min(256, kv_len) positions),
 // so the logit threshold t = m + log(p* * sum_c s_c exp(m_c - m)) needs no
 // second pass over the scores.  The K stream is the only large read.  The
 // host planner (qk_plan) picks nparts so that all waves of a launch fit the
@@ -39,10 +41,10 @@ qk_scores_kernel(QKParams p) {
   const int lane = threadIdx.x & 63;
   const int col = lane & 15;                // MFMA row (position) / column (head)
   const int s = lane >> 4;                  // k-slot group
+  __shared__ float red[3][4][16];  // per wave and head: (max, sum, tail max) of the part
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  // nparts % 4 == 0: the block's 4 waves are parts 4j..4j+3 of one (batch, key head)
   const int64_t item = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + wave;
-  const int64_t nitems = static_cast<int64_t>(p.b) * p.k_h * p.nparts;
-  if (item >= nitems) return;
   const int part = static_cast<int>(item % p.nparts);
   const int unit = static_cast<int>(item / p.nparts);
   const int bi = unit / p.k_h;
@@ -137,28 +139,55 @@ qk_scores_kernel(QKParams p) {
     // the four lane groups holding the same head
     lse_merge(m, sum, __shfl_xor(m, 16), __shfl_xor(sum, 16));
     lse_merge(m, sum, __shfl_xor(m, 32), __shfl_xor(sum, 32));
-    if (s == 0 && hvalid) {
-      const int64_t o = static_cast<int64_t>(bi * p.q_h + h) * p.nparts + part;
+    // max over the tail window [Leff - min(256, Leff), Leff) (x is -inf past Leff)
+    float tm = kNegInf;
+    if (p.ptail) {
+      const int tail_lo = Leff - min(256, Leff);
+#pragma unroll
+      for (int t = 0; t < kQKMaxTiles; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (16 * (t0 + t) + 4 * s + r >= tail_lo) tm = fmaxf(tm, x[t][r]);
+      tm = fmaxf(tm, __shfl_xor(tm, 16));
+      tm = fmaxf(tm, __shfl_xor(tm, 32));
+    }
+    // the block's 4 parts merged into one partial per head
+    if (s == 0) {
+      red[0][wave][col] = m;
+      red[1][wave][col] = sum;
+      red[2][wave][col] = tm;
+    }
+    __syncthreads();
+    if (wave == 0 && s == 0 && hvalid) {
+#pragma unroll
+      for (int q = 1; q < 4; ++q) {
+        lse_merge(m, sum, red[0][q][col], red[1][q][col]);
+        tm = fmaxf(tm, red[2][q][col]);
+      }
+      const int row = bi * p.q_h + h;
+      const int64_t o = static_cast<int64_t>(row) * (p.nparts / 4) + part / 4;
       p.pmax[o] = m;
       p.psum[o] = sum;
+      if (p.ptail) p.ptail[o] = tm;
     }
   }
 }
 
 int64_t qk_plan(int64_t b, int64_t k_h, int64_t L) {
   const int64_t tiles = (L + 15) / 16;
-  if (tiles == 0) return 1;
+  if (tiles == 0) return 4;
   const int64_t units = b * k_h;
   const int64_t minp = (tiles + kQKMaxTiles - 1) / kQKMaxTiles;
   const int64_t rounds = (units * minp + kQKResidentWaves - 1) / kQKResidentWaves;
   const int64_t fill = rounds * kQKResidentWaves / units;  // whole rounds of resident waves
-  return std::max(minp, std::min(tiles, fill));
+  const int64_t np = std::max(minp, std::min(tiles, fill));
+  return (np + 3) / 4 * 4;  // whole blocks of 4 waves per (batch, key head); a part may hold no tile
 }
 
 template <int DT, int D>
 static hipError_t launch_qk_typed(const QKParams& p, hipStream_t st) {
-  const int64_t nitems = static_cast<int64_t>(p.b) * p.k_h * p.nparts;
-  const int64_t blocks = (nitems + 3) / 4;
+  const int64_t nitems = static_cast<int64_t>(p.b) * p.k_h * p.nparts;  // nparts % 4 == 0
+  const int64_t blocks = nitems / 4;
   hipLaunchKernelGGL((qk_scores_kernel<DT, D>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, p);
   return hipGetLastError();
 }

@@ -1,22 +1,14 @@
-// K2: Atop-N selection + sparse softmax . V, one 1024-thread block per score row.
+// K2 of the calibration step and the threshold_topk_fast API kernel, one
+// 1024-thread block per score row (the fast step's K2 is atopn_split.hip).
 //
-// Replaces the Triton stream compaction threshold_select_fast_kernel
-// (attention/triton_atopn.py:6-53), the threshold transform
-// (attention/attention.py:136-149), torch.topk for calibration (:179-187) and
-// _atopn_gather_and_output (:152-170).  Per row, in one block and with no
-// cross-block communication:
-//   1. loads of the tail, the chunk partials and the first row tile are
-//      issued together; the logit threshold t follows from the partials;
-//   2. ordered, deterministic compaction: a row is read in tiles of
-//      1024 x 16 elements (the next tile prefetched); each wave turns its pass
-//      flags into 64-bit ballots, the per-(slot, wave) counts are
-//      prefix-summed in LDS in ascending index order, and every passing
-//      element goes to base + prefix + popcount(ballot & lanes_below).  The
-//      list (position, logit) lands in LDS and in the workspace; past `cap`
-//      entries nothing is kept (the reference keeps a race-dependent subset
-//      there);
-//   3. softmax over the list and the gather of only those V rows
-//      (BlockPV), written as the row's output.
+// Replaces torch.topk + the renormalised gather of
+// approx_top_n_attention_amortized_cal (attention/attention.py:173-189) and
+// the Triton stream compaction threshold_select_fast_kernel
+// (attention/triton_atopn.py:6-53).  Ordered, deterministic compaction: a
+// row is read in tiles of 1024 x 16 elements; each wave turns its pass flags
+// into 64-bit ballots, the per-(slot, wave) counts are prefix-summed in LDS in
+// ascending index order, and every passing element goes to
+// base + prefix + popcount(ballot & lanes_below).
 #include <type_traits>
 
 #include "block_pv.cuh"
@@ -85,101 +77,6 @@ __device__ void row_pv(SelShared& sh, float* accs, int n, const int32_t* gidx, c
     }
   }
   pv.finish(accs, v.out, v.out_dt, bi * v.o_sb + static_cast<int64_t>(h) * v.o_sh, probs);
-}
-
-template <int DT, int D>
-__global__ void __launch_bounds__(kBlkThreads) atopn_fast_kernel(FusedSelParams p, PVParams v) {
-  __shared__ SelShared sh;
-  __shared__ float accs[kBlkWaves * D];
-  const int r = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int bi = r / p.q_h, h = r - bi * p.q_h;
-  int Leff = p.L;
-  if (p.kv_len) Leff = min(Leff, max(p.kv_len[bi], 0));
-  const float* x = p.scores + static_cast<int64_t>(r) * p.ld;
-  const float* prow_m = p.pmax + static_cast<int64_t>(r) * p.nparts;
-  const float* prow_s = p.psum + static_cast<int64_t>(r) * p.nparts;
-
-  // 1. tail, partials and the first tile in flight together
-  const int tail = min(256, Leff);
-  const float tv = tid < tail ? x[Leff - tail + tid] : kNegInf;
-  const int nch = p.nparts;  // parts past kv_len hold (-inf, 0)
-  const float pm0 = tid < nch ? prow_m[tid] : kNegInf;
-  const float ps0 = tid < nch ? prow_s[tid] : 0.f;
-  float xa[kSelEPT];
-#pragma unroll
-  for (int k = 0; k < kSelEPT; ++k) {
-    const int i = k * kBlkThreads + tid;
-    xa[k] = i < Leff ? x[i] : kNegInf;
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  // attention/attention.py:142-147
-  const float mt = block_max<kBlkWaves>(tv, sh.red);
-  float acc = pm0 != kNegInf ? ps0 * __expf(pm0 - mt) : 0.f;
-  for (int c = tid + kBlkThreads; c < nch; c += kBlkThreads) {
-    const float pm = prow_m[c];
-    if (pm != kNegInf) acc += prow_s[c] * __expf(pm - mt);
-  }
-  const float ssum = block_sum<kBlkWaves>(acc, sh.red);
-  const float t = mt + logf(fmaxf(p.pstar[r], 1e-30f) * ssum);
-
-  // 2. ordered compaction (attention/triton_atopn.py:42: strict x > t)
-  int32_t* gidx = p.sel_idx + static_cast<int64_t>(r) * p.cap;
-  float* gval = p.sel_val + static_cast<int64_t>(r) * p.cap;
-  int base = 0;
-  for (int st = 0; st < Leff; st += kSelTile) {
-    float xn[kSelEPT];
-    const bool more = st + kSelTile < Leff;
-    if (more) {
-#pragma unroll
-      for (int k = 0; k < kSelEPT; ++k) {
-        const int i = st + kSelTile + k * kBlkThreads + tid;
-        xn[k] = i < Leff ? x[i] : kNegInf;
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);  // next tile in flight during this one's compaction
-    unsigned long long bal[kSelEPT];
-#pragma unroll
-    for (int k = 0; k < kSelEPT; ++k) {
-      const int i = st + k * kBlkThreads + tid;
-      bal[k] = __ballot(i < Leff && xa[k] > t);
-      if (lane == 0) sh.cnt[k * kBlkWaves + w] = __popcll(bal[k]);
-    }
-    __syncthreads();
-    if (w == 0) scan_slots(sh.cnt, sh.pre, lane);
-    __syncthreads();
-    if (base < p.cap) {
-#pragma unroll
-      for (int k = 0; k < kSelEPT; ++k) {
-        if ((bal[k] >> lane) & 1ull) {
-          const int pos = base + sh.pre[k * kBlkWaves + w] + __popcll(bal[k] & lanes_below(lane));
-          if (pos < p.cap) {
-            const int i = st + k * kBlkThreads + tid;
-            gidx[pos] = i;
-            gval[pos] = xa[k];
-            if (pos < kListLDS) {
-              sh.sidx[pos] = i;
-              sh.sval[pos] = xa[k];
-            }
-          }
-        }
-      }
-    }
-    base += sh.pre[kSelSlots];
-    __syncthreads();
-    if (more) {
-#pragma unroll
-      for (int k = 0; k < kSelEPT; ++k) xa[k] = xn[k];
-    }
-  }
-  const int n = min(base, p.cap);
-  if (tid == 0) {
-    p.sel_cnt[r] = n;
-    if (p.sel_total) p.sel_total[r] = base;
-    if (p.t_out) p.t_out[r] = t;
-  }
-  // 3. softmax over the selected logits . V (attention/attention.py:158-168)
-  row_pv<DT, D>(sh, accs, n, gidx, gval, v, bi, h, false);
 }
 
 // Calibration: exact top-k of the row (k = min(top_n, L)).
@@ -324,23 +221,21 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_kernel(FusedSelPa
 }
 
 template <int DT, int D>
-static hipError_t launch_fused(bool calibrate, const FusedSelParams& p, const PVParams& v, hipStream_t st) {
-  if (calibrate)
-    hipLaunchKernelGGL((atopn_calibrate_kernel<DT, D>), dim3(p.nrows), dim3(kBlkThreads), 0, st, p, v);
-  else
-    hipLaunchKernelGGL((atopn_fast_kernel<DT, D>), dim3(p.nrows), dim3(kBlkThreads), 0, st, p, v);
+static hipError_t launch_calibrate(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
+  hipLaunchKernelGGL((atopn_calibrate_kernel<DT, D>), dim3(p.nrows), dim3(kBlkThreads), 0, st, p, v);
   return hipGetLastError();
 }
 
 template <int DT>
-static hipError_t launch_fused_d(bool calibrate, const FusedSelParams& p, const PVParams& v, hipStream_t st) {
-  return v.d == 128 ? launch_fused<DT, 128>(calibrate, p, v, st) : launch_fused<DT, 64>(calibrate, p, v, st);
+static hipError_t launch_calibrate_d(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
+  return v.d == 128 ? launch_calibrate<DT, 128>(p, v, st) : launch_calibrate<DT, 64>(p, v, st);
 }
 
 hipError_t launch_atopn_select_pv(bool calibrate, const FusedSelParams& p, const PVParams& v, hipStream_t st) {
-  if (v.v_dt == SAGA_DTYPE_BF16) return launch_fused_d<SAGA_DTYPE_BF16>(calibrate, p, v, st);
-  if (v.v_dt == SAGA_DTYPE_F16) return launch_fused_d<SAGA_DTYPE_F16>(calibrate, p, v, st);
-  return launch_fused_d<SAGA_DTYPE_F32>(calibrate, p, v, st);
+  if (!calibrate) return launch_atopn_fast(p, v, st);
+  if (v.v_dt == SAGA_DTYPE_BF16) return launch_calibrate_d<SAGA_DTYPE_BF16>(p, v, st);
+  if (v.v_dt == SAGA_DTYPE_F16) return launch_calibrate_d<SAGA_DTYPE_F16>(p, v, st);
+  return launch_calibrate_d<SAGA_DTYPE_F32>(p, v, st);
 }
 
 // threshold_topk_fast API (attention/triton_atopn.py:59-113): typed rows,

@@ -80,8 +80,9 @@ def _kv_len(kv_len: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
 def qk_scores(query, key, attention_mask=None, scaling=None, kv_len=None, with_partials=False):
     """Scaled, masked logits [b, q_h, 1, L] in fp32 (attention/attention.py:113-128).
 
-    with_partials: also return the per-128-position-chunk max and sum of
-    exp(x - max) [b*q_h, ceil(L/128)].
+    with_partials: also return the max and sum of exp(x - max) of each part
+    of the row [b*q_h, saga_qk_nparts(b, k_h, L)]: part c covers the 16-position
+    tiles [c*T/P, (c+1)*T/P), T = ceil(L/16), P parts (possibly none).
     """
     dev = _need_gpu(query, key, attention_mask, kv_len)
     lib = _lib.load()
@@ -226,9 +227,12 @@ def dense_decode(query, key, value, attention_mask=None, scaling=None, kv_len=No
     return out
 
 
-def atopn_workspace_views(b: int, q_h: int, k_h: int, L: int, d: int, buf_k: int, device) -> dict:
-    """Views into the cached fused-decode workspace (thresholds, counts,
-    selected indices) for inspection after a call; valid until the next call."""
+def atopn_workspace_views(b: int, q_h: int, k_h: int, L: int, d: int, buf_k: int, device, fast: bool = False) -> dict:
+    """The cached fused-decode workspace after a call, for inspection (valid
+    until the next call): thresholds, counts, the selected list and the scores.
+    The calibration step writes its list to sel_idx / sel_val; the fast step
+    (fast=True) leaves it in per-slice lists, concatenated here in slice order
+    (ascending positions) and cut at buf_k."""
     lay = _lib.atopn_layout(b, q_h, k_h, L, d, buf_k)
     ws = _WORKSPACES[(torch.device(device), "atopn")]
     nr = b * q_h
@@ -237,7 +241,7 @@ def atopn_workspace_views(b: int, q_h: int, k_h: int, L: int, d: int, buf_k: int
         es = torch.tensor([], dtype=dt).element_size()
         return ws[off:off + n * es].view(dt)
 
-    return {
+    out = {
         "thresh": view(lay.thresh, nr, torch.float32),
         "sel_cnt": view(lay.sel_cnt, nr, torch.int32),
         "sel_total": view(lay.sel_total, nr, torch.int32),
@@ -245,6 +249,22 @@ def atopn_workspace_views(b: int, q_h: int, k_h: int, L: int, d: int, buf_k: int
         "sel_val": view(lay.sel_val, nr * buf_k, torch.float32).reshape(nr, buf_k),
         "scores": view(lay.scores, nr * lay.scores_ld, torch.float32).reshape(nr, lay.scores_ld)[:, :L],
     }
+    if fast:
+        ns, cap = lay.nslice, lay.slice_cap
+        cnt = view(lay.slice_cnt, nr * ns, torch.int32).reshape(nr, ns).cpu()
+        sidx = view(lay.slice_idx, nr * ns * cap, torch.int32).reshape(nr, ns, cap).cpu()
+        sval = view(lay.slice_val, nr * ns * cap, torch.float32).reshape(nr, ns, cap).cpu()
+        idx = torch.full((nr, buf_k), -1, dtype=torch.int32)
+        val = torch.full((nr, buf_k), float("nan"))
+        for r in range(nr):
+            parts = [(sidx[r, s, :min(int(cnt[r, s]), cap)], sval[r, s, :min(int(cnt[r, s]), cap)])
+                     for s in range(ns)]
+            ri = torch.cat([a for a, _ in parts])[:buf_k]
+            rv = torch.cat([v for _, v in parts])[:buf_k]
+            idx[r, :ri.numel()] = ri
+            val[r, :rv.numel()] = rv
+        out["sel_idx"], out["sel_val"] = idx, val
+    return out
 
 
 # ----------------------------------------------------------- decode-step ops

@@ -140,17 +140,18 @@ def test_workspace_sizes_and_layout():
 @pytest.mark.parametrize("b", [1, 4, 8, 32])
 @pytest.mark.parametrize("k_h", [1, 2])
 def test_qk_part_plan(b, k_h):
-    """K1 splits each (batch, key head) row into nparts balanced ranges of at
-    most 6 sixteen-position tiles, in whole rounds of 3072 resident waves."""
+    """K1 splits each (batch, key head) row into 4n balanced ranges of at most
+    6 sixteen-position tiles (n partials, one per block of 4 waves), in whole
+    rounds of 3072 resident waves up to the rounding to blocks."""
     lib = _lib.load()
     for L in (1, 15, 16, 17, 100, 4096, 32769, 33024, 131072, 131328):
         n = lib.saga_qk_nparts(b, k_h, L)
         T = (L + 15) // 16
-        assert 1 <= n <= T
-        assert -(-T // n) <= 6
+        assert 1 <= n and 4 * n <= T + 3
+        assert -(-T // (4 * n)) <= 6
         rounds = -(-(b * k_h * -(-T // 6)) // 3072)
-        assert b * k_h * n <= rounds * 3072
-    assert lib.saga_qk_nparts(8, 1, 33024) == 384
+        assert b * k_h * 4 * n <= rounds * 3072 + 3 * b * k_h
+    assert lib.saga_qk_nparts(8, 1, 33024) == 96
     assert lib.saga_qk_nparts(0, 1, 10) == 0
 
 

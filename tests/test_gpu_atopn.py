@@ -27,8 +27,9 @@ from saga_amd import ops
 pytestmark = pytest.mark.gpu
 
 
-def _views(b, q_h, k_h, L, d, buf_k):
-    return {k: v.cpu().numpy() for k, v in ops.atopn_workspace_views(b, q_h, k_h, L, d, buf_k, "cuda:0").items()}
+def _views(b, q_h, k_h, L, d, buf_k, fast=True):
+    return {k: v.cpu().numpy()
+            for k, v in ops.atopn_workspace_views(b, q_h, k_h, L, d, buf_k, "cuda:0", fast=fast).items()}
 
 
 def _run_fast(qd, kd, vd, table_row, N, mask=None, scale=None, out_dtype=torch.float32, kv_len=None):
@@ -75,7 +76,7 @@ def test_against_reference_golden(name, golden):
     cal = host(ops.atopn_calibrate(q1, k, v, N, table, mask, sc, out_dtype=torch.float32))
     np.testing.assert_allclose(host(table), g["cal_threshold" + sfx], rtol=1e-4)
     kk = min(N, L)
-    views = _views(b, q_h, k.shape[1], L, d, kk)
+    views = _views(b, q_h, k.shape[1], L, d, kk, fast=False)
     for r in range(nr):
         assert views["sel_cnt"][r] == kk
         got = np.sort(views["sel_idx"][r, :kk])
@@ -207,9 +208,9 @@ def test_fast_step_is_deterministic():
     (_, _, _), (qd, kd, vd) = qkv(rng, 4, 12, 1, 2, 128, 20000, "bf16")
     table = torch.full((48,), 1e-4, device="cuda")
     a = ops.atopn_decode(qd, kd, vd, table, 256)
-    idx_a = ops.atopn_workspace_views(4, 12, 1, 20000, 128, 512, "cuda:0")["sel_idx"].clone()
+    idx_a = ops.atopn_workspace_views(4, 12, 1, 20000, 128, 512, "cuda:0", fast=True)["sel_idx"].clone()
     bb = ops.atopn_decode(qd, kd, vd, table, 256)
-    idx_b = ops.atopn_workspace_views(4, 12, 1, 20000, 128, 512, "cuda:0")["sel_idx"].clone()
+    idx_b = ops.atopn_workspace_views(4, 12, 1, 20000, 128, 512, "cuda:0", fast=True)["sel_idx"].clone()
     assert torch.equal(a, bb) and torch.equal(idx_a, idx_b)
 
 
@@ -236,3 +237,29 @@ def test_reference_api_module_end_to_end():
     assert float(A.AMORTIZED_THRESHOLD_TENSOR.abs().sum()) == 0.0
     import saga_amd.attention.attention as B
     assert B.EXEMPT_LAYERS == {0}
+
+
+@pytest.mark.parametrize("cut_pos", [2500, 5200])
+def test_fast_overflow_cut_inside_a_later_slice(cut_pos):
+    """More than buf_k positions pass and rank buf_k falls inside a slice
+    after the first: the earlier slices count whole, the straddling one over
+    its first entries, later ones not at all (the ordered cap of the oracle)."""
+    rng = np.random.default_rng(cut_pos)
+    b, q_h, k_h, v_h, d, L, N = 2, 4, 1, 2, 128, 6000, 256
+    q = O.round_bf16(rng.standard_normal((b, q_h, 1, d), dtype=np.float32))
+    k = O.round_bf16(rng.standard_normal((b, k_h, L, d), dtype=np.float32) * np.float32(0.2))
+    # positions >= cut_pos - 700 align with the queries: their logits are large
+    k[:, :, cut_pos - 700:, :] += O.round_bf16(q.mean(axis=1, keepdims=True)[:, :, 0:1, :] * np.float32(0.3))
+    k = O.round_bf16(k)
+    v = O.round_bf16(rng.standard_normal((b, v_h, L, d), dtype=np.float32))
+    table = np.full(b * q_h, 1e-7, dtype=np.float32)
+    out = host(ops.atopn_decode(dev(q, "bf16"), dev(k, "bf16"), dev(v, "bf16"), torch.from_numpy(table).cuda(), N,
+                                out_dtype=torch.float32))
+    views = _views(b, q_h, k_h, L, d, 2 * N)
+    ref_out, t_ref, idx_ref, cnt_ref = O.fast(q, k, v, table, None, N, None)
+    buf_k = 2 * N
+    assert (views["sel_total"] > buf_k).all(), "the case must overflow"
+    np.testing.assert_array_equal(views["sel_cnt"], np.full(b * q_h, buf_k))
+    for r in range(b * q_h):
+        np.testing.assert_array_equal(views["sel_idx"][r], idx_ref.reshape(b * q_h, buf_k)[r])
+    assert np.max(np.abs(out - ref_out)) < 2e-3 and rel_l2(out, ref_out) < 1e-4

@@ -59,9 +59,12 @@ def test_scores_and_partials(dt, shape, mask_kind):
     T, nparts = (L + 15) // 16, pm.shape[1]
     pm, ps = host(pm), host(ps)
     for c in range(nparts):
-        # part c: tiles [c*T/nparts, (c+1)*T/nparts) of 16 positions
+        # part c: tiles [c*T/nparts, (c+1)*T/nparts) of 16 positions (4 K1 waves)
         t0, t1 = c * T // nparts, (c + 1) * T // nparts
-        assert 1 <= t1 - t0 <= 6
+        assert 0 <= t1 - t0 <= 24
+        if t1 == t0:
+            assert np.isneginf(pm[:, c]).all() and (ps[:, c] == 0).all()
+            continue
         blk = x[:, 16 * t0:min(16 * t1, L)].astype(np.float64)
         mx = blk.max(axis=1)
         np.testing.assert_array_equal(pm[:, c], mx.astype(np.float32))
