@@ -221,12 +221,20 @@ int saga_silu_mul(const saga_tensor* gate_up, saga_tensor* y, saga_stream_t stre
  *   SAGA_GEMV_SILU_PAIRS  w rows are interleaved (gate_i, up_i); y[m, i] =
  *                         silu(gate_i) * up_i, y is [M, N / 2]
  * Replaces the hipBLASLt calls of the decode step (no reference counterpart:
- * the reference's projections are torch nn.Linear).  N % 16 == 0, K % 32 == 0. */
+ * the reference's projections are torch nn.Linear).  N % 16 == 0, K % 32 == 0.
+ * workspace (optional, 256-byte aligned, saga_gemv_workspace_bytes(M, N, K)
+ * bytes, no initial contents needed): with it, weights with few 16-row
+ * tiles and long rows (the MLP down projection) are read by workgroups over
+ * (tile, K range) whose fp32 partial sums a second kernel adds up in a fixed
+ * order (results do not depend on scheduling).  Without it, or when the size
+ * function returns 0, one workgroup per tile. */
 #define SAGA_GEMV_STORE 0
 #define SAGA_GEMV_ADD 1
 #define SAGA_GEMV_SILU_PAIRS 2
+size_t saga_gemv_workspace_bytes(int64_t M, int64_t N, int64_t K);
 int saga_gemv(const saga_tensor* x, const saga_tensor* w, const saga_tensor* bias, float rms_eps,
-              int32_t epilogue, saga_tensor* y, saga_stream_t stream);
+              int32_t epilogue, saga_tensor* y, void* workspace, size_t workspace_bytes,
+              saga_stream_t stream);
 
 /* saga_gemv (STORE, bias, fused RMSNorm) of the fused q/k/v projection with
  * saga_rope_kv_append applied in its epilogue: one launch per layer for

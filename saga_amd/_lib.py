@@ -68,7 +68,8 @@ _SIGS = {
     "saga_rope_kv_append": (ctypes.c_int, [_T, _I64, _I64, _I64, ctypes.c_float, _P, _P, _T, _T, _T, _P]),
     "saga_rmsnorm": (ctypes.c_int, [_T, _T, ctypes.c_float, _T, _P]),
     "saga_silu_mul": (ctypes.c_int, [_T, _T, _P]),
-    "saga_gemv": (ctypes.c_int, [_T, _T, _T, ctypes.c_float, ctypes.c_int32, _T, _P]),
+    "saga_gemv_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64]),
+    "saga_gemv": (ctypes.c_int, [_T, _T, _T, ctypes.c_float, ctypes.c_int32, _T, _P, ctypes.c_size_t, _P]),
     "saga_gemv_rope_kv": (ctypes.c_int, [_T, _T, _T, ctypes.c_float, _I64, _I64, _I64, ctypes.c_float, _P, _P,
                                          _T, _T, _T, _P]),
     "saga_argmax": (ctypes.c_int, [_T, _P, _P]),

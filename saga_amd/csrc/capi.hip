@@ -621,6 +621,7 @@ int make_gemv(const saga_tensor* x, const saga_tensor* w, const saga_tensor* bia
   p.K = static_cast<int32_t>(K);
   p.rms = rms_eps >= 0.f;
   p.eps = rms_eps;
+  p.splits = 1;
   return SAGA_OK;
 }
 
@@ -698,8 +699,15 @@ int saga_silu_mul(const saga_tensor* gate_up, saga_tensor* y, saga_stream_t stre
   return row_op(true, gate_up, nullptr, 0.f, y, stream);
 }
 
+size_t saga_gemv_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M < 1 || N < 16 || K < 32) return 0;
+  const int s = gemv_splits(N, K);
+  if (s <= 1) return 0;
+  return static_cast<size_t>(align256(s * M * N * 4) + align256(s * M * 4));
+}
+
 int saga_gemv(const saga_tensor* x, const saga_tensor* w, const saga_tensor* bias, float rms_eps, int32_t epilogue,
-              saga_tensor* y, saga_stream_t stream) {
+              saga_tensor* y, void* workspace, size_t workspace_bytes, saga_stream_t stream) {
   int rc;
   GemvParams p;
   if ((rc = make_gemv(x, w, bias, rms_eps, p))) return rc;
@@ -715,6 +723,14 @@ int saga_gemv(const saga_tensor* x, const saga_tensor* w, const saga_tensor* bia
   p.y = y->data;
   p.y_ld = y->stride[0];
   p.epilogue = epilogue;
+  const int splits = gemv_splits(p.N, p.K);
+  const size_t need = saga_gemv_workspace_bytes(p.M, p.N, p.K);
+  if (workspace && splits > 1 && workspace_bytes >= need) {
+    if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(SAGA_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+    p.splits = splits;
+    p.part = static_cast<float*>(workspace);
+    p.part_ssq = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256(int64_t(splits) * p.M * p.N * 4));
+  }
   if ((rc = hip_status(launch_gemv(p, static_cast<hipStream_t>(stream)), "gemv launch"))) return rc;
   return ok();
 }

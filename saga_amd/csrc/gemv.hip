@@ -11,12 +11,15 @@
 //     the output row, accumulated from the x fragments the waves load anyway;
 //   * epilogues: + bias, += into y (residual stream), or silu(gate) * up for
 //     W rows interleaved as [gate_0, up_0, gate_1, up_1, ...].
+#include <algorithm>
+
 #include "common.cuh"
 #include "kernels.h"
 
 namespace saga {
 
-constexpr int kGemvUnroll = 8;  // 32-wide k steps in flight per wave
+constexpr int kGemvUnroll = 12;  // 32-wide k steps in flight per wave (K = 1536 over 4 waves: one burst)
+constexpr int kSplitBatch = 8;   // split-K partial sums in flight per epilogue thread
 
 template <int WAVES, int EPI>
 __global__ void __launch_bounds__(WAVES * 64) gemv_kernel(GemvParams p) {
@@ -24,11 +27,13 @@ __global__ void __launch_bounds__(WAVES * 64) gemv_kernel(GemvParams p) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int col = lane & 15, s = lane >> 4;
   const int n0 = blockIdx.x * 16;
+  const int split = blockIdx.y;  // K range of this workgroup (split-K: partial sums out)
   const bool mvalid = col < p.M;
   const char* wrow = static_cast<const char*>(p.w) + (static_cast<int64_t>(n0 + col) * p.w_ld + 8 * s) * 2;
   const char* xrow = static_cast<const char*>(p.x) + (static_cast<int64_t>(mvalid ? col : 0) * p.x_ld + 8 * s) * 2;
   const int steps = p.K / 32;
-  const int j0 = w * steps / WAVES, j1 = (w + 1) * steps / WAVES;
+  const int k0 = split * steps / p.splits, k1 = (split + 1) * steps / p.splits;
+  const int j0 = k0 + w * (k1 - k0) / WAVES, j1 = k0 + (w + 1) * (k1 - k0) / WAVES;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   float ssq = 0.f;
   for (int j = j0; j < j1; j += kGemvUnroll) {
@@ -71,8 +76,15 @@ __global__ void __launch_bounds__(WAVES * 64) gemv_kernel(GemvParams p) {
     }
   }
   if (!mvalid) return;
-  const float scale = p.rms ? rsqrtf(sq / static_cast<float>(p.K) + p.eps) : 1.f;
   const int n = n0 + 4 * s;
+  if (p.part) {
+    // split-K: this K range's sums; gemv_splitk_epilogue finishes the rows
+    *reinterpret_cast<f32x4*>(p.part + (static_cast<int64_t>(split) * p.M + col) * p.N + n) =
+        f32x4{v[0], v[1], v[2], v[3]};
+    if (s == 0 && blockIdx.x == 0) p.part_ssq[split * p.M + col] = sq;
+    return;
+  }
+  const float scale = p.rms ? rsqrtf(sq / static_cast<float>(p.K) + p.eps) : 1.f;
   if constexpr (EPI == kGemvRopeKV) {
     // token row m = col; the 4 rows n..n+3 lie in one head (d % 16 == 0).  q/k
     // heads are stored in rotary-pair order [0, d/2, 1, d/2 + 1, ...], so rows
@@ -138,15 +150,80 @@ __global__ void __launch_bounds__(WAVES * 64) gemv_kernel(GemvParams p) {
   }
 }
 
+// Split-K finish, one thread per output pair (n, n+1) of a token row m: the
+// sums over the K ranges of the partial sums (and of the partial sums of
+// squares for the RMS scale), then the epilogue of gemv_kernel.  64-thread
+// blocks spread the few thousand threads over many CUs; every partial of a
+// thread is loaded in one burst.
+template <int EPI>
+__global__ void __launch_bounds__(64) gemv_splitk_epilogue(GemvParams p) {
+  const int64_t q = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
+  const int np = p.N / 2;
+  if (q >= static_cast<int64_t>(p.M) * np) return;
+  const int m = static_cast<int>(q / np), n = 2 * static_cast<int>(q - static_cast<int64_t>(m) * np);
+  float v0 = 0.f, v1 = 0.f, sq = 0.f;
+  for (int s0 = 0; s0 < p.splits; s0 += kSplitBatch) {
+    f32x2 a[kSplitBatch];
+    float b[kSplitBatch];
+#pragma unroll
+    for (int u = 0; u < kSplitBatch; ++u) {
+      const int s = s0 + u;
+      a[u] = s < p.splits ? *reinterpret_cast<const f32x2*>(p.part + (static_cast<int64_t>(s) * p.M + m) * p.N + n)
+                          : f32x2{0.f, 0.f};
+      b[u] = (p.rms && s < p.splits) ? p.part_ssq[s * p.M + m] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kSplitBatch; ++u) {
+      v0 += a[u].x;
+      v1 += a[u].y;
+      sq += b[u];
+    }
+  }
+  const float scale = p.rms ? rsqrtf(sq / static_cast<float>(p.K) + p.eps) : 1.f;
+  uint16_t* y = static_cast<uint16_t*>(p.y) + static_cast<int64_t>(m) * p.y_ld;
+  if constexpr (EPI == SAGA_GEMV_SILU_PAIRS) {
+    // rows (n, n+1) are a (gate, up) pair -> output n/2
+    const float g = v0 * scale, u = v1 * scale;
+    y[n / 2] = f32_to_bf16_bits(g / (1.0f + expf(-g)) * u);
+  } else {
+    float o0 = v0 * scale, o1 = v1 * scale;
+    if (p.bias) {
+      o0 += bf16_bits_to_f32(static_cast<const uint16_t*>(p.bias)[n]);
+      o1 += bf16_bits_to_f32(static_cast<const uint16_t*>(p.bias)[n + 1]);
+    }
+    if constexpr (EPI == SAGA_GEMV_ADD) {
+      o0 += bf16_bits_to_f32(y[n]);
+      o1 += bf16_bits_to_f32(y[n + 1]);
+    }
+    y[n] = f32_to_bf16_bits(o0);
+    y[n + 1] = f32_to_bf16_bits(o1);
+  }
+}
+
 template <int EPI>
 static hipError_t launch_gemv_epi(const GemvParams& p, hipStream_t st) {
   const unsigned blocks = static_cast<unsigned>(p.N / 16);
-  // long rows of W: more waves per workgroup split K
-  if (p.K >= 4096)
-    hipLaunchKernelGGL((gemv_kernel<16, EPI>), dim3(blocks), dim3(1024), 0, st, p);
-  else
-    hipLaunchKernelGGL((gemv_kernel<4, EPI>), dim3(blocks), dim3(256), 0, st, p);
+  if (p.part) {
+    hipLaunchKernelGGL((gemv_kernel<4, EPI>), dim3(blocks, p.splits), dim3(256), 0, st, p);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int64_t pairs = static_cast<int64_t>(p.M) * (p.N / 2);
+    hipLaunchKernelGGL((gemv_splitk_epilogue<EPI>), dim3(static_cast<unsigned>((pairs + 63) / 64)), dim3(64), 0, st,
+                       p);
+  } else if (p.K >= 4096) {
+    // long rows of W: more waves per workgroup split K
+    hipLaunchKernelGGL((gemv_kernel<16, EPI>), dim3(blocks, 1), dim3(1024), 0, st, p);
+  } else {
+    hipLaunchKernelGGL((gemv_kernel<4, EPI>), dim3(blocks, 1), dim3(256), 0, st, p);
+  }
   return hipGetLastError();
+}
+
+int gemv_splits(int64_t N, int64_t K) {
+  const int64_t tiles = N / 16, steps = K / 32;
+  int64_t s = (512 + tiles - 1) / tiles;       // about 512 workgroups
+  s = std::min<int64_t>(s, steps / (4 * 8));   // >= 8 k steps per wave
+  return static_cast<int>(std::max<int64_t>(s, 1));
 }
 
 hipError_t launch_gemv(const GemvParams& p, hipStream_t st) {

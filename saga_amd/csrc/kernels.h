@@ -192,7 +192,13 @@ struct GemvParams {
   // kGemvRopeKV: y is unused; rows of w are the fused q/k/v projection with
   // the q and k heads in rotary-pair order, written through `rope` (qkv unused)
   RopeParams rope;
+  // split-K (part != null): K cut into `splits` ranges, one workgroup each;
+  // part [splits][M][N] and part_ssq [splits][M] fp32, finished by an epilogue kernel
+  int32_t splits;
+  float* part;
+  float* part_ssq;
 };
+int gemv_splits(int64_t N, int64_t K);  // K ranges worth launching for an N x K weight
 constexpr int kGemvRopeKV = 3;
 hipError_t launch_gemv(const GemvParams& p, hipStream_t st);
 hipError_t launch_argmax(const void* x, int64_t ld, int rows, int N, int64_t* out, hipStream_t st);

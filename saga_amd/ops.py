@@ -305,12 +305,14 @@ def silu_mul(gate_up, out=None):
     return out
 
 
-def gemv(x, w, bias=None, rms_eps=None, epilogue="store", out=None):
+def gemv(x, w, bias=None, rms_eps=None, epilogue="store", out=None, split_k=True):
     """Skinny projection for decode (x [M <= 16, K] bf16, w [N, K] bf16):
     y = s * x @ w.T (+ bias), s = 1/sqrt(mean(x^2) + rms_eps) per row when
     rms_eps is given (RMSNorm fused, norm weight folded into w).
     epilogue: "store", "add" (out += result, in place) or "silu_pairs" (w rows
-    interleaved gate/up; out = silu(gate) * up, [M, N/2])."""
+    interleaved gate/up; out = silu(gate) * up, [M, N/2]).  split_k: pass
+    the cached workspace, so that long-row weights with few tiles are read
+    split over K (deterministic two-kernel reduction)."""
     _need_gpu(x, w, bias, out)
     codes = {"store": _lib.GEMV_STORE, "add": _lib.GEMV_ADD, "silu_pairs": _lib.GEMV_SILU_PAIRS}
     code = codes[epilogue]
@@ -320,8 +322,11 @@ def gemv(x, w, bias=None, rms_eps=None, epilogue="store", out=None):
             raise ValueError("saga_amd: epilogue 'add' needs out")
         out = torch.empty(M, N // 2 if code == _lib.GEMV_SILU_PAIRS else N, dtype=x.dtype, device=x.device)
     eps = -1.0 if rms_eps is None else float(rms_eps)
-    _lib.check(_lib.load().saga_gemv(_lib.tensor(x), _lib.tensor(w), _lib.tensor(bias), eps, code, _lib.tensor(out),
-                                     _lib.stream_of(x)), "gemv")
+    lib = _lib.load()
+    need = lib.saga_gemv_workspace_bytes(M, N, x.shape[1]) if split_k else 0
+    ws = workspace(x.device, "gemv", need) if need else None
+    _lib.check(lib.saga_gemv(_lib.tensor(x), _lib.tensor(w), _lib.tensor(bias), eps, code, _lib.tensor(out),
+                             _lib.ptr(ws), ws.numel() if ws is not None else 0, _lib.stream_of(x)), "gemv")
     return out
 
 

@@ -155,6 +155,14 @@ def test_qk_part_plan(b, k_h):
     assert lib.saga_qk_nparts(0, 1, 10) == 0
 
 
+def test_gemv_split_plan():
+    """Split-K only for weights with few 16-row tiles and long rows."""
+    lib = _lib.load()
+    assert lib.saga_gemv_workspace_bytes(8, 1536, 8960) > 0       # MLP down projection
+    for n, k in ((17920, 1536), (1920, 1536), (1536, 1536), (151936, 1536)):
+        assert lib.saga_gemv_workspace_bytes(8, n, k) == 0
+
+
 def test_ops_refuse_cpu_tensors():
     import torch
     from saga_amd import ops

@@ -6,7 +6,7 @@ import torch
 from conftest import rel_l2
 from gpu_util import dev, host
 from oracle import saga_oracle as O
-from saga_amd import ops
+from saga_amd import _lib, ops
 
 pytestmark = pytest.mark.gpu
 
@@ -114,3 +114,25 @@ def test_rope_pair_order_is_a_permutation():
     order = ops.rope_pair_order(3, 1, 2, 8)
     assert sorted(order.tolist()) == list(range(6 * 8))
     assert order[:8].tolist() == [0, 4, 1, 5, 2, 6, 3, 7] and order[32:].tolist() == list(range(32, 48))
+
+
+@pytest.mark.parametrize("epilogue", ["store", "add", "silu_pairs"])
+@pytest.mark.parametrize("rms", [False, True])
+def test_gemv_split_k_matches_single_pass_and_is_deterministic(epilogue, rms):
+    """Long rows with few tiles (the down projection shape) go through the
+    split-K path; it agrees with the one-workgroup-per-tile path and repeats
+    bit for bit."""
+    rng = np.random.default_rng(77)
+    M, K, N = 8, 8960, 1536
+    x, w, _ = _data(rng, M, K, N)
+    xd, wd = dev(x, "bf16"), dev(w, "bf16")
+    assert _lib.load().saga_gemv_workspace_bytes(M, N, K) > 0
+    y0 = dev(O.round_bf16(rng.standard_normal((M, N // 2 if epilogue == "silu_pairs" else N), dtype=np.float32)),
+             "bf16")
+    outs = []
+    for split in (False, True, True):
+        y = y0.clone()
+        outs.append(ops.gemv(xd, wd, rms_eps=1e-6 if rms else None, epilogue=epilogue, out=y, split_k=split))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[1], outs[2])
+    assert torch.allclose(outs[0].float(), outs[1].float(), rtol=2 ** -7, atol=2e-3)
