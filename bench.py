@@ -282,7 +282,7 @@ def main():
             "kv_cache": {"k": list(saga_cache[0]), "v": list(saga_cache[1]), "dtype": "bf16"},
         },
         "roofline": {
-            "kernel": "saga::qk_scores_kernel<bf16,128,8> (K1)",
+            "kernel": "saga::qk_scores_kernel<bf16,128> (K1)",
             "bound": "hbm",
             "achieved": round(k1_gbs, 1),
             "peak": HBM_PEAK_GBS,
