@@ -170,6 +170,66 @@ def profile_kernels(batch, ctx, shape, launches=8):
     return 0
 
 
+def sweep(copies=8):
+    """Attention-only timings on synthetic bf16 caches: every shape is timed
+    as a graph of 2 x `copies` launches cycling over `copies` distinct K/V
+    caches (the same cache in a row would sit in the 256 MB Infinity Cache).
+    Atop-N: the table is calibrated first (N-th largest probability of a
+    nearby query), then the fast step is timed.  Bytes are algorithmic: K
+    (+ V rows actually selected, counted from the workspace) for Atop-N, K + V
+    for dense."""
+    from saga_amd import ops
+    dev = "cuda"
+    grid = []
+    for L in (4096, 16384, 65536, 131072):          # lengths x batches, 12Q / 1K / 2V, N = 256
+        for b in (1, 8, 32):
+            if b * L <= 32 * 65536:
+                grid.append(("len-batch", b, 12, 1, 2, L, 256))
+    for k_h, v_h, q_h in ((1, 2, 12), (1, 4, 12), (2, 2, 12), (2, 4, 12), (1, 8, 16), (2, 8, 16)):
+        grid.append(("heads", 8, q_h, k_h, v_h, 16384, 256))   # head groupings
+    for N in (64, 256, 1024):
+        grid.append(("top-n", 8, 12, 1, 2, 16384, N))
+    grid.append(("C5 SAGA", 4, 12, 1, 2, 131072, 1024))
+    grid.append(("C5 dense-GQA", 4, 12, 2, 2, 131072, None))
+    for tag, b, q_h, k_h, v_h, L, N in grid:
+        g = torch.Generator(device=dev).manual_seed(L + b)
+        q = torch.randn(b, q_h, 1, 128, device=dev, generator=g).to(torch.bfloat16)
+        q2 = (q.float() + 0.3 * torch.randn(q.shape, device=dev, generator=g)).to(torch.bfloat16)
+        ncp = max(1, min(copies, int(6e9 // (b * (k_h + v_h) * L * 256))))
+        ks, vs = [], []
+        for _ in range(ncp):
+            k = torch.randn(b, k_h, L, 128, device=dev, generator=g)
+            k[:, :, torch.randperm(L, device=dev, generator=g)[: L // 100]] *= 8  # 1% outlier keys
+            ks.append(k.to(torch.bfloat16))
+            vs.append(torch.randn(b, v_h, L, 128, device=dev, generator=g).to(torch.bfloat16))
+        out = torch.empty(b, q_h, 1, 128, device=dev, dtype=torch.bfloat16)
+        kv_bytes = b * k_h * L * 256
+        if N is None:
+            us = timed_graph(lambda i: ops.dense_decode(q2, ks[i % ncp], vs[i % ncp], out=out), 2 * ncp)
+            byts = kv_bytes + b * v_h * L * 256
+            line = {"sweep": tag, "b": b, "q_h": q_h, "k_h": k_h, "v_h": v_h, "L": L, "kernel": "dense",
+                    "us": round(us, 2), "GBs": round(byts / us / 1e3, 1)}
+        else:
+            tabs = [torch.zeros(b * q_h, device=dev) for _ in range(ncp)]
+            for i in range(ncp):
+                ops.atopn_calibrate(q, ks[i], vs[i], N, tabs[i])
+            us = timed_graph(lambda i: ops.atopn_decode(q2, ks[i % ncp], vs[i % ncp], tabs[i % ncp], N, out=out),
+                             2 * ncp)
+            k1 = timed_graph(lambda i: ops.qk_scores(q2, ks[i % ncp], with_partials=True), 2 * ncp)
+            ops.atopn_decode(q2, ks[0], vs[0], tabs[0], N, out=out)
+            torch.cuda.synchronize()
+            cnt = ops.atopn_workspace_views(b, q_h, k_h, L, 128, min(2 * N, L), dev)["sel_cnt"]
+            sel = int(cnt.sum())
+            byts = kv_bytes + sel * 256
+            line = {"sweep": tag, "b": b, "q_h": q_h, "k_h": k_h, "v_h": v_h, "L": L, "N": N, "kernel": "atopn",
+                    "us": round(us, 2), "k1_us": round(k1, 2), "k1_GBs": round(kv_bytes / k1 / 1e3, 1),
+                    "selected_per_row": round(sel / (b * q_h), 1), "GBs": round(byts / us / 1e3, 1)}
+        print(json.dumps(line), flush=True)
+        del ks, vs
+        torch.cuda.empty_cache()
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -181,6 +241,9 @@ def main():
     ap.add_argument("--no-dense", action="store_true", help="skip the dense-GQA comparator")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--synthetic-kv", action="store_true", help="fill the caches with N(0,1) instead of a prefill")
+    ap.add_argument("--sweep", action="store_true",
+                    help="attention kernels alone over a grid of shapes (lengths, batches, head groupings, N) "
+                         "and the 128k dense-GQA vs SAGA comparison; one JSON line per shape")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="only launch K1 (qk_scores) at the workload shape and a 1 GiB device copy, "
                          "for hardware-counter runs")
@@ -199,6 +262,8 @@ def main():
     B, ctx, K, W = args.batch, args.ctx, args.steps, args.warmup
     if args.profile_kernels:
         return profile_kernels(B, ctx, QWEN25_15B_SAGA)
+    if args.sweep:
+        return sweep()
     max_len = ctx + K
     torch.manual_seed(0)
     prompt = torch.randint(0, QWEN25_15B_SAGA.vocab, (ctx,), dtype=torch.int64)

@@ -90,9 +90,9 @@ typedef struct saga_atopn_layout {
   int64_t slice_idx; /* i32 [b*q_h, nslice, slice_cap] passing positions per slice */
   int64_t slice_val; /* f32 [b*q_h, nslice, slice_cap] their logits */
   int64_t slice_cnt; /* i32 [b*q_h, nslice] passing per slice */
-  int64_t slice_pre; /* i32 [b*q_h, nslice + 1] prefix of slice_cnt */
-  int64_t slice_o;   /* f32 [b*q_h, nslice, d] partial sum_e exp(x_e - m) V[e] */
-  int64_t slice_ml;  /* f32 [b*q_h, nslice, 2] partial (m, sum_e exp(x_e - m)) */
+  int64_t slice_pre; /* i32 [b*q_h, 2, nslice + 1] slice ranks (rows of > 2048 slices) */
+  int64_t slice_o;   /* f32 [b*q_h, nslice, d] partial sum_e exp(x_e - m) V[e] of short slices */
+  int64_t slice_ml;  /* f32 [b*q_h, nslice, 2] partial (m, sum_e exp(x_e - m)) of short slices */
   int64_t total_bytes;
 } saga_atopn_layout;
 

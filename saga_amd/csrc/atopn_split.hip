@@ -1,7 +1,4 @@
-// K2 of the Atop-N fast step, split across the GPU: each score row is cut
-// into slices of kSliceLen positions, one wave per (row, slice), with no
-// block barrier (wave-level DPP reductions, ballot ranks); then one merge
-// block per row.
+// K2 of the Atop-N fast step, in two kernels.
 //
 // Replaces the threshold transform (attention/attention.py:136-149), the
 // Triton stream compaction threshold_select_fast_kernel
@@ -9,26 +6,28 @@
 // (attention/attention.py:152-170) of approx_top_n_attention_amortized
 // (:192-209).
 //
-// Slice wave (atopn_slice_kernel):
+// Slice waves (atopn_slice_kernel), one wave per (row, kSliceLen positions),
+// four independent waves per block, no block barrier:
 //   1. loads of the K1 block partials (max, sum of exp, tail-window max) and
 //      of the slice's scores are issued together; t = m + log(max(p*, 1e-30)
-//      * sum_j exp(x_j - m)) from the partials (every wave of a row runs the
-//      same reduction in the same order, so all of them hold the
-//      bit-identical t);
-//   2. ordered compaction of {x > t} (strict, triton_atopn.py:42) within the
-//      slice: 64-bit ballots and mbcnt put every passing element at its rank
-//      in ascending position order; the slice's list goes to LDS and to the
-//      workspace;
-//   3. softmax . V over the slice's list relative to its own max:
-//      (m_s, l_s, o_s = sum_e exp(x_e - m_s) V[e]) to the workspace.
-// Merge block (atopn_merge_kernel), per row: the log-sum-exp merge of the
-// slice partials; when more than buf_k positions pass, exactly the first
-// buf_k in ascending order count (the reference keeps a race-dependent subset
-// there): slices past rank buf_k are dropped and the slice straddling it is
-// recomputed over its first entries.  The selected list stays in the slice
-// lists of the workspace (concatenated in slice order, cut at buf_k).
-// The kernel boundary between the two orders the slice writes before the
-// merge reads (no device-scope fences or counters).
+//      * sum_j exp(x_j - m)) from the partials with DPP wave reductions
+//      (every wave of a row runs the same reduction in the same order, so all
+//      of them hold the bit-identical t);
+//   2. ordered compaction of {x > t} (strict, triton_atopn.py:42): 64-bit
+//      ballots and mbcnt put every passing element at its rank in ascending
+//      position order; the slice's list and count go to the workspace;
+//   3. a list of at most kSliceSmall entries (the usual case) is gathered by
+//      the wave itself in one burst: its (m, l, o) softmax . V partial.
+// Row blocks (atopn_gather_kernel), one 256-thread block per row: a block scan
+// of the slice counts ranks the slices; exactly the first n = min(total,
+// buf_k) passing positions in ascending order count (the reference keeps a
+// race-dependent subset when more than buf_k pass).  Short slices wholly
+// among them contribute their partials (log-sum-exp merge); the entries of
+// long slices and of the slice cut at rank buf_k are gathered here, 256 V
+// rows per burst.  So no wave carries a long gather chain: balanced rows stay
+// one gather burst deep, skewed or overflowing rows cost at most buf_k
+// block-parallel gathers.  The kernel boundary orders the slice writes before
+// the row reads (no device-scope fences or counters).
 #include "block_pv.cuh"
 #include "kernels.h"
 
@@ -38,10 +37,16 @@ constexpr int kSliceThreads = 256;                    // 4 independent slice wav
 constexpr int kSliceWaves = kSliceThreads / kWave;    // 4
 constexpr int kSliceLoads = kSliceLen / (4 * kWave);  // f32x4 loads per lane: 4
 constexpr int kSlicePrefetch = 4;                     // partials per lane in the first burst
-constexpr int kMergeSlices = 8;                       // slices per merge thread in one burst
-constexpr int kMergeMaxSlices = 2048;                 // slice ranks kept in LDS
+constexpr int kRowThreads = 1024;
+constexpr int kRowWaves = kRowThreads / kWave;
+constexpr int kRowBatch = 2048;                       // list entries per LDS batch
+constexpr int kRowMaxSlices = 2048;                   // slice ranks kept in LDS
+constexpr int kRowUnroll = 16;                        // V rows in flight per lane group
+constexpr int kWaveUnroll = 16;                       // slice wave: 4 groups x 16 = 64 V rows in flight
+constexpr int kRowMergeSlices = 8;                    // slice partials per merge thread in one burst
 
 static_assert(kSliceLen == kSliceLoads * 4 * kWave, "slice = whole f32x4 loads of every lane");
+static_assert(kSliceSmall == 4 * kWaveUnroll, "a small slice list is one gather burst of its wave");
 
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -49,104 +54,64 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Wave-level sparse softmax . V with a running max (online softmax over
-// batches): 4 lane groups of 16 lanes, lane c of group G owns dims
-// [c*DPL, c*DPL + DPL) and walks entries G, G+4, ...; eight V rows per group
-// in flight.
+// One wave's softmax . V over n <= kSliceSmall entries (one burst): 4 lane
+// groups of 16 lanes, lane c of group G owns dims [c*DPL, c*DPL + DPL) and
+// loads the rows G, G+4, ...; weights are relative to the list's max m.
+// Writes o (unnormalised, D floats) and returns (m, l) in every lane.
 template <int DT, int D>
-struct WavePV {
-  static constexpr int DPL = D / 16;
+__device__ void wave_pv_small(int n, const int* sidx, const float* sval, const char* vbase, int64_t vrow,
+                              float* scratch, float* o, float& m, float& l) {
+  using PV = BlockPV<DT, D>;
+  constexpr int DPL = D / 16;
+  const int lane = threadIdx.x & 63, G = lane >> 4, c = lane & 15;
+  const float xv = lane < n ? sval[lane] : kNegInf;
+  m = wave_max(xv);
+  l = wave_sum(lane < n ? __expf(xv - m) : 0.f);
   float acc[DPL];
-  float m, l;
-
-  __device__ void init() {
 #pragma unroll
-    for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
-    m = kNegInf;
-    l = 0.f;
+  for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
+  const char* vb = vbase + static_cast<int64_t>(c) * PV::BYTES;
+  u32x4 raw[kWaveUnroll][PV::NV];
+#pragma unroll
+  for (int u = 0; u < kWaveUnroll; ++u) {
+    const int e = G + 4 * u;
+    if (e < n) PV::load_raw(vb + static_cast<int64_t>(sidx[e]) * vrow, raw[u]);
   }
-
-  __device__ void add(int n, const int* sidx, const float* sval, const char* vbase, int64_t vrow) {
-    const int lane = threadIdx.x & 63;
-    float cm = kNegInf;
-    for (int i = lane; i < n; i += kWave) cm = fmaxf(cm, sval[i]);
-    const float mn = fmaxf(m, wave_max(cm));
-    const float scale_old = m == kNegInf ? 0.f : __expf(m - mn);
-    float ls = 0.f;
-    if (mn != kNegInf)
-      for (int i = lane; i < n; i += kWave) ls += __expf(sval[i] - mn);
-    l = l * scale_old + wave_sum(ls);
-    m = mn;
+  __builtin_amdgcn_sched_barrier(0);  // all gathers in flight before the FMAs
 #pragma unroll
-    for (int i = 0; i < DPL; ++i) acc[i] *= scale_old;
-    if (mn == kNegInf) return;
-    const int G = lane >> 4, c = lane & 15;
-    const char* vb = vbase + static_cast<int64_t>(c) * BlockPV<DT, D>::BYTES;
-    for (int e0 = G; e0 < n; e0 += 4 * kPVUnroll) {
-      u32x4 raw[kPVUnroll][BlockPV<DT, D>::NV];
+  for (int u = 0; u < kWaveUnroll; ++u) {
+    const int e = G + 4 * u;
+    if (e < n) {
+      const float w = __expf(sval[e] - m);
+      float f[DPL];
+      PV::unpack(raw[u], f);
 #pragma unroll
-      for (int u = 0; u < kPVUnroll; ++u) {
-        const int e = e0 + 4 * u;
-        if (e < n) BlockPV<DT, D>::load_raw(vb + static_cast<int64_t>(sidx[e]) * vrow, raw[u]);
-      }
-      __builtin_amdgcn_sched_barrier(0);  // all gathers in flight before the FMAs
-#pragma unroll
-      for (int u = 0; u < kPVUnroll; ++u) {
-        const int e = e0 + 4 * u;
-        if (e < n) {
-          const float w = __expf(sval[e] - mn);
-          float f[DPL];
-          BlockPV<DT, D>::unpack(raw[u], f);
-#pragma unroll
-          for (int i = 0; i < DPL; ++i) acc[i] += w * f[i];
-        }
-      }
+      for (int i = 0; i < DPL; ++i) acc[i] += w * f[i];
     }
   }
-
-  // Sum the 4 groups through the wave's LDS scratch (>= 4 * D floats); o[q]
-  // then holds dim lane + 64 q (< D) of sum_e w_e V[e].
-  template <int DQ>
-  __device__ void reduce(float* scratch, float (&o)[DQ]) {
-    const int lane = threadIdx.x & 63, G = lane >> 4, c = lane & 15;
+  // the 4 groups summed through the wave's LDS scratch (>= 4 * D floats)
+  wave_lds_sync();
 #pragma unroll
-    for (int i = 0; i < DPL; ++i) scratch[G * D + c * DPL + i] = acc[i];
-    wave_lds_sync();
-#pragma unroll
-    for (int q = 0; q < DQ; ++q) {
-      const int i = lane + q * kWave;
-      o[q] = i < D ? (scratch[i] + scratch[D + i]) + (scratch[2 * D + i] + scratch[3 * D + i]) : 0.f;
-    }
-    wave_lds_sync();
-  }
-};
+  for (int i = 0; i < DPL; ++i) scratch[G * D + c * DPL + i] = acc[i];
+  wave_lds_sync();
+  for (int i = lane; i < D; i += kWave) o[i] = (scratch[i] + scratch[D + i]) + (scratch[2 * D + i] + scratch[3 * D + i]);
+}
 
 struct SliceWaveShared {
-  int sidx[kSliceLen];
-  float sval[kSliceLen];
+  int sidx[kSliceSmall];
+  float sval[kSliceSmall];
+  float scratch[4 * 128];
 };
-
-// The slice holding list entry j of a row (pre[s] <= j < pre[s+1]).
-__device__ __forceinline__ int slice_of(const int* pre, int nslice, int j) {
-  int lo = 0, hi = nslice - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (pre[mid] <= j) lo = mid; else hi = mid - 1;
-  }
-  return lo;
-}
 
 template <int DT, int D>
 __global__ void __launch_bounds__(kSliceThreads) atopn_slice_kernel(FusedSelParams p, PVParams v) {
   __shared__ SliceWaveShared shw[kSliceWaves];
-  constexpr int DQ = (D + kWave - 1) / kWave;  // output dims per lane
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t gw = static_cast<int64_t>(blockIdx.x) * kSliceWaves + w;
   if (gw >= static_cast<int64_t>(p.nrows) * p.nslice) return;
   const int r = static_cast<int>(gw / p.nslice), sl = static_cast<int>(gw - static_cast<int64_t>(r) * p.nslice);
-  SliceWaveShared& sh = shw[w];
-  const int bi = r / p.q_h, h = r - bi * p.q_h;
+  const int bi = r / p.q_h;
   const float* x = p.scores + static_cast<int64_t>(r) * p.ld;
   const float* prow_m = p.pmax + static_cast<int64_t>(r) * p.nparts;
   const float* prow_s = p.psum + static_cast<int64_t>(r) * p.nparts;
@@ -194,7 +159,8 @@ __global__ void __launch_bounds__(kSliceThreads) atopn_slice_kernel(FusedSelPara
   // 2. ordered compaction; element (k, lane, j) is position s0 + 4*(k*64 + lane) + j.
   //    Ballot j of load k holds flag j of every lane; a passing element's rank
   //    is the passing elements of earlier loads + those of lower lanes (mbcnt
-  //    of the four ballots) + its own lower flags.
+  //    of the four ballots) + its own lower flags.  Ranks past slice_cap
+  //    (= min(kSliceLen, buf_k)) can never be among a row's first buf_k.
   unsigned long long bal[kSliceLoads][4];
   int n = 0;
   int base[kSliceLoads];
@@ -222,11 +188,13 @@ __global__ void __launch_bounds__(kSliceThreads) atopn_slice_kernel(FusedSelPara
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       if ((bal[k][j] >> lane) & 1ull) {
-        sh.sidx[pos] = e + j;
-        sh.sval[pos] = xv[k][j];
         if (pos < p.slice_cap) {
           gidx[pos] = e + j;
           gval[pos] = xv[k][j];
+        }
+        if (pos < kSliceSmall) {
+          shw[w].sidx[pos] = e + j;
+          shw[w].sval[pos] = xv[k][j];
         }
         ++pos;
       }
@@ -236,124 +204,150 @@ __global__ void __launch_bounds__(kSliceThreads) atopn_slice_kernel(FusedSelPara
     p.sl_cnt[gw] = n;
     if (sl == 0 && p.t_out) p.t_out[r] = t;
   }
-  wave_lds_sync();
-
-  // 3. the slice's softmax . V partial (skipped when the row overflows for
-  //    sure: the merge recomputes it from the capped list)
-  const int vh = h / (v.q_h / v.v_h);
-  const char* vbase = v.v + (bi * v.v_sb + static_cast<int64_t>(vh) * v.v_sh) * Elt<DT>::kBytes;
-  WavePV<DT, D> pv;
-  pv.init();
-  if (n <= p.cap) pv.add(n, sh.sidx, sh.sval, vbase, v.v_sl * Elt<DT>::kBytes);
-  wave_lds_sync();
-  float o[DQ];
-  pv.reduce(sh.sval, o);  // the list is consumed: its LDS is the scratch
-#pragma unroll
-  for (int q = 0; q < DQ; ++q)
-    if (lane + q * kWave < D) p.sl_o[gw * D + lane + q * kWave] = o[q];
-  if (lane == 0) {
-    p.sl_ml[2 * gw] = pv.m;
-    p.sl_ml[2 * gw + 1] = pv.l;
+  // 3. a short list is gathered here, in one burst: (m, l, o) partial of the
+  //    slice (its count tells the row kernel that the partial exists)
+  if (n > 0 && n <= kSliceSmall) {
+    wave_lds_sync();
+    const int h = r - bi * p.q_h;
+    const int vh = h / (v.q_h / v.v_h);
+    const char* vbase = v.v + (bi * v.v_sb + static_cast<int64_t>(vh) * v.v_sh) * Elt<DT>::kBytes;
+    float m, l;
+    wave_pv_small<DT, D>(n, shw[w].sidx, shw[w].sval, vbase, v.v_sl * Elt<DT>::kBytes, shw[w].scratch,
+                         p.sl_o + gw * D, m, l);
+    if (lane == 0) {
+      p.sl_ml[2 * gw] = m;
+      p.sl_ml[2 * gw + 1] = l;
+    }
   }
 }
 
-// Merge of row r's slice partials, one 256-thread block per row.
-//   1. the slice counts and a first batch of partials in one burst; a block
-//      scan of the counts gives each slice's first rank;
-//   2. slices whose passing positions all rank below buf_k ("included") are
-//      merged from their partials: out = sum_s o_s exp(m_s - M) / sum_s l_s
-//      exp(m_s - M), thread t owning dims [4c, 4c + 4), c = t % (D/4), of the
-//      slices g, g + G, ... (g = t / (D/4));
-//   3. overflow (total > buf_k): the one slice straddling rank buf_k
-//      contributes softmax . V over its first k* entries, recomputed here;
-//      later slices are dropped.
+// The slice holding list entry j of a row (pre[s] <= j < pre[s+1]).
+__device__ __forceinline__ int slice_of(const int* pre, int nslice, int j) {
+  int lo = 0, hi = nslice - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (pre[mid] <= j) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+// Exclusive block scans of a(s) and b(s) over s in [0, ns) into pa / pb
+// [0..ns] (pa[ns], pb[ns] = totals; pa may be null); returns the totals.
+template <class FA, class FB>
+__device__ int2 block_scan_slices(int ns, int* pa, int* pb, int2* wsum, FA fa, FB fb) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  int ra = 0, rb = 0;
+  for (int c0 = 0; c0 < ns; c0 += kRowThreads) {
+    const int s = c0 + tid;
+    const int xa = s < ns ? fa(s) : 0;
+    const int xb = s < ns ? fb(s) : 0;
+    const int ia = wave_incl_scan(xa, lane), ib = wave_incl_scan(xb, lane);
+    if (lane == kWave - 1) wsum[w] = int2{ia, ib};
+    __syncthreads();
+    int ba = ra, bb = rb, ta = 0, tb = 0;
+#pragma unroll
+    for (int q = 0; q < kRowWaves; ++q) {
+      const int2 v = wsum[q];
+      if (q < w) {
+        ba += v.x;
+        bb += v.y;
+      }
+      ta += v.x;
+      tb += v.y;
+    }
+    if (s < ns) {
+      if (pa) pa[s] = ba + ia - xa;
+      pb[s] = bb + ib - xb;
+    }
+    ra += ta;
+    rb += tb;
+    __syncthreads();
+  }
+  if (tid == 0) {
+    if (pa) pa[ns] = ra;
+    pb[ns] = rb;
+  }
+  __threadfence_block();
+  __syncthreads();
+  return int2{ra, rb};
+}
+
 template <int DT, int D>
-__global__ void __launch_bounds__(kSliceThreads) atopn_merge_kernel(FusedSelParams p, PVParams v) {
-  __shared__ float red[kSliceWaves];
-  __shared__ int wsum[kSliceWaves];
-  __shared__ int spre[kMergeMaxSlices + 1];
-  __shared__ int sidx[kSliceLen];
-  __shared__ float sval[kSliceLen];
-  __shared__ f32x4 accs[kSliceThreads];
-  constexpr int C = D / 4;              // 16-byte chunks per output row
-  constexpr int G = kSliceThreads / C;  // slice groups
-  const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+__global__ void __launch_bounds__(kRowThreads) atopn_gather_kernel(FusedSelParams p, PVParams v) {
+  __shared__ float red[kRowWaves];
+  __shared__ int2 wsum[kRowWaves];
+  __shared__ int spre[kRowMaxSlices + 1];
+  __shared__ int sgpre[kRowMaxSlices + 1];
+  __shared__ int sidx[kRowBatch];
+  __shared__ float sval[kRowBatch];
+  __shared__ f32x4 accs[kRowThreads];
+  constexpr int C = D / 4;             // 16-byte chunks of an output row
+  constexpr int G = kRowThreads / C;   // slice groups of the partial merge
+  const int r = blockIdx.x, tid = threadIdx.x;
   const int c = tid % C, g = tid / C;
   const int ns = p.nslice;
   const int64_t row0 = static_cast<int64_t>(r) * ns;
   const int bi = r / p.q_h, h = r - bi * p.q_h;
-  const int64_t ooff = bi * v.o_sb + static_cast<int64_t>(h) * v.o_sh;
   // the row's slice ranks: LDS, or the workspace for very long rows
-  int* pre = ns <= kMergeMaxSlices ? spre : p.sl_pre + static_cast<int64_t>(r) * (ns + 1);
+  const bool in_lds = ns <= kRowMaxSlices;
+  int* pre = in_lds ? spre : p.sl_pre + static_cast<int64_t>(r) * 2 * (ns + 1);
+  int* gpre = in_lds ? sgpre : pre + (ns + 1);
 
-  // 1. counts + the first batch of partials, then the block scan of the counts
-  float ms[kMergeSlices], lsv[kMergeSlices];
-  f32x4 ov[kMergeSlices];
-  auto load_batch = [&](int b0) {
-#pragma unroll
-    for (int u = 0; u < kMergeSlices; ++u) {
-      const int s = b0 + g + G * u;
-      ms[u] = s < ns ? p.sl_ml[2 * (row0 + s)] : kNegInf;
-      lsv[u] = s < ns ? p.sl_ml[2 * (row0 + s) + 1] : 0.f;
-      ov[u] = s < ns ? *reinterpret_cast<const f32x4*>(p.sl_o + (row0 + s) * D + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+  // 1. ranks of the slices (pre) and of the entries gathered here (gpre); the
+  //    first n = min(total, buf_k) passing positions count.  One pass when no
+  //    more than buf_k pass (every slice is then taken whole); a second one
+  //    re-ranks the gathers of an overflowing row.
+  auto cnt_of = [&](int s) { return p.sl_cnt[row0 + s]; };
+  auto whole_gather = [&](int s) {
+    const int cnt = p.sl_cnt[row0 + s];
+    return cnt > kSliceSmall ? cnt : 0;
   };
-  int run = 0;
-  for (int c0 = 0; c0 < ns; c0 += kSliceThreads) {
-    const int s = c0 + tid;
-    const int cnt = s < ns ? p.sl_cnt[row0 + s] : 0;
-    if (c0 == 0) load_batch(0);
-    const int incl = wave_incl_scan(cnt, lane);
-    if (lane == kWave - 1) wsum[w] = incl;
-    __syncthreads();
-    int before = run, tot = 0;
-#pragma unroll
-    for (int q = 0; q < kSliceWaves; ++q) {
-      before += q < w ? wsum[q] : 0;
-      tot += wsum[q];
-    }
-    if (s < ns) pre[s] = before + incl - cnt;
-    run += tot;
-    __syncthreads();
-  }
-  if (tid == 0) pre[ns] = run;
-  __threadfence_block();
-  __syncthreads();
-  const int total = run;
-  // included slices: pre[s + 1] <= cap; the straddling slice s_cut takes its
-  // first k_cut entries
-  int s_cut = ns, k_cut = 0;
-  if (total > p.cap) {
-    s_cut = slice_of(pre, ns, p.cap - 1);
-    k_cut = p.cap - pre[s_cut];
-    if (k_cut == pre[s_cut + 1] - pre[s_cut]) {  // the cut falls on a slice boundary
-      ++s_cut;
-      k_cut = 0;
-    }
-  }
+  const int2 tot = block_scan_slices(ns, pre, gpre, wsum, cnt_of, whole_gather);
+  const int total = tot.x;
+  const int n = min(total, p.cap);
   if (tid == 0) {
-    p.sel_cnt[r] = min(total, p.cap);
+    p.sel_cnt[r] = n;
     if (p.sel_total) p.sel_total[r] = total;
   }
+  // slice s contributes its first take(s) entries; a short slice contributing
+  // all of them has its partial from the slice wave, the rest are gathered here
+  auto take = [&](int s) { return max(0, min(n - pre[s], pre[s + 1] - pre[s])); };
+  auto has_partial = [&](int s) {
+    const int cnt = pre[s + 1] - pre[s];
+    return cnt > 0 && cnt <= kSliceSmall && take(s) == cnt;
+  };
+  int ng = tot.y;
+  if (total > p.cap) {
+    ng = block_scan_slices(ns, static_cast<int*>(nullptr), gpre, wsum, cnt_of,
+                           [&](int s) { return has_partial(s) ? 0 : take(s); }).y;
+  }
 
-  // 2. log-sum-exp merge of the included slices
+  // 2. log-sum-exp merge of the slice partials
   float M = kNegInf, lsum = 0.f;
   f32x4 on = {0.f, 0.f, 0.f, 0.f};
-  for (int b0 = 0; b0 < ns; b0 += G * kMergeSlices) {
-    if (b0 > 0) load_batch(b0);
+  for (int b0 = 0; b0 < ns; b0 += G * kRowMergeSlices) {
+    float ms[kRowMergeSlices], lsv[kRowMergeSlices];
+    f32x4 ov[kRowMergeSlices];
+#pragma unroll
+    for (int u = 0; u < kRowMergeSlices; ++u) {
+      const int s = b0 + g + G * u;
+      const bool use = s < ns && has_partial(s);
+      ms[u] = use ? p.sl_ml[2 * (row0 + s)] : kNegInf;
+      lsv[u] = use ? p.sl_ml[2 * (row0 + s) + 1] : 0.f;
+      ov[u] = use ? *reinterpret_cast<const f32x4*>(p.sl_o + (row0 + s) * D + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
     float mb = kNegInf;
 #pragma unroll
-    for (int u = 0; u < kMergeSlices; ++u)
-      if (b0 + g + G * u < s_cut) mb = fmaxf(mb, ms[u]);
-    const float Mn = fmaxf(M, block_max<kSliceWaves>(mb, red));
+    for (int u = 0; u < kRowMergeSlices; ++u) mb = fmaxf(mb, ms[u]);
+    const float Mn = fmaxf(M, block_max<kRowWaves>(mb, red));
     const float rescale = M == kNegInf ? 0.f : __expf(M - Mn);
     lsum *= rescale;
 #pragma unroll
     for (int i = 0; i < 4; ++i) on[i] *= rescale;
     M = Mn;
 #pragma unroll
-    for (int u = 0; u < kMergeSlices; ++u) {
-      if (b0 + g + G * u < s_cut && ms[u] != kNegInf) {
+    for (int u = 0; u < kRowMergeSlices; ++u) {
+      if (ms[u] != kNegInf) {
         const float wgt = __expf(ms[u] - M);
         lsum += lsv[u] * wgt;
 #pragma unroll
@@ -362,7 +356,7 @@ __global__ void __launch_bounds__(kSliceThreads) atopn_merge_kernel(FusedSelPara
     }
   }
   // l is the same in every thread of a slice group: one thread per group adds it
-  float L = block_sum<kSliceWaves>(c == 0 ? lsum : 0.f, red);
+  float L = block_sum<kRowWaves>(c == 0 ? lsum : 0.f, red);
   accs[tid] = on;
   __syncthreads();
   f32x4 o = {0.f, 0.f, 0.f, 0.f};
@@ -376,24 +370,31 @@ __global__ void __launch_bounds__(kSliceThreads) atopn_merge_kernel(FusedSelPara
     }
   }
 
-  // 3. the straddling slice's first k_cut entries (block-uniform branch)
-  if (k_cut > 0) {
-    const int64_t src = (row0 + s_cut) * p.slice_cap;
-    for (int i = tid; i < k_cut; i += kSliceThreads) {
-      sidx[i] = p.sl_idx[src + i];
-      sval[i] = p.sl_val[src + i];
-    }
-    __syncthreads();
+  // 3. the remaining entries (long slices, the slice cut at rank buf_k), batch
+  //    by batch through softmax . V (block-uniform branch)
+  if (ng > 0) {
     const int vh = h / (v.q_h / v.v_h);
     const char* vbase = v.v + (bi * v.v_sb + static_cast<int64_t>(vh) * v.v_sh) * Elt<DT>::kBytes;
-    BlockPV<DT, D, kSliceThreads> pv;
+    BlockPV<DT, D, kRowThreads, kRowUnroll> pv;
     pv.init();
-    pv.add(k_cut, sidx, sval, vbase, v.v_sl * Elt<DT>::kBytes, false, red);
+    for (int b0 = 0; b0 < ng; b0 += kRowBatch) {
+      const int nb = min(kRowBatch, ng - b0);
+      __syncthreads();  // the LDS list of the previous batch (or accs) is free
+      for (int i = tid; i < nb; i += kRowThreads) {
+        const int j = b0 + i;
+        const int s = slice_of(gpre, ns, j);
+        const int64_t src = (row0 + s) * p.slice_cap + (j - gpre[s]);
+        sidx[i] = p.sl_idx[src];
+        sval[i] = p.sl_val[src];
+      }
+      __syncthreads();
+      pv.add(nb, sidx, sval, vbase, v.v_sl * Elt<DT>::kBytes, false, red);
+    }
     float* accs_f = reinterpret_cast<float*>(accs);
     __syncthreads();
-    const float oc = pv.reduce(accs_f);  // thread i < D: dim i of the slice prefix
+    const float og = pv.reduce(accs_f);  // thread i < D: dim i
     __syncthreads();
-    if (tid < D) accs_f[tid] = oc;
+    if (tid < D) accs_f[tid] = og;
     __syncthreads();
     const float Mn = fmaxf(M, pv.m);
     const float a = M == kNegInf ? 0.f : __expf(M - Mn);
@@ -405,10 +406,11 @@ __global__ void __launch_bounds__(kSliceThreads) atopn_merge_kernel(FusedSelPara
     }
   }
   if (tid < C) {
+    const int64_t ooff = bi * v.o_sb + static_cast<int64_t>(h) * v.o_sh;
     // no passing position: softmax over an empty (all -inf) list is NaN
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      store_from_f32(v.out, v.out_dt, ooff + 4 * tid + i, total == 0 ? __builtin_nanf("") : o[i] / L);
+      store_from_f32(v.out, v.out_dt, ooff + 4 * tid + i, n == 0 ? __builtin_nanf("") : o[i] / L);
   }
 }
 
@@ -419,7 +421,7 @@ static hipError_t launch_split(const FusedSelParams& p, const PVParams& v, hipSt
   hipLaunchKernelGGL((atopn_slice_kernel<DT, D>), dim3(blocks), dim3(kSliceThreads), 0, st, p, v);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((atopn_merge_kernel<DT, D>), dim3(p.nrows), dim3(kSliceThreads), 0, st, p, v);
+  hipLaunchKernelGGL((atopn_gather_kernel<DT, D>), dim3(p.nrows), dim3(kRowThreads), 0, st, p, v);
   return hipGetLastError();
 }
 

@@ -2,9 +2,9 @@
 //
 // The selected positions and their logits (or probabilities) sit in LDS.
 // Lane c of group G owns dims [c*DPL, c*DPL + DPL) of the head dim and walks
-// entries G, G + NT/16, ...; eight V rows per group are in flight at a time
-// (raw 16-byte fragments), so a 1024-thread block keeps 512 rows (128 KiB of
-// bf16 V) of gathers outstanding.  Lists longer than one LDS batch are
+// entries G, G + NT/16, ...; UNROLL V rows per group are in flight at a time
+// (raw 16-byte fragments): a 1024-thread block with the default 8 keeps 512
+// rows (128 KiB of bf16 V) of gathers outstanding.  Lists longer than one LDS batch are
 // accumulated with a running max and rescaled sums (online softmax).
 #pragma once
 
@@ -17,7 +17,7 @@ constexpr int kBlkWaves = kBlkThreads / kWave;  // 16
 constexpr int kBlkGroups = kBlkThreads / 16;    // 64 lane groups
 constexpr int kPVUnroll = 8;
 
-template <int DT, int D, int NT = kBlkThreads>
+template <int DT, int D, int NT = kBlkThreads, int UNROLL = kPVUnroll>
 struct BlockPV {
   static constexpr int NW = NT / kWave;      // waves
   static constexpr int NG = NT / 16;         // lane groups
@@ -91,16 +91,16 @@ struct BlockPV {
 
     const int G = tid >> 4, c = tid & 15;
     const char* vb = vbase + static_cast<int64_t>(c) * BYTES;
-    for (int e0 = G; e0 < n; e0 += NG * kPVUnroll) {
-      u32x4 raw[kPVUnroll][NV];
+    for (int e0 = G; e0 < n; e0 += NG * UNROLL) {
+      u32x4 raw[UNROLL][NV];
 #pragma unroll
-      for (int u = 0; u < kPVUnroll; ++u) {
+      for (int u = 0; u < UNROLL; ++u) {
         const int e = e0 + u * NG;
         if (e < n) load_raw(vb + static_cast<int64_t>(sidx[e]) * vrow, raw[u]);
       }
       __builtin_amdgcn_sched_barrier(0);  // all gathers in flight before the FMAs
 #pragma unroll
-      for (int u = 0; u < kPVUnroll; ++u) {
+      for (int u = 0; u < UNROLL; ++u) {
         const int e = e0 + u * NG;
         if (e < n) {
           const float w = sval[e];

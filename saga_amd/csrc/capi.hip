@@ -195,7 +195,7 @@ void atopn_layout(int64_t b, int64_t q_h, int64_t k_h, int64_t L, int64_t d, int
   o->slice_idx = take(nr * o->nslice * o->slice_cap * 4);
   o->slice_val = take(nr * o->nslice * o->slice_cap * 4);
   o->slice_cnt = take(nr * o->nslice * 4);
-  o->slice_pre = take(nr * (o->nslice + 1) * 4);
+  o->slice_pre = take(nr * 2 * (o->nslice + 1) * 4);
   o->slice_o = take(nr * o->nslice * d * 4);
   o->slice_ml = take(nr * o->nslice * 2 * 4);
   o->total_bytes = off;

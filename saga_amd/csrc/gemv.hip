@@ -32,22 +32,30 @@ __global__ void __launch_bounds__(WAVES * 64) gemv_kernel(GemvParams p) {
   const char* wrow = static_cast<const char*>(p.w) + (static_cast<int64_t>(n0 + col) * p.w_ld + 8 * s) * 2;
   const char* xrow = static_cast<const char*>(p.x) + (static_cast<int64_t>(mvalid ? col : 0) * p.x_ld + 8 * s) * 2;
   const int steps = p.K / 32;
+  // this workgroup's k steps [k0, k1): split-K workgroups deal them to their
+  // waves round robin (wave w: k0 + w, k0 + w + WAVES, ...), so the waves
+  // sweep each long W row together; otherwise each wave takes a contiguous
+  // quarter
   const int k0 = split * steps / p.splits, k1 = (split + 1) * steps / p.splits;
-  const int j0 = k0 + w * (k1 - k0) / WAVES, j1 = k0 + (w + 1) * (k1 - k0) / WAVES;
+  const bool rr = p.part != nullptr;
+  const int j0 = rr ? 0 : w * (k1 - k0) / WAVES;
+  const int nmine = rr ? (k1 - k0 - w + WAVES - 1) / WAVES : (w + 1) * (k1 - k0) / WAVES - j0;
+  const int jstride = rr ? WAVES : 1;
+  const int jbase = k0 + (rr ? w : j0);
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   float ssq = 0.f;
-  for (int j = j0; j < j1; j += kGemvUnroll) {
+  for (int i0 = 0; i0 < nmine; i0 += kGemvUnroll) {
     u32x4 a[kGemvUnroll], b[kGemvUnroll];
 #pragma unroll
     for (int u = 0; u < kGemvUnroll; ++u) {
-      const int jj = min(j + u, j1 - 1);
+      const int jj = jbase + jstride * min(i0 + u, nmine - 1);
       a[u] = ld16(wrow + static_cast<int64_t>(jj) * 64);
       b[u] = mvalid ? ld16(xrow + static_cast<int64_t>(jj) * 64) : u32x4{0u, 0u, 0u, 0u};
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < kGemvUnroll; ++u) {
-      if (j + u < j1) {
+      if (i0 + u < nmine) {
         acc = mfma_16b<SAGA_DTYPE_BF16>(a[u], b[u], acc);
         if (p.rms) {
           float f[8];

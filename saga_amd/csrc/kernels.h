@@ -94,13 +94,14 @@ struct FusedSelParams {
   int32_t* sl_idx;            // [row][slice][slice_cap]
   float* sl_val;
   int32_t* sl_cnt;  // [row][slice] passing count in the slice
-  float* sl_o;      // [row][slice][d] unnormalised sum_e w_e V[e]
-  float* sl_ml;     // [row][slice][2] (max logit, sum of weights)
-  int32_t* sl_pre;  // [row][nslice + 1] exclusive prefix of sl_cnt (overflow merge scratch)
+  float* sl_o;      // [row][slice][d] unnormalised sum_e w_e V[e] of short slices
+  float* sl_ml;     // [row][slice][2] (max logit, sum of weights) of short slices
+  int32_t* sl_pre;  // [row][2][nslice + 1] slice ranks (rows of > 2048 slices)
 };
-// calibrate: one block per row; fast step: slice kernel + merge kernel
+// calibrate: one block per row; fast step: slice kernel + per-row gather kernel
 hipError_t launch_atopn_select_pv(bool calibrate, const FusedSelParams& p, const PVParams& v, hipStream_t st);
 constexpr int kSliceLen = 1024;  // score positions per slice wave of the fast step
+constexpr int kSliceSmall = 64;  // slice lists this short are gathered by their slice wave
 hipError_t launch_atopn_fast(const FusedSelParams& p, const PVParams& v, hipStream_t st);
 
 // API selection (threshold_topk_fast): typed rows, typed values out.

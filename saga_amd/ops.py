@@ -227,14 +227,18 @@ def dense_decode(query, key, value, attention_mask=None, scaling=None, kv_len=No
     return out
 
 
-def atopn_workspace_views(b: int, q_h: int, k_h: int, L: int, d: int, buf_k: int, device, fast: bool = False) -> dict:
+def atopn_workspace_views(b: int, q_h: int, k_h: int, L: int, d: int, buf_k: int, device, fast: bool = True) -> dict:
     """The cached fused-decode workspace after a call, for inspection (valid
-    until the next call): thresholds, counts, the selected list and the scores.
-    The calibration step writes its list to sel_idx / sel_val; the fast step
-    (fast=True) leaves it in per-slice lists, concatenated here in slice order
-    (ascending positions) and cut at buf_k."""
+    until the next call): logit thresholds (fast step), kept / passing counts,
+    the selected positions and logits in ascending order, and the scores.
+    The calibration step (fast=False) writes its list to sel_idx / sel_val;
+    the fast step keeps it in per-slice lists, concatenated here in slice
+    order and cut at buf_k (host copies)."""
     lay = _lib.atopn_layout(b, q_h, k_h, L, d, buf_k)
-    ws = _WORKSPACES[(torch.device(device), "atopn")]
+    dev = torch.device(device)
+    if dev.type == "cuda" and dev.index is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    ws = _WORKSPACES[(dev, "atopn")]
     nr = b * q_h
 
     def view(off, n, dt):
@@ -257,10 +261,9 @@ def atopn_workspace_views(b: int, q_h: int, k_h: int, L: int, d: int, buf_k: int
         idx = torch.full((nr, buf_k), -1, dtype=torch.int32)
         val = torch.full((nr, buf_k), float("nan"))
         for r in range(nr):
-            parts = [(sidx[r, s, :min(int(cnt[r, s]), cap)], sval[r, s, :min(int(cnt[r, s]), cap)])
-                     for s in range(ns)]
-            ri = torch.cat([a for a, _ in parts])[:buf_k]
-            rv = torch.cat([v for _, v in parts])[:buf_k]
+            keep = [min(int(cnt[r, s]), cap) for s in range(ns)]
+            ri = torch.cat([sidx[r, s, :keep[s]] for s in range(ns)])[:buf_k]
+            rv = torch.cat([sval[r, s, :keep[s]] for s in range(ns)])[:buf_k]
             idx[r, :ri.numel()] = ri
             val[r, :rv.numel()] = rv
         out["sel_idx"], out["sel_val"] = idx, val

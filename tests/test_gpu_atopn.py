@@ -208,16 +208,17 @@ def test_fast_step_is_deterministic():
     (_, _, _), (qd, kd, vd) = qkv(rng, 4, 12, 1, 2, 128, 20000, "bf16")
     table = torch.full((48,), 1e-4, device="cuda")
     a = ops.atopn_decode(qd, kd, vd, table, 256)
-    idx_a = ops.atopn_workspace_views(4, 12, 1, 20000, 128, 512, "cuda:0", fast=True)["sel_idx"].clone()
+    idx_a = ops.atopn_workspace_views(4, 12, 1, 20000, 128, 512, "cuda:0")["sel_idx"].clone()
     bb = ops.atopn_decode(qd, kd, vd, table, 256)
-    idx_b = ops.atopn_workspace_views(4, 12, 1, 20000, 128, 512, "cuda:0", fast=True)["sel_idx"].clone()
+    idx_b = ops.atopn_workspace_views(4, 12, 1, 20000, 128, 512, "cuda:0")["sel_idx"].clone()
     assert torch.equal(a, bb) and torch.equal(idx_a, idx_b)
 
 
-def test_reference_api_module_end_to_end():
+def test_reference_api_module_end_to_end(monkeypatch):
     """The mirror of attention/attention.py: table init, calibration step,
     fast step, exempt-layer global, reset."""
     import attention.attention as A
+    monkeypatch.setattr(A, "EXEMPT_LAYERS", A.EXEMPT_LAYERS)  # restored after the test
     rng = np.random.default_rng(23)
     b, q_h, k_h, v_h, d, L, N = 2, 12, 1, 2, 128, 5000, 128
     (q, k, v), (qd, kd, vd) = qkv(rng, b, q_h, k_h, v_h, d, L, "bf16")

@@ -39,8 +39,10 @@ def _greedy(model, ids, steps):
 
 
 @pytest.fixture
-def restore_sdpa():
+def restore_sdpa(monkeypatch):
     from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+    from saga_amd.attention import attention as A
+    monkeypatch.setattr(A, "EXEMPT_LAYERS", set())
     orig = ALL_ATTENTION_FUNCTIONS["sdpa"]
     yield orig
     ALL_ATTENTION_FUNCTIONS["sdpa"] = orig
