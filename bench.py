@@ -244,6 +244,8 @@ def main():
     ap.add_argument("--sweep", action="store_true",
                     help="attention kernels alone over a grid of shapes (lengths, batches, head groupings, N) "
                          "and the 128k dense-GQA vs SAGA comparison; one JSON line per shape")
+    ap.add_argument("--no-fused", action="store_true",
+                    help="run the Atop-N fast step as three kernels (scores, slice, row) for every shape")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="only launch K1 (qk_scores) at the workload shape and a 1 GiB device copy, "
                          "for hardware-counter runs")
@@ -258,6 +260,9 @@ def main():
 
     from saga_amd import ops
     from saga_amd.decoder import QWEN25_15B_GQA, QWEN25_15B_SAGA, SagaDecoder
+
+    if args.no_fused:
+        ops.set_fused_fast_step(False)
 
     B, ctx, K, W = args.batch, args.ctx, args.steps, args.warmup
     if args.profile_kernels:

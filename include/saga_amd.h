@@ -33,7 +33,10 @@
  *     the last error on the calling thread is in saga_last_error().  Nothing
  *     aborts and no C++ exception crosses this boundary.
  *   - Workspaces are caller-allocated device buffers of the size the
- *     matching *_workspace_bytes() returns; no initial contents are needed.
+ *     matching *_workspace_bytes() returns.  No initial contents are needed,
+ *     except that an Atop-N workspace must be zero-filled once when it is
+ *     allocated (its first saga_atopn_layout.sync_bytes bytes hold the fused
+ *     fast step's barrier state, which every call leaves consistent).
  *     Calls that share a workspace must be ordered (same stream).
  */
 #ifndef SAGA_AMD_H
@@ -72,7 +75,11 @@ typedef void* saga_stream_t;
 
 /* Byte offsets of the fused decode workspace (for tests and inspection). */
 typedef struct saga_atopn_layout {
-  int64_t scores;    /* f32 [b*q_h, scores_ld] */
+  int64_t sync;       /* barrier state of the fused fast step, always at offset 0: must be
+                         zero before the first saga_atopn_decode on a workspace; every
+                         call leaves it consistent for the next (any shape) */
+  int64_t sync_bytes;
+  int64_t scores;    /* f32 [b*q_h, scores_ld] (not written by the fused fast step) */
   int64_t scores_ld; /* elements */
   int64_t part_max;  /* f32 [b*q_h, nparts] */
   int64_t part_sum;  /* f32 [b*q_h, nparts] */
@@ -84,9 +91,13 @@ typedef struct saga_atopn_layout {
   int64_t sel_val;   /* f32 [b*q_h, buf_k] their logits */
   int64_t sel_cnt;   /* i32 [b*q_h] kept (<= buf_k) */
   int64_t sel_total; /* i32 [b*q_h] passing before the cap */
-  /* fast step: rows cut into nslice slices of 1024 positions */
+  /* fast step: each row's passing positions in nslice ordered lists ("slices"):
+     fused = 1: one per block of the fused kernel (nslice = nparts), capacity
+     min(block positions, buf_k); fused = 0: one per 1024 positions,
+     capacity min(1024, buf_k) */
+  int64_t fused;     /* the fast step of this shape runs fused on the current device */
   int64_t nslice;
-  int64_t slice_cap; /* min(1024, buf_k) */
+  int64_t slice_cap;
   int64_t slice_idx; /* i32 [b*q_h, nslice, slice_cap] passing positions per slice */
   int64_t slice_val; /* f32 [b*q_h, nslice, slice_cap] their logits */
   int64_t slice_cnt; /* i32 [b*q_h, nslice] passing per slice */
@@ -156,6 +167,16 @@ int saga_sparse_softmax_pv(const saga_tensor* weights, const saga_tensor* indice
 size_t saga_atopn_workspace_bytes(int64_t b, int64_t q_h, int64_t k_h, int64_t L, int64_t d, int64_t buf_k);
 int saga_atopn_workspace_layout(int64_t b, int64_t q_h, int64_t k_h, int64_t L, int64_t d, int64_t buf_k,
                                 saga_atopn_layout* layout);
+
+/* Process-wide switch of the fused fast step (default 0).  With 1,
+ * saga_atopn_decode runs scores, threshold, compaction and the short lists'
+ * softmax . V in one kernel (a flag barrier per (batch, key head) across its
+ * co-resident blocks), then the row kernel, for shapes whose grid fits the
+ * GPU at once; with 0 (and for other shapes) it runs the three-kernel path
+ * (scores, slice kernel, row kernel).  Results agree to fp32 rounding.  No
+ * counterpart in the reference: an A/B alternative, measured slower on
+ * MI355X.  Returns the previous setting. */
+int saga_set_fused_fast_step(int enable);
 
 /* Atop-N fast decode step: scores, logit threshold from the stored
  * softmax-space thresholds, ordered compaction capped at

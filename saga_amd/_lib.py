@@ -41,9 +41,9 @@ class SagaTensor(ctypes.Structure):
 
 class AtopnLayout(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int64) for n in (
-        "scores", "scores_ld", "part_max", "part_sum", "part_tail", "nparts", "thresh", "sel_idx", "sel_val",
-        "sel_cnt", "sel_total", "nslice", "slice_cap", "slice_idx", "slice_val", "slice_cnt", "slice_pre",
-        "slice_o", "slice_ml", "total_bytes")]
+        "sync", "sync_bytes", "scores", "scores_ld", "part_max", "part_sum", "part_tail", "nparts", "thresh",
+        "sel_idx", "sel_val", "sel_cnt", "sel_total", "fused", "nslice", "slice_cap", "slice_idx", "slice_val",
+        "slice_cnt", "slice_pre", "slice_o", "slice_ml", "total_bytes")]
 
 
 # Every symbol include/saga_amd.h declares, with its ctypes signature.
@@ -58,6 +58,7 @@ _SIGS = {
     "saga_threshold_select": (ctypes.c_int, [_T, _P, _I64, _I64, _T, _P, _P, _P]),
     "saga_sparse_softmax_pv": (ctypes.c_int, [_T, _T, _T, ctypes.c_int32, _T, _P]),
     "saga_qk_nparts": (ctypes.c_int64, [_I64, _I64, _I64]),
+    "saga_set_fused_fast_step": (ctypes.c_int, [ctypes.c_int]),
     "saga_atopn_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "saga_atopn_workspace_layout": (ctypes.c_int, [_I64, _I64, _I64, _I64, _I64, _I64,
                                                    ctypes.POINTER(AtopnLayout)]),

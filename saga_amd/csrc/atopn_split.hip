@@ -293,6 +293,23 @@ __global__ void __launch_bounds__(kRowThreads) atopn_gather_kernel(FusedSelParam
   int* pre = in_lds ? spre : p.sl_pre + static_cast<int64_t>(r) * 2 * (ns + 1);
   int* gpre = in_lds ? sgpre : pre + (ns + 1);
 
+  // 0. the first merge batch's slice partials, loaded before the counts
+  //    (whether a slice's partial counts is known only after the scan; the
+  //    loads of unused ones are discarded): counts and partials arrive in one
+  //    round trip instead of two (16-bit V only: the f32 kernel has no
+  //    registers to spare at 1024 threads)
+  constexpr bool kPrefetch = DT != SAGA_DTYPE_F32;
+  float ms0[kRowMergeSlices], ls0[kRowMergeSlices];
+  f32x4 ov0[kRowMergeSlices];
+#pragma unroll
+  for (int u = 0; u < kRowMergeSlices; ++u) {
+    const int s = g + G * u;
+    const bool in = kPrefetch && s < ns;
+    ms0[u] = in ? p.sl_ml[2 * (row0 + s)] : kNegInf;
+    ls0[u] = in ? p.sl_ml[2 * (row0 + s) + 1] : 0.f;
+    ov0[u] = in ? *reinterpret_cast<const f32x4*>(p.sl_o + (row0 + s) * D + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
   // 1. ranks of the slices (pre) and of the entries gathered here (gpre); the
   //    first n = min(total, buf_k) passing positions count.  One pass when no
   //    more than buf_k pass (every slice is then taken whole); a second one
@@ -332,9 +349,15 @@ __global__ void __launch_bounds__(kRowThreads) atopn_gather_kernel(FusedSelParam
     for (int u = 0; u < kRowMergeSlices; ++u) {
       const int s = b0 + g + G * u;
       const bool use = s < ns && has_partial(s);
-      ms[u] = use ? p.sl_ml[2 * (row0 + s)] : kNegInf;
-      lsv[u] = use ? p.sl_ml[2 * (row0 + s) + 1] : 0.f;
-      ov[u] = use ? *reinterpret_cast<const f32x4*>(p.sl_o + (row0 + s) * D + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
+      if (kPrefetch && b0 == 0) {  // prefetched
+        ms[u] = use ? ms0[u] : kNegInf;
+        lsv[u] = use ? ls0[u] : 0.f;
+        ov[u] = use ? ov0[u] : f32x4{0.f, 0.f, 0.f, 0.f};
+      } else {
+        ms[u] = use ? p.sl_ml[2 * (row0 + s)] : kNegInf;
+        lsv[u] = use ? p.sl_ml[2 * (row0 + s) + 1] : 0.f;
+        ov[u] = use ? *reinterpret_cast<const f32x4*>(p.sl_o + (row0 + s) * D + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
     }
     float mb = kNegInf;
 #pragma unroll
@@ -428,6 +451,21 @@ static hipError_t launch_split(const FusedSelParams& p, const PVParams& v, hipSt
 template <int DT>
 static hipError_t launch_split_d(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
   return v.d == 128 ? launch_split<DT, 128>(p, v, st) : launch_split<DT, 64>(p, v, st);
+}
+
+template <int DT>
+static hipError_t launch_rows_d(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
+  if (v.d == 128)
+    hipLaunchKernelGGL((atopn_gather_kernel<DT, 128>), dim3(p.nrows), dim3(kRowThreads), 0, st, p, v);
+  else
+    hipLaunchKernelGGL((atopn_gather_kernel<DT, 64>), dim3(p.nrows), dim3(kRowThreads), 0, st, p, v);
+  return hipGetLastError();
+}
+
+hipError_t launch_atopn_rows(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
+  if (v.v_dt == SAGA_DTYPE_BF16) return launch_rows_d<SAGA_DTYPE_BF16>(p, v, st);
+  if (v.v_dt == SAGA_DTYPE_F16) return launch_rows_d<SAGA_DTYPE_F16>(p, v, st);
+  return launch_rows_d<SAGA_DTYPE_F32>(p, v, st);
 }
 
 hipError_t launch_atopn_fast(const FusedSelParams& p, const PVParams& v, hipStream_t st) {

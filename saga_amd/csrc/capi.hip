@@ -179,6 +179,10 @@ void atopn_layout(int64_t b, int64_t q_h, int64_t k_h, int64_t L, int64_t d, int
     off = align256(off + bytes);
     return at;
   };
+  // the fused fast step's barrier state: first, at a fixed offset, so that
+  // calls of every shape sharing the workspace find it in place
+  o->sync = take(kFusedSyncBytes);
+  o->sync_bytes = kFusedSyncBytes;
   o->scores_ld = ld;
   o->nparts = nparts;
   o->scores = take(nr * ld * 4);
@@ -190,14 +194,23 @@ void atopn_layout(int64_t b, int64_t q_h, int64_t k_h, int64_t L, int64_t d, int
   o->sel_val = take(nr * buf_k * 4);
   o->sel_cnt = take(nr * 4);
   o->sel_total = take(nr * 4);
-  o->nslice = (L + kSliceLen - 1) / kSliceLen;
-  o->slice_cap = std::min<int64_t>(kSliceLen, buf_k);
-  o->slice_idx = take(nr * o->nslice * o->slice_cap * 4);
-  o->slice_val = take(nr * o->nslice * o->slice_cap * 4);
-  o->slice_cnt = take(nr * o->nslice * 4);
-  o->slice_pre = take(nr * 2 * (o->nslice + 1) * 4);
-  o->slice_o = take(nr * o->nslice * d * 4);
-  o->slice_ml = take(nr * o->nslice * 2 * 4);
+  // fast-step lists: per 1024-position slice (split path) or per fused block;
+  // the regions hold either
+  const int64_t ns_split = (L + kSliceLen - 1) / kSliceLen;
+  const int64_t cap_split = std::min<int64_t>(kSliceLen, buf_k);
+  const int64_t ns_fused = nparts;
+  const int64_t cap_fused = atopn_fused_slice_cap(b, k_h, L, buf_k);
+  const int64_t ns_max = std::max(ns_split, ns_fused);
+  const int64_t ent_max = std::max(ns_split * cap_split, ns_fused * cap_fused);
+  o->fused = k_h > 0 && q_h % k_h == 0 && atopn_fused_fits(b, k_h, q_h / k_h, L) ? 1 : 0;
+  o->nslice = o->fused ? ns_fused : ns_split;
+  o->slice_cap = o->fused ? cap_fused : cap_split;
+  o->slice_idx = take(nr * ent_max * 4);
+  o->slice_val = take(nr * ent_max * 4);
+  o->slice_cnt = take(nr * ns_max * 4);
+  o->slice_pre = take(nr * 2 * (ns_max + 1) * 4);
+  o->slice_o = take(nr * ns_max * d * 4);
+  o->slice_ml = take(nr * ns_max * 2 * 4);
   o->total_bytes = off;
 }
 
@@ -240,15 +253,18 @@ int atopn_run(bool calibrate, const saga_tensor* query, const saga_tensor* key, 
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t nr = s.b * s.q_h;
 
+  const bool fused = !calibrate && lay.fused;
   QKParams qp = make_qk(query, key, mask, kv_len, scale, s);
-  qp.scores = reinterpret_cast<float*>(ws + lay.scores);
-  qp.s_sb = s.q_h * lay.scores_ld;
-  qp.s_sh = lay.scores_ld;
-  qp.vec_store = 1;
   qp.pmax = reinterpret_cast<float*>(ws + lay.part_max);
   qp.psum = reinterpret_cast<float*>(ws + lay.part_sum);
   qp.ptail = reinterpret_cast<float*>(ws + lay.part_tail);
-  if ((rc = hip_status(launch_qk_scores(s.dt, static_cast<int>(s.d), qp, st), "qk_scores launch"))) return rc;
+  if (!fused) {
+    qp.scores = reinterpret_cast<float*>(ws + lay.scores);
+    qp.s_sb = s.q_h * lay.scores_ld;
+    qp.s_sh = lay.scores_ld;
+    qp.vec_store = 1;
+    if ((rc = hip_status(launch_qk_scores(s.dt, static_cast<int>(s.d), qp, st), "qk_scores launch"))) return rc;
+  }
 
   FusedSelParams sp{};
   sp.scores = qp.scores;
@@ -280,6 +296,20 @@ int atopn_run(bool calibrate, const saga_tensor* query, const saga_tensor* key, 
   if (nr * lay.nslice >= (1LL << 31)) return fail(SAGA_ERR_UNSUPPORTED, "too many score rows x slices");
   // calibration: softmax over the top-k logits == renormalised top-k probabilities
   const PVParams pp = make_pv(value, out, s);
+  if (fused) {
+    FusedSync sy{};
+    int32_t* sync = reinterpret_cast<int32_t*>(ws + lay.sync);
+    sy.epoch = sync;
+    sy.flags = sync + kFusedMaxUnits;
+    // the last 256 bytes of the region hold the error word
+    static_assert(static_cast<int64_t>(kFusedMaxUnits) * (kFusedMaxBlocks + 1) * 4 == kFusedSyncBytes - 256,
+                  "sync region: epochs, flags, then one 256-byte line for the error word");
+    sy.error = sync + static_cast<int64_t>(kFusedMaxUnits) * (kFusedMaxBlocks + 1);
+    sy.xcd_map = (s.b * s.k_h) % 8 == 0 ? 1 : 0;
+    if ((rc = hip_status(launch_atopn_fused(s.dt, static_cast<int>(s.d), qp, sp, pp, sy, st), "atopn fused launch")))
+      return rc;
+    return ok();
+  }
   if ((rc = hip_status(launch_atopn_select_pv(calibrate, sp, pp, st), "atopn select/pv launch"))) return rc;
   return ok();
 }
@@ -444,6 +474,8 @@ int saga_sparse_softmax_pv(const saga_tensor* weights, const saga_tensor* indice
   if ((rc = hip_status(launch_sparse_pv(p, static_cast<hipStream_t>(stream)), "sparse_pv launch"))) return rc;
   return ok();
 }
+
+int saga_set_fused_fast_step(int enable) { return set_fused_enabled(enable); }
 
 int64_t saga_qk_nparts(int64_t b, int64_t k_h, int64_t L) {
   if (b < 1 || k_h < 1 || L < 1) return 0;

@@ -183,6 +183,17 @@ __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
   return v;
 }
 
+// Block barrier that publishes LDS only: it waits for the wave's LDS
+// operations, not for its outstanding global stores (__syncthreads' release
+// fence waits for those, one memory round trip).  Global loads after it may
+// still be reordered above it: use __syncthreads where they depend on the
+// barrier.
+__device__ __forceinline__ void lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Merge two (max, sum of exp(x - max)) pairs.  Empty sets are (-inf, 0).
 __device__ __forceinline__ void lse_merge(float& m, float& s, float m2, float s2) {
   const float M = fmaxf(m, m2);

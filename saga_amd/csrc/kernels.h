@@ -103,6 +103,29 @@ hipError_t launch_atopn_select_pv(bool calibrate, const FusedSelParams& p, const
 constexpr int kSliceLen = 1024;  // score positions per slice wave of the fast step
 constexpr int kSliceSmall = 64;  // slice lists this short are gathered by their slice wave
 hipError_t launch_atopn_fast(const FusedSelParams& p, const PVParams& v, hipStream_t st);
+// The per-row kernel of the fast step alone (ranks, cut at buf_k, merge, long gathers).
+hipError_t launch_atopn_rows(const FusedSelParams& p, const PVParams& v, hipStream_t st);
+
+// Fused fast step: sync region of the workspace (zero before the first call on
+// it; every call leaves it consistent).  Unit u = batch * k_h + key head.
+struct FusedSync {
+  int32_t* epoch;   // [kFusedMaxUnits] calls completed per unit
+  int32_t* flags;   // [kFusedMaxUnits][kFusedMaxBlocks] arrival flags
+  int32_t* error;   // set when a barrier wait gave up (the call's output is invalid)
+  int32_t xcd_map;  // units % 8 == 0: unit u runs on block ids == u (mod 8)
+};
+constexpr int kFusedMaxUnits = 1024;
+constexpr int kFusedMaxBlocks = 128;    // 4-wave blocks per unit
+constexpr int kFusedBlocksPerCU = 3;    // resident blocks per CU the fused plan counts on
+constexpr int64_t kFusedSyncBytes = (static_cast<int64_t>(kFusedMaxUnits) * (kFusedMaxBlocks + 1) + 64) * 4;
+int fused_device_cus();  // CUs of the current device (cached)
+int set_fused_enabled(int enable);  // process-wide, off by default; returns the previous setting
+// Whether the fused fast step runs for this shape on the current device:
+// g = q_h / k_h <= 16 and the planned grid resident at once.
+bool atopn_fused_fits(int64_t b, int64_t k_h, int64_t g, int64_t L);
+int64_t atopn_fused_slice_cap(int64_t b, int64_t k_h, int64_t L, int64_t buf_k);  // list capacity per block
+hipError_t launch_atopn_fused(int dtype, int d, const QKParams& q, const FusedSelParams& p, const PVParams& v,
+                              const FusedSync& sy, hipStream_t st);
 
 // API selection (threshold_topk_fast): typed rows, typed values out.
 struct ApiSelParams {

@@ -19,25 +19,13 @@
 // GPU in whole rounds: no round runs a handful of leftover waves.
 #include <algorithm>
 
-#include "common.cuh"
-#include "kernels.h"
+#include "qk_wave.cuh"
 
 namespace saga {
 
 template <int DT, int D>
-struct QKShape {
-  static constexpr int E16 = Elt<DT>::kPer16B;  // elements per 16-byte fragment
-  static constexpr int NLOAD = D / (4 * E16);   // fragments per K row per lane
-  // tiles per load burst: at most 24 fragments (96 VGPRs) in flight per lane
-  static constexpr int BURST = (24 / NLOAD) < kQKMaxTiles ? (24 / NLOAD) : kQKMaxTiles;
-};
-
-template <int DT, int D>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8)))
 qk_scores_kernel(QKParams p) {
-  using E = Elt<DT>;
-  using S = QKShape<DT, D>;
-  constexpr int E16 = S::E16, NLOAD = S::NLOAD, BURST = S::BURST;
   const int lane = threadIdx.x & 63;
   const int col = lane & 15;                // MFMA row (position) / column (head)
   const int s = lane >> 4;                  // k-slot group
@@ -47,77 +35,17 @@ qk_scores_kernel(QKParams p) {
   const int64_t item = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + wave;
   const int part = static_cast<int>(item % p.nparts);
   const int unit = static_cast<int>(item / p.nparts);
-  const int bi = unit / p.k_h;
-  const int kh = unit - bi * p.k_h;
-  const bool hvalid = col < p.g;
-  const int h = kh * p.g + (hvalid ? col : 0);
-  // this wave's tiles [t0, t0 + nt), nt <= kQKMaxTiles
-  const int t0 = static_cast<int>(static_cast<int64_t>(part) * p.ntiles / p.nparts);
-  const int nt = static_cast<int>(static_cast<int64_t>(part + 1) * p.ntiles / p.nparts) - t0;
-
-  // B fragment: query head (kh*g + col), dims [j*4*E16 + s*E16, +E16).
-  u32x4 qf[NLOAD];
-  const char* qrow = p.q + (bi * p.q_sb + static_cast<int64_t>(h) * p.q_sh) * E::kBytes;
-#pragma unroll
-  for (int j = 0; j < NLOAD; ++j) {
-    qf[j] = hvalid ? ld16(qrow + (j * 4 * E16 + s * E16) * E::kBytes) : u32x4{0u, 0u, 0u, 0u};
-  }
-
-  const char* kbase = p.k + (bi * p.k_sb + static_cast<int64_t>(kh) * p.k_sh) * E::kBytes;
+  const QKWaveSpan w = qk_wave_span(p, unit, part, col);
   float x[kQKMaxTiles][4];
-#pragma unroll
-  for (int tb = 0; tb < kQKMaxTiles; tb += BURST) {
-    if (tb >= nt) break;
-    u32x4 kf[BURST][NLOAD];
-#pragma unroll
-    for (int t = 0; t < BURST; ++t) {
-      // A fragment: key row (16*(t0+tb+t) + col), rows past L clamped (their
-      // scores are discarded below); tiles past the range are not loaded
-      const int pos = min(16 * (t0 + tb + t) + col, p.L - 1);
-      const char* krow = kbase + static_cast<int64_t>(pos) * p.k_sl * E::kBytes;
-#pragma unroll
-      for (int j = 0; j < NLOAD; ++j)
-        kf[t][j] = tb + t < nt ? ld16(krow + (j * 4 * E16 + s * E16) * E::kBytes) : u32x4{0u, 0u, 0u, 0u};
-    }
-    // keep the whole burst in flight: no MFMA may be hoisted between the loads
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int t = 0; t < BURST; ++t) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int j = 0; j < NLOAD; ++j) acc = mfma_16b<DT>(kf[t][j], qf[j], acc);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) x[tb + t][r] = acc[r];
-    }
-  }
+  int Leff;
+  const float m = qk_wave_scores<DT, D>(p, w, s, col, x, Leff);
 
-  int Leff = p.L;
-  if (p.kv_len) Leff = min(Leff, max(p.kv_len[bi], 0));
-  // Lane holds head `col`, positions 16*(t0+t) + 4*s + r.
-  float m = kNegInf;
-#pragma unroll
-  for (int t = 0; t < kQKMaxTiles; ++t) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int pos = 16 * (t0 + t) + 4 * s + r;
-      float v = x[t][r] * p.scale;
-      if (p.mask) {
-        const int mp = min(pos, p.L - 1);
-        v = v + load_as_f32(p.mask, p.mask_dt, bi * p.m_sb + static_cast<int64_t>(h) * p.m_sh +
-                                                   static_cast<int64_t>(mp) * p.m_sl);
-      }
-      if (pos >= Leff || t >= nt) v = kNegInf;
-      x[t][r] = v;
-      m = fmaxf(m, v);
-    }
-  }
-
-  if (p.scores && hvalid) {
-    float* srow = p.scores + bi * p.s_sb + static_cast<int64_t>(h) * p.s_sh;
+  if (p.scores && w.hvalid) {
+    float* srow = p.scores + w.bi * p.s_sb + static_cast<int64_t>(w.h) * p.s_sh;
 #pragma unroll
     for (int t = 0; t < kQKMaxTiles; ++t) {
-      if (t >= nt) break;
-      const int pos0 = 16 * (t0 + t) + 4 * s;
+      if (t >= w.nt) break;
+      const int pos0 = 16 * (w.t0 + t) + 4 * s;
       if (p.vec_store && pos0 + 3 < p.L) {
         *reinterpret_cast<f32x4*>(srow + pos0) = f32x4{x[t][0], x[t][1], x[t][2], x[t][3]};
       } else {
@@ -129,46 +57,15 @@ qk_scores_kernel(QKParams p) {
   }
 
   if (p.pmax) {
-    float sum = 0.f;
-    if (m != kNegInf) {
-#pragma unroll
-      for (int t = 0; t < kQKMaxTiles; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sum += __expf(x[t][r] - m);
-    }
-    // the four lane groups holding the same head
-    lse_merge(m, sum, __shfl_xor(m, 16), __shfl_xor(sum, 16));
-    lse_merge(m, sum, __shfl_xor(m, 32), __shfl_xor(sum, 32));
-    // max over the tail window [Leff - min(256, Leff), Leff) (x is -inf past Leff)
-    float tm = kNegInf;
-    if (p.ptail) {
-      const int tail_lo = Leff - min(256, Leff);
-#pragma unroll
-      for (int t = 0; t < kQKMaxTiles; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (16 * (t0 + t) + 4 * s + r >= tail_lo) tm = fmaxf(tm, x[t][r]);
-      tm = fmaxf(tm, __shfl_xor(tm, 16));
-      tm = fmaxf(tm, __shfl_xor(tm, 32));
-    }
     // the block's 4 parts merged into one partial per head
-    if (s == 0) {
-      red[0][wave][col] = m;
-      red[1][wave][col] = sum;
-      red[2][wave][col] = tm;
-    }
-    __syncthreads();
-    if (wave == 0 && s == 0 && hvalid) {
-#pragma unroll
-      for (int q = 1; q < 4; ++q) {
-        lse_merge(m, sum, red[0][q][col], red[1][q][col]);
-        tm = fmaxf(tm, red[2][q][col]);
-      }
-      const int row = bi * p.q_h + h;
+    float pm, ps, pt;
+    qk_block_partial(x, m, w, Leff, p.ptail != nullptr, s, col, wave, red, pm, ps, pt);
+    if (wave == 0 && s == 0 && w.hvalid) {
+      const int row = w.bi * p.q_h + w.h;
       const int64_t o = static_cast<int64_t>(row) * (p.nparts / 4) + part / 4;
-      p.pmax[o] = m;
-      p.psum[o] = sum;
-      if (p.ptail) p.ptail[o] = tm;
+      p.pmax[o] = pm;
+      p.psum[o] = ps;
+      if (p.ptail) p.ptail[o] = pt;
     }
   }
 }

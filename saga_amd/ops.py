@@ -227,13 +227,22 @@ def dense_decode(query, key, value, attention_mask=None, scaling=None, kv_len=No
     return out
 
 
+def set_fused_fast_step(enable: bool) -> bool:
+    """Process-wide switch of the fused Atop-N fast step (off by default: it
+    measured slower than the three-kernel path); on, shapes whose grid fits
+    the GPU at once run it.  Returns the previous setting."""
+    return bool(_lib.load().saga_set_fused_fast_step(1 if enable else 0))
+
+
 def atopn_workspace_views(b: int, q_h: int, k_h: int, L: int, d: int, buf_k: int, device, fast: bool = True) -> dict:
     """The cached fused-decode workspace after a call, for inspection (valid
     until the next call): logit thresholds (fast step), kept / passing counts,
     the selected positions and logits in ascending order, and the scores.
     The calibration step (fast=False) writes its list to sel_idx / sel_val;
     the fast step keeps it in per-slice lists, concatenated here in slice
-    order and cut at buf_k (host copies)."""
+    order and cut at buf_k (host copies).  The fused fast step (layout field
+    `fused`) writes no scores; `sync_error` is non-zero if one of its barrier
+    waits gave up."""
     lay = _lib.atopn_layout(b, q_h, k_h, L, d, buf_k)
     dev = torch.device(device)
     if dev.type == "cuda" and dev.index is None:
@@ -252,6 +261,8 @@ def atopn_workspace_views(b: int, q_h: int, k_h: int, L: int, d: int, buf_k: int
         "sel_idx": view(lay.sel_idx, nr * buf_k, torch.int32).reshape(nr, buf_k),
         "sel_val": view(lay.sel_val, nr * buf_k, torch.float32).reshape(nr, buf_k),
         "scores": view(lay.scores, nr * lay.scores_ld, torch.float32).reshape(nr, lay.scores_ld)[:, :L],
+        "sync_error": view(lay.sync + lay.sync_bytes - 256, 1, torch.int32),
+        "fused": bool(lay.fused),
     }
     if fast:
         ns, cap = lay.nslice, lay.slice_cap

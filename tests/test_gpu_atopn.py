@@ -27,9 +27,19 @@ from saga_amd import ops
 pytestmark = pytest.mark.gpu
 
 
-def _views(b, q_h, k_h, L, d, buf_k, fast=True):
-    return {k: v.cpu().numpy()
-            for k, v in ops.atopn_workspace_views(b, q_h, k_h, L, d, buf_k, "cuda:0", fast=fast).items()}
+def _views(b, q_h, k_h, L, d, buf_k, fast=True, scores_of=None):
+    """Workspace views as numpy.  scores_of = (query, key, mask, scale,
+    kv_len): the fast step's fp32 scores, recomputed by the score kernel (the
+    fused fast step keeps them in registers; both run the same tile code, so
+    the values are bit-identical)."""
+    raw = ops.atopn_workspace_views(b, q_h, k_h, L, d, buf_k, "cuda:0", fast=fast)
+    views = {k: (v.cpu().numpy() if isinstance(v, torch.Tensor) else v) for k, v in raw.items()}
+    if scores_of is not None:
+        qd, kd, mask, scale, kv_len = scores_of
+        views["scores"] = host(ops.qk_scores(qd, kd, mask, scale, kv_len)).reshape(b * q_h, L)
+    if fast:
+        assert int(views["sync_error"][0]) == 0
+    return views
 
 
 def _run_fast(qd, kd, vd, table_row, N, mask=None, scale=None, out_dtype=torch.float32, kv_len=None):
@@ -88,7 +98,7 @@ def test_against_reference_golden(name, golden):
     for tag, tab in (("fast", torch.from_numpy(g["cal_threshold" + sfx]).cuda()),
                      ("zero", torch.zeros(nr, device="cuda"))):
         out = host(_run_fast(q2, k, v, tab.contiguous(), N, mask, sc))
-        views = _views(b, q_h, k.shape[1], L, d, buf_k)
+        views = _views(b, q_h, k.shape[1], L, d, buf_k, scores_of=(q2, k, mask, sc, None))
         _check_selection_rule(views, nr, L, buf_k)
         t_ref = g[f"{tag}_t" + sfx]
         fin = np.isfinite(t_ref)
@@ -143,7 +153,7 @@ def test_bf16_benchmark_shapes_vs_fp32_path(name):
 
     out32 = host(_run_fast(q2d, kd, vd, table, N, out_dtype=torch.float32))
     buf_k = min(2 * N, L)
-    views = _views(b, q_h, k_h, L, d, buf_k)
+    views = _views(b, q_h, k_h, L, d, buf_k, scores_of=(q2d, kd, None, None, None))
     _check_selection_rule(views, nr, L, buf_k)
     out16 = host(_run_fast(q2d, kd, vd, table, N, out_dtype=torch.bfloat16))
 
@@ -188,7 +198,7 @@ def test_kv_len_equals_truncated_reference():
     cal = host(ops.atopn_calibrate(qd, kd, vd, N, table, kv_len=kvl, out_dtype=torch.float32))
     fast = host(_run_fast(dev(q2, "bf16"), kd, vd, table, N, kv_len=kvl))
     dense = host(ops.dense_decode(qd, kd, vd, kv_len=kvl, out_dtype=torch.float32))
-    views = _views(b, q_h, k_h, L, d, min(2 * N, L))
+    views = _views(b, q_h, k_h, L, d, min(2 * N, L), scores_of=(dev(q2, "bf16"), kd, None, None, kvl))
     _check_selection_rule(views, b * q_h, L, min(2 * N, L), kv_len=lens, q_h=q_h)
     thr = host(table)
     for i, n in enumerate(lens):
@@ -264,3 +274,96 @@ def test_fast_overflow_cut_inside_a_later_slice(cut_pos):
     for r in range(b * q_h):
         np.testing.assert_array_equal(views["sel_idx"][r], idx_ref.reshape(b * q_h, buf_k)[r])
     assert np.max(np.abs(out - ref_out)) < 2e-3 and rel_l2(out, ref_out) < 1e-4
+
+
+FUSED_SHAPES = {  # name: b, q_h, k_h, v_h, d, L, N, dtype
+    "qwen1.5b_32k_b8": (8, 12, 1, 2, 128, 33024, 512, "bf16"),
+    "b32_4k_g12": (32, 12, 1, 2, 128, 4096, 256, "bf16"),
+    "b2_k2_v8_16h": (2, 16, 2, 8, 128, 6000, 64, "f16"),
+    "b1_d64_15h": (1, 15, 1, 5, 64, 4100, 128, "f32"),
+    "b3_ragged": (3, 6, 1, 3, 64, 777, 100, "bf16"),
+}
+
+
+@pytest.mark.parametrize("name", list(FUSED_SHAPES))
+def test_fused_fast_step_matches_three_kernel_path(name):
+    """The fused fast step (scores kept on chip, a flag barrier per (batch,
+    key head)) against the three-kernel path on the same inputs: identical
+    thresholds, counts and ordered lists; outputs equal to fp32 rounding (the
+    merge order differs); the selection rule on the recomputed scores."""
+    b, q_h, k_h, v_h, d, L, N, dt = FUSED_SHAPES[name]
+    print(f"atopn fused vs split shape={name}", flush=True)
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    (q, k, v), (qd, kd, vd) = qkv(rng, b, q_h, k_h, v_h, d, L, dt, outliers=0.01)
+    lens = None
+    if name == "b3_ragged":
+        lens = torch.tensor([777, 300, 1], dtype=torch.int32, device="cuda")
+    table = torch.zeros(b * q_h, device="cuda")
+    ops.atopn_calibrate(qd, kd, vd, N, table, kv_len=lens)
+    q2 = O.round_bf16(q + np.float32(0.3) * rng.standard_normal(q.shape, dtype=np.float32))
+    q2d = dev(q2, dt)
+    buf_k = min(2 * N, L)
+    res = {}
+    prev = ops.set_fused_fast_step(True)
+    try:
+        for fused in (True, False):
+            ops.set_fused_fast_step(fused)
+            out = host(_run_fast(q2d, kd, vd, table, N, out_dtype=torch.float32, kv_len=lens))
+            views = _views(b, q_h, k_h, L, d, buf_k, scores_of=(q2d, kd, None, None, lens))
+            assert views["fused"] == fused, "shape expected on the fused path"
+            _check_selection_rule(views, b * q_h, L, buf_k, kv_len=None if lens is None else host(lens), q_h=q_h)
+            res[fused] = (out, views)
+    finally:
+        ops.set_fused_fast_step(prev)
+    (of, vf), (os_, vs) = res[True], res[False]
+    np.testing.assert_array_equal(vf["sel_cnt"], vs["sel_cnt"])
+    np.testing.assert_array_equal(vf["sel_total"], vs["sel_total"])
+    np.testing.assert_array_equal(vf["sel_idx"], vs["sel_idx"])
+    np.testing.assert_allclose(vf["thresh"], vs["thresh"], rtol=2e-6, atol=2e-6)
+    nan = np.isnan(os_)
+    np.testing.assert_array_equal(np.isnan(of), nan)
+    assert rel_l2(of[~nan], os_[~nan]) < 1e-5
+    print(f"  mean_count={vf['sel_cnt'].mean():.1f}", flush=True)
+
+
+def test_fused_fast_step_overflow_and_repeated_calls():
+    """An overflowing row through the fused path (cut at buf_k inside a
+    block's list), then calls of other shapes sharing the workspace's
+    barrier state, then the first shape again: same results each time."""
+    rng = np.random.default_rng(31)
+    b, q_h, k_h, v_h, d, L, N = 8, 4, 1, 2, 128, 6000, 256
+    q = O.round_bf16(rng.standard_normal((b, q_h, 1, d), dtype=np.float32))
+    k = O.round_bf16(rng.standard_normal((b, k_h, L, d), dtype=np.float32) * np.float32(0.2))
+    k[:, :, 2500:, :] += O.round_bf16(q.mean(axis=1, keepdims=True)[:, :, 0:1, :] * np.float32(0.3))
+    k = O.round_bf16(k)
+    v = O.round_bf16(rng.standard_normal((b, v_h, L, d), dtype=np.float32))
+    table = np.full(b * q_h, 1e-7, dtype=np.float32)
+    args = (dev(q, "bf16"), dev(k, "bf16"), dev(v, "bf16"), torch.from_numpy(table).cuda(), N)
+    ref_out, _, idx_ref, _ = O.fast(q, k, v, table, None, N, None)
+    prev = ops.set_fused_fast_step(True)
+    try:
+        _fused_overflow_reps(args, b, q_h, k_h, L, d, N, ref_out, idx_ref, rng)
+    finally:
+        ops.set_fused_fast_step(prev)
+
+
+def _fused_overflow_reps(args, b, q_h, k_h, L, d, N, ref_out, idx_ref, rng):
+    first = None
+    for rep in range(3):
+        out = host(ops.atopn_decode(*args, out_dtype=torch.float32))
+        views = _views(b, q_h, k_h, L, d, 2 * N)
+        assert views["fused"]
+        assert (views["sel_total"] > 2 * N).all(), "the case must overflow"
+        for r in range(b * q_h):
+            np.testing.assert_array_equal(views["sel_idx"][r], idx_ref.reshape(b * q_h, 2 * N)[r])
+        assert np.max(np.abs(out - ref_out)) < 2e-3 and rel_l2(out, ref_out) < 1e-4
+        if first is None:
+            first = out
+        np.testing.assert_array_equal(out, first)
+        # other shapes (other unit and block counts) in between
+        for bb, LL in ((1, 3000), (16, 2048)):
+            (_, _, _), (q3, k3, v3) = qkv(rng, bb, 12, 1, 2, 128, LL, "bf16")
+            t3 = torch.full((bb * 12,), 1e-3, device="cuda")
+            ops.atopn_decode(q3, k3, v3, t3, 64)
+            torch.cuda.synchronize()
+            assert int(_views(bb, 12, 1, LL, 128, 128)["sync_error"][0]) == 0
