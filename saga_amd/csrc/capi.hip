@@ -629,14 +629,25 @@ int make_rope(int64_t N, int32_t dt, int64_t n_q, int64_t n_k, int64_t n_v, floa
 // bias [N] of a skinny GEMM and fills the shared fields of p.
 int make_gemv(const saga_tensor* x, const saga_tensor* w, const saga_tensor* bias, float rms_eps, GemvParams& p) {
   int rc;
-  if ((rc = check_tensor(x, "x", 2)) || (rc = check_tensor(w, "w", 2))) return rc;
+  if ((rc = check_tensor(x, "x", 2))) return rc;
+  const bool packed = w && w->ndim == 4;
+  if ((rc = check_tensor(w, "w", packed ? 4 : 2))) return rc;
   if (x->dtype != SAGA_DTYPE_BF16 || w->dtype != SAGA_DTYPE_BF16) return fail(SAGA_ERR_UNSUPPORTED, "gemv: bf16 only");
-  const int64_t M = x->shape[0], K = x->shape[1], N = w->shape[0];
-  if (w->shape[1] != K) return fail(SAGA_ERR_INVALID, "gemv: w must be [N, K] with K = x.shape[1]");
+  const int64_t M = x->shape[0], K = x->shape[1];
+  const int64_t N = packed ? w->shape[0] * 16 : w->shape[0];
+  if (packed) {
+    // [N/16][K/32][16][32], contiguous
+    if (w->shape[2] != 16 || w->shape[3] != 32 || w->shape[1] * 32 != K || w->stride[3] != 1 || w->stride[2] != 32 ||
+        w->stride[1] != 512 || w->stride[0] != w->shape[1] * 512)
+      return fail(SAGA_ERR_INVALID, "gemv: packed w must be contiguous [N/16, K/32, 16, 32] with K = x.shape[1]");
+    if (reinterpret_cast<uintptr_t>(w->data) % 16) return fail(SAGA_ERR_INVALID, "gemv: packed w must be 16-byte aligned");
+  } else if (w->shape[1] != K) {
+    return fail(SAGA_ERR_INVALID, "gemv: w must be [N, K] with K = x.shape[1]");
+  }
   if (M > 16) return fail(SAGA_ERR_UNSUPPORTED, "gemv: at most 16 rows");
   if (N % 16 || K % 32 || K >= (1LL << 30) || N >= (1LL << 30))
     return fail(SAGA_ERR_UNSUPPORTED, "gemv: N %% 16 == 0 and K %% 32 == 0 required");
-  if ((rc = check_vec_rows(x, "x")) || (rc = check_vec_rows(w, "w"))) return rc;
+  if ((rc = check_vec_rows(x, "x")) || (!packed && (rc = check_vec_rows(w, "w")))) return rc;
   if (bias) {
     if ((rc = check_tensor(bias, "bias", 1))) return rc;
     if (bias->dtype != SAGA_DTYPE_BF16 || bias->shape[0] != N || bias->stride[0] != 1)
@@ -646,7 +657,8 @@ int make_gemv(const saga_tensor* x, const saga_tensor* w, const saga_tensor* bia
   p.x = x->data;
   p.x_ld = x->stride[0];
   p.w = w->data;
-  p.w_ld = w->stride[0];
+  p.w_ld = packed ? 0 : w->stride[0];
+  p.w_packed = packed ? 1 : 0;
   p.bias = bias ? bias->data : nullptr;
   p.M = static_cast<int32_t>(M);
   p.N = static_cast<int32_t>(N);

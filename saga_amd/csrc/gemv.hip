@@ -1,5 +1,9 @@
 // Skinny GEMM for decode projections: y[m, n] = sum_k x[m, k] * W[n, k], m < 16.
 //
+// W is row-major [N, K], or packed [N/16][K/32][16][32] (each 16-row x 32-k
+// MFMA A fragment 1 KB contiguous: a load instruction reads 1 KB of one
+// DRAM region instead of 64 B from 16 rows one row stride apart).
+//
 // Decode steps multiply a handful of token rows (the batch) by every weight
 // matrix once, so the kernel is a weight stream: 16 rows of W per MFMA tile,
 // loaded 16 bytes per lane straight into the A fragment of
@@ -21,42 +25,94 @@ namespace saga {
 constexpr int kGemvUnroll = 12;  // 32-wide k steps in flight per wave (K = 1536 over 4 waves: one burst)
 constexpr int kSplitBatch = 8;   // split-K partial sums in flight per epilogue thread
 
-template <int WAVES, int EPI>
-__global__ void __launch_bounds__(WAVES * 64) gemv_kernel(GemvParams p) {
-  __shared__ float red[WAVES][64][5];
+// Epilogue inputs of one lane, loaded before the weight burst (as loads they
+// return with it; after the reduction each would cost one more round trip):
+// the residual of output rows n..n+3 of token row m (SAGA_GEMV_ADD), and the
+// bias, position and batch row of the fused q/k/v projection (kGemvRopeKV).
+// Absent inputs read a valid dummy address instead of branching (a load under
+// a branch is waited for at the join, ahead of the burst).  Other epilogues
+// load their (rare) bias after the reduction, keeping registers for the burst.
+struct GemvPre {
+  uint16_t bias[4], y[4];
+  int pos, batch;
+};
+
+template <int EPI>
+__device__ __forceinline__ GemvPre gemv_prefetch(const GemvParams& p, int m, int n, const void* dummy) {
+  GemvPre e{};
+  if constexpr (EPI == SAGA_GEMV_ADD) {
+    const uint16_t* yp = static_cast<const uint16_t*>(p.y) + static_cast<int64_t>(m) * p.y_ld + n;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) e.y[r] = yp[r];
+  }
+  if constexpr (EPI == kGemvRopeKV) {
+    const uint16_t* bp = p.bias ? static_cast<const uint16_t*>(p.bias) + n : static_cast<const uint16_t*>(dummy);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) e.bias[r] = bp[r];
+    e.pos = p.rope.pos[m];
+    e.batch = *(p.rope.batch ? p.rope.batch + m : p.rope.pos + m);
+    if (!p.rope.batch) e.batch = m;
+  }
+  return e;
+}
+
+// TPW tiles of 16 W rows per workgroup (rows n0 .. n0 + 16*TPW): each k step
+// loads one x fragment and TPW W fragments, so a wave keeps TPW x more weight
+// bytes in flight per register of x.
+template <int WAVES, int EPI, int TPW>
+__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(TPW == 2 ? 3 : 4, 8)))
+gemv_kernel(GemvParams p) {
+  __shared__ float red[WAVES][TPW][64][4];
+  __shared__ float rsq[WAVES][64];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int col = lane & 15, s = lane >> 4;
-  const int n0 = blockIdx.x * 16;
+  const int n0 = blockIdx.x * 16 * TPW;
   const int split = blockIdx.y;  // K range of this workgroup (split-K: partial sums out)
   const bool mvalid = col < p.M;
-  const char* wrow = static_cast<const char*>(p.w) + (static_cast<int64_t>(n0 + col) * p.w_ld + 8 * s) * 2;
-  const char* xrow = static_cast<const char*>(p.x) + (static_cast<int64_t>(mvalid ? col : 0) * p.x_ld + 8 * s) * 2;
-  const int steps = p.K / 32;
-  // this workgroup's k steps [k0, k1): split-K workgroups deal them to their
-  // waves round robin (wave w: k0 + w, k0 + w + WAVES, ...), so the waves
-  // sweep each long W row together; otherwise each wave takes a contiguous
-  // quarter
-  const int k0 = split * steps / p.splits, k1 = (split + 1) * steps / p.splits;
-  const bool rr = p.part != nullptr;
-  const int j0 = rr ? 0 : w * (k1 - k0) / WAVES;
-  const int nmine = rr ? (k1 - k0 - w + WAVES - 1) / WAVES : (w + 1) * (k1 - k0) / WAVES - j0;
-  const int jstride = rr ? WAVES : 1;
-  const int jbase = k0 + (rr ? w : j0);
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  float ssq = 0.f;
-  for (int i0 = 0; i0 < nmine; i0 += kGemvUnroll) {
-    u32x4 a[kGemvUnroll], b[kGemvUnroll];
+  const int m = mvalid ? col : 0;
+  // A fragment of tile t at k step j: wrow[t] + j * wstep.  Row-major W:
+  // 16 rows x 64 B, one row per W row stride; packed W: 1 KB contiguous
+  const int64_t wstep = p.w_packed ? 1024 : 64;
+  const char* wrow[TPW];
 #pragma unroll
-    for (int u = 0; u < kGemvUnroll; ++u) {
+  for (int t = 0; t < TPW; ++t)
+    wrow[t] = static_cast<const char*>(p.w) +
+              (p.w_packed ? static_cast<int64_t>(n0 / 16 + t) * (p.K / 32) * 1024 + col * 64 + s * 16
+                          : (static_cast<int64_t>(n0 + 16 * t + col) * p.w_ld + 8 * s) * 2);
+  const char* xrow = static_cast<const char*>(p.x) + (static_cast<int64_t>(m) * p.x_ld + 8 * s) * 2;
+  // the tile this wave finishes (waves 0..TPW-1) and its epilogue inputs
+  const int tf = w < TPW ? w : TPW - 1;
+  const int nf = n0 + 16 * tf + 4 * s;
+  const GemvPre pre = gemv_prefetch<EPI>(p, m, nf, wrow[0]);
+  const int steps = p.K / 32;
+  // this workgroup's k steps [k0, k1), dealt to its waves round robin (wave
+  // w: k0 + w, k0 + w + WAVES, ...): at any moment the workgroup's waves
+  // read neighbouring fragments of its tiles (measured faster than a
+  // contiguous share per wave, for packed and row-major W)
+  const int k0 = split * steps / p.splits, k1 = (split + 1) * steps / p.splits;
+  const int nmine = (k1 - k0 - w + WAVES - 1) / WAVES;
+  const int jstride = WAVES;
+  const int jbase = k0 + w;
+  constexpr int UNROLL = kGemvUnroll;
+  f32x4 acc[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float ssq = 0.f;
+  for (int i0 = 0; i0 < nmine; i0 += UNROLL) {
+    u32x4 a[UNROLL][TPW], b[UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
       const int jj = jbase + jstride * min(i0 + u, nmine - 1);
-      a[u] = ld16(wrow + static_cast<int64_t>(jj) * 64);
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) a[u][t] = ld16(wrow[t] + static_cast<int64_t>(jj) * wstep);
       b[u] = mvalid ? ld16(xrow + static_cast<int64_t>(jj) * 64) : u32x4{0u, 0u, 0u, 0u};
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 0; u < kGemvUnroll; ++u) {
+    for (int u = 0; u < UNROLL; ++u) {
       if (i0 + u < nmine) {
-        acc = mfma_16b<SAGA_DTYPE_BF16>(a[u], b[u], acc);
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) acc[t] = mfma_16b<SAGA_DTYPE_BF16>(a[u][t], b[u], acc[t]);
         if (p.rms) {
           float f[8];
           unpack16<SAGA_DTYPE_BF16>(b[u], f);
@@ -66,48 +122,59 @@ __global__ void __launch_bounds__(WAVES * 64) gemv_kernel(GemvParams p) {
       }
     }
   }
-  // lane (col, s): rows n0 + 4s + r of the tile for token row m = col
+  // lane (col, s): rows n0 + 16t + 4s + r of tile t for token row m = col
 #pragma unroll
-  for (int r = 0; r < 4; ++r) red[w][lane][r] = acc[r];
-  red[w][lane][4] = ssq;
-  __syncthreads();
-  if (w != 0) return;
+  for (int t = 0; t < TPW; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[w][t][lane][r] = acc[t][r];
+  rsq[w][lane] = ssq;
+  lds_sync();
+  if (w >= TPW) return;
+  const int t = w;
   float v[4] = {0.f, 0.f, 0.f, 0.f};
   float sq = 0.f;
 #pragma unroll
   for (int q = 0; q < WAVES; ++q) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) v[r] += red[q][lane][r];
+    for (int r = 0; r < 4; ++r) v[r] += red[q][t][lane][r];
     if (p.rms) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) sq += red[q][col + 16 * g][4];  // all k-slot groups of row m
+      for (int g = 0; g < 4; ++g) sq += rsq[q][col + 16 * g];  // all k-slot groups of row m
     }
   }
   if (!mvalid) return;
-  const int n = n0 + 4 * s;
+  const int n = nf;
   if (p.part) {
     // split-K: this K range's sums; gemv_splitk_epilogue finishes the rows
     *reinterpret_cast<f32x4*>(p.part + (static_cast<int64_t>(split) * p.M + col) * p.N + n) =
         f32x4{v[0], v[1], v[2], v[3]};
-    if (s == 0 && blockIdx.x == 0) p.part_ssq[split * p.M + col] = sq;
+    if (s == 0 && blockIdx.x == 0 && t == 0) p.part_ssq[split * p.M + col] = sq;
     return;
   }
   const float scale = p.rms ? rsqrtf(sq / static_cast<float>(p.K) + p.eps) : 1.f;
+  float bias[4] = {0.f, 0.f, 0.f, 0.f};
+  if (EPI == kGemvRopeKV) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) bias[r] = bf16_bits_to_f32(pre.bias[r]);
+  } else if (p.bias) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) bias[r] = bf16_bits_to_f32(static_cast<const uint16_t*>(p.bias)[nf + r]);
+  }
   if constexpr (EPI == kGemvRopeKV) {
     // token row m = col; the 4 rows n..n+3 lie in one head (d % 16 == 0).  q/k
     // heads are stored in rotary-pair order [0, d/2, 1, d/2 + 1, ...], so rows
     // (n, n+1) and (n+2, n+3) are the pairs (i, i + d/2) of i = j/2, j/2 + 1.
     const RopeParams& rp = p.rope;
-    const int pos = rp.pos[col];
-    const int b = rp.batch ? rp.batch[col] : col;
+    const int pos = pre.pos;
+    const int b = pre.batch;
     const bool ok = pos >= 0 && pos < rp.Lmax && b >= 0 && b < rp.B;
     const int hh = n / rp.d, j = n - hh * rp.d;
     float o[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      float t = v[r] * scale;
-      if (p.bias) t += bf16_bits_to_f32(static_cast<const uint16_t*>(p.bias)[n + r]);
-      o[r] = bf16_bits_to_f32(f32_to_bf16_bits(t));  // the projection output, rounded as stored
+      float tt = v[r] * scale;
+      if (p.bias) tt += bias[r];
+      o[r] = bf16_bits_to_f32(f32_to_bf16_bits(tt));  // the projection output, rounded as stored
     }
     if (hh < rp.n_q + rp.n_k) {
       const int half = rp.d / 2;
@@ -151,8 +218,8 @@ __global__ void __launch_bounds__(WAVES * 64) gemv_kernel(GemvParams p) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       float o = v[r] * scale;
-      if (p.bias) o += bf16_bits_to_f32(static_cast<const uint16_t*>(p.bias)[n + r]);
-      if constexpr (EPI == SAGA_GEMV_ADD) o += bf16_bits_to_f32(y[n + r]);
+      if (p.bias) o += bias[r];
+      if constexpr (EPI == SAGA_GEMV_ADD) o += bf16_bits_to_f32(pre.y[r]);
       y[n + r] = f32_to_bf16_bits(o);
     }
   }
@@ -169,6 +236,15 @@ __global__ void __launch_bounds__(64) gemv_splitk_epilogue(GemvParams p) {
   const int np = p.N / 2;
   if (q >= static_cast<int64_t>(p.M) * np) return;
   const int m = static_cast<int>(q / np), n = 2 * static_cast<int>(q - static_cast<int64_t>(m) * np);
+  uint16_t* y = static_cast<uint16_t*>(p.y) + static_cast<int64_t>(m) * p.y_ld;
+  // bias and residual issued with the first partials (one round trip)
+  const uint16_t* bp = p.bias ? static_cast<const uint16_t*>(p.bias) + n : y + n;
+  const uint16_t b0 = bp[0], b1 = bp[1];
+  uint16_t r0 = 0, r1 = 0;
+  if constexpr (EPI == SAGA_GEMV_ADD) {
+    r0 = y[n];
+    r1 = y[n + 1];
+  }
   float v0 = 0.f, v1 = 0.f, sq = 0.f;
   for (int s0 = 0; s0 < p.splits; s0 += kSplitBatch) {
     f32x2 a[kSplitBatch];
@@ -188,7 +264,6 @@ __global__ void __launch_bounds__(64) gemv_splitk_epilogue(GemvParams p) {
     }
   }
   const float scale = p.rms ? rsqrtf(sq / static_cast<float>(p.K) + p.eps) : 1.f;
-  uint16_t* y = static_cast<uint16_t*>(p.y) + static_cast<int64_t>(m) * p.y_ld;
   if constexpr (EPI == SAGA_GEMV_SILU_PAIRS) {
     // rows (n, n+1) are a (gate, up) pair -> output n/2
     const float g = v0 * scale, u = v1 * scale;
@@ -196,12 +271,12 @@ __global__ void __launch_bounds__(64) gemv_splitk_epilogue(GemvParams p) {
   } else {
     float o0 = v0 * scale, o1 = v1 * scale;
     if (p.bias) {
-      o0 += bf16_bits_to_f32(static_cast<const uint16_t*>(p.bias)[n]);
-      o1 += bf16_bits_to_f32(static_cast<const uint16_t*>(p.bias)[n + 1]);
+      o0 += bf16_bits_to_f32(b0);
+      o1 += bf16_bits_to_f32(b1);
     }
     if constexpr (EPI == SAGA_GEMV_ADD) {
-      o0 += bf16_bits_to_f32(y[n]);
-      o1 += bf16_bits_to_f32(y[n + 1]);
+      o0 += bf16_bits_to_f32(r0);
+      o1 += bf16_bits_to_f32(r1);
     }
     y[n] = f32_to_bf16_bits(o0);
     y[n + 1] = f32_to_bf16_bits(o1);
@@ -210,9 +285,9 @@ __global__ void __launch_bounds__(64) gemv_splitk_epilogue(GemvParams p) {
 
 template <int EPI>
 static hipError_t launch_gemv_epi(const GemvParams& p, hipStream_t st) {
-  const unsigned blocks = static_cast<unsigned>(p.N / 16);
+  const unsigned tiles = static_cast<unsigned>(p.N / 16);
   if (p.part) {
-    hipLaunchKernelGGL((gemv_kernel<4, EPI>), dim3(blocks, p.splits), dim3(256), 0, st, p);
+    hipLaunchKernelGGL((gemv_kernel<4, EPI, 1>), dim3(tiles, p.splits), dim3(256), 0, st, p);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int64_t pairs = static_cast<int64_t>(p.M) * (p.N / 2);
@@ -220,11 +295,22 @@ static hipError_t launch_gemv_epi(const GemvParams& p, hipStream_t st) {
                        p);
   } else if (p.K >= 4096) {
     // long rows of W: more waves per workgroup split K
-    hipLaunchKernelGGL((gemv_kernel<16, EPI>), dim3(blocks, 1), dim3(1024), 0, st, p);
+    hipLaunchKernelGGL((gemv_kernel<16, EPI, 1>), dim3(tiles, 1), dim3(1024), 0, st, p);
+  } else if (gemv_tiles_per_wave(p.N, p.K) == 2) {
+    hipLaunchKernelGGL((gemv_kernel<4, EPI, 2>), dim3(tiles / 2, 1), dim3(256), 0, st, p);
   } else {
-    hipLaunchKernelGGL((gemv_kernel<4, EPI>), dim3(blocks, 1), dim3(256), 0, st, p);
+    hipLaunchKernelGGL((gemv_kernel<4, EPI, 1>), dim3(tiles, 1), dim3(256), 0, st, p);
   }
   return hipGetLastError();
+}
+
+// Two tiles per wave (24 KB of W in flight per wave, 3 waves per SIMD) for
+// weights of many tiles (the LM head: 9.3 rounds of 4096 one-tile waves),
+// one tile (12 KB, 4 waves per SIMD) otherwise: measured on MI355X, two tiles
+// lose below about two rounds (the gate/up projection, 1.1 rounds).
+int gemv_tiles_per_wave(int64_t N, int64_t K) {
+  if (N % 32 != 0 || K >= 4096) return 1;
+  return (N / 16) * 4 > 2 * 4096 ? 2 : 1;
 }
 
 int gemv_splits(int64_t N, int64_t K) {

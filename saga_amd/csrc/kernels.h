@@ -204,8 +204,9 @@ hipError_t launch_silu_mul(const RowParams& p, hipStream_t st);
 struct GemvParams {
   const void* x;  // bf16 [M, K]
   int64_t x_ld;
-  const void* w;  // bf16 [N, K]
+  const void* w;  // bf16 [N, K] (row stride w_ld), or packed [N/16][K/32][16][32]
   int64_t w_ld;
+  int32_t w_packed;  // packed: every MFMA A fragment (16 rows x 32 k) is 1 KB contiguous
   const void* bias;  // bf16 [N] or null
   void* y;           // bf16 [M, N] (SILU_PAIRS: [M, N / 2])
   int64_t y_ld;
@@ -223,6 +224,7 @@ struct GemvParams {
   float* part_ssq;
 };
 int gemv_splits(int64_t N, int64_t K);  // K ranges worth launching for an N x K weight
+int gemv_tiles_per_wave(int64_t N, int64_t K);  // 16-row W tiles per wave of the one-range kernel
 constexpr int kGemvRopeKV = 3;
 hipError_t launch_gemv(const GemvParams& p, hipStream_t st);
 hipError_t launch_argmax(const void* x, int64_t ld, int rows, int N, int64_t* out, hipStream_t st);

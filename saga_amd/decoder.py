@@ -76,7 +76,8 @@ class SagaDecoder:
     """
 
     def __init__(self, shape: DecoderShape, batch: int, max_len: int, mode: str = "atopn", top_n: int = 512,
-                 exempt_layers=(), device="cuda", dtype=torch.bfloat16, seed: int = 0, fuse_rope: bool = True):
+                 exempt_layers=(), device="cuda", dtype=torch.bfloat16, seed: int = 0, fuse_rope: bool = True,
+                 pack_weights: bool = True):
         if mode not in ("atopn", "dense"):
             raise ValueError(f"mode must be 'atopn' or 'dense', got {mode!r}")
         self.shape, self.batch, self.max_len, self.mode, self.top_n = shape, batch, max_len, mode, top_n
@@ -124,6 +125,7 @@ class SagaDecoder:
                          and (s.n_q * d) % 32 == 0 and s.qkv_width % 16 == 0 and s.vocab % 16 == 0)
         # q/k/v projection, RoPE and cache append in one launch (pair-ordered rows)
         self.fuse_rope = fuse_rope and self.use_gemv and d % 16 == 0
+        self.pack_weights = pack_weights
         self.prepare_kernel_weights()
         self.graph_cal: Optional[torch.cuda.CUDAGraph] = None
         self.graph_fast: Optional[torch.cuda.CUDAGraph] = None
@@ -133,7 +135,9 @@ class SagaDecoder:
         """Decode-layout copies of the weights for the skinny GEMM: RMSNorm
         weights folded into the following projection (w * diag(norm)), gate
         and up rows interleaved (gate_0, up_0, gate_1, ...) so one output tile
-        holds both halves of silu(gate) * up, and a normed LM head."""
+        holds both halves of silu(gate) * up, and a normed LM head; with
+        pack_weights every decode weight in the packed MFMA-fragment layout
+        (ops.pack_gemv_weight; the prefill keeps the row-major originals)."""
         if not self.use_gemv:
             return
         s = self.shape
@@ -150,6 +154,16 @@ class SagaDecoder:
                 self.kw_gu.append(torch.stack([w[:s.intermediate], w[s.intermediate:]], dim=1)
                                   .reshape(2 * s.intermediate, s.hidden).contiguous())
             self.kw_lm = (self.embed.float() * self.ln_f.float()).to(self.dtype)
+            self.kw_o = list(self.w_o)
+            self.kw_d = list(self.w_d)
+            if self.pack_weights:
+                # MFMA-fragment order: every 16 x 32 fragment 1 KB contiguous
+                pk = ops.pack_gemv_weight
+                self.kw_qkv = [pk(w) for w in self.kw_qkv]
+                self.kw_gu = [pk(w) for w in self.kw_gu]
+                self.kw_o = [pk(w) for w in self.w_o]
+                self.kw_d = [pk(w) for w in self.w_d]
+                self.kw_lm = pk(self.kw_lm)
 
     # ------------------------------------------------------------------ prefill
     @torch.no_grad()
@@ -235,9 +249,9 @@ class SagaDecoder:
             else:
                 ops.atopn_decode(q4, K, V, self.table[l], self.top_n, kv_len=self.kv_len, out=self._attn)
             if self.use_gemv:
-                ops.gemv(self._attn.view(B, s.n_q * d), self.w_o[l], epilogue="add", out=x)
+                ops.gemv(self._attn.view(B, s.n_q * d), self.kw_o[l], epilogue="add", out=x)
                 ops.gemv(x, self.kw_gu[l], rms_eps=s.eps, epilogue="silu_pairs", out=self._act)
-                ops.gemv(self._act, self.w_d[l], epilogue="add", out=x)
+                ops.gemv(self._act, self.kw_d[l], epilogue="add", out=x)
             else:
                 x.addmm_(self._attn.view(B, s.n_q * d), self.w_o[l].t())
                 ops.rmsnorm(x, self.ln2[l], s.eps, out=self._h)

@@ -319,8 +319,23 @@ def silu_mul(gate_up, out=None):
     return out
 
 
+def pack_gemv_weight(w: torch.Tensor) -> torch.Tensor:
+    """W [N, K] -> the packed layout [N/16, K/32, 16, 32] that gemv and
+    gemv_rope_kv also accept: every 16-row x 32-column MFMA fragment is 1 KB
+    contiguous (one DRAM region per load instruction)."""
+    N, K = w.shape
+    if N % 16 or K % 32:
+        raise ValueError("saga_amd: packing needs N % 16 == 0 and K % 32 == 0")
+    return w.reshape(N // 16, 16, K // 32, 32).permute(0, 2, 1, 3).contiguous()
+
+
+def _gemv_n(w: torch.Tensor) -> int:
+    return w.shape[0] * 16 if w.dim() == 4 else w.shape[0]
+
+
 def gemv(x, w, bias=None, rms_eps=None, epilogue="store", out=None, split_k=True):
-    """Skinny projection for decode (x [M <= 16, K] bf16, w [N, K] bf16):
+    """Skinny projection for decode (x [M <= 16, K] bf16, w [N, K] bf16, or
+    packed by pack_gemv_weight):
     y = s * x @ w.T (+ bias), s = 1/sqrt(mean(x^2) + rms_eps) per row when
     rms_eps is given (RMSNorm fused, norm weight folded into w).
     epilogue: "store", "add" (out += result, in place) or "silu_pairs" (w rows
@@ -330,7 +345,7 @@ def gemv(x, w, bias=None, rms_eps=None, epilogue="store", out=None, split_k=True
     _need_gpu(x, w, bias, out)
     codes = {"store": _lib.GEMV_STORE, "add": _lib.GEMV_ADD, "silu_pairs": _lib.GEMV_SILU_PAIRS}
     code = codes[epilogue]
-    M, N = x.shape[0], w.shape[0]
+    M, N = x.shape[0], _gemv_n(w)
     if out is None:
         if code == _lib.GEMV_ADD:
             raise ValueError("saga_amd: epilogue 'add' needs out")

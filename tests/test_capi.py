@@ -175,3 +175,22 @@ def test_ops_refuse_cpu_tensors():
     A.init_amortized_threshold_tensor("cpu", A.MAX_LAYERS, 2)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         A.approx_top_n_attention_amortized(q, k, v, top_n_attention=4)
+
+
+def test_gemv_packed_weight_layout_checks():
+    """A 4-D w is the packed layout [N/16, K/32, 16, 32]: K must match x,
+    the tensor must be contiguous, 16-byte aligned; errors come back before
+    any launch."""
+    lib = _lib.load()
+    x = _t((8, 1536))
+    y = _t((8, 1920))
+
+    def call(w):
+        return lib.saga_gemv(ctypes.byref(x), ctypes.byref(w), None, -1.0, 0, ctypes.byref(y), None, 0, None)
+
+    assert call(_t((120, 47, 16, 32))) == -1 and "packed" in _err()          # K / 32 = 48 expected
+    assert call(_t((120, 48, 32, 16))) == -1 and "packed" in _err()          # fragment dims swapped
+    bad = _t((120, 48, 16, 32), strides=(48 * 512, 512, 1, 16))               # transposed fragments
+    assert call(bad) == -1 and "packed" in _err()
+    assert call(_t((120, 48, 16, 32), data=0x100008)) == -1 and "aligned" in _err()
+    assert call(_t((120, 48, 16, 16))) == -1

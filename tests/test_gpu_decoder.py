@@ -145,3 +145,21 @@ def test_fused_rope_projection_equals_unfused_step():
     torch.cuda.synchronize()
     for a, b in ((ms[0].k_cache, ms[1].k_cache), (ms[0].v_cache, ms[1].v_cache), (ms[0]._logits, ms[1]._logits)):
         assert torch.allclose(a.float(), b.float(), rtol=2 ** -7, atol=1e-3)
+
+
+def test_packed_weights_decode_step_identical():
+    """The decoder with its decode weights packed (the default) produces the
+    caches and logits of the row-major decoder bit for bit."""
+    from saga_amd.decoder import DecoderShape, SagaDecoder
+    shape = DecoderShape(layers=2, hidden=256, n_q=4, n_k=1, n_v=2, head_dim=64, intermediate=512, vocab=1024,
+                         rope_theta=1e4, eps=1e-6, qkv_bias=True)
+    ms = [SagaDecoder(shape, batch=3, max_len=300, mode="atopn", pack_weights=p) for p in (True, False)]
+    assert ms[0].kw_gu[0].dim() == 4 and ms[1].kw_gu[0].dim() == 2
+    for m in ms:
+        m.fill_synthetic(200)
+        m.tokens.copy_(torch.tensor([5, 77, 1000], device="cuda"))
+        m.step(calibrate=True)
+        m.step(calibrate=False)
+    torch.cuda.synchronize()
+    for a, b in ((ms[0].k_cache, ms[1].k_cache), (ms[0].v_cache, ms[1].v_cache), (ms[0]._logits, ms[1]._logits)):
+        assert torch.equal(a, b)

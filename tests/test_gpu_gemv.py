@@ -136,3 +136,43 @@ def test_gemv_split_k_matches_single_pass_and_is_deterministic(epilogue, rms):
     torch.cuda.synchronize()
     assert torch.equal(outs[1], outs[2])
     assert torch.allclose(outs[0].float(), outs[1].float(), rtol=2 ** -7, atol=2e-3)
+
+
+@pytest.mark.parametrize("M,K,N", [(8, 1536, 1920), (8, 1536, 17920), (8, 8960, 1536), (3, 64, 32), (8, 1536, 151936)])
+@pytest.mark.parametrize("epilogue", ["store", "add", "silu_pairs"])
+def test_packed_weights_give_identical_results(M, K, N, epilogue):
+    """W in the packed MFMA-fragment layout [N/16, K/32, 16, 32] feeds the same
+    fragments in the same order: every epilogue (and the split-K path of
+    the long-row shape) returns bit-identical outputs."""
+    rng = np.random.default_rng(M * 7 + N)
+    x, w, b = _data(rng, M, K, N)
+    xd, wd = dev(x, "bf16"), dev(w, "bf16")
+    wp = ops.pack_gemv_weight(wd)
+    assert wp.shape == (N // 16, K // 32, 16, 32)
+    # the packing is the fragment order: fragment (t, j) = rows 16t.., columns 32j..
+    assert torch.equal(wp[1, 2], wd[16:32, 64:96]) if N >= 32 and K >= 96 else True
+    y0 = dev(O.round_bf16(rng.standard_normal((M, N // 2 if epilogue == "silu_pairs" else N), dtype=np.float32)),
+             "bf16")
+    bias = dev(b, "bf16") if epilogue == "store" else None
+    for rms in (None, 1e-6):
+        ya = ops.gemv(xd, wd, bias=bias, rms_eps=rms, epilogue=epilogue, out=y0.clone())
+        yb = ops.gemv(xd, wp, bias=bias, rms_eps=rms, epilogue=epilogue, out=y0.clone())
+        torch.cuda.synchronize()
+        assert torch.equal(ya, yb)
+
+
+def test_packed_rope_kv_projection_identical():
+    rng = np.random.default_rng(81)
+    M, K, n_q, n_k, n_v, d = 8, 1536, 12, 1, 2, 128
+    x, w, b = _data(rng, M, K, (n_q + n_k + n_v) * d)
+    xd, wd, bd = dev(x, "bf16"), dev(w, "bf16"), dev(b, "bf16")
+    pos = torch.arange(M, dtype=torch.int32, device="cuda") * 3 + 1
+    outs = []
+    for wt in (wd, ops.pack_gemv_weight(wd)):
+        kc = torch.zeros(M, n_k, 64, d, dtype=torch.bfloat16, device="cuda")
+        vc = torch.zeros(M, n_v, 64, d, dtype=torch.bfloat16, device="cuda")
+        q = ops.gemv_rope_kv(xd, wt, bd, n_q, n_k, n_v, 1e6, pos, kc, vc, rms_eps=1e-6)
+        outs.append((q, kc, vc))
+    torch.cuda.synchronize()
+    for a, c in zip(outs[0], outs[1]):
+        assert torch.equal(a, c)
