@@ -278,8 +278,14 @@ int saga_gemv_rope_kv(const saga_tensor* x, const saga_tensor* w, const saga_ten
                       saga_tensor* v_cache, saga_stream_t stream);
 
 /* out[r] = first index of the maximum of row r of x [rows, N] (bf16); the
- * greedy next token of speedup.py:169/193 (logits.argmax(dim=-1)). */
-int saga_argmax(const saga_tensor* x, int64_t* out, saga_stream_t stream);
+ * greedy next token of speedup.py:169/193 (logits.argmax(dim=-1)).  NaN is
+ * never the maximum.  workspace (optional, 256-byte aligned,
+ * saga_argmax_workspace_bytes(rows, N) bytes, no initial contents): with it,
+ * long rows are reduced in two passes over many workgroups per row; without
+ * it, or when the size is 0, one workgroup per row. */
+size_t saga_argmax_workspace_bytes(int64_t rows, int64_t N);
+int saga_argmax(const saga_tensor* x, int64_t* out, void* workspace, size_t workspace_bytes,
+                saga_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -322,10 +322,8 @@ __global__ void __launch_bounds__(kRowThreads) atopn_gather_kernel(FusedSelParam
   const int2 tot = block_scan_slices(ns, pre, gpre, wsum, cnt_of, whole_gather);
   const int total = tot.x;
   const int n = min(total, p.cap);
-  if (tid == 0) {
-    p.sel_cnt[r] = n;
-    if (p.sel_total) p.sel_total[r] = total;
-  }
+  // sel_cnt / sel_total are stored at the end: a global store here would make
+  // every later block barrier wait for its acknowledgement
   // slice s contributes its first take(s) entries; a short slice contributing
   // all of them has its partial from the slice wave, the rest are gathered here
   auto take = [&](int s) { return max(0, min(n - pre[s], pre[s + 1] - pre[s])); };
@@ -434,6 +432,10 @@ __global__ void __launch_bounds__(kRowThreads) atopn_gather_kernel(FusedSelParam
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       store_from_f32(v.out, v.out_dt, ooff + 4 * tid + i, n == 0 ? __builtin_nanf("") : o[i] / L);
+  }
+  if (tid == 0) {
+    p.sel_cnt[r] = n;
+    if (p.sel_total) p.sel_total[r] = total;
   }
 }
 

@@ -779,15 +779,23 @@ int saga_gemv(const saga_tensor* x, const saga_tensor* w, const saga_tensor* bia
   return ok();
 }
 
-int saga_argmax(const saga_tensor* x, int64_t* out, saga_stream_t stream) {
+size_t saga_argmax_workspace_bytes(int64_t rows, int64_t N) {
+  if (rows < 1 || N < 1 || rows >= (1LL << 31) || N >= (1LL << 31)) return 0;
+  return static_cast<size_t>(argmax_workspace_bytes(rows, N));
+}
+
+int saga_argmax(const saga_tensor* x, int64_t* out, void* workspace, size_t workspace_bytes, saga_stream_t stream) {
   int rc;
   if ((rc = check_tensor(x, "x", 2))) return rc;
   if (x->dtype != SAGA_DTYPE_BF16 || x->stride[1] != 1) return fail(SAGA_ERR_UNSUPPORTED, "argmax: bf16 rows with unit stride");
   if (!out) return fail(SAGA_ERR_INVALID, "out: null");
   if (x->shape[0] >= (1LL << 31) || x->shape[1] >= (1LL << 31)) return fail(SAGA_ERR_UNSUPPORTED, "argmax: too large");
   if (x->shape[0] == 0) return ok();
+  const int64_t need = argmax_workspace_bytes(x->shape[0], x->shape[1]);
+  void* ws = workspace && need > 0 && workspace_bytes >= static_cast<size_t>(need) ? workspace : nullptr;
+  if (ws && reinterpret_cast<uintptr_t>(ws) % 256) return fail(SAGA_ERR_WORKSPACE, "workspace must be 256-byte aligned");
   if ((rc = hip_status(launch_argmax(x->data, x->stride[0], static_cast<int>(x->shape[0]), static_cast<int>(x->shape[1]),
-                                     out, static_cast<hipStream_t>(stream)),
+                                     out, ws, static_cast<hipStream_t>(stream)),
                        "argmax launch")))
     return rc;
   return ok();

@@ -379,7 +379,82 @@ __global__ void __launch_bounds__(1024) argmax_kernel(const uint16_t* x, int64_t
   }
 }
 
-hipError_t launch_argmax(const void* x, int64_t ld, int rows, int N, int64_t* out, hipStream_t st) {
+// Two-pass argmax over long rows (the LM head's vocabulary): pass 1 reduces
+// chunks of kArgmaxChunk elements, one 256-thread block each (every load of
+// a row in flight at once over many CUs), into (value, index) partials;
+// pass 2 reduces a row's partials in one wave.  Ties keep the lowest index.
+constexpr int kArgmaxChunk = 256 * 16;
+
+__global__ void __launch_bounds__(256) argmax_chunk_kernel(const uint16_t* x, int64_t ld, int N, float* pval,
+                                                           int* pidx, int nchunk) {
+  __shared__ float bv[4];
+  __shared__ int bi[4];
+  const int r = blockIdx.y, c = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const uint16_t* row = x + static_cast<int64_t>(r) * ld;
+  const int e0 = c * kArgmaxChunk + tid * 8;
+  u32x4 v[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int e = e0 + u * 256 * 8;
+    v[u] = e + 8 <= N ? ld16(row + e) : u32x4{0u, 0u, 0u, 0u};
+  }
+  float best = kNegInf;
+  int idx = 0x7fffffff;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int e = e0 + u * 256 * 8;
+    if (e + 8 <= N) {
+      float f[8];
+      unpack16<SAGA_DTYPE_BF16>(v[u], f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) argmax_take(f[i], e + i, best, idx);
+    } else {
+      for (int i = e; i < N && i < e + 8; ++i) argmax_take(bf16_bits_to_f32(row[i]), i, best, idx);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) argmax_take(__shfl_xor(best, o), __shfl_xor(idx, o), best, idx);
+  if (lane == 0) {
+    bv[w] = best;
+    bi[w] = idx;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int q = 1; q < 4; ++q) argmax_take(bv[q], bi[q], best, idx);
+    pval[r * nchunk + c] = best;
+    pidx[r * nchunk + c] = idx;
+  }
+}
+
+__global__ void __launch_bounds__(64) argmax_final_kernel(const float* pval, const int* pidx, int nchunk,
+                                                          int64_t* out) {
+  const int r = blockIdx.x, lane = threadIdx.x;
+  float best = kNegInf;
+  int idx = 0x7fffffff;
+  for (int c = lane; c < nchunk; c += 64) argmax_take(pval[r * nchunk + c], pidx[r * nchunk + c], best, idx);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) argmax_take(__shfl_xor(best, o), __shfl_xor(idx, o), best, idx);
+  if (lane == 0) out[r] = idx == 0x7fffffff ? 0 : idx;
+}
+
+int64_t argmax_workspace_bytes(int64_t rows, int64_t N) {
+  const int64_t nchunk = (N + kArgmaxChunk - 1) / kArgmaxChunk;
+  return nchunk > 1 ? rows * nchunk * 8 : 0;
+}
+
+hipError_t launch_argmax(const void* x, int64_t ld, int rows, int N, int64_t* out, void* ws, hipStream_t st) {
+  const int nchunk = (N + kArgmaxChunk - 1) / kArgmaxChunk;
+  const bool vec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ld % 8 == 0;
+  if (ws && vec && nchunk > 1 && nchunk <= 65535) {
+    float* pval = static_cast<float*>(ws);
+    int* pidx = reinterpret_cast<int*>(pval + static_cast<int64_t>(rows) * nchunk);
+    hipLaunchKernelGGL(argmax_chunk_kernel, dim3(nchunk, rows), dim3(256), 0, st, static_cast<const uint16_t*>(x), ld,
+                       N, pval, pidx, nchunk);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(rows), dim3(64), 0, st, pval, pidx, nchunk, out);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(1024), 0, st, static_cast<const uint16_t*>(x), ld, N, out);
   return hipGetLastError();
 }

@@ -227,6 +227,8 @@ int gemv_splits(int64_t N, int64_t K);  // K ranges worth launching for an N x K
 int gemv_tiles_per_wave(int64_t N, int64_t K);  // 16-row W tiles per wave of the one-range kernel
 constexpr int kGemvRopeKV = 3;
 hipError_t launch_gemv(const GemvParams& p, hipStream_t st);
-hipError_t launch_argmax(const void* x, int64_t ld, int rows, int N, int64_t* out, hipStream_t st);
+// ws (optional, argmax_workspace_bytes): two passes over many blocks per row
+int64_t argmax_workspace_bytes(int64_t rows, int64_t N);
+hipError_t launch_argmax(const void* x, int64_t ld, int rows, int N, int64_t* out, void* ws, hipStream_t st);
 
 }  // namespace saga

@@ -395,5 +395,9 @@ def argmax_rows(x, out=None):
     """First index of each row's maximum (bf16 [rows, N]) -> int64 [rows]."""
     _need_gpu(x, out)
     out = torch.empty(x.shape[0], dtype=torch.int64, device=x.device) if out is None else out
-    _lib.check(_lib.load().saga_argmax(_lib.tensor(x), _lib.ptr(out), _lib.stream_of(x)), "argmax")
+    lib = _lib.load()
+    need = lib.saga_argmax_workspace_bytes(x.shape[0], x.shape[1])
+    ws = workspace(x.device, "argmax", need) if need else None
+    _lib.check(lib.saga_argmax(_lib.tensor(x), _lib.ptr(out), _lib.ptr(ws), ws.numel() if ws is not None else 0,
+                               _lib.stream_of(x)), "argmax")
     return out

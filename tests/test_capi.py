@@ -159,6 +159,8 @@ def test_gemv_split_plan():
     """Split-K only for weights with few 16-row tiles and long rows."""
     lib = _lib.load()
     assert lib.saga_gemv_workspace_bytes(8, 1536, 8960) > 0       # MLP down projection
+    assert lib.saga_argmax_workspace_bytes(8, 151936) == 8 * 38 * 8  # 38 chunks of 4096, (value, index) each
+    assert lib.saga_argmax_workspace_bytes(8, 4096) == 0             # one chunk: single pass
     for n, k in ((17920, 1536), (1920, 1536), (1536, 1536), (151936, 1536)):
         assert lib.saga_gemv_workspace_bytes(8, n, k) == 0
 

@@ -176,3 +176,23 @@ def test_packed_rope_kv_projection_identical():
     torch.cuda.synchronize()
     for a, c in zip(outs[0], outs[1]):
         assert torch.equal(a, c)
+
+
+@pytest.mark.parametrize("N", [4097, 151936])
+def test_argmax_two_pass_ties_across_chunks(N):
+    """The two-pass argmax (chunks of 4096 per workgroup) keeps the first
+    index of the maximum when it repeats in later chunks, and agrees with
+    the one-workgroup-per-row pass (no workspace)."""
+    rng = np.random.default_rng(N)
+    x = O.round_bf16(rng.standard_normal((5, N), dtype=np.float32))
+    x[0, [N - 1, 4096, 5000 % N]] = 30.0          # tie: first one wins
+    x[1, :] = -1.0                                 # all equal -> index 0
+    x[2, [3, N - 2]] = 7.0
+    xd = dev(x, "bf16")
+    got = ops.argmax_rows(xd).cpu().numpy()
+    np.testing.assert_array_equal(got, np.argmax(x, axis=1))
+    lib = _lib.load()
+    assert lib.saga_argmax_workspace_bytes(5, N) > 0
+    one = torch.empty(5, dtype=torch.int64, device="cuda")
+    _lib.check(lib.saga_argmax(_lib.tensor(xd), _lib.ptr(one), None, 0, _lib.stream_of(xd)), "argmax")
+    np.testing.assert_array_equal(one.cpu().numpy(), got)
