@@ -18,7 +18,8 @@
 //      position order; the slice's list and count go to the workspace;
 //   3. a list of at most kSliceSmall entries (the usual case) is gathered by
 //      the wave itself in one burst: its (m, l, o) softmax . V partial.
-// Row blocks (atopn_gather_kernel), one 256-thread block per row: a block scan
+// Row blocks (atopn_gather_kernel), one block per row (256 threads when buf_k
+// <= 1024, else 1024): a block scan
 // of the slice counts ranks the slices; exactly the first n = min(total,
 // buf_k) passing positions in ascending order count (the reference keeps a
 // race-dependent subset when more than buf_k pass).  Short slices wholly
@@ -37,8 +38,12 @@ constexpr int kSliceThreads = 256;                    // 4 independent slice wav
 constexpr int kSliceWaves = kSliceThreads / kWave;    // 4
 constexpr int kSliceLoads = kSliceLen / (4 * kWave);  // f32x4 loads per lane: 4
 constexpr int kSlicePrefetch = 4;                     // partials per lane in the first burst
-constexpr int kRowThreads = 1024;
-constexpr int kRowWaves = kRowThreads / kWave;
+// row kernel block: 256 threads when at most 1024 positions count per row
+// (buf_k <= 1024: the partial merge dominates, a small block launches and
+// synchronises faster), 1024 threads for longer lists (block-wide gathers)
+constexpr int kRowThreadsSmall = 256;
+constexpr int kRowThreadsLarge = 1024;
+constexpr int kRowSmallCap = 1024;
 constexpr int kRowBatch = 2048;                       // list entries per LDS batch
 constexpr int kRowMaxSlices = 2048;                   // slice ranks kept in LDS
 constexpr int kRowUnroll = 16;                        // V rows in flight per lane group
@@ -233,11 +238,12 @@ __device__ __forceinline__ int slice_of(const int* pre, int nslice, int j) {
 
 // Exclusive block scans of a(s) and b(s) over s in [0, ns) into pa / pb
 // [0..ns] (pa[ns], pb[ns] = totals; pa may be null); returns the totals.
-template <class FA, class FB>
+template <int NT, class FA, class FB>
 __device__ int2 block_scan_slices(int ns, int* pa, int* pb, int2* wsum, FA fa, FB fb) {
+  constexpr int NW = NT / kWave;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   int ra = 0, rb = 0;
-  for (int c0 = 0; c0 < ns; c0 += kRowThreads) {
+  for (int c0 = 0; c0 < ns; c0 += NT) {
     const int s = c0 + tid;
     const int xa = s < ns ? fa(s) : 0;
     const int xb = s < ns ? fb(s) : 0;
@@ -246,7 +252,7 @@ __device__ int2 block_scan_slices(int ns, int* pa, int* pb, int2* wsum, FA fa, F
     __syncthreads();
     int ba = ra, bb = rb, ta = 0, tb = 0;
 #pragma unroll
-    for (int q = 0; q < kRowWaves; ++q) {
+    for (int q = 0; q < NW; ++q) {
       const int2 v = wsum[q];
       if (q < w) {
         ba += v.x;
@@ -272,17 +278,18 @@ __device__ int2 block_scan_slices(int ns, int* pa, int* pb, int2* wsum, FA fa, F
   return int2{ra, rb};
 }
 
-template <int DT, int D>
-__global__ void __launch_bounds__(kRowThreads) atopn_gather_kernel(FusedSelParams p, PVParams v) {
-  __shared__ float red[kRowWaves];
-  __shared__ int2 wsum[kRowWaves];
+template <int DT, int D, int NT>
+__global__ void __launch_bounds__(NT) atopn_gather_kernel(FusedSelParams p, PVParams v) {
+  constexpr int NW = NT / kWave;
+  __shared__ float red[NW];
+  __shared__ int2 wsum[NW];
   __shared__ int spre[kRowMaxSlices + 1];
   __shared__ int sgpre[kRowMaxSlices + 1];
   __shared__ int sidx[kRowBatch];
   __shared__ float sval[kRowBatch];
-  __shared__ f32x4 accs[kRowThreads];
+  __shared__ f32x4 accs[NT];
   constexpr int C = D / 4;             // 16-byte chunks of an output row
-  constexpr int G = kRowThreads / C;   // slice groups of the partial merge
+  constexpr int G = NT / C;            // slice groups of the partial merge
   const int r = blockIdx.x, tid = threadIdx.x;
   const int c = tid % C, g = tid / C;
   const int ns = p.nslice;
@@ -319,7 +326,7 @@ __global__ void __launch_bounds__(kRowThreads) atopn_gather_kernel(FusedSelParam
     const int cnt = p.sl_cnt[row0 + s];
     return cnt > kSliceSmall ? cnt : 0;
   };
-  const int2 tot = block_scan_slices(ns, pre, gpre, wsum, cnt_of, whole_gather);
+  const int2 tot = block_scan_slices<NT>(ns, pre, gpre, wsum, cnt_of, whole_gather);
   const int total = tot.x;
   const int n = min(total, p.cap);
   // sel_cnt / sel_total are stored at the end: a global store here would make
@@ -333,7 +340,7 @@ __global__ void __launch_bounds__(kRowThreads) atopn_gather_kernel(FusedSelParam
   };
   int ng = tot.y;
   if (total > p.cap) {
-    ng = block_scan_slices(ns, static_cast<int*>(nullptr), gpre, wsum, cnt_of,
+    ng = block_scan_slices<NT>(ns, static_cast<int*>(nullptr), gpre, wsum, cnt_of,
                            [&](int s) { return has_partial(s) ? 0 : take(s); }).y;
   }
 
@@ -360,7 +367,7 @@ __global__ void __launch_bounds__(kRowThreads) atopn_gather_kernel(FusedSelParam
     float mb = kNegInf;
 #pragma unroll
     for (int u = 0; u < kRowMergeSlices; ++u) mb = fmaxf(mb, ms[u]);
-    const float Mn = fmaxf(M, block_max<kRowWaves>(mb, red));
+    const float Mn = fmaxf(M, block_max<NW>(mb, red));
     const float rescale = M == kNegInf ? 0.f : __expf(M - Mn);
     lsum *= rescale;
 #pragma unroll
@@ -377,7 +384,7 @@ __global__ void __launch_bounds__(kRowThreads) atopn_gather_kernel(FusedSelParam
     }
   }
   // l is the same in every thread of a slice group: one thread per group adds it
-  float L = block_sum<kRowWaves>(c == 0 ? lsum : 0.f, red);
+  float L = block_sum<NW>(c == 0 ? lsum : 0.f, red);
   accs[tid] = on;
   __syncthreads();
   f32x4 o = {0.f, 0.f, 0.f, 0.f};
@@ -396,12 +403,12 @@ __global__ void __launch_bounds__(kRowThreads) atopn_gather_kernel(FusedSelParam
   if (ng > 0) {
     const int vh = h / (v.q_h / v.v_h);
     const char* vbase = v.v + (bi * v.v_sb + static_cast<int64_t>(vh) * v.v_sh) * Elt<DT>::kBytes;
-    BlockPV<DT, D, kRowThreads, kRowUnroll> pv;
+    BlockPV<DT, D, NT, kRowUnroll> pv;
     pv.init();
     for (int b0 = 0; b0 < ng; b0 += kRowBatch) {
       const int nb = min(kRowBatch, ng - b0);
       __syncthreads();  // the LDS list of the previous batch (or accs) is free
-      for (int i = tid; i < nb; i += kRowThreads) {
+      for (int i = tid; i < nb; i += NT) {
         const int j = b0 + i;
         const int s = slice_of(gpre, ns, j);
         const int64_t src = (row0 + s) * p.slice_cap + (j - gpre[s]);
@@ -440,14 +447,24 @@ __global__ void __launch_bounds__(kRowThreads) atopn_gather_kernel(FusedSelParam
 }
 
 template <int DT, int D>
+static hipError_t launch_rows_typed(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
+  if (p.cap <= kRowSmallCap)
+    hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsSmall>), dim3(p.nrows), dim3(kRowThreadsSmall), 0, st, p,
+                       v);
+  else
+    hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsLarge>), dim3(p.nrows), dim3(kRowThreadsLarge), 0, st, p,
+                       v);
+  return hipGetLastError();
+}
+
+template <int DT, int D>
 static hipError_t launch_split(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
   const int64_t waves = static_cast<int64_t>(p.nslice) * p.nrows;
   const unsigned blocks = static_cast<unsigned>((waves + kSliceWaves - 1) / kSliceWaves);
   hipLaunchKernelGGL((atopn_slice_kernel<DT, D>), dim3(blocks), dim3(kSliceThreads), 0, st, p, v);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((atopn_gather_kernel<DT, D>), dim3(p.nrows), dim3(kRowThreads), 0, st, p, v);
-  return hipGetLastError();
+  return launch_rows_typed<DT, D>(p, v, st);
 }
 
 template <int DT>
@@ -457,11 +474,7 @@ static hipError_t launch_split_d(const FusedSelParams& p, const PVParams& v, hip
 
 template <int DT>
 static hipError_t launch_rows_d(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
-  if (v.d == 128)
-    hipLaunchKernelGGL((atopn_gather_kernel<DT, 128>), dim3(p.nrows), dim3(kRowThreads), 0, st, p, v);
-  else
-    hipLaunchKernelGGL((atopn_gather_kernel<DT, 64>), dim3(p.nrows), dim3(kRowThreads), 0, st, p, v);
-  return hipGetLastError();
+  return v.d == 128 ? launch_rows_typed<DT, 128>(p, v, st) : launch_rows_typed<DT, 64>(p, v, st);
 }
 
 hipError_t launch_atopn_rows(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
