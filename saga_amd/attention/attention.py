@@ -24,8 +24,14 @@ from typing import Optional, Tuple
 import torch
 
 from .. import _lib, ops
+from .. import torch_ops  # noqa: F401  (registers torch.ops.saga.*)
 
 _lib.load()  # fail at import when the HIP library is missing
+
+# The decode entry points below call the kernels through torch.ops.saga.*
+# (torch.library custom operators with fake implementations), so that
+# torch.compile'd callers (speedup.py:502-508) trace them as graph nodes.
+_saga = torch.ops.saga
 
 
 def _expand_heads(x: torch.Tensor, n_rep: int) -> torch.Tensor:
@@ -88,7 +94,7 @@ def full_einsum_forward(query, key, value, attention_mask=None, is_causal=False,
     Returns [b, q_h, 1, d] in the input dtype."""
     if query.shape[2] != 1:
         raise NotImplementedError("full_einsum_forward: the MI355X build implements the decode case (l_q == 1)")
-    return ops.dense_decode(query, key, value, attention_mask, scaling)
+    return _saga.dense_decode(query, key, value, attention_mask, scaling)
 
 
 # =============================================================================
@@ -159,7 +165,7 @@ def approx_top_n_attention_amortized_cal(query, key, value, attention_mask=None,
     output = renormalised top-k probabilities . V."""
     b, q_h = query.shape[0], query.shape[1]
     row = _table_row(layer_idx, b * q_h)
-    return ops.atopn_calibrate(query, key, value, top_n_attention, row, attention_mask, scaling)
+    return _saga.atopn_calibrate(query, key, value, row, top_n_attention, attention_mask, scaling)
 
 
 def approx_top_n_attention_amortized(query, key, value, attention_mask=None, is_causal=False,
@@ -169,4 +175,4 @@ def approx_top_n_attention_amortized(query, key, value, attention_mask=None, is_
     (at most 2 * top_n_attention), sparse softmax . V over those rows."""
     b, q_h = query.shape[0], query.shape[1]
     row = _table_row(layer_idx, b * q_h)
-    return ops.atopn_decode(query, key, value, row, top_n_attention, attention_mask, scaling)
+    return _saga.atopn_decode(query, key, value, row, top_n_attention, attention_mask, scaling)

@@ -27,6 +27,7 @@ import torch
 
 from . import ops
 from .attention.attention import sdpa_attention_forward
+from .kv_cache import KVCache, kv_cache_bytes  # noqa: F401  (kv_cache_bytes re-exported)
 
 
 @dataclass(frozen=True)
@@ -57,11 +58,6 @@ QWEN25_15B_GQA = replace(QWEN25_15B_SAGA, n_k=2)
 SMOLLM2_360M_SAGA = DecoderShape(32, 960, 15, 1, 5, 64, 2560, 49152, 1e5, 1e-5, False)
 
 
-def kv_cache_bytes(shape: DecoderShape, batch: int, max_len: int, dtype=torch.bfloat16) -> int:
-    es = torch.tensor([], dtype=dtype).element_size()
-    return shape.layers * batch * (shape.n_k + shape.n_v) * max_len * shape.head_dim * es
-
-
 class _HeadGroups(torch.nn.Module):
     """Stand-in for the HF attention module passed to sdpa_attention_forward."""
     num_key_value_groups = 1
@@ -83,10 +79,6 @@ class SagaDecoder:
         self.shape, self.batch, self.max_len, self.mode, self.top_n = shape, batch, max_len, mode, top_n
         self.exempt = set(exempt_layers)
         self.device, self.dtype = torch.device(device), dtype
-        free, _ = torch.cuda.mem_get_info(self.device)
-        need = kv_cache_bytes(shape, batch, max_len, dtype)
-        if need > 0.8 * free:
-            raise MemoryError(f"KV cache of {need / 2**30:.1f} GiB does not fit in {free / 2**30:.1f} GiB free HBM")
         g = torch.Generator(device=self.device).manual_seed(seed)
         s, d = shape, shape.head_dim
 
@@ -104,8 +96,8 @@ class SagaDecoder:
         self.w_d = [w(s.hidden, s.intermediate) for _ in range(s.layers)]
         self.ln_f = torch.ones(s.hidden, device=self.device, dtype=dtype)
         # separate key-head and value-head caches [layer][batch, heads, max_len, d]
-        self.k_cache = torch.zeros(s.layers, batch, s.n_k, max_len, d, device=self.device, dtype=dtype)
-        self.v_cache = torch.zeros(s.layers, batch, s.n_v, max_len, d, device=self.device, dtype=dtype)
+        self.kv = KVCache(s, batch, max_len, self.device, dtype)
+        self.k_cache, self.v_cache = self.kv.k, self.kv.v
         # Atop-N threshold table, rows = batch * n_q (attention/attention.py:92-99)
         self.table = torch.zeros(max(s.layers, 1), batch * s.n_q, device=self.device, dtype=torch.float32)
         # static decode-step state (fixed addresses for graph replay)
