@@ -22,7 +22,14 @@
 
 namespace saga {
 
-constexpr int kDenseSub = 16;  // positions per wave step (one MFMA tile)
+constexpr int kDenseSubDefault = 16;  // positions per wave step (MFMA tiles of 16)
+
+// Wave-local LDS ordering: the P and alpha buffers of a wave are private to it.
+__device__ __forceinline__ void dense_wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 // One V row per wave load: lane l holds dims [l*DL, l*DL + DL), DL = D / 64.
 template <int DT, int DL>
@@ -47,7 +54,7 @@ struct VLane {
   }
 };
 
-template <int DT, int D>
+template <int DT, int D, int kDenseSub>
 __global__ void __launch_bounds__(256) dense_split_kernel(DenseParams p) {
   using E = Elt<DT>;
   constexpr int E16 = E::kPer16B;
@@ -160,7 +167,7 @@ __global__ void __launch_bounds__(256) dense_split_kernel(DenseParams p) {
       m_run = m_new;
       if (s == 0) Al[w][col] = alpha;
     }
-    __syncthreads();
+    dense_wave_sync();  // this wave's P and alpha (waves advance independently)
     if (active) {
       {
         const f32x4* a4 = reinterpret_cast<const f32x4*>(&Al[w][0]);
@@ -205,7 +212,7 @@ __global__ void __launch_bounds__(256) dense_split_kernel(DenseParams p) {
         }
       }
     }
-    __syncthreads();
+    dense_wave_sync();  // P is rewritten by this wave's next step
   }
 
   if (s == 0) {
@@ -287,10 +294,10 @@ static hipError_t launch_dense_typed(int d, const DenseParams& p, hipStream_t st
   const unsigned blocks = static_cast<unsigned>(p.b * p.k_h * p.nsplit);
   const unsigned heads = static_cast<unsigned>(p.b * p.k_h * p.g);
   if (d == 128) {
-    hipLaunchKernelGGL((dense_split_kernel<DT, 128>), dim3(blocks), dim3(256), 0, st, p);
+    hipLaunchKernelGGL((dense_split_kernel<DT, 128, kDenseSubDefault>), dim3(blocks), dim3(256), 0, st, p);
     if (p.nsplit > 1) hipLaunchKernelGGL((dense_merge_kernel<128>), dim3(heads), dim3(128), 0, st, p);
   } else {
-    hipLaunchKernelGGL((dense_split_kernel<DT, 64>), dim3(blocks), dim3(256), 0, st, p);
+    hipLaunchKernelGGL((dense_split_kernel<DT, 64, kDenseSubDefault>), dim3(blocks), dim3(256), 0, st, p);
     if (p.nsplit > 1) hipLaunchKernelGGL((dense_merge_kernel<64>), dim3(heads), dim3(64), 0, st, p);
   }
   return hipGetLastError();
