@@ -196,3 +196,18 @@ def test_argmax_two_pass_ties_across_chunks(N):
     one = torch.empty(5, dtype=torch.int64, device="cuda")
     _lib.check(lib.saga_argmax(_lib.tensor(xd), _lib.ptr(one), None, 0, _lib.stream_of(xd)), "argmax")
     np.testing.assert_array_equal(one.cpu().numpy(), got)
+
+
+def test_split_k_shapes_share_one_workspace():
+    """Split-K calls of different shapes, one after the other on the cached
+    workspace (the tile counters sit at a fixed offset and are left at zero):
+    each matches its single-pass result."""
+    rng = np.random.default_rng(90)
+    for M, K, N in [(8, 2560, 960), (8, 8960, 1536), (4, 2560, 960), (8, 8960, 1536), (2, 4096, 256)]:
+        x, w, _ = _data(rng, M, K, N)
+        xd, wd = dev(x, "bf16"), dev(w, "bf16")
+        for rms in (None, 1e-6):
+            a = ops.gemv(xd, wd, rms_eps=rms, split_k=False)
+            b = ops.gemv(xd, wd, rms_eps=rms, split_k=True)
+            torch.cuda.synchronize()
+            assert torch.allclose(a.float(), b.float(), rtol=2 ** -7, atol=2e-3), (M, K, N, rms)
