@@ -230,14 +230,35 @@ def sweep(copies=8):
     return 0
 
 
+def _shapes():
+    from saga_amd import decoder as D
+    return D
+
+
+# workloads: the headline (the metric's 1.5B shape at 32k, batch 8, 256 steps,
+# N=512) and the SmolLM2-360M-shaped decoder (batch 1, 8192-token prompt, 128
+# greedy tokens, N=256; its dense-GQA comparator keeps 5 key/value heads)
+MODELS = {
+    "qwen2.5-1.5b": dict(name="Qwen2.5-1.5B", shape=lambda: _shapes().QWEN25_15B_SAGA,
+                         gqa=lambda: _shapes().QWEN25_15B_GQA, batch=8, ctx=32768, top_n=512, steps=256,
+                         metric=None),
+    "smollm2-360m": dict(name="SmolLM2-360M", shape=lambda: _shapes().SMOLLM2_360M_SAGA,
+                         gqa=lambda: _shapes().SMOLLM2_360M_GQA, batch=1, ctx=8192, top_n=256, steps=128,
+                         metric="decode tokens/sec @360M-shape 8k ctx, batch 1"),
+}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--model", choices=sorted(MODELS), default="qwen2.5-1.5b",
+                    help="workload: the 1.5B-shaped decoder at 32k (the headline) or the SmolLM2-360M-shaped "
+                         "decoder at 8k (batch 1, 128 greedy tokens, N=256)")
+    ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--batch", type=int, default=8)
-    ap.add_argument("--ctx", type=int, default=32768)
-    ap.add_argument("--top-n", type=int, default=512)
+    ap.add_argument("--batch", type=int, default=None)
+    ap.add_argument("--ctx", type=int, default=None)
+    ap.add_argument("--top-n", type=int, default=None)
     ap.add_argument("--no-dense", action="store_true", help="skip the dense-GQA comparator")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--synthetic-kv", action="store_true", help="fill the caches with N(0,1) instead of a prefill")
@@ -259,19 +280,25 @@ def main():
         return 2
 
     from saga_amd import ops
-    from saga_amd.decoder import QWEN25_15B_GQA, QWEN25_15B_SAGA, SagaDecoder
+    from saga_amd.decoder import SagaDecoder
+
+    mdl = MODELS[args.model]
+    SAGA_SHAPE, GQA_SHAPE = mdl["shape"](), mdl["gqa"]()
+    for k in ("batch", "ctx", "top_n", "steps"):
+        if getattr(args, k) is None:
+            setattr(args, k, mdl[k])
 
     if args.no_fused:
         ops.set_fused_fast_step(False)
 
     B, ctx, K, W = args.batch, args.ctx, args.steps, args.warmup
     if args.profile_kernels:
-        return profile_kernels(B, ctx, QWEN25_15B_SAGA)
+        return profile_kernels(B, ctx, SAGA_SHAPE)
     if args.sweep:
         return sweep()
     max_len = ctx + K
     torch.manual_seed(0)
-    prompt = torch.randint(0, QWEN25_15B_SAGA.vocab, (ctx,), dtype=torch.int64)
+    prompt = torch.randint(0, SAGA_SHAPE.vocab, (ctx,), dtype=torch.int64)
 
     def build(shape, mode):
         m = SagaDecoder(shape, B, max_len, mode=mode, top_n=args.top_n)
@@ -285,8 +312,8 @@ def main():
         m.capture()
         return m
 
-    log("SAGA model (12Q/1K/2V, Atop-N)")
-    saga = build(QWEN25_15B_SAGA, "atopn")
+    log(f"SAGA model ({SAGA_SHAPE.n_q}Q/{SAGA_SHAPE.n_k}K/{SAGA_SHAPE.n_v}V, Atop-N)")
+    saga = build(SAGA_SHAPE, "atopn")
     ms, tps, wall = decode_rate(saga, K, W)
     log(f"SAGA decode: {ms:.3f} ms/step, {tps:.0f} tokens/s (host wall {wall:.3f}s)")
 
@@ -309,8 +336,8 @@ def main():
 
     dense = None
     if not args.no_dense:
-        log("dense-GQA comparator (12Q/2K/2V, dense decode)")
-        gqa = build(QWEN25_15B_GQA, "dense")
+        log(f"dense-GQA comparator ({GQA_SHAPE.n_q}Q/{GQA_SHAPE.n_k}K/{GQA_SHAPE.n_v}V, dense decode)")
+        gqa = build(GQA_SHAPE, "dense")
         d_ms, d_tps, _ = decode_rate(gqa, K, W)
         gs = gqa.shape
         dq = gqa._q.view(B, gs.n_q, 1, gs.head_dim)
@@ -326,12 +353,12 @@ def main():
     cpu = None
     if not args.no_cpu:
         log("CPU baseline (oracle, fp32)")
-        cpu = cpu_baseline(B, ctx, QWEN25_15B_SAGA, args.top_n, QWEN25_15B_SAGA.layers)
+        cpu = cpu_baseline(B, ctx, SAGA_SHAPE, args.top_n, SAGA_SHAPE.layers)
         log(f"CPU: {cpu['value']} attention tokens/s on {cpu['cores']} cores")
 
-    traffic, traffic_src = k1_traffic(B, ctx, QWEN25_15B_SAGA)
+    traffic, traffic_src = k1_traffic(B, ctx, SAGA_SHAPE)
     out = {
-        "metric": METRIC,
+        "metric": METRIC if args.model == "qwen2.5-1.5b" else mdl["metric"],
         "value": round(tps, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -344,15 +371,17 @@ def main():
         "dtype": "bf16",
         "data": "synthetic: random-init weights, random prompt ids" + (", N(0,1) KV cache" if args.synthetic_kv else ""),
         "config": {
-            "workload": (f"Qwen2.5-1.5B-shaped SAGA decoder (28 layers, hidden 1536, 12Q/1K/2V heads, d128, "
-                         f"vocab 151936), batch {B}, {ctx}-token context, {K} decode steps, Atop-N N={args.top_n}"),
+            "workload": (f"{mdl['name']}-shaped SAGA decoder ({SAGA_SHAPE.layers} layers, hidden {SAGA_SHAPE.hidden}, "
+                         f"{SAGA_SHAPE.n_q}Q/{SAGA_SHAPE.n_k}K/{SAGA_SHAPE.n_v}V heads, d{SAGA_SHAPE.head_dim}, "
+                         f"vocab {SAGA_SHAPE.vocab}), batch {B}, {ctx}-token context, {K} decode steps, "
+                         f"Atop-N N={args.top_n}"),
             "global_batch": B,
             "seq_len": ctx,
             "parallelism": "single GPU",
             "kv_cache": {"k": list(saga_cache[0]), "v": list(saga_cache[1]), "dtype": "bf16"},
         },
         "roofline": {
-            "kernel": "saga::qk_scores_kernel<bf16,128> (K1)",
+            "kernel": f"saga::qk_scores_kernel<bf16,{SAGA_SHAPE.head_dim}> (K1)",
             "bound": "hbm",
             "achieved": round(k1_gbs, 1),
             "peak": HBM_PEAK_GBS,
@@ -364,7 +393,7 @@ def main():
             "algorithmic_bytes_per_launch": k1_bytes,
         },
         "attention_us_per_layer": round(attn_us, 2),
-        "attention_tokens_per_s_gpu": round(B / (attn_us * 1e-6 * QWEN25_15B_SAGA.layers), 1),
+        "attention_tokens_per_s_gpu": round(B / (attn_us * 1e-6 * SAGA_SHAPE.layers), 1),
         "dense_gqa": dense,
         "cpu_baseline": cpu,
     }

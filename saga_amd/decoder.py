@@ -56,6 +56,7 @@ QWEN25_15B_SAGA = DecoderShape(28, 1536, 12, 1, 2, 128, 8960, 151936, 1e6, 1e-6,
 QWEN25_15B_GQA = replace(QWEN25_15B_SAGA, n_k=2)
 # SmolLM2-360M with 1 key head / 5 value heads (Llama: no q/k/v bias).
 SMOLLM2_360M_SAGA = DecoderShape(32, 960, 15, 1, 5, 64, 2560, 49152, 1e5, 1e-5, False)
+SMOLLM2_360M_GQA = replace(SMOLLM2_360M_SAGA, n_k=5)
 
 
 class _HeadGroups(torch.nn.Module):
