@@ -5,8 +5,9 @@ separate key-head / value-head KV caches (initialize_kv_cache, :119-139), a
 batch-1 prefill replicated to the whole batch (prefill, :146-161), and decode
 steps captured as two HIP graphs -- one for the Atop-N calibration step and
 one for the fast steps -- replayed once per token (capture_cuda_graphs /
-decode_with_graph, :179-291).  Weights are random (no checkpoints here); the
-shapes are the benchmarked models'.
+decode_with_graph, :179-291).  Weights are random by default (the benchmarked
+models' shapes) or come from a SAGA checkpoint (saga_amd.checkpoint,
+SagaDecoder.from_pretrained).
 
 Per layer and step (7 launches): q/k/v projection with the RMSNorm and bias
 fused -> RoPE + cache append -> attention (Atop-N: scores, then
@@ -74,7 +75,7 @@ class SagaDecoder:
 
     def __init__(self, shape: DecoderShape, batch: int, max_len: int, mode: str = "atopn", top_n: int = 512,
                  exempt_layers=(), device="cuda", dtype=torch.bfloat16, seed: int = 0, fuse_rope: bool = True,
-                 pack_weights: bool = True):
+                 pack_weights: bool = True, weights: Optional[dict] = None):
         if mode not in ("atopn", "dense"):
             raise ValueError(f"mode must be 'atopn' or 'dense', got {mode!r}")
         self.shape, self.batch, self.max_len, self.mode, self.top_n = shape, batch, max_len, mode, top_n
@@ -83,19 +84,23 @@ class SagaDecoder:
         g = torch.Generator(device=self.device).manual_seed(seed)
         s, d = shape, shape.head_dim
 
-        def w(*size, std=0.02):
-            return (torch.randn(*size, generator=g, device=self.device, dtype=torch.float32) * std).to(dtype)
+        if weights is not None:
+            self._take_weights(weights)
+        else:
+            def w(*size, std=0.02):
+                return (torch.randn(*size, generator=g, device=self.device, dtype=torch.float32) * std).to(dtype)
 
-        self.embed = w(s.vocab, s.hidden)  # tied with the LM head
-        self.ln1 = [torch.ones(s.hidden, device=self.device, dtype=dtype) for _ in range(s.layers)]
-        self.ln2 = [torch.ones(s.hidden, device=self.device, dtype=dtype) for _ in range(s.layers)]
-        self.w_qkv = [w(s.qkv_width, s.hidden) for _ in range(s.layers)]
-        self.b_qkv = [w(s.qkv_width) if s.qkv_bias else torch.zeros(s.qkv_width, device=self.device, dtype=dtype)
-                      for _ in range(s.layers)]
-        self.w_o = [w(s.hidden, s.n_q * d) for _ in range(s.layers)]
-        self.w_gu = [w(2 * s.intermediate, s.hidden) for _ in range(s.layers)]
-        self.w_d = [w(s.hidden, s.intermediate) for _ in range(s.layers)]
-        self.ln_f = torch.ones(s.hidden, device=self.device, dtype=dtype)
+            self.embed = w(s.vocab, s.hidden)
+            self.lm_head = self.embed  # tied
+            self.ln1 = [torch.ones(s.hidden, device=self.device, dtype=dtype) for _ in range(s.layers)]
+            self.ln2 = [torch.ones(s.hidden, device=self.device, dtype=dtype) for _ in range(s.layers)]
+            self.w_qkv = [w(s.qkv_width, s.hidden) for _ in range(s.layers)]
+            self.b_qkv = [w(s.qkv_width) if s.qkv_bias else torch.zeros(s.qkv_width, device=self.device, dtype=dtype)
+                          for _ in range(s.layers)]
+            self.w_o = [w(s.hidden, s.n_q * d) for _ in range(s.layers)]
+            self.w_gu = [w(2 * s.intermediate, s.hidden) for _ in range(s.layers)]
+            self.w_d = [w(s.hidden, s.intermediate) for _ in range(s.layers)]
+            self.ln_f = torch.ones(s.hidden, device=self.device, dtype=dtype)
         # separate key-head and value-head caches [layer][batch, heads, max_len, d]
         self.kv = KVCache(s, batch, max_len, self.device, dtype)
         self.k_cache, self.v_cache = self.kv.k, self.kv.v
@@ -124,6 +129,55 @@ class SagaDecoder:
         self.graph_fast: Optional[torch.cuda.CUDAGraph] = None
         self.prompt_len = 0
 
+    # (attribute, shape as a function of the decoder shape) of every weight
+    _WEIGHT_SHAPES = {
+        "embed": lambda s: (s.vocab, s.hidden),
+        "lm_head": lambda s: (s.vocab, s.hidden),
+        "ln_f": lambda s: (s.hidden,),
+        "ln1": lambda s: (s.hidden,),
+        "ln2": lambda s: (s.hidden,),
+        "w_qkv": lambda s: (s.qkv_width, s.hidden),
+        "b_qkv": lambda s: (s.qkv_width,),
+        "w_o": lambda s: (s.hidden, s.n_q * s.head_dim),
+        "w_gu": lambda s: (2 * s.intermediate, s.hidden),
+        "w_d": lambda s: (s.hidden, s.intermediate),
+    }
+    _PER_LAYER = ("ln1", "ln2", "w_qkv", "b_qkv", "w_o", "w_gu", "w_d")
+
+    def _take_weights(self, weights: dict) -> None:
+        """Weights given as tensors in the decoder's layout (one per name of
+        _WEIGHT_SHAPES; per-layer names hold a list; lm_head None = tied),
+        moved to the decoder's device and dtype, shapes checked."""
+        s = self.shape
+        for name, shape_of in self._WEIGHT_SHAPES.items():
+            want = tuple(shape_of(s))
+            val = weights.get(name)
+            if name == "lm_head" and val is None:
+                continue
+            if val is None:
+                raise KeyError(f"weights: missing {name!r}")
+            vals = val if name in self._PER_LAYER else [val]
+            if name in self._PER_LAYER and len(vals) != s.layers:
+                raise ValueError(f"weights: {name!r} has {len(vals)} layers, the shape {s.layers}")
+            out = []
+            for t in vals:
+                if tuple(t.shape) != want:
+                    raise ValueError(f"weights: {name!r} is {tuple(t.shape)}, the shape needs {want}")
+                out.append(t.to(device=self.device, dtype=self.dtype).contiguous())
+            setattr(self, name, out if name in self._PER_LAYER else out[0])
+        if weights.get("lm_head") is None:
+            self.lm_head = self.embed
+
+    @classmethod
+    def from_pretrained(cls, path: str, batch: int, max_len: int, num_key_heads: Optional[int] = None,
+                        **kwargs) -> "SagaDecoder":
+        """A decoder with the weights of a SAGA (or plain GQA) checkpoint
+        directory: config.json + safetensors (saga_amd.checkpoint).
+        num_key_heads merges a checkpoint's key heads at load time."""
+        from .checkpoint import load_checkpoint
+        shape, weights = load_checkpoint(path, num_key_heads=num_key_heads)
+        return cls(shape, batch, max_len, weights=weights, **kwargs)
+
     def prepare_kernel_weights(self) -> None:
         """Decode-layout copies of the weights for the skinny GEMM: RMSNorm
         weights folded into the following projection (w * diag(norm)), gate
@@ -146,7 +200,7 @@ class SagaDecoder:
                 w = (self.w_gu[l].float() * self.ln2[l].float()).to(self.dtype)
                 self.kw_gu.append(torch.stack([w[:s.intermediate], w[s.intermediate:]], dim=1)
                                   .reshape(2 * s.intermediate, s.hidden).contiguous())
-            self.kw_lm = (self.embed.float() * self.ln_f.float()).to(self.dtype)
+            self.kw_lm = (self.lm_head.float() * self.ln_f.float()).to(self.dtype)
             self.kw_o = list(self.w_o)
             self.kw_d = list(self.w_d)
             if self.pack_weights:
@@ -187,7 +241,7 @@ class SagaDecoder:
                 gu = torch.mm(ops.rmsnorm(xc, self.ln2[l], s.eps), self.w_gu[l].t())
                 xc.addmm_(ops.silu_mul(gu), self.w_d[l].t())
         last = ops.rmsnorm(x[-1:], self.ln_f, s.eps)
-        first = torch.mm(last, self.embed.t()).argmax(dim=-1)
+        first = torch.mm(last, self.lm_head.t()).argmax(dim=-1)
         self.k_cache[:, 1:, :, :T] = self.k_cache[:, 0:1, :, :T]
         self.v_cache[:, 1:, :, :T] = self.v_cache[:, 0:1, :, :T]
         self.prompt_len = T
@@ -256,7 +310,7 @@ class SagaDecoder:
             ops.argmax_rows(self._logits, out=self.tokens)
         else:
             ops.rmsnorm(x, self.ln_f, s.eps, out=self._h)
-            torch.mm(self._h, self.embed.t(), out=self._logits)
+            torch.mm(self._h, self.lm_head.t(), out=self._logits)
             torch.argmax(self._logits, dim=-1, out=self.tokens)
         self.pos.add_(1)
         self.kv_len.add_(1)
