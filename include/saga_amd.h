@@ -287,6 +287,26 @@ size_t saga_argmax_workspace_bytes(int64_t rows, int64_t N);
 int saga_argmax(const saga_tensor* x, int64_t* out, void* workspace, size_t workspace_bytes,
                 saga_stream_t stream);
 
+/* ---- prefill ---- */
+
+/* Prefill attention with separate key and value head counts; replaces the
+ * reference's sdpa_attention_forward (attention/attention.py:13-53: torch SDPA
+ * over repeat_kv-expanded keys and values) without expanding the caches.
+ *   out[b, i, h, :] = sum_j softmax_j(scale * q[b, h, i] . k[b, h / (q_h/k_h), j]
+ *                                     + mask[b, h, i, j]) * v[b, h / (q_h/v_h), j]
+ * query [b, q_h, Lq, d], key [b, k_h, Lk, d], value [b, v_h, Lk, d] (bf16 or
+ * f16, d in {64, 128}, innermost stride 1, 16-byte aligned rows); out
+ * [b, Lq, q_h, d] of the same dtype: the layout the reference returns after
+ * its transpose(1, 2).  mask (optional) [b | 1, q_h | 1, Lq, Lk]: bool keeps
+ * True entries (False -> -inf), f32 / bf16 / f16 are added to the scaled
+ * scores, as in torch SDPA.  causal != 0: key j is visible to query i only if
+ * j <= i + causal_offset (SDPA's is_causal is causal_offset = 0; a chunk of
+ * queries after P cached positions uses causal_offset = P).  A query that
+ * sees no key gets 0 (torch SDPA's math path does the same). */
+int saga_prefill_attention(const saga_tensor* query, const saga_tensor* key, const saga_tensor* value,
+                           const saga_tensor* mask, float scale, int32_t causal, int64_t causal_offset,
+                           saga_tensor* out, saga_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

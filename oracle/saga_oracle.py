@@ -28,6 +28,10 @@ How each function is pinned (tests/test_oracle.py):
   calibrate          golden vectors + brute-force sort / k-th order statistic
   fast               golden vectors (composition of the above)
   dense              golden vectors + torch scaled_dot_product_attention
+  prefill            torch scaled_dot_product_attention on repeat_kv-expanded
+                     heads (causal, bool and float masks) + causality and
+                     single-key closed forms (no reference golden vectors
+                     exist for the prefill path)
 The only behaviour not pinned by the reference is the overflow rule of
 threshold_select (more than k elements pass): the reference keeps a
 race-dependent subset (attention/triton_atopn.py:47-53); this oracle and the
@@ -228,6 +232,40 @@ def dense(query, key, value, attention_mask=None, scaling=None):
     pv = p.reshape(b, v_h, (q_h // v_h) * l_q, L)                   # :81
     out = np.matmul(pv, value.astype(p.dtype))                      # :82-83
     return out.reshape(b, q_h, l_q, d)
+
+
+def prefill(query, key, value, attention_mask=None, scaling=None, is_causal=None):
+    """Prefill attention, attention/attention.py:13-53 (sdpa_attention_forward).
+
+    Keys and values are expanded to the query heads by repeat_kv (:24-26:
+    query head h reads key head h // (q_h // k_h), value head
+    h // (q_h // v_h)); the mask is cut to the key length (:28-30); with
+    is_causal None the call is causal iff l_q > 1 and there is no mask
+    (:35-36; SDPA's causal mask is top-left: key j <= query i); then SDPA
+    (:41-49): softmax(q k^T * scale + mask) v, a bool mask keeping True
+    entries.  A query that sees no key gives 0 (torch's math path).
+    Returns [b, l_q, q_h, d] (:50, transpose(1, 2))."""
+    q = np.asarray(query)
+    dt = np.result_type(q.dtype, np.float32)
+    q = q.astype(dt)
+    b, q_h, l_q, d = q.shape
+    k = np.repeat(np.asarray(key, dtype=dt), q_h // key.shape[1], axis=1)      # :24
+    v = np.repeat(np.asarray(value, dtype=dt), q_h // value.shape[1], axis=1)  # :25
+    L = k.shape[2]
+    mask = None if attention_mask is None else np.asarray(attention_mask)[:, :, :, :L]  # :28-30
+    if is_causal is None:
+        is_causal = l_q > 1 and mask is None                        # :35-36
+    x = np.matmul(q, np.swapaxes(k, -1, -2)) * dt.type(_scale(q, scaling))
+    if mask is not None:
+        x = np.where(mask, x, -np.inf) if mask.dtype == np.bool_ else x + mask.astype(dt)
+    if is_causal:
+        x = np.where(np.arange(L)[None, :] <= np.arange(l_q)[:, None], x, -np.inf)
+    m = x.max(axis=-1, keepdims=True)
+    m = np.where(np.isfinite(m), m, 0)
+    e = np.exp(x - m)
+    ssum = e.sum(axis=-1, keepdims=True)
+    out = np.matmul(e / np.where(ssum > 0, ssum, 1), v)            # :41-49
+    return np.ascontiguousarray(np.swapaxes(out, 1, 2))             # :50
 
 
 def truncate_kv(key, value, kv_len):

@@ -3,9 +3,10 @@
 Same public names, signatures, module globals and return conventions as the
 reference (noamelata/SAGA, attention/attention.py), so its callers
 (speedup.py, lm_eval_saga.py) import this module unchanged.  Decode calls
-(l_q == 1) run the HIP kernels of libsaga_amd.so; prefill stays on torch's
-scaled_dot_product_attention, as in the reference (:13-53).  There is no
-CPU path: tensors must be on a ROCm device.
+(l_q == 1) run the HIP kernels of libsaga_amd.so; prefill of bf16 / f16
+operands with head_dim 64 / 128 runs the HIP prefill kernel on the
+unexpanded caches, other prefill operands torch's
+scaled_dot_product_attention, as in the reference (:13-53).
 
 Deliberate differences from the reference (results otherwise agree with its
 fp32 path within rounding):
@@ -43,7 +44,7 @@ def _expand_heads(x: torch.Tensor, n_rep: int) -> torch.Tensor:
 
 
 # =============================================================================
-# Prefill (torch SDPA with separate key / value head expansion)
+# Prefill (separate key / value head maps)
 # =============================================================================
 
 def sdpa_attention_forward(
@@ -57,13 +58,11 @@ def sdpa_attention_forward(
         is_causal: Optional[bool] = None,
         **kwargs,
 ) -> Tuple[torch.Tensor, None]:
-    """attention/attention.py:13-53: key heads are expanded by q_h / k_h and
-    value heads by q_h / v_h (they differ in SAGA), then torch SDPA.
-    Returns ([b, l_q, q_h, d] contiguous, None)."""
-    if hasattr(module, "num_key_value_groups"):
-        n_q = query.shape[-3]
-        key = _expand_heads(key, n_q // key.shape[-3])
-        value = _expand_heads(value, n_q // value.shape[-3])
+    """attention/attention.py:13-53: attention over keys expanded by q_h / k_h
+    and values by q_h / v_h (they differ in SAGA).  CUDA bf16 / f16 operands
+    with d 64 / 128 run the HIP prefill kernel on the unexpanded caches
+    (torch.ops.saga.prefill_attention); other operands keep the reference's
+    expansion + torch SDPA.  Returns ([b, l_q, q_h, d] contiguous, None)."""
     mask = attention_mask
     if mask is not None:
         mask = mask[:, :, :, : key.shape[-2]]
@@ -71,6 +70,15 @@ def sdpa_attention_forward(
         is_causal = query.shape[2] > 1 and mask is None
     if torch.jit.is_tracing() and isinstance(is_causal, torch.Tensor):
         is_causal = is_causal.item()
+    expand = hasattr(module, "num_key_value_groups")
+    same_heads = key.shape[-3] == query.shape[-3] and value.shape[-3] == query.shape[-3]
+    if (expand or same_heads) and not (is_causal and mask is not None) \
+            and ops.prefill_supported(query, key, value, mask, dropout):
+        return _saga.prefill_attention(query, key, value, mask, scaling, bool(is_causal)), None
+    if expand:
+        n_q = query.shape[-3]
+        key = _expand_heads(key, n_q // key.shape[-3])
+        value = _expand_heads(value, n_q // value.shape[-3])
     out = torch.nn.functional.scaled_dot_product_attention(
         query.contiguous(), key.contiguous(), value.contiguous(),
         attn_mask=mask, dropout_p=dropout, scale=scaling, is_causal=is_causal)

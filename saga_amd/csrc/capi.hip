@@ -802,3 +802,89 @@ int saga_argmax(const saga_tensor* x, int64_t* out, void* workspace, size_t work
 }
 
 }  // extern "C"
+
+extern "C" {
+
+int saga_prefill_attention(const saga_tensor* query, const saga_tensor* key, const saga_tensor* value,
+                           const saga_tensor* mask, float scale, int32_t causal, int64_t causal_offset,
+                           saga_tensor* out, saga_stream_t stream) {
+  int rc;
+  if ((rc = check_tensor(query, "query", 4)) || (rc = check_tensor(key, "key", 4)) ||
+      (rc = check_tensor(value, "value", 4)) || (rc = check_tensor(out, "out", 4)))
+    return rc;
+  const int64_t b = query->shape[0], q_h = query->shape[1], Lq = query->shape[2], d = query->shape[3];
+  const int64_t k_h = key->shape[1], Lk = key->shape[2], v_h = value->shape[1];
+  const int dt = query->dtype;
+  if (dt != SAGA_DTYPE_BF16 && dt != SAGA_DTYPE_F16)
+    return fail(SAGA_ERR_UNSUPPORTED, "prefill: query dtype must be bf16 or f16");
+  if (key->dtype != dt || value->dtype != dt || out->dtype != dt)
+    return fail(SAGA_ERR_INVALID, "prefill: key, value and out must have the query's dtype");
+  if (d != 64 && d != 128) return fail(SAGA_ERR_UNSUPPORTED, "prefill: head_dim %lld not built (64, 128)", (long long)d);
+  if (key->shape[0] != b || key->shape[3] != d || value->shape[0] != b || value->shape[2] != Lk || value->shape[3] != d)
+    return fail(SAGA_ERR_INVALID, "prefill: key [b, k_h, Lk, d] / value [b, v_h, Lk, d] do not match the query");
+  if (q_h % k_h || q_h % v_h)
+    return fail(SAGA_ERR_INVALID, "prefill: q_h (%lld) must be a multiple of k_h (%lld) and v_h (%lld)", (long long)q_h,
+                (long long)k_h, (long long)v_h);
+  if (out->shape[0] != b || out->shape[1] != Lq || out->shape[2] != q_h || out->shape[3] != d)
+    return fail(SAGA_ERR_INVALID, "prefill: out must be [b, Lq, q_h, d]");
+  if (Lq >= kMaxLen || Lk >= kMaxLen) return fail(SAGA_ERR_UNSUPPORTED, "prefill: sequence too long");
+  if (causal_offset < -kMaxLen || causal_offset > kMaxLen)
+    return fail(SAGA_ERR_INVALID, "prefill: causal_offset out of range");
+  const int64_t nmb = prefill_query_blocks(Lq, static_cast<int>(d));
+  if (nmb * q_h * b >= (1LL << 31)) return fail(SAGA_ERR_UNSUPPORTED, "prefill: grid too large");
+  if ((rc = check_vec_rows(query, "query")) || (rc = check_vec_rows(key, "key")) || (rc = check_vec_rows(value, "value")))
+    return rc;
+  // 8-byte stores of 4 output dims
+  if (out->stride[3] != 1 || reinterpret_cast<uintptr_t>(out->data) % 8 || out->stride[0] % 4 || out->stride[1] % 4 ||
+      out->stride[2] % 4)
+    return fail(SAGA_ERR_INVALID, "prefill: out needs unit innermost stride, 8-byte aligned rows");
+  PrefillParams p{};
+  if (mask) {
+    if ((rc = check_tensor(mask, "mask", 4))) return rc;
+    if (!is_float(mask->dtype) && mask->dtype != SAGA_DTYPE_BOOL)
+      return fail(SAGA_ERR_INVALID, "mask: dtype must be f32, bf16, f16 or bool");
+    if ((mask->shape[0] != 1 && mask->shape[0] != b) || (mask->shape[1] != 1 && mask->shape[1] != q_h) ||
+        mask->shape[2] != Lq || mask->shape[3] != Lk)
+      return fail(SAGA_ERR_INVALID, "mask: shape [%lld,%lld,%lld,%lld] does not broadcast to [b, q_h, Lq, Lk]",
+                  (long long)mask->shape[0], (long long)mask->shape[1], (long long)mask->shape[2],
+                  (long long)mask->shape[3]);
+    p.mask = mask->data;
+    p.mask_dt = mask->dtype;
+    p.m_sb = mask->shape[0] == 1 ? 0 : mask->stride[0];
+    p.m_sh = mask->shape[1] == 1 ? 0 : mask->stride[1];
+    p.m_sq = mask->stride[2];
+    p.m_sk = mask->stride[3];
+  }
+  p.q = static_cast<const char*>(query->data);
+  p.q_sb = query->stride[0];
+  p.q_sh = query->stride[1];
+  p.q_sl = query->stride[2];
+  p.k = static_cast<const char*>(key->data);
+  p.k_sb = key->stride[0];
+  p.k_sh = key->stride[1];
+  p.k_sl = key->stride[2];
+  p.v = static_cast<const char*>(value->data);
+  p.v_sb = value->stride[0];
+  p.v_sh = value->stride[1];
+  p.v_sl = value->stride[2];
+  p.out = out->data;
+  p.o_sb = out->stride[0];
+  p.o_sq = out->stride[1];
+  p.o_sh = out->stride[2];
+  p.b = static_cast<int32_t>(b);
+  p.q_h = static_cast<int32_t>(q_h);
+  p.k_h = static_cast<int32_t>(k_h);
+  p.v_h = static_cast<int32_t>(v_h);
+  p.Lq = static_cast<int32_t>(Lq);
+  p.Lk = static_cast<int32_t>(Lk);
+  p.nmb = static_cast<int32_t>(nmb);
+  p.causal = causal ? 1 : 0;
+  p.causal_off = static_cast<int32_t>(causal_offset);
+  p.scale = scale;
+  if ((rc = hip_status(launch_prefill_attention(dt, static_cast<int>(d), p, static_cast<hipStream_t>(stream)),
+                       "prefill launch")))
+    return rc;
+  return ok();
+}
+
+}  // extern "C"

@@ -231,4 +231,28 @@ hipError_t launch_gemv(const GemvParams& p, hipStream_t st);
 int64_t argmax_workspace_bytes(int64_t rows, int64_t N);
 hipError_t launch_argmax(const void* x, int64_t ld, int rows, int N, int64_t* out, void* ws, hipStream_t st);
 
+// Prefill attention with separate key / value head maps (csrc/prefill.hip).
+// Strides in elements; q [b, q_h, Lq, d], k [b, k_h, Lk, d], v [b, v_h, Lk, d],
+// mask [b|1, q_h|1, Lq, Lk] (broadcast dims stride 0), out [b, Lq, q_h, d].
+struct PrefillParams {
+  const char* q;
+  int64_t q_sb, q_sh, q_sl;
+  const char* k;
+  int64_t k_sb, k_sh, k_sl;
+  const char* v;
+  int64_t v_sb, v_sh, v_sl;
+  const void* mask;  // null: none; bool keeps True, float is added
+  int32_t mask_dt;
+  int64_t m_sb, m_sh, m_sq, m_sk;
+  void* out;
+  int64_t o_sb, o_sq, o_sh;
+  int32_t b, q_h, k_h, v_h, Lq, Lk;
+  int32_t nmb;         // query blocks per (batch, head)
+  int32_t causal;      // key j visible to query i iff j <= i + causal_off
+  int32_t causal_off;
+  float scale;
+};
+int prefill_query_blocks(int64_t Lq, int d);
+hipError_t launch_prefill_attention(int dtype, int d, const PrefillParams& p, hipStream_t st);
+
 }  // namespace saga

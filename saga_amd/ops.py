@@ -227,6 +227,59 @@ def dense_decode(query, key, value, attention_mask=None, scaling=None, kv_len=No
     return out
 
 
+_PREFILL_MASK_DTYPES = (torch.bool, torch.float32, torch.bfloat16, torch.float16)
+
+
+def prefill_supported(query, key, value, attention_mask=None, dropout: float = 0.0) -> bool:
+    """Whether prefill_attention takes these operands (else the caller keeps
+    torch SDPA, as the reference does for every prefill)."""
+    return (query.is_cuda and query.dim() == 4 and query.dtype in (torch.bfloat16, torch.float16)
+            and key.dtype == query.dtype and value.dtype == query.dtype and query.shape[-1] in (64, 128)
+            and not dropout and query.shape[1] % key.shape[1] == 0 and query.shape[1] % value.shape[1] == 0
+            and (attention_mask is None or (attention_mask.dim() == 4 and attention_mask.dtype in _PREFILL_MASK_DTYPES
+                                            and attention_mask.shape[2] in (1, query.shape[2]))))
+
+
+def prefill_attention(query, key, value, attention_mask=None, scaling=None, is_causal=None, causal_offset: int = 0,
+                      out=None):
+    """Prefill attention with separate key / value head counts
+    (attention/attention.py:13-53: torch SDPA over keys expanded by q_h / k_h
+    and values by q_h / v_h), one HIP kernel over the unexpanded caches.
+
+    query [b, q_h, Lq, d], key [b, k_h, Lk, d], value [b, v_h, Lk, d] (bf16 /
+    f16, d 64 or 128); attention_mask [b|1, q_h|1, Lq|1, >= Lk] (bool keeps
+    True, float is added), cut to Lk as the reference does (:31-32).
+    is_causal None: causal iff Lq > 1 and there is no mask (:37-38); causal
+    means key j <= query i + causal_offset (SDPA: causal_offset 0).
+    Returns out [b, Lq, q_h, d]: the reference's output after its transpose."""
+    dev = _need_gpu(query, key, value, attention_mask)
+    query, key, value = _vec_ready(query), _vec_ready(key), _vec_ready(value)
+    b, q_h, Lq, d = query.shape
+    Lk = key.shape[2]
+    mask = attention_mask
+    if mask is not None:
+        if mask.dim() != 4:
+            raise ValueError(f"saga_amd: attention mask must be 4-D, got {tuple(mask.shape)}")
+        mask = mask[:, :, :, :Lk]
+        if mask.shape[2] == 1 and Lq > 1:
+            mask = mask.expand(-1, -1, Lq, -1)
+    if is_causal is None:
+        is_causal = Lq > 1 and mask is None
+    if is_causal and mask is not None:
+        raise ValueError("saga_amd: a mask and is_causal cannot both be given (as in torch SDPA)")
+    if out is None:
+        out = torch.empty(b, Lq, q_h, d, dtype=query.dtype, device=dev)
+    if out.numel() == 0:
+        return out
+    if Lk == 0:
+        return out.zero_()
+    _lib.check(_lib.load().saga_prefill_attention(_lib.tensor(query), _lib.tensor(key), _lib.tensor(value),
+                                                  _lib.tensor(mask), _scale(query, scaling), 1 if is_causal else 0,
+                                                  int(causal_offset), _lib.tensor(out), _lib.stream_of(query)),
+               "prefill_attention")
+    return out
+
+
 def set_fused_fast_step(enable: bool) -> bool:
     """Process-wide switch of the fused Atop-N fast step (off by default: it
     measured slower than the three-kernel path); on, shapes whose grid fits

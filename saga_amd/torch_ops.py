@@ -14,6 +14,8 @@ Operators (namespace "saga"):
     scaling, kv_len) -> out [b, q_h, 1, d]        (attention/attention.py:173-189)
   * dense_decode(query, key, value, attention_mask, scaling, kv_len)
     -> out [b, q_h, 1, d]                         (attention/attention.py:64-85)
+  * prefill_attention(query, key, value, attention_mask, scaling, is_causal)
+    -> out [b, l_q, q_h, d]                       (attention/attention.py:13-53)
 """
 from typing import Optional
 
@@ -63,3 +65,16 @@ def dense_decode(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
 @dense_decode.register_fake
 def _dense_decode_fake(query, key, value, attention_mask=None, scaling=None, kv_len=None):
     return _out_like(query)
+
+
+@torch.library.custom_op("saga::prefill_attention", mutates_args=())
+def prefill_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                      attention_mask: Optional[torch.Tensor] = None, scaling: Optional[float] = None,
+                      is_causal: bool = False) -> torch.Tensor:
+    return ops.prefill_attention(query, key, value, attention_mask, scaling, is_causal)
+
+
+@prefill_attention.register_fake
+def _prefill_attention_fake(query, key, value, attention_mask=None, scaling=None, is_causal=False):
+    b, q_h, l_q, d = query.shape
+    return query.new_empty(b, l_q, q_h, d)

@@ -365,3 +365,66 @@ def test_rmsnorm_and_silu_mul_closed_forms():
     np.testing.assert_allclose(O.silu_mul(gu), ref)
     t = torch.from_numpy(gu[:, :4])
     np.testing.assert_allclose(O.silu_mul(gu), (torch.nn.functional.silu(t) * torch.from_numpy(gu[:, 4:])).numpy())
+
+
+def _sdpa_expanded(q, k, v, mask, scale, is_causal):
+    """torch's own SDPA (float64, CPU) over repeat_interleave-expanded heads,
+    [b, l_q, q_h, d]."""
+    q_h = q.shape[1]
+    tk = torch.from_numpy(k).repeat_interleave(q_h // k.shape[1], dim=1)
+    tv = torch.from_numpy(v).repeat_interleave(q_h // v.shape[1], dim=1)
+    tm = None if mask is None else torch.from_numpy(mask)
+    out = torch.nn.functional.scaled_dot_product_attention(torch.from_numpy(q), tk, tv, attn_mask=tm, scale=scale,
+                                                           is_causal=is_causal)
+    return out.transpose(1, 2).numpy()
+
+
+@pytest.mark.parametrize("q_h,k_h,v_h", [(6, 1, 2), (6, 2, 3), (4, 4, 4), (15, 1, 5)])
+@pytest.mark.parametrize("kind", ["causal", "full", "bool", "float", "causal_short_q", "masked_row"])
+def test_prefill_matches_torch_sdpa(q_h, k_h, v_h, kind):
+    rng = np.random.default_rng(31)
+    b, d = 2, 16
+    Lq, Lk = (5, 37) if kind == "causal_short_q" else (37, 37)
+    q, k, v = _rand(rng, b, q_h, Lq, d), _rand(rng, b, k_h, Lk, d), _rand(rng, b, v_h, Lk, d)
+    mask, causal = None, kind.startswith("causal")
+    if kind in ("bool", "masked_row"):
+        mask = rng.random((b, 1, Lq, Lk + 3)) < 0.7  # wider than Lk: cut by the function (:28-30)
+        mask[..., 0] = True
+        if kind == "masked_row":
+            mask[1, 0, 4] = False  # a query that sees no key
+    elif kind == "float":
+        mask = np.where(rng.random((b, q_h, Lq, Lk)) < 0.3, -np.inf, rng.standard_normal((b, q_h, Lq, Lk)))
+        mask[..., 0] = 0.0
+    ours = O.prefill(q, k, v, mask, 0.3, causal)
+    ref = _sdpa_expanded(q, k, v, None if mask is None else mask[..., :Lk], 0.3, causal)
+    assert ours.shape == (b, Lq, q_h, d)
+    np.testing.assert_allclose(ours, ref, rtol=1e-10, atol=1e-12)
+    if kind == "masked_row":
+        assert not ours[1, 4].any()
+
+
+def test_prefill_default_causal_rule():
+    """is_causal None: causal for l_q > 1 without a mask (attention/attention.py:35-36)."""
+    rng = np.random.default_rng(32)
+    q, k, v = _rand(rng, 1, 2, 6, 8), _rand(rng, 1, 1, 6, 8), _rand(rng, 1, 2, 6, 8)
+    np.testing.assert_array_equal(O.prefill(q, k, v), O.prefill(q, k, v, is_causal=True))
+    assert not np.allclose(O.prefill(q, k, v), O.prefill(q, k, v, is_causal=False))
+    one = O.prefill(q[:, :, :1], k, v)  # l_q == 1: not causal
+    np.testing.assert_array_equal(one, O.prefill(q[:, :, :1], k, v, is_causal=False))
+
+
+def test_prefill_causality_and_single_key():
+    """Causal output at query i does not depend on keys / values after i;
+    query 0 of a causal call sees one key, so its output is that value row of
+    its value head."""
+    rng = np.random.default_rng(33)
+    q, k, v = _rand(rng, 1, 6, 20, 8), _rand(rng, 1, 1, 20, 8), _rand(rng, 1, 3, 20, 8)
+    out = O.prefill(q, k, v, is_causal=True)
+    k2, v2 = k.copy(), v.copy()
+    k2[:, :, 11:] = rng.standard_normal(k2[:, :, 11:].shape)
+    v2[:, :, 11:] = rng.standard_normal(v2[:, :, 11:].shape)
+    out2 = O.prefill(q, k2, v2, is_causal=True)
+    np.testing.assert_array_equal(out[:, :11], out2[:, :11])
+    assert not np.allclose(out[:, 11:], out2[:, 11:])
+    for h in range(6):
+        np.testing.assert_allclose(out[0, 0, h], v[0, h // 2, 0], rtol=1e-12)
