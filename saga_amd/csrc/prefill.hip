@@ -22,7 +22,9 @@
 //    with the 16-byte units of each row XOR-swizzled by the row so that both
 //    the transposed writes and the fragment reads spread over the banks;
 //  * online softmax in base 2: per lane partial sums, reduced across the
-//    four lane groups of a query only at the end.
+//    four lane groups of a query only at the end; the running max is moved
+//    (and O rescaled) only when a score exceeds it by 2^8, and the causal /
+//    length masks are applied only to the tiles that cross them.
 // Blocks are ordered heaviest first (causal: the last query blocks see the
 // most keys) and, within one query block, by head: blocks in flight together
 // share the key / value head.
@@ -34,6 +36,7 @@ namespace {
 
 constexpr int kPfBN = 64;  // keys per tile
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kPfRescale = 8.0f;  // log2 headroom of the running max
 
 // waves per block: the tile loads are spread over 512 threads for d = 128
 // (two 16-byte fragments per thread and operand, which keeps the kernel
@@ -65,12 +68,17 @@ __device__ __forceinline__ int pf_swz(int d) { return (d ^ (d >> 3)) & 7; }
 
 __device__ __forceinline__ u32x4 lds16(const uint32_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
+// Two floats -> two 16-bit elements, round to nearest even
+// (v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 template <int DT>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
+  const f32x2 v = {a, b};
   if constexpr (DT == SAGA_DTYPE_BF16) {
-    return static_cast<uint32_t>(f32_to_bf16_bits(a)) | (static_cast<uint32_t>(f32_to_bf16_bits(b)) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
   } else {
-    return static_cast<uint32_t>(f32_to_f16_bits(a)) | (static_cast<uint32_t>(f32_to_f16_bits(b)) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_t));
   }
 }
 
@@ -153,6 +161,7 @@ __global__ __launch_bounds__(PfShape<D>::THREADS, 2) void prefill_attn_kernel(Pr
 #pragma unroll
     for (int dt = 0; dt < S::NDT; ++dt) o[ct][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float mrun[2] = {kNegInf, kNegInf}, lsum[2] = {0.f, 0.f};
+  const float sl2 = p.scale * kLog2e;
 
   if (ntiles > 0) load_tile(0);
   for (int it = 0; it < ntiles; ++it) {
@@ -183,58 +192,78 @@ __global__ __launch_bounds__(PfShape<D>::THREADS, 2) void prefill_attn_kernel(Pr
           }
         }
 
+      // per-element masks only where needed: the wave's diagonal, the last
+      // (partial) tile, an explicit mask
+      const bool edge = MASKED || (p.causal && k0 + kPfBN - 1 > q0w + p.causal_off) || k0 + kPfBN > p.Lk;
       u32x4 pf[2][2];  // [ct][ch]: B fragments of P^T
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) {
         const int q = q0w + 16 * ct + c;
         float x[2][2][4];
+#pragma unroll
+        for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) x[ch][t][r] = sc[ch][t][ct][r] * sl2;
+        if (edge) {
+#pragma unroll
+          for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const int key = k0 + 32 * ch + 8 * s + 4 * t + r;
+                float v = x[ch][t][r];
+                if constexpr (MASKED) {
+                  const int64_t mo = bi * p.m_sb + static_cast<int64_t>(h) * p.m_sh +
+                                     static_cast<int64_t>(min(q, p.Lq - 1)) * p.m_sq +
+                                     static_cast<int64_t>(min(key, p.Lk - 1)) * p.m_sk;
+                  if (p.mask_dt == SAGA_DTYPE_BOOL) {
+                    if (!static_cast<const uint8_t*>(p.mask)[mo]) v = kNegInf;
+                  } else {
+                    v += load_as_f32(p.mask, p.mask_dt, mo) * kLog2e;
+                  }
+                }
+                if (key >= p.Lk || (p.causal && key > q + p.causal_off)) v = kNegInf;
+                x[ch][t][r] = v;
+              }
+        }
         float mx = kNegInf;
 #pragma unroll
         for (int ch = 0; ch < 2; ++ch)
 #pragma unroll
           for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int key = k0 + 32 * ch + 8 * s + 4 * t + r;
-              float v = sc[ch][t][ct][r] * p.scale;
-              if constexpr (MASKED) {
-                const int64_t mo = bi * p.m_sb + static_cast<int64_t>(h) * p.m_sh +
-                                   static_cast<int64_t>(min(q, p.Lq - 1)) * p.m_sq +
-                                   static_cast<int64_t>(min(key, p.Lk - 1)) * p.m_sk;
-                if (p.mask_dt == SAGA_DTYPE_BOOL) {
-                  if (!static_cast<const uint8_t*>(p.mask)[mo]) v = kNegInf;
-                } else {
-                  v += load_as_f32(p.mask, p.mask_dt, mo);
-                }
-              }
-              if (key >= p.Lk || (p.causal && key > q + p.causal_off)) v = kNegInf;
-              v *= kLog2e;
-              x[ch][t][r] = v;
-              mx = fmaxf(mx, v);
-            }
+            for (int r = 0; r < 4; ++r) mx = fmaxf(mx, x[ch][t][r]);
         mx = fmaxf(mx, __shfl_xor(mx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float mnew = fmaxf(mrun[ct], mx);
-        const float msub = mnew == kNegInf ? 0.f : mnew;
-        const float alpha = exp2f(mrun[ct] - msub);  // 0 from -inf, 1 while nothing is seen
-        mrun[ct] = mnew;
+        // lazy rescale: the reference max moves only when a score exceeds it
+        // by more than 2^8, so p <= 256 and most tiles skip the O rescale
+        const bool grow = mx > mrun[ct] + kPfRescale;
+        if (__any(grow)) {
+          const float alpha = grow ? __builtin_amdgcn_exp2f(mrun[ct] - mx) : 1.0f;
+          mrun[ct] = grow ? mx : mrun[ct];
+          lsum[ct] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < S::NDT; ++dt) o[ct][dt] *= alpha;
+        }
+        const float msub = mrun[ct] == kNegInf ? 0.f : mrun[ct];
         float ps = 0.f;
 #pragma unroll
         for (int ch = 0; ch < 2; ++ch) {
-          float pv[2][4];
+          float pv[8];
 #pragma unroll
           for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              pv[t][r] = exp2f(x[ch][t][r] - msub);
-              ps += pv[t][r];
+              pv[4 * t + r] = __builtin_amdgcn_exp2f(x[ch][t][r] - msub);
+              ps += pv[4 * t + r];
             }
-          pf[ct][ch] = u32x4{pack2<DT>(pv[0][0], pv[0][1]), pack2<DT>(pv[0][2], pv[0][3]),
-                             pack2<DT>(pv[1][0], pv[1][1]), pack2<DT>(pv[1][2], pv[1][3])};
+          pf[ct][ch] = u32x4{pack2<DT>(pv[0], pv[1]), pack2<DT>(pv[2], pv[3]), pack2<DT>(pv[4], pv[5]),
+                             pack2<DT>(pv[6], pv[7])};
         }
-        lsum[ct] = lsum[ct] * alpha + ps;
-#pragma unroll
-        for (int dt = 0; dt < S::NDT; ++dt) o[ct][dt] *= alpha;
+        lsum[ct] += ps;
       }
 
       // O^T += V^T . P^T; A fragment: V^T row 16 dt + c, keys 32 ch + 8 s ..
