@@ -302,7 +302,8 @@ int saga_argmax(const saga_tensor* x, int64_t* out, void* workspace, size_t work
  * scores, as in torch SDPA.  causal != 0: key j is visible to query i only if
  * j <= i + causal_offset (SDPA's is_causal is causal_offset = 0; a chunk of
  * queries after P cached positions uses causal_offset = P).  A query that
- * sees no key gets 0 (torch SDPA's math path does the same). */
+ * sees no key gets 0 (torch SDPA's math path does the same).  scale must be
+ * positive (SAGA_ERR_UNSUPPORTED otherwise). */
 int saga_prefill_attention(const saga_tensor* query, const saga_tensor* key, const saga_tensor* value,
                            const saga_tensor* mask, float scale, int32_t causal, int64_t causal_offset,
                            saga_tensor* out, saga_stream_t stream);

@@ -73,7 +73,7 @@ def sdpa_attention_forward(
     expand = hasattr(module, "num_key_value_groups")
     same_heads = key.shape[-3] == query.shape[-3] and value.shape[-3] == query.shape[-3]
     if (expand or same_heads) and not (is_causal and mask is not None) \
-            and ops.prefill_supported(query, key, value, mask, dropout):
+            and ops.prefill_supported(query, key, value, mask, dropout, scaling):
         return _saga.prefill_attention(query, key, value, mask, scaling, bool(is_causal)), None
     if expand:
         n_q = query.shape[-3]

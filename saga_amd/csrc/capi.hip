@@ -2,6 +2,7 @@
 // launch sequences of the fused decode entry points.  Declarations and the
 // reference function each entry point replaces: include/saga_amd.h.
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
@@ -830,6 +831,8 @@ int saga_prefill_attention(const saga_tensor* query, const saga_tensor* key, con
   if (Lq >= kMaxLen || Lk >= kMaxLen) return fail(SAGA_ERR_UNSUPPORTED, "prefill: sequence too long");
   if (causal_offset < -kMaxLen || causal_offset > kMaxLen)
     return fail(SAGA_ERR_INVALID, "prefill: causal_offset out of range");
+  if (!(scale > 0.f) || !std::isfinite(scale))
+    return fail(SAGA_ERR_UNSUPPORTED, "prefill: scale must be positive and finite");
   const int64_t nmb = prefill_query_blocks(Lq, static_cast<int>(d));
   if (nmb * q_h * b >= (1LL << 31)) return fail(SAGA_ERR_UNSUPPORTED, "prefill: grid too large");
   if ((rc = check_vec_rows(query, "query")) || (rc = check_vec_rows(key, "key")) || (rc = check_vec_rows(value, "value")))

@@ -91,7 +91,9 @@ __global__ __launch_bounds__(PfShape<D>::THREADS, 2) void prefill_attn_kernel(Pr
   __shared__ __attribute__((aligned(16))) uint32_t ks[kPfBN * S::KROW];
   __shared__ __attribute__((aligned(16))) uint32_t vt[D * S::VROW];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the wave index through readfirstlane: every per-wave condition below is
+  // then a scalar branch, not an exec-masked region issued by every wave
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int s = lane >> 4, c = lane & 15;
   const int nhb = p.q_h * p.b;
   const int id = blockIdx.x;
@@ -122,17 +124,21 @@ __global__ __launch_bounds__(PfShape<D>::THREADS, 2) void prefill_attn_kernel(Pr
   }
 
   // tile loads: thread (chunk lc, key group lg) holds keys lg*KPT + i, dims 8 lc ..
+  // (row pointers advance one tile per call; rows at or past Lk are not read)
   const int lc = tid % S::NDC, lg = tid / S::NDC;
   u32x4 kr[S::KPT], vr[S::KPT];
+  const char* kcur = kb + (static_cast<int64_t>(lg * S::KPT) * p.k_sl + 8 * lc) * E::kBytes;
+  const char* vcur = vb + (static_cast<int64_t>(lg * S::KPT) * p.v_sl + 8 * lc) * E::kBytes;
+  const int64_t krow = p.k_sl * E::kBytes, vrow = p.v_sl * E::kBytes;
   auto load_tile = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < S::KPT; ++i) {
-      const int key = k0 + lg * S::KPT + i;
-      const int64_t kk = min(key, p.Lk - 1);
-      const bool ok = key < p.Lk;
-      kr[i] = ok ? ld16(kb + (kk * p.k_sl + 8 * lc) * E::kBytes) : u32x4{0u, 0u, 0u, 0u};
-      vr[i] = ok ? ld16(vb + (kk * p.v_sl + 8 * lc) * E::kBytes) : u32x4{0u, 0u, 0u, 0u};
+      const bool ok = k0 + lg * S::KPT + i < p.Lk;
+      kr[i] = ok ? ld16(kcur + i * krow) : u32x4{0u, 0u, 0u, 0u};
+      vr[i] = ok ? ld16(vcur + i * vrow) : u32x4{0u, 0u, 0u, 0u};
     }
+    kcur += kPfBN * krow;
+    vcur += kPfBN * vrow;
   };
   auto store_tile = [&]() {
 #pragma unroll
@@ -161,7 +167,8 @@ __global__ __launch_bounds__(PfShape<D>::THREADS, 2) void prefill_attn_kernel(Pr
 #pragma unroll
     for (int dt = 0; dt < S::NDT; ++dt) o[ct][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float mrun[2] = {kNegInf, kNegInf}, lsum[2] = {0.f, 0.f};
-  const float sl2 = p.scale * kLog2e;
+  const float sl2 = p.scale * kLog2e;  // > 0 (checked by the host)
+  const float inv_scale = 1.0f / p.scale;
 
   if (ntiles > 0) load_tile(0);
   for (int it = 0; it < ntiles; ++it) {
@@ -199,13 +206,14 @@ __global__ __launch_bounds__(PfShape<D>::THREADS, 2) void prefill_attn_kernel(Pr
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) {
         const int q = q0w + 16 * ct + c;
+        // raw scores q.k (scaled only inside the exponent below)
         float x[2][2][4];
 #pragma unroll
         for (int ch = 0; ch < 2; ++ch)
 #pragma unroll
           for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) x[ch][t][r] = sc[ch][t][ct][r] * sl2;
+            for (int r = 0; r < 4; ++r) x[ch][t][r] = sc[ch][t][ct][r];
         if (edge) {
 #pragma unroll
           for (int ch = 0; ch < 2; ++ch)
@@ -222,7 +230,7 @@ __global__ __launch_bounds__(PfShape<D>::THREADS, 2) void prefill_attn_kernel(Pr
                   if (p.mask_dt == SAGA_DTYPE_BOOL) {
                     if (!static_cast<const uint8_t*>(p.mask)[mo]) v = kNegInf;
                   } else {
-                    v += load_as_f32(p.mask, p.mask_dt, mo) * kLog2e;
+                    v += load_as_f32(p.mask, p.mask_dt, mo) * inv_scale;
                   }
                 }
                 if (key >= p.Lk || (p.causal && key > q + p.causal_off)) v = kNegInf;
@@ -238,10 +246,12 @@ __global__ __launch_bounds__(PfShape<D>::THREADS, 2) void prefill_attn_kernel(Pr
             for (int r = 0; r < 4; ++r) mx = fmaxf(mx, x[ch][t][r]);
         mx = fmaxf(mx, __shfl_xor(mx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx *= sl2;  // base-2 units (scale > 0 keeps the max)
         // lazy rescale: the reference max moves only when a score exceeds it
         // by more than 2^8, so p <= 256 and most tiles skip the O rescale
         const bool grow = mx > mrun[ct] + kPfRescale;
         if (__any(grow)) {
+          asm volatile("" ::: "memory");  // a real branch: not flattened into every tile
           const float alpha = grow ? __builtin_amdgcn_exp2f(mrun[ct] - mx) : 1.0f;
           mrun[ct] = grow ? mx : mrun[ct];
           lsum[ct] *= alpha;
@@ -257,7 +267,7 @@ __global__ __launch_bounds__(PfShape<D>::THREADS, 2) void prefill_attn_kernel(Pr
           for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              pv[4 * t + r] = __builtin_amdgcn_exp2f(x[ch][t][r] - msub);
+              pv[4 * t + r] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[ch][t][r], sl2, -msub));
               ps += pv[4 * t + r];
             }
           pf[ct][ch] = u32x4{pack2<DT>(pv[0], pv[1]), pack2<DT>(pv[2], pv[3]), pack2<DT>(pv[4], pv[5]),

@@ -230,10 +230,10 @@ def dense_decode(query, key, value, attention_mask=None, scaling=None, kv_len=No
 _PREFILL_MASK_DTYPES = (torch.bool, torch.float32, torch.bfloat16, torch.float16)
 
 
-def prefill_supported(query, key, value, attention_mask=None, dropout: float = 0.0) -> bool:
+def prefill_supported(query, key, value, attention_mask=None, dropout: float = 0.0, scaling=None) -> bool:
     """Whether prefill_attention takes these operands (else the caller keeps
     torch SDPA, as the reference does for every prefill)."""
-    return (query.is_cuda and query.dim() == 4 and query.dtype in (torch.bfloat16, torch.float16)
+    return ((scaling is None or 0 < scaling < float("inf")) and query.is_cuda and query.dim() == 4 and query.dtype in (torch.bfloat16, torch.float16)
             and key.dtype == query.dtype and value.dtype == query.dtype and query.shape[-1] in (64, 128)
             and not dropout and query.shape[1] % key.shape[1] == 0 and query.shape[1] % value.shape[1] == 0
             and (attention_mask is None or (attention_mask.dim() == 4 and attention_mask.dtype in _PREFILL_MASK_DTYPES
