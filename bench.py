@@ -18,6 +18,10 @@ Also reported on the same line:
                 28 layers at the same shapes, as attention tokens/s;
   dense_gqa     the same harness with 2 key / 2 value heads and the dense
                 split-L decode kernel (the in-house dense-GQA comparator).
+
+--prefill prints a separate line for the prefill attention kernel (causal,
+batch 1, the decoder's head shape) against the bf16 MFMA peak, with torch
+SDPA over expanded heads and the CPU oracle beside it.
 """
 import argparse
 import json
@@ -170,6 +174,97 @@ def profile_kernels(batch, ctx, shape, launches=8):
     return 0
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def prefill_bench(ctx, shape, reps=10, no_cpu=False):
+    """Prefill attention alone (saga_prefill_attention, the reference's
+    sdpa_attention_forward with separate key / value heads) at the decoder's
+    head shape, batch 1, a causal prompt of `ctx` tokens, N(0,1) bf16 q/k/v.
+    Algorithmic flops: 4 * q_h * d * L (L + 1) / 2 (q.k and p.v over the
+    causal triangle).  Beside it: torch SDPA over the repeat_interleave-
+    expanded heads (the reference's path), with and without the expansion."""
+    from saga_amd import ops
+    L, q_h, d = ctx, shape.n_q, shape.head_dim
+    g = torch.Generator(device="cuda").manual_seed(0)
+    q = torch.randn(1, q_h, L, d, generator=g, device="cuda").to(torch.bfloat16)
+    k = torch.randn(1, shape.n_k, L, d, generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn(1, shape.n_v, L, d, generator=g, device="cuda").to(torch.bfloat16)
+    out = torch.empty(1, L, q_h, d, device="cuda", dtype=torch.bfloat16)
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    ms = timed(lambda: ops.prefill_attention(q, k, v, is_causal=True, out=out))
+    flops = 4.0 * q_h * d * L * (L + 1) / 2
+    tflops = flops / (ms * 1e-3) / 1e12
+    sdpa = torch.nn.functional.scaled_dot_product_attention
+    kx, vx = k.repeat_interleave(q_h // shape.n_k, dim=1), v.repeat_interleave(q_h // shape.n_v, dim=1)
+    t_sdpa = timed(lambda: sdpa(q, kx, vx, is_causal=True))
+    t_sdpa_x = timed(lambda: sdpa(q, k.repeat_interleave(q_h // shape.n_k, dim=1),
+                                  v.repeat_interleave(q_h // shape.n_v, dim=1), is_causal=True))
+    log(f"prefill attention L={L}: {ms:.3f} ms, {tflops:.1f} TFLOP/s; torch SDPA (expanded heads) {t_sdpa:.3f} ms "
+        f"({t_sdpa_x:.3f} ms with the expansion)")
+    line = {
+        "metric": f"prefill attention TFLOP/s @1.5B-shape {L // 1024}k causal",
+        "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": reps, "warmup": 2,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic: N(0,1) q/k/v",
+        "config": {"workload": f"SAGA prefill attention, {q_h} query / {shape.n_k} key / {shape.n_v} value heads, "
+                               f"d{d}, batch 1, {L} tokens, causal",
+                   "global_batch": 1, "seq_len": L, "parallelism": "single GPU"},
+        "roofline": {"kernel": "saga::prefill_attn_kernel<bf16,128>", "bound": "mfma", "achieved": round(tflops, 1),
+                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "algorithmic_flops_per_launch": flops},
+        "torch_sdpa_expanded": {"ms": round(t_sdpa, 4), "ms_with_expand": round(t_sdpa_x, 4),
+                                "speedup_saga": round(t_sdpa_x / ms, 3)},
+    }
+    if not no_cpu:
+        from oracle import saga_oracle as O
+        try:
+            from threadpoolctl import threadpool_limits
+        except ImportError:  # pragma: no cover
+            threadpool_limits = None
+        cores = min(16, os.cpu_count() or 1)
+        Ls = 2048
+        rng = np.random.default_rng(0)
+        qs = rng.standard_normal((1, q_h, Ls, d), dtype=np.float32)
+        ks = rng.standard_normal((1, shape.n_k, Ls, d), dtype=np.float32)
+        vs = rng.standard_normal((1, shape.n_v, Ls, d), dtype=np.float32)
+
+        def run():
+            n, t0 = 0, time.perf_counter()
+            while True:
+                O.prefill(qs, ks, vs, is_causal=True)
+                n += 1
+                secs = time.perf_counter() - t0
+                if secs >= 10.0 or n >= 30:
+                    return n, secs
+
+        if threadpool_limits is not None:
+            with threadpool_limits(limits=cores):
+                n, secs = run()
+        else:
+            n, secs = run()
+        fl_s = 4.0 * q_h * d * Ls * (Ls + 1) / 2
+        line["cpu_baseline"] = {"value": round(fl_s * n / secs / 1e12, 5), "unit": "TFLOP/s (causal flops)",
+                                "cores": cores, "kind": "port",
+                                "sample": f"{n} causal prefills of {Ls} tokens, {q_h}/{shape.n_k}/{shape.n_v} heads "
+                                          f"d{d}, fp32 numpy oracle, {secs:.1f} s"}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def sweep(copies=8):
     """Attention-only timings on synthetic bf16 caches: every shape is timed
     as a graph of 2 x `copies` launches cycling over `copies` distinct K/V
@@ -267,6 +362,8 @@ def main():
                          "and the 128k dense-GQA vs SAGA comparison; one JSON line per shape")
     ap.add_argument("--no-fused", action="store_true",
                     help="run the Atop-N fast step as three kernels (scores, slice, row) for every shape")
+    ap.add_argument("--prefill", action="store_true",
+                    help="measure the prefill attention kernel alone (its own JSON line) instead of decode")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="only launch K1 (qk_scores) at the workload shape and a 1 GiB device copy, "
                          "for hardware-counter runs")
@@ -294,6 +391,8 @@ def main():
     B, ctx, K, W = args.batch, args.ctx, args.steps, args.warmup
     if args.profile_kernels:
         return profile_kernels(B, ctx, SAGA_SHAPE)
+    if args.prefill:
+        return prefill_bench(ctx, SAGA_SHAPE, no_cpu=args.no_cpu)
     if args.sweep:
         return sweep()
     max_len = ctx + K

@@ -90,7 +90,8 @@ def qk_scores(query, key, attention_mask=None, scaling=None, kv_len=None, with_p
     b, q_h, _, _ = query.shape
     L = key.shape[2]
     mask = _mask_view(attention_mask, L)
-    scores = torch.empty(b, q_h, 1, L, dtype=torch.float32, device=dev)
+    # rows padded to 16 bytes (the kernel's vector stores), returned as a view
+    scores = torch.empty(b, q_h, 1, (L + 3) // 4 * 4, dtype=torch.float32, device=dev)[..., :L]
     pm = ps = None
     if with_partials:
         nparts = lib.saga_qk_nparts(b, key.shape[1], L)
