@@ -362,6 +362,9 @@ def main():
                          "and the 128k dense-GQA vs SAGA comparison; one JSON line per shape")
     ap.add_argument("--no-fused", action="store_true",
                     help="run the Atop-N fast step as three kernels (scores, slice, row) for every shape")
+    ap.add_argument("--exempt", default="",
+                    help="comma-separated layers that run dense attention in the SAGA model (speedup.py:65-66), "
+                         "e.g. 0,14 for Qwen2.5-1.5B")
     ap.add_argument("--prefill", action="store_true",
                     help="measure the prefill attention kernel alone (its own JSON line) instead of decode")
     ap.add_argument("--profile-kernels", action="store_true",
@@ -399,8 +402,10 @@ def main():
     torch.manual_seed(0)
     prompt = torch.randint(0, SAGA_SHAPE.vocab, (ctx,), dtype=torch.int64)
 
+    exempt = tuple(int(x) for x in args.exempt.split(",") if x.strip())
+
     def build(shape, mode):
-        m = SagaDecoder(shape, B, max_len, mode=mode, top_n=args.top_n)
+        m = SagaDecoder(shape, B, max_len, mode=mode, top_n=args.top_n, exempt_layers=exempt if mode == "atopn" else ())
         t0 = time.perf_counter()
         if args.synthetic_kv:
             m.fill_synthetic(ctx)
@@ -473,7 +478,7 @@ def main():
             "workload": (f"{mdl['name']}-shaped SAGA decoder ({SAGA_SHAPE.layers} layers, hidden {SAGA_SHAPE.hidden}, "
                          f"{SAGA_SHAPE.n_q}Q/{SAGA_SHAPE.n_k}K/{SAGA_SHAPE.n_v}V heads, d{SAGA_SHAPE.head_dim}, "
                          f"vocab {SAGA_SHAPE.vocab}), batch {B}, {ctx}-token context, {K} decode steps, "
-                         f"Atop-N N={args.top_n}"),
+                         f"Atop-N N={args.top_n}" + (f", dense layers {list(exempt)}" if exempt else "")),
             "global_batch": B,
             "seq_len": ctx,
             "parallelism": "single GPU",
