@@ -241,10 +241,10 @@ def prefill(query, key, value, attention_mask=None, scaling=None, is_causal=None
     query head h reads key head h // (q_h // k_h), value head
     h // (q_h // v_h)); the mask is cut to the key length (:28-30); with
     is_causal None the call is causal iff l_q > 1 and there is no mask
-    (:35-36; SDPA's causal mask is top-left: key j <= query i); then SDPA
-    (:41-49): softmax(q k^T * scale + mask) v, a bool mask keeping True
+    (:36-37; SDPA's causal mask is top-left: key j <= query i); then SDPA
+    (:42-50): softmax(q k^T * scale + mask) v, a bool mask keeping True
     entries.  A query that sees no key gives 0 (torch's math path).
-    Returns [b, l_q, q_h, d] (:50, transpose(1, 2))."""
+    Returns [b, l_q, q_h, d] (:51, transpose(1, 2))."""
     q = np.asarray(query)
     dt = np.result_type(q.dtype, np.float32)
     q = q.astype(dt)
@@ -254,7 +254,7 @@ def prefill(query, key, value, attention_mask=None, scaling=None, is_causal=None
     L = k.shape[2]
     mask = None if attention_mask is None else np.asarray(attention_mask)[:, :, :, :L]  # :28-30
     if is_causal is None:
-        is_causal = l_q > 1 and mask is None                        # :35-36
+        is_causal = l_q > 1 and mask is None                        # :36-37
     x = np.matmul(q, np.swapaxes(k, -1, -2)) * dt.type(_scale(q, scaling))
     if mask is not None:
         x = np.where(mask, x, -np.inf) if mask.dtype == np.bool_ else x + mask.astype(dt)
@@ -264,8 +264,8 @@ def prefill(query, key, value, attention_mask=None, scaling=None, is_causal=None
     m = np.where(np.isfinite(m), m, 0)
     e = np.exp(x - m)
     ssum = e.sum(axis=-1, keepdims=True)
-    out = np.matmul(e / np.where(ssum > 0, ssum, 1), v)            # :41-49
-    return np.ascontiguousarray(np.swapaxes(out, 1, 2))             # :50
+    out = np.matmul(e / np.where(ssum > 0, ssum, 1), v)            # :42-50
+    return np.ascontiguousarray(np.swapaxes(out, 1, 2))             # :51
 
 
 def truncate_kv(key, value, kv_len):

@@ -14,7 +14,7 @@ What the reference reads (lm_eval_saga.py:52-146):
     hidden], each with its optional bias, at the checkpoint's own sizes
     (lm_eval_saga.py:101-130), d = hidden_size // num_attention_heads
     (lm_eval_saga.py:99; a config `head_dim` is taken when given).
-Pair-merged checkpoints (merge_heads.py:101-208) are saved with q/v/o already
+Pair-merged checkpoints (merge_heads.py:101-202) are saved with q/v/o already
 permuted to the merged grouping, so `kv_merge_pairs` is not needed to load
 them.  A plain GQA checkpoint can be merged at load time to fewer key heads by
 averaging consecutive groups of key heads and their biases

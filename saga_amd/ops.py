@@ -249,8 +249,8 @@ def prefill_attention(query, key, value, attention_mask=None, scaling=None, is_c
 
     query [b, q_h, Lq, d], key [b, k_h, Lk, d], value [b, v_h, Lk, d] (bf16 /
     f16, d 64 or 128); attention_mask [b|1, q_h|1, Lq|1, >= Lk] (bool keeps
-    True, float is added), cut to Lk as the reference does (:31-32).
-    is_causal None: causal iff Lq > 1 and there is no mask (:37-38); causal
+    True, float is added), cut to Lk as the reference does (:28-30).
+    is_causal None: causal iff Lq > 1 and there is no mask (:36-37); causal
     means key j <= query i + causal_offset (SDPA: causal_offset 0).
     Returns out [b, Lq, q_h, d]: the reference's output after its transpose."""
     dev = _need_gpu(query, key, value, attention_mask)

@@ -404,7 +404,7 @@ def test_prefill_matches_torch_sdpa(q_h, k_h, v_h, kind):
 
 
 def test_prefill_default_causal_rule():
-    """is_causal None: causal for l_q > 1 without a mask (attention/attention.py:35-36)."""
+    """is_causal None: causal for l_q > 1 without a mask (attention/attention.py:36-37)."""
     rng = np.random.default_rng(32)
     q, k, v = _rand(rng, 1, 2, 6, 8), _rand(rng, 1, 1, 6, 8), _rand(rng, 1, 2, 6, 8)
     np.testing.assert_array_equal(O.prefill(q, k, v), O.prefill(q, k, v, is_causal=True))
