@@ -178,6 +178,15 @@ int saga_atopn_workspace_layout(int64_t b, int64_t q_h, int64_t k_h, int64_t L, 
  * MI355X.  Returns the previous setting. */
 int saga_set_fused_fast_step(int enable);
 
+/* How the fast step's selection and softmax.V run (no counterpart in the
+ * reference; results are identical in every mode): 0 (default) by shape,
+ * 1 one block per (batch, head) row -- its waves run the row's 1024-position
+ * slices, then, after a block barrier, the row merge: one launch; the
+ * default for rows of at most 8 slices at head_dim 128 --, 2 a slice kernel
+ * over every (row, slice) and a row kernel.  Returns the previous mode (process-wide),
+ * or SAGA_ERR_INVALID for another value. */
+int saga_set_k2_mode(int mode);
+
 /* Atop-N fast decode step: scores, logit threshold from the stored
  * softmax-space thresholds, ordered compaction capped at
  * buf_k = min(2*top_n, L), sparse softmax . V.

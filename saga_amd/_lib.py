@@ -75,6 +75,7 @@ _SIGS = {
                                          _T, _T, _T, _P]),
     "saga_argmax_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
     "saga_argmax": (ctypes.c_int, [_T, _P, _P, ctypes.c_size_t, _P]),
+    "saga_set_k2_mode": (ctypes.c_int, [ctypes.c_int]),
     "saga_prefill_attention": (ctypes.c_int, [_T, _T, _T, _T, ctypes.c_float, ctypes.c_int32, ctypes.c_int64, _T, _P]),
 }
 GEMV_STORE, GEMV_ADD, GEMV_SILU_PAIRS = 0, 1, 2

@@ -49,6 +49,11 @@ constexpr int kRowMaxSlices = 2048;                   // slice ranks kept in LDS
 constexpr int kRowUnroll = 16;                        // V rows in flight per lane group
 constexpr int kWaveUnroll = 16;                       // slice wave: 4 groups x 16 = 64 V rows in flight
 constexpr int kRowMergeSlices = 8;                    // slice partials per merge thread in one burst
+// auto mode: one block per row when a row has at most this many slices and
+// d = 128 (measured on MI355X, b1-b32: 1.03-1.12x at 4k-8k positions; with
+// more slices per row, or d = 64, the serialised slice waves cost more than
+// the saved launch: 0.73-0.92x)
+constexpr int kRowBlockAutoSlices = 8;
 
 static_assert(kSliceLen == kSliceLoads * 4 * kWave, "slice = whole f32x4 loads of every lane");
 static_assert(kSliceSmall == 4 * kWaveUnroll, "a small slice list is one gather burst of its wave");
@@ -108,14 +113,12 @@ struct SliceWaveShared {
   float scratch[4 * 128];
 };
 
+// One slice wave: slice sl of row r (see the file comment), LDS scratch sh.
 template <int DT, int D>
-__global__ void __launch_bounds__(kSliceThreads) atopn_slice_kernel(FusedSelParams p, PVParams v) {
-  __shared__ SliceWaveShared shw[kSliceWaves];
+__device__ __forceinline__ void slice_wave(const FusedSelParams& p, const PVParams& v, int r, int sl,
+                                           SliceWaveShared& sh) {
   const int lane = threadIdx.x & 63;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t gw = static_cast<int64_t>(blockIdx.x) * kSliceWaves + w;
-  if (gw >= static_cast<int64_t>(p.nrows) * p.nslice) return;
-  const int r = static_cast<int>(gw / p.nslice), sl = static_cast<int>(gw - static_cast<int64_t>(r) * p.nslice);
+  const int64_t gw = static_cast<int64_t>(r) * p.nslice + sl;
   const int bi = r / p.q_h;
   const float* x = p.scores + static_cast<int64_t>(r) * p.ld;
   const float* prow_m = p.pmax + static_cast<int64_t>(r) * p.nparts;
@@ -198,8 +201,8 @@ __global__ void __launch_bounds__(kSliceThreads) atopn_slice_kernel(FusedSelPara
           gval[pos] = xv[k][j];
         }
         if (pos < kSliceSmall) {
-          shw[w].sidx[pos] = e + j;
-          shw[w].sval[pos] = xv[k][j];
+          sh.sidx[pos] = e + j;
+          sh.sval[pos] = xv[k][j];
         }
         ++pos;
       }
@@ -217,13 +220,23 @@ __global__ void __launch_bounds__(kSliceThreads) atopn_slice_kernel(FusedSelPara
     const int vh = h / (v.q_h / v.v_h);
     const char* vbase = v.v + (bi * v.v_sb + static_cast<int64_t>(vh) * v.v_sh) * Elt<DT>::kBytes;
     float m, l;
-    wave_pv_small<DT, D>(n, shw[w].sidx, shw[w].sval, vbase, v.v_sl * Elt<DT>::kBytes, shw[w].scratch,
+    wave_pv_small<DT, D>(n, sh.sidx, sh.sval, vbase, v.v_sl * Elt<DT>::kBytes, sh.scratch,
                          p.sl_o + gw * D, m, l);
     if (lane == 0) {
       p.sl_ml[2 * gw] = m;
       p.sl_ml[2 * gw + 1] = l;
     }
   }
+}
+
+template <int DT, int D>
+__global__ void __launch_bounds__(kSliceThreads) atopn_slice_kernel(FusedSelParams p, PVParams v) {
+  __shared__ SliceWaveShared shw[kSliceWaves];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t gw = static_cast<int64_t>(blockIdx.x) * kSliceWaves + w;
+  if (gw >= static_cast<int64_t>(p.nrows) * p.nslice) return;
+  const int r = static_cast<int>(gw / p.nslice), sl = static_cast<int>(gw - static_cast<int64_t>(r) * p.nslice);
+  slice_wave<DT, D>(p, v, r, sl, shw[w]);
 }
 
 // The slice holding list entry j of a row (pre[s] <= j < pre[s+1]).
@@ -278,19 +291,32 @@ __device__ int2 block_scan_slices(int ns, int* pa, int* pb, int2* wsum, FA fa, F
   return int2{ra, rb};
 }
 
+// LDS of one row merge (NT threads).
+template <int NT>
+struct RowShared {
+  f32x4 accs[NT];
+  float red[NT / kWave];
+  int2 wsum[NT / kWave];
+  int spre[kRowMaxSlices + 1];
+  int sgpre[kRowMaxSlices + 1];
+  int sidx[kRowBatch];
+  float sval[kRowBatch];
+};
+
+// The row merge of row r by the NT threads of a block (see the file comment).
 template <int DT, int D, int NT>
-__global__ void __launch_bounds__(NT) atopn_gather_kernel(FusedSelParams p, PVParams v) {
+__device__ __forceinline__ void row_merge(const FusedSelParams& p, const PVParams& v, int r, RowShared<NT>& sh) {
   constexpr int NW = NT / kWave;
-  __shared__ float red[NW];
-  __shared__ int2 wsum[NW];
-  __shared__ int spre[kRowMaxSlices + 1];
-  __shared__ int sgpre[kRowMaxSlices + 1];
-  __shared__ int sidx[kRowBatch];
-  __shared__ float sval[kRowBatch];
-  __shared__ f32x4 accs[NT];
+  float* red = sh.red;
+  int2* wsum = sh.wsum;
+  int* spre = sh.spre;
+  int* sgpre = sh.sgpre;
+  int* sidx = sh.sidx;
+  float* sval = sh.sval;
+  f32x4* accs = sh.accs;
   constexpr int C = D / 4;             // 16-byte chunks of an output row
   constexpr int G = NT / C;            // slice groups of the partial merge
-  const int r = blockIdx.x, tid = threadIdx.x;
+  const int tid = threadIdx.x;
   const int c = tid % C, g = tid / C;
   const int ns = p.nslice;
   const int64_t row0 = static_cast<int64_t>(r) * ns;
@@ -446,6 +472,32 @@ __global__ void __launch_bounds__(NT) atopn_gather_kernel(FusedSelParams p, PVPa
   }
 }
 
+template <int DT, int D, int NT>
+__global__ void __launch_bounds__(NT) atopn_gather_kernel(FusedSelParams p, PVParams v) {
+  __shared__ RowShared<NT> sh;
+  row_merge<DT, D, NT>(p, v, blockIdx.x, sh);
+}
+
+// One block per row: its waves run the row's slice waves, then (after a
+// block barrier, which orders their workspace writes before the reads) the
+// row merge -- one launch and no kernel boundary between the two phases, for
+// calls with few rows and slices.  The two phases' LDS overlap.
+template <int NT>
+union RowBlockShared {
+  SliceWaveShared shw[NT / kWave];
+  RowShared<NT> row;
+};
+
+template <int DT, int D, int NT>
+__global__ void __launch_bounds__(NT) atopn_rowblock_kernel(FusedSelParams p, PVParams v) {
+  __shared__ RowBlockShared<NT> sh;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = blockIdx.x;
+  for (int sl = w; sl < p.nslice; sl += NT / kWave) slice_wave<DT, D>(p, v, r, sl, sh.shw[w]);
+  __syncthreads();
+  row_merge<DT, D, NT>(p, v, r, sh.row);
+}
+
 template <int DT, int D>
 static hipError_t launch_rows_typed(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
   if (p.cap <= kRowSmallCap)
@@ -457,8 +509,29 @@ static hipError_t launch_rows_typed(const FusedSelParams& p, const PVParams& v, 
   return hipGetLastError();
 }
 
+int g_k2_mode = 0;  // 0: by shape, 1: one block per row, 2: slice kernel + row kernel
+
+int set_k2_mode(int mode) {
+  const int prev = g_k2_mode;
+  g_k2_mode = mode;
+  return prev;
+}
+
+bool k2_row_block(int64_t nslice, int d) {
+  if (g_k2_mode == 1) return true;
+  if (g_k2_mode == 2) return false;
+  return nslice <= kRowBlockAutoSlices && d == 128;
+}
+
 template <int DT, int D>
 static hipError_t launch_split(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
+  if (k2_row_block(p.nslice, D)) {
+    if (p.nslice <= 4)
+      hipLaunchKernelGGL((atopn_rowblock_kernel<DT, D, 256>), dim3(p.nrows), dim3(256), 0, st, p, v);
+    else
+      hipLaunchKernelGGL((atopn_rowblock_kernel<DT, D, 1024>), dim3(p.nrows), dim3(1024), 0, st, p, v);
+    return hipGetLastError();
+  }
   const int64_t waves = static_cast<int64_t>(p.nslice) * p.nrows;
   const unsigned blocks = static_cast<unsigned>((waves + kSliceWaves - 1) / kSliceWaves);
   hipLaunchKernelGGL((atopn_slice_kernel<DT, D>), dim3(blocks), dim3(kSliceThreads), 0, st, p, v);

@@ -478,6 +478,11 @@ int saga_sparse_softmax_pv(const saga_tensor* weights, const saga_tensor* indice
 
 int saga_set_fused_fast_step(int enable) { return set_fused_enabled(enable); }
 
+int saga_set_k2_mode(int mode) {
+  if (mode < 0 || mode > 2) return fail(SAGA_ERR_INVALID, "k2 mode must be 0, 1 or 2");
+  return set_k2_mode(mode);
+}
+
 int64_t saga_qk_nparts(int64_t b, int64_t k_h, int64_t L) {
   if (b < 1 || k_h < 1 || L < 1) return 0;
   return qk_plan(b, k_h, L) / 4;

@@ -105,6 +105,11 @@ constexpr int kSliceSmall = 64;  // slice lists this short are gathered by their
 hipError_t launch_atopn_fast(const FusedSelParams& p, const PVParams& v, hipStream_t st);
 // The per-row kernel of the fast step alone (ranks, cut at buf_k, merge, long gathers).
 hipError_t launch_atopn_rows(const FusedSelParams& p, const PVParams& v, hipStream_t st);
+// Fast-step K2 shape: 0 by shape (one block per row for rows of few slices),
+// 1 always one block per row, 2 always slice kernel + row kernel.  Returns
+// the previous mode; process-wide.
+int set_k2_mode(int mode);
+bool k2_row_block(int64_t nslice, int d);
 
 // Fused fast step: sync region of the workspace (zero before the first call on
 // it; every call leaves it consistent).  Unit u = batch * k_h + key head.

@@ -288,6 +288,18 @@ def set_fused_fast_step(enable: bool) -> bool:
     return bool(_lib.load().saga_set_fused_fast_step(1 if enable else 0))
 
 
+def set_k2_mode(mode: int) -> int:
+    """Process-wide shape of the fast step's selection + softmax.V: 0 by
+    shape (default: one block per row for rows of at most 8 slices of 1024
+    positions at head_dim 128), 1 always one block per row (one launch), 2
+    always slice kernel + row kernel.  Results are identical in every mode.  Returns the
+    previous mode."""
+    prev = _lib.load().saga_set_k2_mode(int(mode))
+    if prev < 0:
+        raise ValueError(f"saga_amd: k2 mode must be 0, 1 or 2, got {mode}")
+    return prev
+
+
 def atopn_workspace_views(b: int, q_h: int, k_h: int, L: int, d: int, buf_k: int, device, fast: bool = True) -> dict:
     """The cached fused-decode workspace after a call, for inspection (valid
     until the next call): logit thresholds (fast step), kept / passing counts,

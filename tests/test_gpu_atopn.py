@@ -250,11 +250,22 @@ def test_reference_api_module_end_to_end(monkeypatch):
     assert B.EXEMPT_LAYERS == {0}
 
 
+@pytest.fixture
+def k2_mode(request):
+    """Force one shape of the fast step's K2 (1: one block per row, 2: slice
+    kernel + row kernel) for the test, restoring the default after it."""
+    prev = ops.set_k2_mode(request.param)
+    yield request.param
+    ops.set_k2_mode(prev)
+
+
+@pytest.mark.parametrize("k2_mode", [1, 2], indirect=True)
 @pytest.mark.parametrize("cut_pos", [2500, 5200])
-def test_fast_overflow_cut_inside_a_later_slice(cut_pos):
+def test_fast_overflow_cut_inside_a_later_slice(cut_pos, k2_mode):
     """More than buf_k positions pass and rank buf_k falls inside a slice
     after the first: the earlier slices count whole, the straddling one over
-    its first entries, later ones not at all (the ordered cap of the oracle)."""
+    its first entries, later ones not at all (the ordered cap of the oracle).
+    Both K2 shapes."""
     rng = np.random.default_rng(cut_pos)
     b, q_h, k_h, v_h, d, L, N = 2, 4, 1, 2, 128, 6000, 256
     q = O.round_bf16(rng.standard_normal((b, q_h, 1, d), dtype=np.float32))
@@ -367,3 +378,51 @@ def _fused_overflow_reps(args, b, q_h, k_h, L, d, N, ref_out, idx_ref, rng):
             ops.atopn_decode(q3, k3, v3, t3, 64)
             torch.cuda.synchronize()
             assert int(_views(bb, 12, 1, LL, 128, 128)["sync_error"][0]) == 0
+
+
+K2_SHAPES = dict(FUSED_SHAPES, **{  # + long slice lists (N = 1024) and a row with no passing position
+    "b4_long_lists": (4, 12, 1, 2, 128, 20000, 1024, "bf16"),
+})
+
+
+@pytest.mark.parametrize("name", list(K2_SHAPES))
+def test_row_block_k2_matches_slice_and_row_kernels(name):
+    """One block per row (slice waves, block barrier, row merge) against the
+    slice kernel + row kernel on the same inputs: identical thresholds,
+    counts, totals and ordered lists; outputs equal to fp32 rounding (the
+    merge's block size may differ); the selection rule holds in both."""
+    b, q_h, k_h, v_h, d, L, N, dt = K2_SHAPES[name]
+    print(f"atopn k2 row-block vs split shape={name}", flush=True)
+    rng = np.random.default_rng(zlib.crc32(name.encode()) + 7)
+    (q, k, v), (qd, kd, vd) = qkv(rng, b, q_h, k_h, v_h, d, L, dt, outliers=0.01)
+    lens = None
+    if name == "b3_ragged":
+        lens = torch.tensor([777, 300, 1], dtype=torch.int32, device="cuda")
+    table = torch.zeros(b * q_h, device="cuda")
+    ops.atopn_calibrate(qd, kd, vd, N, table, kv_len=lens)
+    q2 = O.round_bf16(q + np.float32(0.3) * rng.standard_normal(q.shape, dtype=np.float32))
+    q2d = dev(q2, dt)
+    buf_k = min(2 * N, L)
+    res = {}
+    prev = ops.set_k2_mode(0)
+    try:
+        for mode in (1, 2):
+            ops.set_k2_mode(mode)
+            out = host(_run_fast(q2d, kd, vd, table, N, out_dtype=torch.float32, kv_len=lens))
+            views = _views(b, q_h, k_h, L, d, buf_k, scores_of=(q2d, kd, None, None, lens))
+            _check_selection_rule(views, b * q_h, L, buf_k, kv_len=None if lens is None else host(lens), q_h=q_h)
+            res[mode] = (out, views)
+    finally:
+        ops.set_k2_mode(prev)
+    (o1, v1), (o2, v2) = res[1], res[2]
+    for key in ("sel_cnt", "sel_total", "sel_idx", "thresh"):
+        np.testing.assert_array_equal(v1[key], v2[key])
+    nan = np.isnan(o2)
+    np.testing.assert_array_equal(np.isnan(o1), nan)
+    assert rel_l2(o1[~nan], o2[~nan]) < 1e-6
+    print(f"  mean_count={v1['sel_cnt'].mean():.1f} max={v1['sel_cnt'].max()}", flush=True)
+
+
+def test_k2_mode_switch_rejects_other_values():
+    with pytest.raises(ValueError):
+        ops.set_k2_mode(3)
