@@ -372,8 +372,8 @@ def main():
                          "for hardware-counter runs")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(sharding is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: there is no multi-GPU path (the design shards the "
+              "caches by sequence, not built); run with --gpus 1", file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)

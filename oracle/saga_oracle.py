@@ -1,6 +1,7 @@
 """CPU oracle for the SAGA + Atop-N decode-attention path (numpy restatement).
 
-TEST INFRASTRUCTURE ONLY.  This module is the checker: only ``tests/``,
+TEST INFRASTRUCTURE ONLY.  This module is what the GPU results are checked
+against: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
 import it.  The product path (``saga_amd``) never calls it and has no CPU
 fallback.

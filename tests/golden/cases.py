@@ -18,8 +18,8 @@ import numpy as np
 # reference, attention/attention.py:125); qscale: multiplier on the queries
 # (larger -> more peaked softmax); bf16: round inputs to bfloat16.
 CASES = {
-    # configs[0] of the benchmark definition: b1, 15 Q / 1 K / 5 V heads, d64,
-    # context 4096, fp32, N(0,1) q/k/v, N=128.
+    # the CPU-runnable single-layer decode step: b1, 15 Q / 1 K / 5 V heads,
+    # d64, context 4096, fp32, N(0,1) q/k/v, N=128.
     "c1": dict(seed=1, b=1, q_h=15, k_h=1, v_h=5, d=64, L=4096, N=128, mask=None,
                scaling=None, qscale=1.0, bf16=False),
     "bool_mask": dict(seed=2, b=2, q_h=6, k_h=1, v_h=2, d=64, L=700, N=32, mask="bool",
