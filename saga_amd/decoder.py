@@ -66,7 +66,8 @@ class _HeadGroups(torch.nn.Module):
 
 
 class SagaDecoder:
-    """Random-init decoder with SAGA attention on MI355X.
+    """Qwen2 / Llama-shaped decoder with SAGA attention on MI355X: random-init
+    weights, or a checkpoint's (weights=..., from_pretrained).
 
     mode: "atopn" (calibration + fast Atop-N steps) or "dense" (every layer
     dense; with n_k == n_v this is plain GQA).  exempt_layers run dense in
@@ -342,3 +343,29 @@ class SagaDecoder:
             self.graph_cal.replay()
         else:
             self.graph_fast.replay()
+
+    @torch.no_grad()
+    def generate(self, prompt: torch.Tensor, max_new_tokens: int, graphs: bool = True) -> torch.Tensor:
+        """Greedy generation for every batch row from a batch-1 prompt (the
+        reference benchmark's protocol, speedup.py:146-193): prefill, then
+        max_new_tokens decode steps (calibration first in Atop-N mode).
+        Returns the generated ids [batch, max_new_tokens]: the token picked
+        after the prompt, then the pick of every decode step but the last.
+        graphs: replay the captured HIP graphs (captured on first use), else
+        run the steps eagerly (same kernels, same results)."""
+        if max_new_tokens < 1:
+            return torch.empty(self.batch, 0, dtype=torch.int64, device=self.device)
+        if int(prompt.numel()) + max_new_tokens > self.max_len:
+            raise ValueError("prompt + max_new_tokens does not fit the cache (max_len)")
+        self.prefill(prompt)
+        if graphs and self.graph_fast is None:
+            self.capture()  # leaves the state rewound to just after the prompt
+        out = torch.empty(self.batch, max_new_tokens, dtype=torch.int64, device=self.device)
+        out[:, 0] = self.tokens
+        for i in range(max_new_tokens - 1):
+            if graphs:
+                self.replay(i)
+            else:
+                self.step(calibrate=(self.mode == "atopn" and i == 0))
+            out[:, i + 1] = self.tokens
+        return out

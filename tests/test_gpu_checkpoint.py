@@ -53,3 +53,26 @@ def test_loaded_checkpoint_decodes_like_float64_forward(tmp_path, kind, tie, mod
         top2 = np.sort(ref)[-2:]
         if top2[1] - top2[0] > 0.05:  # bf16 rounding may flip a near tie
             assert int(m.tokens[0]) == int(np.argmax(ref))
+
+
+def test_generate_graphs_equal_eager_steps(tmp_path):
+    """SagaDecoder.generate on a loaded checkpoint: the replayed HIP graphs
+    give the tokens of eager steps, and the first token is the prefill's
+    argmax of the float64 forward when its margin is clear."""
+    from saga_amd.checkpoint import load_checkpoint
+    from saga_amd.decoder import SagaDecoder
+    model = tiny_hf_model("llama", n_kv=2, n_k_shared=1, tie=False, d=64, intermediate=512, vocab=1024)
+    path = str(tmp_path / "saga")
+    save_saga_checkpoint(model, path, n_k=1)
+    m = SagaDecoder.from_pretrained(path, batch=3, max_len=256, mode="atopn", top_n=512)
+    prompt = torch.tensor(np.random.default_rng(9).integers(0, 1024, 90))
+    g = m.generate(prompt, 8)
+    e = m.generate(prompt, 8, graphs=False)
+    torch.cuda.synchronize()
+    assert g.shape == (3, 8) and torch.equal(g, e)
+    assert torch.equal(g[0], g[1]) and torch.equal(g[0], g[2])
+    shape, w = load_checkpoint(path)
+    ref = forward64(shape, w, [int(t) for t in prompt])[-1]
+    top2 = np.sort(ref)[-2:]
+    if top2[1] - top2[0] > 0.05:
+        assert int(g[0, 0]) == int(np.argmax(ref))
