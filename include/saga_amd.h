@@ -181,8 +181,10 @@ int saga_set_fused_fast_step(int enable);
 /* How the fast step's selection and softmax.V run (no counterpart in the
  * reference; results are identical in every mode): 0 (default) by shape,
  * 1 one block per (batch, head) row -- its waves run the row's 1024-position
- * slices, then, after a block barrier, the row merge: one launch; the
- * default for rows of at most 8 slices at head_dim 128 --, 2 a slice kernel
+ * slices and the row's list is kept in LDS (or, for rows of more than 64
+ * slices or buf_k > 2048, written to the workspace and merged after a block
+ * barrier): one launch; the default for rows of at most 12 slices with
+ * buf_k <= 2048 --, 2 a slice kernel
  * over every (row, slice) and a row kernel.  Returns the previous mode (process-wide),
  * or SAGA_ERR_INVALID for another value. */
 int saga_set_k2_mode(int mode);

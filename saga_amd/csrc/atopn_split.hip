@@ -50,10 +50,11 @@ constexpr int kRowUnroll = 16;                        // V rows in flight per la
 constexpr int kWaveUnroll = 16;                       // slice wave: 4 groups x 16 = 64 V rows in flight
 constexpr int kRowMergeSlices = 8;                    // slice partials per merge thread in one burst
 // auto mode: one block per row when a row has at most this many slices and
-// d = 128 (measured on MI355X, b1-b32: 1.03-1.12x at 4k-8k positions; with
-// more slices per row, or d = 64, the serialised slice waves cost more than
-// the saved launch: 0.73-0.92x)
-constexpr int kRowBlockAutoSlices = 8;
+// its list fits one LDS batch (measured on MI355X, attention call at b1-b32,
+// d 64 and 128: 1.02-1.48x at 4k-12k positions; from 16k positions a row's
+// scores and V rows are too much for one CU and the spread slice waves win:
+// 0.84-0.99x)
+constexpr int kRowBlockAutoSlices = 12;
 
 static_assert(kSliceLen == kSliceLoads * 4 * kWave, "slice = whole f32x4 loads of every lane");
 static_assert(kSliceSmall == 4 * kWaveUnroll, "a small slice list is one gather burst of its wave");
@@ -113,62 +114,86 @@ struct SliceWaveShared {
   float scratch[4 * 128];
 };
 
-// One slice wave: slice sl of row r (see the file comment), LDS scratch sh.
-template <int DT, int D>
-__device__ __forceinline__ void slice_wave(const FusedSelParams& p, const PVParams& v, int r, int sl,
-                                           SliceWaveShared& sh) {
-  const int lane = threadIdx.x & 63;
-  const int64_t gw = static_cast<int64_t>(r) * p.nslice + sl;
-  const int bi = r / p.q_h;
-  const float* x = p.scores + static_cast<int64_t>(r) * p.ld;
+// The K1 block partials of row r held by one wave (kSlicePrefetch per lane;
+// rows of more than 256 parts read the rest in row_threshold).
+struct RowPartials {
+  float pm[kSlicePrefetch], ps[kSlicePrefetch], pt[kSlicePrefetch];
+  float pstar;
+};
+
+__device__ __forceinline__ void load_row_partials(const FusedSelParams& p, int r, int lane, RowPartials& rp) {
   const float* prow_m = p.pmax + static_cast<int64_t>(r) * p.nparts;
   const float* prow_s = p.psum + static_cast<int64_t>(r) * p.nparts;
   const float* prow_t = p.ptail + static_cast<int64_t>(r) * p.nparts;
-  const int s0 = sl * kSliceLen;
-
-  // 1. the block partials and the slice's scores in flight together; nothing
-  //    waits for kv_len, which only masks
-  float pm[kSlicePrefetch], ps[kSlicePrefetch], pt[kSlicePrefetch];
 #pragma unroll
   for (int k = 0; k < kSlicePrefetch; ++k) {
     const int c = lane + k * kWave;
-    pm[k] = c < p.nparts ? prow_m[c] : kNegInf;
-    ps[k] = c < p.nparts ? prow_s[c] : 0.f;
-    pt[k] = c < p.nparts ? prow_t[c] : kNegInf;
+    rp.pm[k] = c < p.nparts ? prow_m[c] : kNegInf;
+    rp.ps[k] = c < p.nparts ? prow_s[c] : 0.f;
+    rp.pt[k] = c < p.nparts ? prow_t[c] : kNegInf;
   }
-  f32x4 xv[kSliceLoads];
-#pragma unroll
-  for (int k = 0; k < kSliceLoads; ++k) {
-    const int64_t e = s0 + 4 * (k * kWave + lane);
-    xv[k] = e < p.ld ? *reinterpret_cast<const f32x4*>(x + e) : f32x4{kNegInf, kNegInf, kNegInf, kNegInf};
-  }
-  const float pstar = p.pstar[r];
-  int Leff = p.L;
-  if (p.kv_len) Leff = min(Leff, max(p.kv_len[bi], 0));
-  __builtin_amdgcn_sched_barrier(0);
+  rp.pstar = p.pstar[r];
+}
 
-  // attention/attention.py:142-147: m = max of the last min(256, L) logits
+// t = m + log(max(p*, 1e-30) * sum_j exp(x_j - m)) from the partials
+// (attention/attention.py:142-147: m = max of the last min(256, L) logits);
+// every wave of a row runs the same reductions in the same order, so all of
+// them hold the bit-identical t.
+__device__ __forceinline__ float row_threshold(const FusedSelParams& p, int r, int lane, const RowPartials& rp) {
+  const float* prow_m = p.pmax + static_cast<int64_t>(r) * p.nparts;
+  const float* prow_s = p.psum + static_cast<int64_t>(r) * p.nparts;
+  const float* prow_t = p.ptail + static_cast<int64_t>(r) * p.nparts;
   float tl = kNegInf;
 #pragma unroll
-  for (int k = 0; k < kSlicePrefetch; ++k) tl = fmaxf(tl, pt[k]);
+  for (int k = 0; k < kSlicePrefetch; ++k) tl = fmaxf(tl, rp.pt[k]);
   for (int c = lane + kSlicePrefetch * kWave; c < p.nparts; c += kWave) tl = fmaxf(tl, prow_t[c]);
   const float mt = wave_max(tl);
   float acc = 0.f;
 #pragma unroll
   for (int k = 0; k < kSlicePrefetch; ++k)
-    if (pm[k] != kNegInf) acc += ps[k] * __expf(pm[k] - mt);
+    if (rp.pm[k] != kNegInf) acc += rp.ps[k] * __expf(rp.pm[k] - mt);
   for (int c = lane + kSlicePrefetch * kWave; c < p.nparts; c += kWave) {
     const float m2 = prow_m[c];
     if (m2 != kNegInf) acc += prow_s[c] * __expf(m2 - mt);
   }
   const float ssum = wave_sum(acc);
-  const float t = mt + logf(fmaxf(pstar, 1e-30f) * ssum);
+  return mt + logf(fmaxf(rp.pstar, 1e-30f) * ssum);
+}
 
-  // 2. ordered compaction; element (k, lane, j) is position s0 + 4*(k*64 + lane) + j.
-  //    Ballot j of load k holds flag j of every lane; a passing element's rank
-  //    is the passing elements of earlier loads + those of lower lanes (mbcnt
-  //    of the four ballots) + its own lower flags.  Ranks past slice_cap
-  //    (= min(kSliceLen, buf_k)) can never be among a row's first buf_k.
+// The scores of slice sl of row r: element (k, lane, j) is position
+// sl * kSliceLen + 4*(k*64 + lane) + j (-inf past the row).
+__device__ __forceinline__ void load_slice_scores(const FusedSelParams& p, int r, int sl, int lane,
+                                                  f32x4 (&xv)[kSliceLoads]) {
+  const float* x = p.scores + static_cast<int64_t>(r) * p.ld;
+  const int s0 = sl * kSliceLen;
+#pragma unroll
+  for (int k = 0; k < kSliceLoads; ++k) {
+    const int64_t e = s0 + 4 * (k * kWave + lane);
+    xv[k] = e < p.ld ? *reinterpret_cast<const f32x4*>(x + e) : f32x4{kNegInf, kNegInf, kNegInf, kNegInf};
+  }
+}
+
+// Number of {x > t} in a slice (the predicate of compact_slice).
+__device__ __forceinline__ int count_slice(int s0, float t, int Leff, const f32x4 (&xv)[kSliceLoads], int lane) {
+  int n = 0;
+#pragma unroll
+  for (int k = 0; k < kSliceLoads; ++k) {
+    const int e = s0 + 4 * (k * kWave + lane);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) n += __popcll(__ballot(e + j < Leff && xv[k][j] > t));
+  }
+  return n;
+}
+
+// Ordered compaction of {x > t} over a slice into its workspace list (ranks
+// past slice_cap = min(kSliceLen, buf_k) can never be among a row's first
+// buf_k) and into sidx / sval (if given) at lds_off + rank, below lds_lim.
+// Ballot j of load k holds flag j of every lane; a passing element's rank is
+// the passing elements of earlier loads + those of lower lanes (mbcnt of the
+// four ballots) + its own lower flags.  Returns the slice's count.
+__device__ __forceinline__ int compact_slice(const FusedSelParams& p, int64_t gw, int s0, float t, int Leff,
+                                             const f32x4 (&xv)[kSliceLoads], int lane, int* sidx, float* sval,
+                                             int lds_off, int lds_lim) {
   unsigned long long bal[kSliceLoads][4];
   int n = 0;
   int base[kSliceLoads];
@@ -200,14 +225,36 @@ __device__ __forceinline__ void slice_wave(const FusedSelParams& p, const PVPara
           gidx[pos] = e + j;
           gval[pos] = xv[k][j];
         }
-        if (pos < kSliceSmall) {
-          sh.sidx[pos] = e + j;
-          sh.sval[pos] = xv[k][j];
+        if (sidx && lds_off + pos < lds_lim) {
+          sidx[lds_off + pos] = e + j;
+          sval[lds_off + pos] = xv[k][j];
         }
         ++pos;
       }
     }
   }
+  return n;
+}
+
+// One slice wave: slice sl of row r (see the file comment), LDS scratch sh.
+template <int DT, int D>
+__device__ __forceinline__ void slice_wave(const FusedSelParams& p, const PVParams& v, int r, int sl,
+                                           SliceWaveShared& sh) {
+  const int lane = threadIdx.x & 63;
+  const int64_t gw = static_cast<int64_t>(r) * p.nslice + sl;
+  const int bi = r / p.q_h;
+  // 1. the block partials and the slice's scores in flight together; nothing
+  //    waits for kv_len, which only masks
+  RowPartials rp;
+  load_row_partials(p, r, lane, rp);
+  f32x4 xv[kSliceLoads];
+  load_slice_scores(p, r, sl, lane, xv);
+  int Leff = p.L;
+  if (p.kv_len) Leff = min(Leff, max(p.kv_len[bi], 0));
+  __builtin_amdgcn_sched_barrier(0);
+  const float t = row_threshold(p, r, lane, rp);
+  // 2. ordered compaction
+  const int n = compact_slice(p, gw, sl * kSliceLen, t, Leff, xv, lane, sh.sidx, sh.sval, 0, kSliceSmall);
   if (lane == 0) {
     p.sl_cnt[gw] = n;
     if (sl == 0 && p.t_out) p.t_out[r] = t;
@@ -237,6 +284,53 @@ __global__ void __launch_bounds__(kSliceThreads) atopn_slice_kernel(FusedSelPara
   if (gw >= static_cast<int64_t>(p.nrows) * p.nslice) return;
   const int r = static_cast<int>(gw / p.nslice), sl = static_cast<int>(gw - static_cast<int64_t>(r) * p.nslice);
   slice_wave<DT, D>(p, v, r, sl, shw[w]);
+}
+
+// The slice phase of a row block: wave w of nw handles slices w, w + nw, ...
+// of row r.  The partials and the scores of up to kRowBlockBurst of its
+// slices are in flight together; t is computed once; every slice is
+// compacted into its workspace list (no short-list gathers: the block
+// gathers every kept entry after its barrier).
+constexpr int kRowBlockBurst = 4;
+constexpr int kRowLdsMaxSlices = 64;  // slices of a row in the all-LDS row block
+
+__device__ __forceinline__ void rowblock_slices(const FusedSelParams& p, int r, int w, int nw) {
+  const int lane = threadIdx.x & 63;
+  const int bi = r / p.q_h;
+  RowPartials rp;
+  load_row_partials(p, r, lane, rp);
+  int Leff = p.L;
+  if (p.kv_len) Leff = min(Leff, max(p.kv_len[bi], 0));
+  float t = 0.f;
+  bool have_t = false;
+  for (int g0 = w; g0 < p.nslice; g0 += nw * kRowBlockBurst) {
+    f32x4 xv[kRowBlockBurst][kSliceLoads];
+#pragma unroll
+    for (int u = 0; u < kRowBlockBurst; ++u) {
+      const int sl = g0 + nw * u;
+      if (sl < p.nslice) {
+        load_slice_scores(p, r, sl, lane, xv[u]);
+      } else {
+#pragma unroll
+        for (int k = 0; k < kSliceLoads; ++k) xv[u][k] = f32x4{kNegInf, kNegInf, kNegInf, kNegInf};
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (!have_t) {
+      t = row_threshold(p, r, lane, rp);
+      have_t = true;
+      if (g0 == 0 && lane == 0 && p.t_out) p.t_out[r] = t;
+    }
+#pragma unroll
+    for (int u = 0; u < kRowBlockBurst; ++u) {
+      const int sl = g0 + nw * u;
+      if (sl < p.nslice) {
+        const int64_t gw = static_cast<int64_t>(r) * p.nslice + sl;
+        const int n = compact_slice(p, gw, sl * kSliceLen, t, Leff, xv[u], lane, nullptr, nullptr, 0, 0);
+        if (lane == 0) p.sl_cnt[gw] = n;
+      }
+    }
+  }
 }
 
 // The slice holding list entry j of a row (pre[s] <= j < pre[s+1]).
@@ -304,7 +398,8 @@ struct RowShared {
 };
 
 // The row merge of row r by the NT threads of a block (see the file comment).
-template <int DT, int D, int NT>
+// ALL_GATHER: the slices carry no partials; every kept entry is gathered here.
+template <int DT, int D, int NT, bool ALL_GATHER = false>
 __device__ __forceinline__ void row_merge(const FusedSelParams& p, const PVParams& v, int r, RowShared<NT>& sh) {
   constexpr int NW = NT / kWave;
   float* red = sh.red;
@@ -331,7 +426,7 @@ __device__ __forceinline__ void row_merge(const FusedSelParams& p, const PVParam
   //    loads of unused ones are discarded): counts and partials arrive in one
   //    round trip instead of two (16-bit V only: the f32 kernel has no
   //    registers to spare at 1024 threads)
-  constexpr bool kPrefetch = DT != SAGA_DTYPE_F32;
+  constexpr bool kPrefetch = DT != SAGA_DTYPE_F32 && !ALL_GATHER;
   float ms0[kRowMergeSlices], ls0[kRowMergeSlices];
   f32x4 ov0[kRowMergeSlices];
 #pragma unroll
@@ -350,7 +445,7 @@ __device__ __forceinline__ void row_merge(const FusedSelParams& p, const PVParam
   auto cnt_of = [&](int s) { return p.sl_cnt[row0 + s]; };
   auto whole_gather = [&](int s) {
     const int cnt = p.sl_cnt[row0 + s];
-    return cnt > kSliceSmall ? cnt : 0;
+    return ALL_GATHER || cnt > kSliceSmall ? cnt : 0;
   };
   const int2 tot = block_scan_slices<NT>(ns, pre, gpre, wsum, cnt_of, whole_gather);
   const int total = tot.x;
@@ -362,7 +457,7 @@ __device__ __forceinline__ void row_merge(const FusedSelParams& p, const PVParam
   auto take = [&](int s) { return max(0, min(n - pre[s], pre[s + 1] - pre[s])); };
   auto has_partial = [&](int s) {
     const int cnt = pre[s + 1] - pre[s];
-    return cnt > 0 && cnt <= kSliceSmall && take(s) == cnt;
+    return !ALL_GATHER && cnt > 0 && cnt <= kSliceSmall && take(s) == cnt;
   };
   int ng = tot.y;
   if (total > p.cap) {
@@ -373,7 +468,7 @@ __device__ __forceinline__ void row_merge(const FusedSelParams& p, const PVParam
   // 2. log-sum-exp merge of the slice partials
   float M = kNegInf, lsum = 0.f;
   f32x4 on = {0.f, 0.f, 0.f, 0.f};
-  for (int b0 = 0; b0 < ns; b0 += G * kRowMergeSlices) {
+  for (int b0 = 0; b0 < (ALL_GATHER ? 0 : ns); b0 += G * kRowMergeSlices) {
     float ms[kRowMergeSlices], lsv[kRowMergeSlices];
     f32x4 ov[kRowMergeSlices];
 #pragma unroll
@@ -478,24 +573,115 @@ __global__ void __launch_bounds__(NT) atopn_gather_kernel(FusedSelParams p, PVPa
   row_merge<DT, D, NT>(p, v, blockIdx.x, sh);
 }
 
-// One block per row: its waves run the row's slice waves, then (after a
-// block barrier, which orders their workspace writes before the reads) the
-// row merge -- one launch and no kernel boundary between the two phases, for
-// calls with few rows and slices.  The two phases' LDS overlap.
+// One block per row: its waves compact the row's slices (t once per wave,
+// the scores of several slices in flight together), then, after a block
+// barrier (which orders their workspace writes before the reads), the whole
+// block gathers every kept entry and computes softmax . V -- one launch, no
+// kernel boundary and no per-slice partials.
+template <int DT, int D, int NT>
+__global__ void __launch_bounds__(NT) atopn_rowblock_kernel(FusedSelParams p, PVParams v) {
+  __shared__ RowShared<NT> sh;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = blockIdx.x;
+  rowblock_slices(p, r, w, NT / kWave);
+  __syncthreads();
+  row_merge<DT, D, NT, true>(p, v, r, sh);
+}
+
+// One block per row with the whole selection in LDS (rows of at most
+// NT / 64 * kRowBlockBurst slices, buf_k <= kRowBatch): the waves hold the
+// scores of their slices in registers, count them into LDS, one wave scans
+// the counts, the waves write every kept entry at its rank in the row's list
+// (the first buf_k in position order) in LDS -- and, for inspection, into
+// the workspace lists --, and the block gathers the V rows of the list:
+// no global round trip between the slice phase and the gather.
 template <int NT>
-union RowBlockShared {
-  SliceWaveShared shw[NT / kWave];
-  RowShared<NT> row;
+struct RowLdsShared {
+  float accs[(NT / kWave) * 128];
+  float red[NT / kWave];
+  int cnt[kRowLdsMaxSlices];
+  int pre[kRowLdsMaxSlices + 1];
+  int sidx[kRowBatch];
+  float sval[kRowBatch];
 };
 
 template <int DT, int D, int NT>
-__global__ void __launch_bounds__(NT) atopn_rowblock_kernel(FusedSelParams p, PVParams v) {
-  __shared__ RowBlockShared<NT> sh;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+__global__ void __launch_bounds__(NT) atopn_rowlds_kernel(FusedSelParams p, PVParams v) {
+  constexpr int NW = NT / kWave;
+  static_assert(NW * kRowBlockBurst <= kRowLdsMaxSlices, "slice counts fit the LDS arrays");
+  __shared__ RowLdsShared<NT> sh;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = blockIdx.x;
-  for (int sl = w; sl < p.nslice; sl += NT / kWave) slice_wave<DT, D>(p, v, r, sl, sh.shw[w]);
-  __syncthreads();
-  row_merge<DT, D, NT>(p, v, r, sh.row);
+  const int bi = r / p.q_h, h = r - bi * p.q_h;
+  const int ns = p.nslice;  // <= NW * kRowBlockBurst (host-checked)
+
+  // A. partials and the scores of the wave's slices w, w + NW, ... in flight
+  //    together; t; the slice counts
+  RowPartials rp;
+  load_row_partials(p, r, lane, rp);
+  f32x4 xv[kRowBlockBurst][kSliceLoads];
+#pragma unroll
+  for (int u = 0; u < kRowBlockBurst; ++u) {
+    const int sl = w + NW * u;
+    if (sl < ns) {
+      load_slice_scores(p, r, sl, lane, xv[u]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < kSliceLoads; ++k) xv[u][k] = f32x4{kNegInf, kNegInf, kNegInf, kNegInf};
+    }
+  }
+  int Leff = p.L;
+  if (p.kv_len) Leff = min(Leff, max(p.kv_len[bi], 0));
+  __builtin_amdgcn_sched_barrier(0);
+  const float t = row_threshold(p, r, lane, rp);
+#pragma unroll
+  for (int u = 0; u < kRowBlockBurst; ++u) {
+    const int sl = w + NW * u;
+    if (sl < ns) {
+      const int c = count_slice(sl * kSliceLen, t, Leff, xv[u], lane);
+      if (lane == 0) sh.cnt[sl] = c;
+    }
+  }
+  lds_sync();
+  // B. slice ranks (one wave: ns <= 64)
+  if (w == 0) {
+    const int c = lane < ns ? sh.cnt[lane] : 0;
+    const int incl = wave_incl_scan(c, lane);
+    if (lane < ns) sh.pre[lane] = incl - c;
+    if (lane == ns - 1) sh.pre[ns] = incl;
+  }
+  lds_sync();
+  const int total = sh.pre[ns];
+  const int n = min(total, p.cap);
+  // C. every kept entry at its rank (LDS list of the first n), the workspace lists and counts
+#pragma unroll
+  for (int u = 0; u < kRowBlockBurst; ++u) {
+    const int sl = w + NW * u;
+    if (sl < ns) {
+      const int64_t gw = static_cast<int64_t>(r) * ns + sl;
+      const int c = compact_slice(p, gw, sl * kSliceLen, t, Leff, xv[u], lane, sh.sidx, sh.sval, sh.pre[sl], n);
+      if (lane == 0) p.sl_cnt[gw] = c;
+    }
+  }
+  if (w == 0 && lane == 0 && p.t_out) p.t_out[r] = t;
+  lds_sync();
+  // D. softmax . V over the list
+  const int vh = h / (v.q_h / v.v_h);
+  const char* vbase = v.v + (bi * v.v_sb + static_cast<int64_t>(vh) * v.v_sh) * Elt<DT>::kBytes;
+  BlockPV<DT, D, NT, kRowUnroll> pv;
+  pv.init();
+  if (n > 0) pv.add(n, sh.sidx, sh.sval, vbase, v.v_sl * Elt<DT>::kBytes, false, sh.red);
+  const float o = pv.reduce(sh.accs);  // thread i < D: dim i
+  if (tid < D) {
+    const int64_t ooff = bi * v.o_sb + static_cast<int64_t>(h) * v.o_sh;
+    // no passing position: softmax over an empty (all -inf) list is NaN
+    store_from_f32(v.out, v.out_dt, ooff + tid, n == 0 ? __builtin_nanf("") : o / pv.l);
+  }
+  if (tid == 0) {
+    p.sel_cnt[r] = n;
+    if (p.sel_total) p.sel_total[r] = total;
+  }
 }
 
 template <int DT, int D>
@@ -517,17 +703,19 @@ int set_k2_mode(int mode) {
   return prev;
 }
 
-bool k2_row_block(int64_t nslice, int d) {
+bool k2_row_block(int64_t nslice, int64_t cap) {
   if (g_k2_mode == 1) return true;
   if (g_k2_mode == 2) return false;
-  return nslice <= kRowBlockAutoSlices && d == 128;
+  return nslice <= kRowBlockAutoSlices && cap <= kRowBatch;
 }
 
 template <int DT, int D>
 static hipError_t launch_split(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
-  if (k2_row_block(p.nslice, D)) {
-    if (p.nslice <= 4)
-      hipLaunchKernelGGL((atopn_rowblock_kernel<DT, D, 256>), dim3(p.nrows), dim3(256), 0, st, p, v);
+  if (k2_row_block(p.nslice, p.cap)) {
+    if (p.cap <= kRowBatch && p.nslice <= 4)
+      hipLaunchKernelGGL((atopn_rowlds_kernel<DT, D, 256>), dim3(p.nrows), dim3(256), 0, st, p, v);
+    else if (p.cap <= kRowBatch && p.nslice <= 16 * kRowBlockBurst)
+      hipLaunchKernelGGL((atopn_rowlds_kernel<DT, D, 1024>), dim3(p.nrows), dim3(1024), 0, st, p, v);
     else
       hipLaunchKernelGGL((atopn_rowblock_kernel<DT, D, 1024>), dim3(p.nrows), dim3(1024), 0, st, p, v);
     return hipGetLastError();

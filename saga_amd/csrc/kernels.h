@@ -109,7 +109,7 @@ hipError_t launch_atopn_rows(const FusedSelParams& p, const PVParams& v, hipStre
 // 1 always one block per row, 2 always slice kernel + row kernel.  Returns
 // the previous mode; process-wide.
 int set_k2_mode(int mode);
-bool k2_row_block(int64_t nslice, int d);
+bool k2_row_block(int64_t nslice, int64_t cap);
 
 // Fused fast step: sync region of the workspace (zero before the first call on
 // it; every call leaves it consistent).  Unit u = batch * k_h + key head.

@@ -380,8 +380,10 @@ def _fused_overflow_reps(args, b, q_h, k_h, L, d, N, ref_out, idx_ref, rng):
             assert int(_views(bb, 12, 1, LL, 128, 128)["sync_error"][0]) == 0
 
 
-K2_SHAPES = dict(FUSED_SHAPES, **{  # + long slice lists (N = 1024) and a row with no passing position
+K2_SHAPES = dict(FUSED_SHAPES, **{  # + long slice lists; lists past one LDS batch; rows past 64 slices
     "b4_long_lists": (4, 12, 1, 2, 128, 20000, 1024, "bf16"),
+    "b2_buf4096": (2, 12, 1, 2, 128, 20000, 2048, "bf16"),
+    "b1_70k": (1, 12, 1, 2, 128, 70000, 256, "bf16"),
 })
 
 
