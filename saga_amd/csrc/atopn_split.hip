@@ -37,7 +37,7 @@ namespace saga {
 constexpr int kSliceThreads = 256;                    // 4 independent slice waves per block
 constexpr int kSliceWaves = kSliceThreads / kWave;    // 4
 constexpr int kSliceLoads = kSliceLen / (4 * kWave);  // f32x4 loads per lane: 4
-constexpr int kSlicePrefetch = 4;                     // partials per lane in the first burst
+constexpr int kSlicePrefetch = 8;                     // partials per lane in the first burst
 // row kernel block: 256 threads when at most 1024 positions count per row
 // (buf_k <= 1024: the partial merge dominates, a small block launches and
 // synchronises faster), 1024 threads for longer lists (block-wide gathers)
@@ -114,8 +114,9 @@ struct SliceWaveShared {
   float scratch[4 * 128];
 };
 
-// The K1 block partials of row r held by one wave (kSlicePrefetch per lane;
-// rows of more than 256 parts read the rest in row_threshold).
+// The K1 block partials of row r held by one wave (kSlicePrefetch per lane:
+// 512 parts, b >= 2 at 128k positions, in the first burst; longer rows read
+// the rest in row_threshold, one more round trip).
 struct RowPartials {
   float pm[kSlicePrefetch], ps[kSlicePrefetch], pt[kSlicePrefetch];
   float pstar;
