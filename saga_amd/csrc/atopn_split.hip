@@ -596,9 +596,9 @@ __global__ void __launch_bounds__(NT) atopn_rowblock_kernel(FusedSelParams p, PV
 // (the first buf_k in position order) in LDS -- and, for inspection, into
 // the workspace lists --, and the block gathers the V rows of the list:
 // no global round trip between the slice phase and the gather.
-template <int NT>
+template <int NT, int D>
 struct RowLdsShared {
-  float accs[(NT / kWave) * 128];
+  float accs[(NT / kWave) * D];
   float red[NT / kWave];
   int cnt[kRowLdsMaxSlices];
   int pre[kRowLdsMaxSlices + 1];
@@ -610,7 +610,7 @@ template <int DT, int D, int NT>
 __global__ void __launch_bounds__(NT) atopn_rowlds_kernel(FusedSelParams p, PVParams v) {
   constexpr int NW = NT / kWave;
   static_assert(NW * kRowBlockBurst <= kRowLdsMaxSlices, "slice counts fit the LDS arrays");
-  __shared__ RowLdsShared<NT> sh;
+  __shared__ RowLdsShared<NT, D> sh;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = blockIdx.x;
