@@ -290,8 +290,8 @@ def set_fused_fast_step(enable: bool) -> bool:
 
 def set_k2_mode(mode: int) -> int:
     """Process-wide shape of the fast step's selection + softmax.V: 0 by
-    shape (default: one block per row for rows of at most 8 slices of 1024
-    positions at head_dim 128), 1 always one block per row (one launch), 2
+    shape (default: one block per row for rows of at most 12 slices of 1024
+    positions with buf_k <= 2048), 1 always one block per row (one launch), 2
     always slice kernel + row kernel.  Results are identical in every mode.  Returns the
     previous mode."""
     prev = _lib.load().saga_set_k2_mode(int(mode))
