@@ -20,7 +20,7 @@ import torch
 
 import cases
 from conftest import rel_l2, set_diff_outside_band
-from gpu_util import dev, host, qkv
+from gpu_util import dev, host, qkv, round_to
 from oracle import saga_oracle as O
 from saga_amd import ops
 
@@ -428,3 +428,77 @@ def test_row_block_k2_matches_slice_and_row_kernels(name):
 def test_k2_mode_switch_rejects_other_values():
     with pytest.raises(ValueError):
         ops.set_k2_mode(3)
+
+
+def _random_case(seed):
+    """A seeded shape around the kernels' size boundaries: 1024-position
+    slices (one, 4 / 5 and 12 / 13 per row: the row-block thread-count and
+    auto-rule edges), ragged tails, buf_k around 1024 / 2048, one position,
+    head groupings with more key or more value heads, three dtypes and
+    ragged kv_len."""
+    rng = np.random.default_rng(1000 + seed)
+    k_h, v_h, q_h = [(1, 2, 12), (1, 5, 15), (2, 4, 8), (3, 1, 6), (2, 2, 4), (1, 1, 16), (4, 2, 8)][seed % 7]
+    L, N = [(1, 1), (63, 512), (257, 300), (1023, 7), (1025, 64), (4096, 300), (4097, 512), (5 * 1024 - 3, 1024),
+            (12 * 1024, 1024), (12 * 1024 + 1, 512), (13 * 1024 + 5, 256), (16 * 1024 + 3, 1024), (20000, 2048),
+            (8192, 1), (3000, 1500), (9000, 64)][seed]
+    b = int(rng.integers(1, 4))
+    d = (128, 64)[(seed // 2) % 2]
+    dt = ["bf16", "f16", "f32"][seed % 3]
+    lens = None
+    if seed % 4 == 3 and L > 1:
+        b = 3
+        lens = np.array([L, int(rng.integers(1, L + 1)), 1], dtype=np.int32)
+    return b, q_h, k_h, v_h, d, L, N, dt, lens, rng
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_fast_step_random_shapes_vs_oracle(seed):
+    """Calibration and fast step in the default (by-shape) kernel choice at
+    seeded shapes against the oracle: thresholds, the ordered selection rule
+    on the GPU's own scores, sets outside a near-tie band, and outputs (fp32
+    out) against the reference fp32 path on the GPU's selection."""
+    b, q_h, k_h, v_h, d, L, N, dt, lens, rng = _random_case(seed)
+    print(f"atopn random seed={seed} b={b} q/k/v={q_h}/{k_h}/{v_h} d={d} L={L} N={N} {dt} kv_len={lens}", flush=True)
+    (q, k, v), (qd, kd, vd) = qkv(rng, b, q_h, k_h, v_h, d, L, dt, outliers=0.01 * (seed % 2))
+    q2 = round_to(q + np.float32(0.3) * rng.standard_normal(q.shape, dtype=np.float32), dt)
+    q2d = dev(q2, dt)
+    kvl = None if lens is None else torch.from_numpy(lens).cuda()
+    nr, buf_k = b * q_h, min(2 * N, L)
+    table = torch.zeros(nr, device="cuda")
+    ops.atopn_calibrate(qd, kd, vd, N, table, kv_len=kvl)
+    out = host(_run_fast(q2d, kd, vd, table, N, kv_len=kvl))
+    views = _views(b, q_h, k_h, L, d, buf_k, scores_of=(q2d, kd, None, None, kvl))
+    _check_selection_rule(views, nr, L, buf_k, kv_len=lens, q_h=q_h)
+    thr = host(table)
+    logits = O.qk_scores(q2, k).reshape(nr, L)
+    tol = 1e-5 if dt == "f32" else 1e-3
+    for i in range(b):
+        n = L if lens is None else int(lens[i])
+        rows = slice(i * q_h, (i + 1) * q_h)
+        ki, vi = k[i:i + 1, :, :n], v[i:i + 1, :, :n]
+        _, rt, _ = O.calibrate(q[i:i + 1], ki, vi, None, N, None)
+        np.testing.assert_allclose(thr[rows], rt, rtol=1e-4, atol=1e-30)
+        _, t_ref, idx_ref, cnt_ref = O.fast(q2[i:i + 1], ki, vi, thr[rows], None, N, None)
+        fin = np.isfinite(t_ref)
+        np.testing.assert_array_equal(np.isfinite(views["thresh"][rows]), fin)
+        np.testing.assert_allclose(views["thresh"][rows][fin], t_ref[fin], rtol=1e-5, atol=1e-5)
+        bk = min(2 * N, n)
+        for j in range(q_h):
+            r = i * q_h + j
+            sel = views["sel_idx"][r, :views["sel_cnt"][r]]
+            sel_ref = idx_ref.reshape(q_h, bk)[j, :min(int(cnt_ref[j]), bk)]
+            if cnt_ref[j] > bk:
+                np.testing.assert_array_equal(sel, sel_ref)  # ordered overflow rule
+            elif fin[j]:
+                band = 1e-4 * max(1.0, abs(float(t_ref[j])))
+                assert not set_diff_outside_band(sel, sel_ref, views["scores"][r], t_ref[j], band)
+            # the reference fp32 path on the GPU's own selection
+            cnt = views["sel_cnt"][r]
+            if cnt == 0:
+                assert np.isnan(out.reshape(nr, d)[r]).all()
+                continue
+            vals = logits[r, sel][None, None, None, :]
+            ref = O.gather_output(vals, sel[None, None, None, :].astype(np.int64),
+                                  v[i:i + 1, (j // (q_h // v_h)):(j // (q_h // v_h)) + 1], (1, 1, 1, d),
+                                  input_is_logits=True)
+            assert rel_l2(out.reshape(nr, d)[r], ref.reshape(d)) < tol, (r, cnt)
