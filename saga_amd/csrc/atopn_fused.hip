@@ -43,6 +43,8 @@
 // arrives before it waits, and no block waits on another unit.  A wait that
 // exceeds kFusedSpinLimit polls sets the sync error word, empties the
 // block's lists and returns, so the kernel always ends.
+#include <atomic>
+
 #include "block_pv.cuh"
 #include "qk_wave.cuh"
 
@@ -356,9 +358,10 @@ hipError_t launch_atopn_rows(const FusedSelParams& p, const PVParams& v, hipStre
 
 namespace {
 
+// Per-device facts queried once (a racing first call stores the same values).
 struct FusedDev {
-  int cus = 0;
-  int checked = 0;  // bit per (dtype, d) instantiation: occupancy verified
+  std::atomic<int> cus{0};
+  std::atomic<int> checked{0};  // bit per (dtype, d) instantiation: occupancy verified
 };
 FusedDev g_fused_dev[64];
 
@@ -390,13 +393,9 @@ hipError_t launch_fused_typed(const QKParams& q, const FusedSelParams& p, const 
 
 // Off by default: measured slower than the three-kernel path at every shape
 // it covers on MI355X (see the A/B switch saga_set_fused_fast_step).
-int g_fused_enabled = 0;
+static std::atomic<int> g_fused_enabled{0};
 
-int set_fused_enabled(int enable) {
-  const int prev = g_fused_enabled;
-  g_fused_enabled = enable ? 1 : 0;
-  return prev;
-}
+int set_fused_enabled(int enable) { return g_fused_enabled.exchange(enable ? 1 : 0); }
 
 int fused_device_cus() {
   int dev = 0;
@@ -414,7 +413,7 @@ bool atopn_fused_fits(int64_t b, int64_t k_h, int64_t g, int64_t L) {
   const int64_t units = b * k_h;
   const int64_t nb = qk_plan(b, k_h, L) / 4;
   const int cus = fused_device_cus();
-  return g_fused_enabled && L > 0 && g <= 16 && units <= kFusedMaxUnits && nb <= kFusedMaxBlocks &&
+  return g_fused_enabled.load() && L > 0 && g <= 16 && units <= kFusedMaxUnits && nb <= kFusedMaxBlocks &&
          units * nb <= static_cast<int64_t>(cus) * kFusedBlocksPerCU;
 }
 

@@ -29,6 +29,8 @@
 // one gather burst deep, skewed or overflowing rows cost at most buf_k
 // block-parallel gathers.  The kernel boundary orders the slice writes before
 // the row reads (no device-scope fences or counters).
+#include <atomic>
+
 #include "block_pv.cuh"
 #include "kernels.h"
 
@@ -696,17 +698,15 @@ static hipError_t launch_rows_typed(const FusedSelParams& p, const PVParams& v, 
   return hipGetLastError();
 }
 
-int g_k2_mode = 0;  // 0: by shape, 1: one block per row, 2: slice kernel + row kernel
+// 0: by shape, 1: one block per row, 2: slice kernel + row kernel
+static std::atomic<int> g_k2_mode{0};
 
-int set_k2_mode(int mode) {
-  const int prev = g_k2_mode;
-  g_k2_mode = mode;
-  return prev;
-}
+int set_k2_mode(int mode) { return g_k2_mode.exchange(mode); }
 
 bool k2_row_block(int64_t nslice, int64_t cap) {
-  if (g_k2_mode == 1) return true;
-  if (g_k2_mode == 2) return false;
+  const int mode = g_k2_mode.load();
+  if (mode == 1) return true;
+  if (mode == 2) return false;
   return nslice <= kRowBlockAutoSlices && cap <= kRowBatch;
 }
 
