@@ -55,12 +55,43 @@ constexpr int kMaxGroup = 16;             // query heads per key head (one MFMA 
 
 int64_t align256(int64_t x) { return (x + 255) & ~static_cast<int64_t>(255); }
 
+// Sizes whose Atop-N workspace arithmetic stays far inside int64 (every
+// region below 2^58 bytes): the layout query and the entry points refuse others.
+bool atopn_sizes_ok(int64_t b, int64_t q_h, int64_t k_h, int64_t L, int64_t d, int64_t buf_k) {
+  if (b < 1 || q_h < 1 || k_h < 1 || k_h > q_h || L < 1 || L >= kMaxLen || d < 1 || d > 1024 || buf_k < 1 ||
+      buf_k >= kMaxLen)
+    return false;
+  if (b > ((1LL << 31) - 1) / q_h) return false;
+  const int64_t widest = std::max<int64_t>((L + 15) / 16 * 16 + kSliceLen, buf_k);
+  return b * q_h <= (1LL << 55) / widest;
+}
+
+// Sizes >= 1, strides >= 0, and element counts and offsets that the
+// index arithmetic of the entry points holds without overflow.
+constexpr int64_t kMaxDim = (1LL << 31);   // a size (positions are int32 inside kernels)
+constexpr int64_t kMaxSpan = (1LL << 48);  // elements, a stride, and the last element's offset
+int check_dims(const saga_tensor* t, const char* name) {
+  int64_t elems = 1, span = 0;
+  for (int i = 0; i < t->ndim; ++i) {
+    const int64_t n = t->shape[i], st = t->stride[i];
+    if (n < 1) return fail(SAGA_ERR_INVALID, "%s: dim %d has size %lld", name, i, (long long)n);
+    if (n >= kMaxDim || st < 0 || st > kMaxSpan)
+      return fail(SAGA_ERR_INVALID, "%s: dim %d size %lld or stride %lld out of range", name, i, (long long)n,
+                  (long long)st);
+    if (elems > kMaxSpan / n) return fail(SAGA_ERR_UNSUPPORTED, "%s: too many elements", name);
+    elems *= n;
+    if (st > 0 && n - 1 > (kMaxSpan - span) / st) return fail(SAGA_ERR_UNSUPPORTED, "%s: offsets too large", name);
+    span += (n - 1) * st;
+  }
+  return SAGA_OK;
+}
+
 int check_tensor(const saga_tensor* t, const char* name, int ndim) {
   if (!t) return fail(SAGA_ERR_INVALID, "%s: null tensor descriptor", name);
   if (!t->data) return fail(SAGA_ERR_INVALID, "%s: null data pointer", name);
   if (t->ndim != ndim) return fail(SAGA_ERR_INVALID, "%s: expected %d dims, got %d", name, ndim, t->ndim);
-  for (int i = 0; i < ndim; ++i)
-    if (t->shape[i] < 1) return fail(SAGA_ERR_INVALID, "%s: dim %d has size %lld", name, i, (long long)t->shape[i]);
+  int rc;
+  if ((rc = check_dims(t, name))) return rc;
   if (elt_size(t->dtype) == 0) return fail(SAGA_ERR_INVALID, "%s: unknown dtype %d", name, t->dtype);
   return SAGA_OK;
 }
@@ -244,7 +275,8 @@ int atopn_run(bool calibrate, const saga_tensor* query, const saga_tensor* key, 
   if ((rc = check_qk(query, key, mask, &s)) || (rc = check_v(value, &s)) || (rc = check_out(out, s))) return rc;
   if (top_n < 1) return fail(SAGA_ERR_INVALID, "top_n must be >= 1, got %lld", (long long)top_n);
   if (calibrate ? !pstar_out : !pstar_in) return fail(SAGA_ERR_INVALID, "threshold table row is null");
-  const int64_t buf_k = calibrate ? (top_n < s.L ? top_n : s.L) : (2 * top_n < s.L ? 2 * top_n : s.L);
+  const int64_t buf_k = calibrate ? (top_n < s.L ? top_n : s.L) : (top_n < (s.L + 1) / 2 ? 2 * top_n : s.L);
+  if (!atopn_sizes_ok(s.b, s.q_h, s.k_h, s.L, s.d, buf_k)) return fail(SAGA_ERR_UNSUPPORTED, "workspace too large");
   saga_atopn_layout lay;
   atopn_layout(s.b, s.q_h, s.k_h, s.L, s.d, buf_k, &lay);
   if (!workspace || workspace_bytes < static_cast<size_t>(lay.total_bytes))
@@ -320,6 +352,8 @@ int atopn_run(bool calibrate, const saga_tensor* query, const saga_tensor* key, 
 // step.  The split count never grows with the number of units, so the
 // workspace bound computed for k_h = 1 covers every k_h.
 void dense_plan(int64_t units, int64_t L, int64_t* nsplit, int64_t* split_len) {
+  units = std::max<int64_t>(units, 1);
+  L = std::max<int64_t>(L, 1);
   int64_t ns = (512 + units - 1) / units;
   const int64_t by_len = (L + 511) / 512;
   if (ns > by_len) ns = by_len;
@@ -336,6 +370,8 @@ int rows_of(const saga_tensor* t, const char* name, int64_t* rows, int64_t* ld) 
   if (!t->data) return fail(SAGA_ERR_INVALID, "%s: null data pointer", name);
   if (t->ndim < 1 || t->ndim > 4) return fail(SAGA_ERR_INVALID, "%s: 1 to 4 dims expected", name);
   if (t->stride[t->ndim - 1] != 1) return fail(SAGA_ERR_INVALID, "%s: innermost stride must be 1", name);
+  int rc;
+  if ((rc = check_dims(t, name))) return rc;
   int64_t r = 1;
   for (int i = 0; i + 1 < t->ndim; ++i) r *= t->shape[i];
   *rows = r;
@@ -484,12 +520,12 @@ int saga_set_k2_mode(int mode) {
 }
 
 int64_t saga_qk_nparts(int64_t b, int64_t k_h, int64_t L) {
-  if (b < 1 || k_h < 1 || L < 1) return 0;
+  if (b < 1 || k_h < 1 || L < 1 || L >= kMaxLen || b > ((1LL << 31) - 1) / k_h) return 0;
   return qk_plan(b, k_h, L) / 4;
 }
 
 size_t saga_atopn_workspace_bytes(int64_t b, int64_t q_h, int64_t k_h, int64_t L, int64_t d, int64_t buf_k) {
-  if (b < 1 || q_h < 1 || k_h < 1 || L < 1 || d < 1 || buf_k < 1) return 0;
+  if (!atopn_sizes_ok(b, q_h, k_h, L, d, buf_k)) return 0;
   saga_atopn_layout lay;
   atopn_layout(b, q_h, k_h, L, d, buf_k, &lay);
   return static_cast<size_t>(lay.total_bytes);
@@ -498,7 +534,8 @@ size_t saga_atopn_workspace_bytes(int64_t b, int64_t q_h, int64_t k_h, int64_t L
 int saga_atopn_workspace_layout(int64_t b, int64_t q_h, int64_t k_h, int64_t L, int64_t d, int64_t buf_k,
                                 saga_atopn_layout* layout) {
   if (!layout) return fail(SAGA_ERR_INVALID, "layout: null");
-  if (b < 1 || q_h < 1 || k_h < 1 || L < 1 || d < 1 || buf_k < 1) return fail(SAGA_ERR_INVALID, "sizes must be >= 1");
+  if (!atopn_sizes_ok(b, q_h, k_h, L, d, buf_k))
+    return fail(SAGA_ERR_INVALID, "sizes must be >= 1 (k_h <= q_h) and the workspace must fit int64");
   atopn_layout(b, q_h, k_h, L, d, buf_k, layout);
   return ok();
 }
@@ -520,6 +557,7 @@ int saga_atopn_calibrate(const saga_tensor* query, const saga_tensor* key, const
 }
 
 size_t saga_dense_workspace_bytes(int64_t b, int64_t q_h, int64_t L, int64_t d) {
+  if (b < 1 || q_h < 1 || L < 1 || L >= kMaxLen || d < 1 || d > 1024 || b > ((1LL << 31) - 1) / q_h) return 0;
   int64_t ns, sl;
   dense_plan(b, L, &ns, &sl);
   return static_cast<size_t>(align256(b * q_h * ns * (2 + d) * 4));
@@ -750,7 +788,7 @@ int saga_silu_mul(const saga_tensor* gate_up, saga_tensor* y, saga_stream_t stre
 }
 
 size_t saga_gemv_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-  if (M < 1 || N < 16 || K < 32) return 0;
+  if (M < 1 || M > 16 || N < 16 || K < 32 || N >= (1LL << 31) || K >= (1LL << 31)) return 0;
   const int s = gemv_splits(N, K);
   if (s <= 1) return 0;
   return static_cast<size_t>(align256(s * M * N * 4) + align256(s * M * 4));
