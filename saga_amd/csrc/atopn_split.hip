@@ -188,12 +188,19 @@ __device__ __forceinline__ int count_slice(int s0, float t, int Leff, const f32x
   return n;
 }
 
+// Where compact_slice writes the slice's workspace list: element by element
+// (kListDirect), not at all (kListNone: the caller copies it from LDS), or
+// element by element only when it does not fit the LDS list (kListIfLong;
+// else the caller copies the LDS list with one coalesced store per lane).
+enum ListStores { kListDirect, kListNone, kListIfLong };
+
 // Ordered compaction of {x > t} over a slice into its workspace list (ranks
 // past slice_cap = min(kSliceLen, buf_k) can never be among a row's first
 // buf_k) and into sidx / sval (if given) at lds_off + rank, below lds_lim.
 // Ballot j of load k holds flag j of every lane; a passing element's rank is
 // the passing elements of earlier loads + those of lower lanes (mbcnt of the
 // four ballots) + its own lower flags.  Returns the slice's count.
+template <ListStores LS = kListDirect>
 __device__ __forceinline__ int compact_slice(const FusedSelParams& p, int64_t gw, int s0, float t, int Leff,
                                              const f32x4 (&xv)[kSliceLoads], int lane, int* sidx, float* sval,
                                              int lds_off, int lds_lim) {
@@ -212,6 +219,7 @@ __device__ __forceinline__ int compact_slice(const FusedSelParams& p, int64_t gw
   }
   int32_t* gidx = p.sl_idx + gw * p.slice_cap;
   float* gval = p.sl_val + gw * p.slice_cap;
+  const bool to_global = LS == kListDirect || (LS == kListIfLong && lds_off + n > lds_lim);
 #pragma unroll
   for (int k = 0; k < kSliceLoads; ++k) {
     int pos = base[k];
@@ -224,7 +232,7 @@ __device__ __forceinline__ int compact_slice(const FusedSelParams& p, int64_t gw
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       if ((bal[k][j] >> lane) & 1ull) {
-        if (pos < p.slice_cap) {
+        if (to_global && pos < p.slice_cap) {
           gidx[pos] = e + j;
           gval[pos] = xv[k][j];
         }
@@ -257,10 +265,17 @@ __device__ __forceinline__ void slice_wave(const FusedSelParams& p, const PVPara
   __builtin_amdgcn_sched_barrier(0);
   const float t = row_threshold(p, r, lane, rp);
   // 2. ordered compaction
-  const int n = compact_slice(p, gw, sl * kSliceLen, t, Leff, xv, lane, sh.sidx, sh.sval, 0, kSliceSmall);
+  const int n = compact_slice<kListIfLong>(p, gw, sl * kSliceLen, t, Leff, xv, lane, sh.sidx, sh.sval, 0, kSliceSmall);
   if (lane == 0) {
     p.sl_cnt[gw] = n;
     if (sl == 0 && p.t_out) p.t_out[r] = t;
+  }
+  if (n > 0 && n <= kSliceSmall) {  // the list is in LDS: one coalesced store per lane
+    wave_lds_sync();
+    if (lane < min(n, p.slice_cap)) {
+      p.sl_idx[gw * p.slice_cap + lane] = sh.sidx[lane];
+      p.sl_val[gw * p.slice_cap + lane] = sh.sval[lane];
+    }
   }
   // 3. a short list is gathered here, in one burst: (m, l, o) partial of the
   //    slice (its count tells the row kernel that the partial exists)
@@ -663,12 +678,20 @@ __global__ void __launch_bounds__(NT) atopn_rowlds_kernel(FusedSelParams p, PVPa
     const int sl = w + NW * u;
     if (sl < ns) {
       const int64_t gw = static_cast<int64_t>(r) * ns + sl;
-      const int c = compact_slice(p, gw, sl * kSliceLen, t, Leff, xv[u], lane, sh.sidx, sh.sval, sh.pre[sl], n);
+      const int c = compact_slice<kListNone>(p, gw, sl * kSliceLen, t, Leff, xv[u], lane, sh.sidx, sh.sval, sh.pre[sl], n);
       if (lane == 0) p.sl_cnt[gw] = c;
     }
   }
   if (w == 0 && lane == 0 && p.t_out) p.t_out[r] = t;
   lds_sync();
+  // the kept entries to their slices' workspace lists (inspection only;
+  // entries past the row's first n are not written), coalesced
+  for (int i = tid; i < n; i += NT) {
+    const int sl = slice_of(sh.pre, ns, i);
+    const int64_t dst = (static_cast<int64_t>(r) * ns + sl) * p.slice_cap + (i - sh.pre[sl]);
+    p.sl_idx[dst] = sh.sidx[i];
+    p.sl_val[dst] = sh.sval[i];
+  }
   // D. softmax . V over the list
   const int vh = h / (v.q_h / v.v_h);
   const char* vbase = v.v + (bi * v.v_sb + static_cast<int64_t>(vh) * v.v_sh) * Elt<DT>::kBytes;
