@@ -680,9 +680,9 @@ int make_gemv(const saga_tensor* x, const saga_tensor* w, const saga_tensor* bia
   const int64_t M = x->shape[0], K = x->shape[1];
   const int64_t N = packed ? w->shape[0] * 16 : w->shape[0];
   if (packed) {
-    // [N/16][K/32][16][32], contiguous
+    // [N/16][K/32][16][32], contiguous (the stride of a size-1 dim is immaterial)
     if (w->shape[2] != 16 || w->shape[3] != 32 || w->shape[1] * 32 != K || w->stride[3] != 1 || w->stride[2] != 32 ||
-        w->stride[1] != 512 || w->stride[0] != w->shape[1] * 512)
+        (w->shape[1] > 1 && w->stride[1] != 512) || (w->shape[0] > 1 && w->stride[0] != w->shape[1] * 512))
       return fail(SAGA_ERR_INVALID, "gemv: packed w must be contiguous [N/16, K/32, 16, 32] with K = x.shape[1]");
     if (reinterpret_cast<uintptr_t>(w->data) % 16) return fail(SAGA_ERR_INVALID, "gemv: packed w must be 16-byte aligned");
   } else if (w->shape[1] != K) {

@@ -138,7 +138,9 @@ def test_gemv_split_k_matches_single_pass_and_is_deterministic(epilogue, rms):
     assert torch.allclose(outs[0].float(), outs[1].float(), rtol=2 ** -7, atol=2e-3)
 
 
-@pytest.mark.parametrize("M,K,N", [(8, 1536, 1920), (8, 1536, 17920), (8, 8960, 1536), (3, 64, 32), (8, 1536, 151936)])
+# (5, 32, 64): one 32-column block, whose size-1 dim keeps torch's stride
+@pytest.mark.parametrize("M,K,N", [(8, 1536, 1920), (8, 1536, 17920), (8, 8960, 1536), (3, 64, 32), (8, 1536, 151936),
+                                   (5, 32, 64)])
 @pytest.mark.parametrize("epilogue", ["store", "add", "silu_pairs"])
 def test_packed_weights_give_identical_results(M, K, N, epilogue):
     """W in the packed MFMA-fragment layout [N/16, K/32, 16, 32] feeds the same
