@@ -1,4 +1,6 @@
-// K2 of the Atop-N fast step, in two kernels.
+// K2 of the Atop-N fast step: slice kernel + row kernel, or, for rows of
+// few slices, one block per row (atopn_rowlds_kernel / atopn_rowblock_kernel
+// below); the choice is by shape (k2_row_block) and the results are identical.
 //
 // Replaces the threshold transform (attention/attention.py:136-149), the
 // Triton stream compaction threshold_select_fast_kernel
@@ -610,9 +612,10 @@ __global__ void __launch_bounds__(NT) atopn_rowblock_kernel(FusedSelParams p, PV
 // NT / 64 * kRowBlockBurst slices, buf_k <= kRowBatch): the waves hold the
 // scores of their slices in registers, count them into LDS, one wave scans
 // the counts, the waves write every kept entry at its rank in the row's list
-// (the first buf_k in position order) in LDS -- and, for inspection, into
-// the workspace lists --, and the block gathers the V rows of the list:
-// no global round trip between the slice phase and the gather.
+// (the first buf_k in position order) in LDS, the block copies that list to
+// the workspace slice lists (for inspection; coalesced, nothing waits for
+// it) and gathers the V rows of the list: no global round trip between the
+// slice phase and the gather.
 template <int NT, int D>
 struct RowLdsShared {
   float accs[(NT / kWave) * D];
