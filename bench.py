@@ -362,6 +362,9 @@ def main():
                          "and the 128k dense-GQA vs SAGA comparison; one JSON line per shape")
     ap.add_argument("--no-fused", action="store_true",
                     help="run the Atop-N fast step as three kernels (scores, slice, row) for every shape")
+    ap.add_argument("--k2-mode", type=int, choices=(0, 1, 2), default=0,
+                    help="fast-step selection + softmax.V kernels: 0 by shape (default), 1 one block per row, "
+                         "2 slice kernel + row kernel (results are identical)")
     ap.add_argument("--exempt", default="",
                     help="comma-separated layers that run dense attention in the SAGA model (speedup.py:65-66), "
                          "e.g. 0,14 for Qwen2.5-1.5B")
@@ -390,6 +393,7 @@ def main():
 
     if args.no_fused:
         ops.set_fused_fast_step(False)
+    ops.set_k2_mode(args.k2_mode)
 
     B, ctx, K, W = args.batch, args.ctx, args.steps, args.warmup
     if args.profile_kernels:
