@@ -360,9 +360,7 @@ def main():
     ap.add_argument("--sweep", action="store_true",
                     help="attention kernels alone over a grid of shapes (lengths, batches, head groupings, N) "
                          "and the 128k dense-GQA vs SAGA comparison; one JSON line per shape")
-    ap.add_argument("--no-fused", action="store_true",
-                    help="run the Atop-N fast step as three kernels (scores, slice, row) for every shape")
-    ap.add_argument("--k2-mode", type=int, choices=(0, 1, 2), default=0,
+    ap.add_argument("--k2-variant", type=int, choices=(0, 1, 2), default=0,
                     help="fast-step selection + softmax.V kernels: 0 by shape (default), 1 one block per row, "
                          "2 slice kernel + row kernel (results are identical)")
     ap.add_argument("--exempt", default="",
@@ -391,10 +389,6 @@ def main():
         if getattr(args, k) is None:
             setattr(args, k, mdl[k])
 
-    if args.no_fused:
-        ops.set_fused_fast_step(False)
-    ops.set_k2_mode(args.k2_mode)
-
     B, ctx, K, W = args.batch, args.ctx, args.steps, args.warmup
     if args.profile_kernels:
         return profile_kernels(B, ctx, SAGA_SHAPE)
@@ -409,7 +403,8 @@ def main():
     exempt = tuple(int(x) for x in args.exempt.split(",") if x.strip())
 
     def build(shape, mode):
-        m = SagaDecoder(shape, B, max_len, mode=mode, top_n=args.top_n, exempt_layers=exempt if mode == "atopn" else ())
+        m = SagaDecoder(shape, B, max_len, mode=mode, top_n=args.top_n, exempt_layers=exempt if mode == "atopn" else (),
+                        k2_variant=args.k2_variant)
         t0 = time.perf_counter()
         if args.synthetic_kv:
             m.fill_synthetic(ctx)
@@ -436,7 +431,7 @@ def main():
     k1_gbs = k1_bytes / (k1_us * 1e-6) / 1e9
     attn_us = timed_graph(lambda i: ops.atopn_decode(q4, saga.k_cache[i % s.layers], saga.v_cache[i % s.layers],
                                                      saga.table[i % s.layers], args.top_n, kv_len=kvl,
-                                                     out=saga._attn), nlaunch)
+                                                     out=saga._attn, k2_variant=args.k2_variant), nlaunch)
     log(f"K1 qk_scores: {k1_us:.2f} us/launch, {k1_gbs:.0f} GB/s; Atop-N fast attention {attn_us:.2f} us/layer")
     saga_cache = saga.k_cache.shape, saga.v_cache.shape
     del saga

@@ -33,11 +33,9 @@
  *     the last error on the calling thread is in saga_last_error().  Nothing
  *     aborts and no C++ exception crosses this boundary.
  *   - Workspaces are caller-allocated device buffers of the size the
- *     matching *_workspace_bytes() returns.  No initial contents are needed,
- *     except that an Atop-N workspace must be zero-filled once when it is
- *     allocated (its first saga_atopn_layout.sync_bytes bytes hold the fused
- *     fast step's barrier state, which every call leaves consistent).
- *     Calls that share a workspace must be ordered (same stream).
+ *     matching *_workspace_bytes() returns; no initial contents are needed.
+ *     Calls that share a workspace must be ordered (same stream): calls on
+ *     different streams need workspaces of their own.
  */
 #ifndef SAGA_AMD_H
 #define SAGA_AMD_H
@@ -75,11 +73,7 @@ typedef void* saga_stream_t;
 
 /* Byte offsets of the fused decode workspace (for tests and inspection). */
 typedef struct saga_atopn_layout {
-  int64_t sync;       /* barrier state of the fused fast step, always at offset 0: must be
-                         zero before the first saga_atopn_decode on a workspace; every
-                         call leaves it consistent for the next (any shape) */
-  int64_t sync_bytes;
-  int64_t scores;    /* f32 [b*q_h, scores_ld] (not written by the fused fast step) */
+  int64_t scores;    /* f32 [b*q_h, scores_ld] */
   int64_t scores_ld; /* elements */
   int64_t part_max;  /* f32 [b*q_h, nparts] */
   int64_t part_sum;  /* f32 [b*q_h, nparts] */
@@ -91,11 +85,8 @@ typedef struct saga_atopn_layout {
   int64_t sel_val;   /* f32 [b*q_h, buf_k] their logits */
   int64_t sel_cnt;   /* i32 [b*q_h] kept (<= buf_k) */
   int64_t sel_total; /* i32 [b*q_h] passing before the cap */
-  /* fast step: each row's passing positions in nslice ordered lists ("slices"):
-     fused = 1: one per block of the fused kernel (nslice = nparts), capacity
-     min(block positions, buf_k); fused = 0: one per 1024 positions,
-     capacity min(1024, buf_k) */
-  int64_t fused;     /* the fast step of this shape runs fused on the current device */
+  /* fast step: each row's passing positions in nslice ordered lists
+     ("slices"), one per 1024 positions, capacity slice_cap = min(1024, buf_k) */
   int64_t nslice;
   int64_t slice_cap;
   int64_t slice_idx; /* i32 [b*q_h, nslice, slice_cap] passing positions per slice */
@@ -168,27 +159,6 @@ size_t saga_atopn_workspace_bytes(int64_t b, int64_t q_h, int64_t k_h, int64_t L
 int saga_atopn_workspace_layout(int64_t b, int64_t q_h, int64_t k_h, int64_t L, int64_t d, int64_t buf_k,
                                 saga_atopn_layout* layout);
 
-/* Process-wide switch of the fused fast step (default 0).  With 1,
- * saga_atopn_decode runs scores, threshold, compaction and the short lists'
- * softmax . V in one kernel (a flag barrier per (batch, key head) across its
- * co-resident blocks), then the row kernel, for shapes whose grid fits the
- * GPU at once; with 0 (and for other shapes) it runs the three-kernel path
- * (scores, slice kernel, row kernel).  Results agree to fp32 rounding.  No
- * counterpart in the reference: an A/B alternative, measured slower on
- * MI355X.  Returns the previous setting. */
-int saga_set_fused_fast_step(int enable);
-
-/* How the fast step's selection and softmax.V run (no counterpart in the
- * reference; results are identical in every mode): 0 (default) by shape,
- * 1 one block per (batch, head) row -- its waves run the row's 1024-position
- * slices and the row's list is kept in LDS (or, for rows of more than 64
- * slices or buf_k > 2048, written to the workspace and merged after a block
- * barrier): one launch; the default for rows of at most 12 slices with
- * buf_k <= 2048 --, 2 a slice kernel
- * over every (row, slice) and a row kernel.  Returns the previous mode (process-wide),
- * or SAGA_ERR_INVALID for another value. */
-int saga_set_k2_mode(int mode);
-
 /* Atop-N fast decode step: scores, logit threshold from the stored
  * softmax-space thresholds, ordered compaction capped at
  * buf_k = min(2*top_n, L), sparse softmax . V.
@@ -200,6 +170,27 @@ int saga_atopn_decode(const saga_tensor* query, const saga_tensor* key, const sa
                       const saga_tensor* mask, const int32_t* kv_len, float scale, int64_t top_n,
                       const float* softmax_threshold, saga_tensor* out, void* workspace,
                       size_t workspace_bytes, saga_stream_t stream);
+
+/* saga_atopn_decode with the kernels of its selection and softmax . V chosen
+ * per call (no counterpart in the reference; results are identical in every
+ * variant, so this only serves A/B measurement and tests):
+ *   SAGA_K2_AUTO       by shape, as saga_atopn_decode;
+ *   SAGA_K2_ROW_BLOCK  one block per (batch, head) row: its waves run the
+ *                      row's 1024-position slices, the row's list is kept in
+ *                      LDS (or, for rows of more than 64 slices or
+ *                      buf_k > 2048, written to the workspace and merged
+ *                      after a block barrier); the choice of SAGA_K2_AUTO for
+ *                      rows of at most 12 slices with buf_k <= 2048;
+ *   SAGA_K2_SLICE_ROW  a slice kernel over every (row, slice), then a row
+ *                      kernel.
+ * Another value returns SAGA_ERR_INVALID. */
+#define SAGA_K2_AUTO 0
+#define SAGA_K2_ROW_BLOCK 1
+#define SAGA_K2_SLICE_ROW 2
+int saga_atopn_decode_ex(const saga_tensor* query, const saga_tensor* key, const saga_tensor* value,
+                         const saga_tensor* mask, const int32_t* kv_len, float scale, int64_t top_n,
+                         const float* softmax_threshold, saga_tensor* out, int32_t k2_variant,
+                         void* workspace, size_t workspace_bytes, saga_stream_t stream);
 
 /* Atop-N calibration step: full softmax statistics, exact top-k
  * (k = min(top_n, L), radix select; equal values: lower index first),

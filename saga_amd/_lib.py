@@ -41,8 +41,8 @@ class SagaTensor(ctypes.Structure):
 
 class AtopnLayout(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int64) for n in (
-        "sync", "sync_bytes", "scores", "scores_ld", "part_max", "part_sum", "part_tail", "nparts", "thresh",
-        "sel_idx", "sel_val", "sel_cnt", "sel_total", "fused", "nslice", "slice_cap", "slice_idx", "slice_val",
+        "scores", "scores_ld", "part_max", "part_sum", "part_tail", "nparts", "thresh",
+        "sel_idx", "sel_val", "sel_cnt", "sel_total", "nslice", "slice_cap", "slice_idx", "slice_val",
         "slice_cnt", "slice_pre", "slice_o", "slice_ml", "total_bytes")]
 
 
@@ -58,11 +58,12 @@ _SIGS = {
     "saga_threshold_select": (ctypes.c_int, [_T, _P, _I64, _I64, _T, _P, _P, _P]),
     "saga_sparse_softmax_pv": (ctypes.c_int, [_T, _T, _T, ctypes.c_int32, _T, _P]),
     "saga_qk_nparts": (ctypes.c_int64, [_I64, _I64, _I64]),
-    "saga_set_fused_fast_step": (ctypes.c_int, [ctypes.c_int]),
     "saga_atopn_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "saga_atopn_workspace_layout": (ctypes.c_int, [_I64, _I64, _I64, _I64, _I64, _I64,
                                                    ctypes.POINTER(AtopnLayout)]),
     "saga_atopn_decode": (ctypes.c_int, [_T, _T, _T, _T, _P, ctypes.c_float, _I64, _P, _T, _P, ctypes.c_size_t, _P]),
+    "saga_atopn_decode_ex": (ctypes.c_int, [_T, _T, _T, _T, _P, ctypes.c_float, _I64, _P, _T, ctypes.c_int32, _P,
+                                            ctypes.c_size_t, _P]),
     "saga_atopn_calibrate": (ctypes.c_int, [_T, _T, _T, _T, _P, ctypes.c_float, _I64, _P, _T, _P, ctypes.c_size_t, _P]),
     "saga_dense_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I64]),
     "saga_dense_decode": (ctypes.c_int, [_T, _T, _T, _T, _P, ctypes.c_float, _T, _P, ctypes.c_size_t, _P]),
@@ -75,10 +76,10 @@ _SIGS = {
                                          _T, _T, _T, _P]),
     "saga_argmax_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
     "saga_argmax": (ctypes.c_int, [_T, _P, _P, ctypes.c_size_t, _P]),
-    "saga_set_k2_mode": (ctypes.c_int, [ctypes.c_int]),
     "saga_prefill_attention": (ctypes.c_int, [_T, _T, _T, _T, ctypes.c_float, ctypes.c_int32, ctypes.c_int64, _T, _P]),
 }
 GEMV_STORE, GEMV_ADD, GEMV_SILU_PAIRS = 0, 1, 2
+K2_AUTO, K2_ROW_BLOCK, K2_SLICE_ROW = 0, 1, 2
 
 _lock = threading.Lock()
 _lib = None

@@ -1,7 +1,9 @@
 """Build libsaga_amd.so (HIP kernels + C ABI) for gfx950 with hipcc.
 
 Usage: python -m saga_amd.build   (or __graft_entry__.build())
-The library is written next to this file; it is loaded by saga_amd._lib.
+Every csrc/*.hip is compiled to its own object in saga_amd/_build/ (in
+parallel), then the objects are linked into libsaga_amd.so next to this
+file; saga_amd._lib loads it.  Each call recompiles every source.
 """
 from __future__ import annotations
 
@@ -10,9 +12,11 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
+OBJ_DIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libsaga_amd.so")
 
 HIPCC_FLAGS = [
@@ -20,7 +24,6 @@ HIPCC_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     # selection is defined on the rounded fp32 products of separate
     # multiply and add steps, as in the reference's scale-then-mask
     "-ffp-contract=off",
@@ -28,6 +31,9 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",
 ]
+
+# hipcc's host pass does not know the packed-fp32 target feature: harmless
+_NOISE = "is not a recognized feature for this target"
 
 
 def hipcc() -> str:
@@ -37,19 +43,41 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm toolchain required to build libsaga_amd.so)")
 
 
-def build(verbose: bool = False) -> str:
-    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", os.path.join(HERE, "..", "include"), *srcs, "-o", tmp]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "is not a recognized feature for this target"
-    err = "\n".join(l for l in (res.stdout + res.stderr).splitlines() if noise not in l)
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
-    if verbose and err.strip():
-        print(err)
+    err = "\n".join(l for l in (res.stdout + res.stderr).splitlines() if _NOISE not in l)
+    return res.returncode, err
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> str:
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    cc = hipcc()
+    inc = ["-I", os.path.join(HERE, "..", "include")]
+
+    def compile_one(src):
+        obj = os.path.join(OBJ_DIR, os.path.splitext(os.path.basename(src))[0] + ".o")
+        rc, err = _run([cc, *HIPCC_FLAGS, *inc, "-c", src, "-o", obj], verbose)
+        return src, obj, rc, err
+
+    jobs = jobs or min(len(srcs), max(1, min(16, os.cpu_count() or 1)))
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        results = list(pool.map(compile_one, srcs))
+    failed = [(s, rc, err) for s, _, rc, err in results if rc != 0]
+    if failed:
+        msg = "\n".join(f"{os.path.basename(s)} ({rc}):\n{err}" for s, rc, err in failed)
+        raise RuntimeError(f"hipcc failed:\n{msg}")
+    if verbose:
+        for _, _, _, err in results:
+            if err.strip():
+                print(err)
+    tmp = LIB + ".tmp"
+    rc, err = _run([cc, "--offload-arch=gfx950", "-shared", "-fPIC", *[o for _, o, _, _ in results], "-o", tmp],
+                   verbose)
+    if rc != 0:
+        raise RuntimeError(f"link failed ({rc}):\n{err}")
     os.replace(tmp, LIB)
     return LIB
 

@@ -31,8 +31,6 @@
 // one gather burst deep, skewed or overflowing rows cost at most buf_k
 // block-parallel gathers.  The kernel boundary orders the slice writes before
 // the row reads (no device-scope fences or counters).
-#include <atomic>
-
 #include "block_pv.cuh"
 #include "kernels.h"
 
@@ -724,21 +722,15 @@ static hipError_t launch_rows_typed(const FusedSelParams& p, const PVParams& v, 
   return hipGetLastError();
 }
 
-// 0: by shape, 1: one block per row, 2: slice kernel + row kernel
-static std::atomic<int> g_k2_mode{0};
-
-int set_k2_mode(int mode) { return g_k2_mode.exchange(mode); }
-
-bool k2_row_block(int64_t nslice, int64_t cap) {
-  const int mode = g_k2_mode.load();
-  if (mode == 1) return true;
-  if (mode == 2) return false;
+bool k2_row_block(int64_t nslice, int64_t cap, int variant) {
+  if (variant == kK2RowBlock) return true;
+  if (variant == kK2SliceRow) return false;
   return nslice <= kRowBlockAutoSlices && cap <= kRowBatch;
 }
 
 template <int DT, int D>
 static hipError_t launch_split(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
-  if (k2_row_block(p.nslice, p.cap)) {
+  if (k2_row_block(p.nslice, p.cap, p.k2_variant)) {
     if (p.cap <= kRowBatch && p.nslice <= 4)
       hipLaunchKernelGGL((atopn_rowlds_kernel<DT, D, 256>), dim3(p.nrows), dim3(256), 0, st, p, v);
     else if (p.cap <= kRowBatch && p.nslice <= 16 * kRowBlockBurst)

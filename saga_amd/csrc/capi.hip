@@ -211,10 +211,6 @@ void atopn_layout(int64_t b, int64_t q_h, int64_t k_h, int64_t L, int64_t d, int
     off = align256(off + bytes);
     return at;
   };
-  // the fused fast step's barrier state: first, at a fixed offset, so that
-  // calls of every shape sharing the workspace find it in place
-  o->sync = take(kFusedSyncBytes);
-  o->sync_bytes = kFusedSyncBytes;
   o->scores_ld = ld;
   o->nparts = nparts;
   o->scores = take(nr * ld * 4);
@@ -226,17 +222,11 @@ void atopn_layout(int64_t b, int64_t q_h, int64_t k_h, int64_t L, int64_t d, int
   o->sel_val = take(nr * buf_k * 4);
   o->sel_cnt = take(nr * 4);
   o->sel_total = take(nr * 4);
-  // fast-step lists: per 1024-position slice (split path) or per fused block;
-  // the regions hold either
-  const int64_t ns_split = (L + kSliceLen - 1) / kSliceLen;
-  const int64_t cap_split = std::min<int64_t>(kSliceLen, buf_k);
-  const int64_t ns_fused = nparts;
-  const int64_t cap_fused = atopn_fused_slice_cap(b, k_h, L, buf_k);
-  const int64_t ns_max = std::max(ns_split, ns_fused);
-  const int64_t ent_max = std::max(ns_split * cap_split, ns_fused * cap_fused);
-  o->fused = k_h > 0 && q_h % k_h == 0 && atopn_fused_fits(b, k_h, q_h / k_h, L) ? 1 : 0;
-  o->nslice = o->fused ? ns_fused : ns_split;
-  o->slice_cap = o->fused ? cap_fused : cap_split;
+  // fast-step lists: one per 1024-position slice of a row
+  const int64_t ns_max = (L + kSliceLen - 1) / kSliceLen;
+  const int64_t ent_max = ns_max * std::min<int64_t>(kSliceLen, buf_k);
+  o->nslice = ns_max;
+  o->slice_cap = std::min<int64_t>(kSliceLen, buf_k);
   o->slice_idx = take(nr * ent_max * 4);
   o->slice_val = take(nr * ent_max * 4);
   o->slice_cnt = take(nr * ns_max * 4);
@@ -268,13 +258,15 @@ PVParams make_pv(const saga_tensor* v, const saga_tensor* out, const Shape& s) {
 // Shared body of the two fused Atop-N entry points.
 int atopn_run(bool calibrate, const saga_tensor* query, const saga_tensor* key, const saga_tensor* value,
               const saga_tensor* mask, const int32_t* kv_len, float scale, int64_t top_n,
-              const float* pstar_in, float* pstar_out, saga_tensor* out, void* workspace,
+              const float* pstar_in, float* pstar_out, saga_tensor* out, int32_t k2_variant, void* workspace,
               size_t workspace_bytes, saga_stream_t stream) {
   Shape s{};
   int rc;
   if ((rc = check_qk(query, key, mask, &s)) || (rc = check_v(value, &s)) || (rc = check_out(out, s))) return rc;
   if (top_n < 1) return fail(SAGA_ERR_INVALID, "top_n must be >= 1, got %lld", (long long)top_n);
   if (calibrate ? !pstar_out : !pstar_in) return fail(SAGA_ERR_INVALID, "threshold table row is null");
+  if (k2_variant != kK2Auto && k2_variant != kK2RowBlock && k2_variant != kK2SliceRow)
+    return fail(SAGA_ERR_INVALID, "k2_variant must be 0, 1 or 2, got %d", k2_variant);
   const int64_t buf_k = calibrate ? (top_n < s.L ? top_n : s.L) : (top_n < (s.L + 1) / 2 ? 2 * top_n : s.L);
   if (!atopn_sizes_ok(s.b, s.q_h, s.k_h, s.L, s.d, buf_k)) return fail(SAGA_ERR_UNSUPPORTED, "workspace too large");
   saga_atopn_layout lay;
@@ -285,19 +277,17 @@ int atopn_run(bool calibrate, const saga_tensor* query, const saga_tensor* key, 
   char* ws = static_cast<char*>(workspace);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t nr = s.b * s.q_h;
+  if (nr * lay.nslice >= (1LL << 31)) return fail(SAGA_ERR_UNSUPPORTED, "too many score rows x slices");
 
-  const bool fused = !calibrate && lay.fused;
   QKParams qp = make_qk(query, key, mask, kv_len, scale, s);
   qp.pmax = reinterpret_cast<float*>(ws + lay.part_max);
   qp.psum = reinterpret_cast<float*>(ws + lay.part_sum);
   qp.ptail = reinterpret_cast<float*>(ws + lay.part_tail);
-  if (!fused) {
-    qp.scores = reinterpret_cast<float*>(ws + lay.scores);
-    qp.s_sb = s.q_h * lay.scores_ld;
-    qp.s_sh = lay.scores_ld;
-    qp.vec_store = 1;
-    if ((rc = hip_status(launch_qk_scores(s.dt, static_cast<int>(s.d), qp, st), "qk_scores launch"))) return rc;
-  }
+  qp.scores = reinterpret_cast<float*>(ws + lay.scores);
+  qp.s_sb = s.q_h * lay.scores_ld;
+  qp.s_sh = lay.scores_ld;
+  qp.vec_store = 1;
+  if ((rc = hip_status(launch_qk_scores(s.dt, static_cast<int>(s.d), qp, st), "qk_scores launch"))) return rc;
 
   FusedSelParams sp{};
   sp.scores = qp.scores;
@@ -326,23 +316,9 @@ int atopn_run(bool calibrate, const saga_tensor* query, const saga_tensor* key, 
   sp.sl_pre = reinterpret_cast<int32_t*>(ws + lay.slice_pre);
   sp.sl_o = reinterpret_cast<float*>(ws + lay.slice_o);
   sp.sl_ml = reinterpret_cast<float*>(ws + lay.slice_ml);
-  if (nr * lay.nslice >= (1LL << 31)) return fail(SAGA_ERR_UNSUPPORTED, "too many score rows x slices");
+  sp.k2_variant = k2_variant;
   // calibration: softmax over the top-k logits == renormalised top-k probabilities
   const PVParams pp = make_pv(value, out, s);
-  if (fused) {
-    FusedSync sy{};
-    int32_t* sync = reinterpret_cast<int32_t*>(ws + lay.sync);
-    sy.epoch = sync;
-    sy.flags = sync + kFusedMaxUnits;
-    // the last 256 bytes of the region hold the error word
-    static_assert(static_cast<int64_t>(kFusedMaxUnits) * (kFusedMaxBlocks + 1) * 4 == kFusedSyncBytes - 256,
-                  "sync region: epochs, flags, then one 256-byte line for the error word");
-    sy.error = sync + static_cast<int64_t>(kFusedMaxUnits) * (kFusedMaxBlocks + 1);
-    sy.xcd_map = (s.b * s.k_h) % 8 == 0 ? 1 : 0;
-    if ((rc = hip_status(launch_atopn_fused(s.dt, static_cast<int>(s.d), qp, sp, pp, sy, st), "atopn fused launch")))
-      return rc;
-    return ok();
-  }
   if ((rc = hip_status(launch_atopn_select_pv(calibrate, sp, pp, st), "atopn select/pv launch"))) return rc;
   return ok();
 }
@@ -512,13 +488,6 @@ int saga_sparse_softmax_pv(const saga_tensor* weights, const saga_tensor* indice
   return ok();
 }
 
-int saga_set_fused_fast_step(int enable) { return set_fused_enabled(enable); }
-
-int saga_set_k2_mode(int mode) {
-  if (mode < 0 || mode > 2) return fail(SAGA_ERR_INVALID, "k2 mode must be 0, 1 or 2");
-  return set_k2_mode(mode);
-}
-
 int64_t saga_qk_nparts(int64_t b, int64_t k_h, int64_t L) {
   if (b < 1 || k_h < 1 || L < 1 || L >= kMaxLen || b > ((1LL << 31) - 1) / k_h) return 0;
   return qk_plan(b, k_h, L) / 4;
@@ -544,7 +513,15 @@ int saga_atopn_decode(const saga_tensor* query, const saga_tensor* key, const sa
                       const saga_tensor* mask, const int32_t* kv_len, float scale, int64_t top_n,
                       const float* softmax_threshold, saga_tensor* out, void* workspace, size_t workspace_bytes,
                       saga_stream_t stream) {
-  return atopn_run(false, query, key, value, mask, kv_len, scale, top_n, softmax_threshold, nullptr, out,
+  return atopn_run(false, query, key, value, mask, kv_len, scale, top_n, softmax_threshold, nullptr, out, kK2Auto,
+                   workspace, workspace_bytes, stream);
+}
+
+int saga_atopn_decode_ex(const saga_tensor* query, const saga_tensor* key, const saga_tensor* value,
+                         const saga_tensor* mask, const int32_t* kv_len, float scale, int64_t top_n,
+                         const float* softmax_threshold, saga_tensor* out, int32_t k2_variant, void* workspace,
+                         size_t workspace_bytes, saga_stream_t stream) {
+  return atopn_run(false, query, key, value, mask, kv_len, scale, top_n, softmax_threshold, nullptr, out, k2_variant,
                    workspace, workspace_bytes, stream);
 }
 
@@ -553,7 +530,7 @@ int saga_atopn_calibrate(const saga_tensor* query, const saga_tensor* key, const
                          float* softmax_threshold_out, saga_tensor* out, void* workspace, size_t workspace_bytes,
                          saga_stream_t stream) {
   return atopn_run(true, query, key, value, mask, kv_len, scale, top_n, nullptr, softmax_threshold_out, out,
-                   workspace, workspace_bytes, stream);
+                   kK2Auto, workspace, workspace_bytes, stream);
 }
 
 size_t saga_dense_workspace_bytes(int64_t b, int64_t q_h, int64_t L, int64_t d) {

@@ -7,6 +7,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/saga_amd.h"
+
 namespace saga {
 
 // K1: scores = (Q_group . K^T) * scale (+ mask), per-chunk (max, sumexp).
@@ -97,6 +99,7 @@ struct FusedSelParams {
   float* sl_o;      // [row][slice][d] unnormalised sum_e w_e V[e] of short slices
   float* sl_ml;     // [row][slice][2] (max logit, sum of weights) of short slices
   int32_t* sl_pre;  // [row][2][nslice + 1] slice ranks (rows of > 2048 slices)
+  int32_t k2_variant;  // fast step: kK2Auto / kK2RowBlock / kK2SliceRow
 };
 // calibrate: one block per row; fast step: slice kernel + per-row gather kernel
 hipError_t launch_atopn_select_pv(bool calibrate, const FusedSelParams& p, const PVParams& v, hipStream_t st);
@@ -105,32 +108,11 @@ constexpr int kSliceSmall = 64;  // slice lists this short are gathered by their
 hipError_t launch_atopn_fast(const FusedSelParams& p, const PVParams& v, hipStream_t st);
 // The per-row kernel of the fast step alone (ranks, cut at buf_k, merge, long gathers).
 hipError_t launch_atopn_rows(const FusedSelParams& p, const PVParams& v, hipStream_t st);
-// Fast-step K2 shape: 0 by shape (one block per row for rows of few slices),
-// 1 always one block per row, 2 always slice kernel + row kernel.  Returns
-// the previous mode; process-wide.
-int set_k2_mode(int mode);
-bool k2_row_block(int64_t nslice, int64_t cap);
-
-// Fused fast step: sync region of the workspace (zero before the first call on
-// it; every call leaves it consistent).  Unit u = batch * k_h + key head.
-struct FusedSync {
-  int32_t* epoch;   // [kFusedMaxUnits] calls completed per unit
-  int32_t* flags;   // [kFusedMaxUnits][kFusedMaxBlocks] arrival flags
-  int32_t* error;   // set when a barrier wait gave up (the call's output is invalid)
-  int32_t xcd_map;  // units % 8 == 0: unit u runs on block ids == u (mod 8)
-};
-constexpr int kFusedMaxUnits = 1024;
-constexpr int kFusedMaxBlocks = 128;    // 4-wave blocks per unit
-constexpr int kFusedBlocksPerCU = 3;    // resident blocks per CU the fused plan counts on
-constexpr int64_t kFusedSyncBytes = (static_cast<int64_t>(kFusedMaxUnits) * (kFusedMaxBlocks + 1) + 64) * 4;
-int fused_device_cus();  // CUs of the current device (cached)
-int set_fused_enabled(int enable);  // process-wide, off by default; returns the previous setting
-// Whether the fused fast step runs for this shape on the current device:
-// g = q_h / k_h <= 16 and the planned grid resident at once.
-bool atopn_fused_fits(int64_t b, int64_t k_h, int64_t g, int64_t L);
-int64_t atopn_fused_slice_cap(int64_t b, int64_t k_h, int64_t L, int64_t buf_k);  // list capacity per block
-hipError_t launch_atopn_fused(int dtype, int d, const QKParams& q, const FusedSelParams& p, const PVParams& v,
-                              const FusedSync& sy, hipStream_t st);
+// Fast-step K2 shape (FusedSelParams::k2_variant): 0 by shape (one block per
+// row for rows of few slices), 1 always one block per row, 2 always slice
+// kernel + row kernel.  Results are identical in every variant.
+constexpr int kK2Auto = SAGA_K2_AUTO, kK2RowBlock = SAGA_K2_ROW_BLOCK, kK2SliceRow = SAGA_K2_SLICE_ROW;
+bool k2_row_block(int64_t nslice, int64_t cap, int variant);
 
 // API selection (threshold_topk_fast): typed rows, typed values out.
 struct ApiSelParams {

@@ -1,5 +1,4 @@
-// One wave's share of the decode QK scores, shared by K1 (qk_scores_kernel)
-// and the fused Atop-N fast step (atopn_fused_kernel).
+// One wave's share of the decode QK scores (K1, qk_scores_kernel).
 //
 // A wave owns tiles [t0, t0 + nt) of 16 positions of one (batch, key head),
 // nt <= kQKMaxTiles.  It issues every 16-byte load of its K rows at once,

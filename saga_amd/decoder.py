@@ -72,11 +72,16 @@ class SagaDecoder:
     mode: "atopn" (calibration + fast Atop-N steps) or "dense" (every layer
     dense; with n_k == n_v this is plain GQA).  exempt_layers run dense in
     "atopn" mode (attention/attention.py:94, speedup.py:65-66).
+    With packed decode weights (pack_weights) the row-major projection
+    weights are released after packing unless keep_source_weights: the
+    prefill then unpacks one layer's weights at a time.  k2_variant picks the
+    fast step's selection + softmax.V kernels (ops.atopn_decode).
     """
 
     def __init__(self, shape: DecoderShape, batch: int, max_len: int, mode: str = "atopn", top_n: int = 512,
                  exempt_layers=(), device="cuda", dtype=torch.bfloat16, seed: int = 0, fuse_rope: bool = True,
-                 pack_weights: bool = True, weights: Optional[dict] = None):
+                 pack_weights: bool = True, weights: Optional[dict] = None, keep_source_weights: bool = False,
+                 k2_variant: int = 0):
         if mode not in ("atopn", "dense"):
             raise ValueError(f"mode must be 'atopn' or 'dense', got {mode!r}")
         self.shape, self.batch, self.max_len, self.mode, self.top_n = shape, batch, max_len, mode, top_n
@@ -125,7 +130,10 @@ class SagaDecoder:
         # q/k/v projection, RoPE and cache append in one launch (pair-ordered rows)
         self.fuse_rope = fuse_rope and self.use_gemv and d % 16 == 0
         self.pack_weights = pack_weights
+        self.keep_source_weights = keep_source_weights
+        self.k2_variant = k2_variant
         self.prepare_kernel_weights()
+        self._alloc_workspaces()
         self.graph_cal: Optional[torch.cuda.CUDAGraph] = None
         self.graph_fast: Optional[torch.cuda.CUDAGraph] = None
         self.prompt_len = 0
@@ -185,9 +193,13 @@ class SagaDecoder:
         and up rows interleaved (gate_0, up_0, gate_1, ...) so one output tile
         holds both halves of silu(gate) * up, and a normed LM head; with
         pack_weights every decode weight in the packed MFMA-fragment layout
-        (ops.pack_gemv_weight; the prefill keeps the row-major originals)."""
+        (ops.pack_gemv_weight), after which the row-major projection weights
+        are released (keep_source_weights keeps them)."""
         if not self.use_gemv:
             return
+        if self.w_qkv is None:
+            raise RuntimeError("prepare_kernel_weights: the row-major weights were released after packing "
+                               "(construct with keep_source_weights=True to fold new norm weights)")
         s = self.shape
         with torch.no_grad():
             self.kw_qkv = [(self.w_qkv[l].float() * self.ln1[l].float()).to(self.dtype) for l in range(s.layers)]
@@ -196,6 +208,7 @@ class SagaDecoder:
                 order = ops.rope_pair_order(s.n_q, s.n_k, s.n_v, s.head_dim, device=self.device)
                 self.kw_qkv = [w.index_select(0, order).contiguous() for w in self.kw_qkv]
                 self.kb_qkv = [b.index_select(0, order).contiguous() for b in self.b_qkv]
+                self._unpair = torch.argsort(order)
             self.kw_gu = []
             for l in range(s.layers):
                 w = (self.w_gu[l].float() * self.ln2[l].float()).to(self.dtype)
@@ -212,6 +225,51 @@ class SagaDecoder:
                 self.kw_o = [pk(w) for w in self.w_o]
                 self.kw_d = [pk(w) for w in self.w_d]
                 self.kw_lm = pk(self.kw_lm)
+                if not self.keep_source_weights:
+                    self.w_qkv = self.w_o = self.w_gu = self.w_d = None
+                    if self.lm_head is not self.embed:
+                        self.lm_head = None
+                    self._ones = torch.ones(s.hidden, device=self.device, dtype=self.dtype)
+
+    def _alloc_workspaces(self) -> None:
+        """The decoder's own workspaces (never the shared cache: the captured
+        graphs hold their addresses for the decoder's lifetime)."""
+        s, B, L, d = self.shape, self.batch, self.max_len, self.shape.head_dim
+        lib = ops._lib.load() if self.device.type == "cuda" else None
+        self.ws = {}
+        if lib is None:
+            return
+
+        def buf(n):
+            return torch.empty(max(int(n), 256), dtype=torch.uint8, device=self.device)
+
+        self.ws["atopn"] = buf(max(ops.atopn_workspace_bytes(B, s.n_q, s.n_k, L, d, self.top_n, cal)
+                                   for cal in (True, False)))
+        self.ws["dense"] = buf(lib.saga_dense_workspace_bytes(B, s.n_q, L, d))
+        if self.use_gemv:
+            shapes = ((s.qkv_width, s.hidden), (s.hidden, s.n_q * d), (2 * s.intermediate, s.hidden),
+                      (s.hidden, s.intermediate), (s.vocab, s.hidden))
+            self.ws["gemv"] = buf(max(lib.saga_gemv_workspace_bytes(B, n, k) for n, k in shapes))
+            self.ws["argmax"] = buf(lib.saga_argmax_workspace_bytes(B, s.vocab))
+
+    @staticmethod
+    def _unpack(w: torch.Tensor) -> torch.Tensor:
+        """Row-major [N, K] of a packed [N/16, K/32, 16, 32] weight."""
+        if w.dim() == 2:
+            return w
+        n16, k32 = w.shape[0], w.shape[1]
+        return w.permute(0, 2, 1, 3).reshape(n16 * 16, k32 * 32)
+
+    def _prefill_layer(self, l: int):
+        """(norm-1 weight, w_qkv, b_qkv, qkv column order, w_o, norm-2 weight,
+        w_gu, gate/up interleaved) for the prefill of layer l: the row-major
+        originals, or, once released, the unpacked decode copies (norms
+        folded in, q/k rows in rotary-pair order, gate/up interleaved)."""
+        if self.w_qkv is not None:
+            return self.ln1[l], self.w_qkv[l], self.b_qkv[l], None, self.w_o[l], self.ln2[l], self.w_gu[l], False
+        unpair = self._unpair if self.fuse_rope else None
+        return (self._ones, self._unpack(self.kw_qkv[l]), self.kb_qkv[l], unpair, self._unpack(self.kw_o[l]),
+                self._ones, self._unpack(self.kw_gu[l]), True)
 
     # ------------------------------------------------------------------ prefill
     @torch.no_grad()
@@ -228,21 +286,32 @@ class SagaDecoder:
         zeros = torch.zeros(T, device=self.device, dtype=torch.int32)
         mod = _HeadGroups()
         for l in range(s.layers):
-            h = ops.rmsnorm(x, self.ln1[l], s.eps)
-            qkv = torch.addmm(self.b_qkv[l], h, self.w_qkv[l].t())
+            n1, w_qkv, b_qkv, unpair, w_o, n2, w_gu, interleaved = self._prefill_layer(l)
+            h = ops.rmsnorm(x, n1, s.eps)
+            qkv = torch.addmm(b_qkv, h, w_qkv.t())
+            if unpair is not None:
+                qkv = qkv.index_select(1, unpair)
             q = ops.rope_kv_append(qkv, s.n_q, s.n_k, s.n_v, s.rope_theta, pos, self.k_cache[l], self.v_cache[l],
                                    batch=zeros)
             k = self.k_cache[l, 0:1, :, :T]
             v = self.v_cache[l, 0:1, :, :T]
-            # prefill attention stays on torch SDPA (attention/attention.py:13-53)
+            # the HIP prefill kernel when ops.prefill_supported holds for these
+            # operands, else torch SDPA (attention/attention.py:13-53)
             o, _ = sdpa_attention_forward(mod, q.transpose(0, 1).unsqueeze(0), k, v, None, is_causal=True)
-            x = torch.addmm(x, o.reshape(T, s.n_q * d), self.w_o[l].t())
+            x = torch.addmm(x, o.reshape(T, s.n_q * d), w_o.t())
+            w_d = self.w_d[l] if self.w_d is not None else self._unpack(self.kw_d[l])
             for c0 in range(0, T, chunk):
                 xc = x[c0:c0 + chunk]
-                gu = torch.mm(ops.rmsnorm(xc, self.ln2[l], s.eps), self.w_gu[l].t())
-                xc.addmm_(ops.silu_mul(gu), self.w_d[l].t())
-        last = ops.rmsnorm(x[-1:], self.ln_f, s.eps)
-        first = torch.mm(last, self.lm_head.t()).argmax(dim=-1)
+                gu = torch.mm(ops.rmsnorm(xc, n2, s.eps), w_gu.t())
+                if interleaved:  # (gate_0, up_0, gate_1, ...) -> [gate | up]
+                    gu = gu.view(gu.shape[0], s.intermediate, 2).transpose(1, 2).reshape(gu.shape[0], -1)
+                xc.addmm_(ops.silu_mul(gu), w_d.t())
+            del w_qkv, w_o, w_gu, w_d
+        if self.lm_head is not None:
+            last = ops.rmsnorm(x[-1:], self.ln_f, s.eps)
+            first = torch.mm(last, self.lm_head.t()).argmax(dim=-1)
+        else:
+            first = torch.mm(ops.rmsnorm(x[-1:], self._ones, s.eps), self._unpack(self.kw_lm).t()).argmax(dim=-1)
         self.k_cache[:, 1:, :, :T] = self.k_cache[:, 0:1, :, :T]
         self.v_cache[:, 1:, :, :T] = self.v_cache[:, 0:1, :, :T]
         self.prompt_len = T
@@ -274,6 +343,7 @@ class SagaDecoder:
     def step(self, calibrate: bool) -> None:
         """One decode step for every batch row (static buffers only)."""
         s, d, B = self.shape, self.shape.head_dim, self.batch
+        ws = self.ws
         x = self._x
         torch.index_select(self.embed, 0, self.tokens, out=x)
         q4 = self._q.view(B, s.n_q, 1, d)
@@ -283,7 +353,7 @@ class SagaDecoder:
                                  self.k_cache[l], self.v_cache[l], rms_eps=s.eps, q_out=self._q)
             else:
                 if self.use_gemv:
-                    ops.gemv(x, self.kw_qkv[l], bias=self.b_qkv[l], rms_eps=s.eps, out=self._qkv)
+                    ops.gemv(x, self.kw_qkv[l], bias=self.b_qkv[l], rms_eps=s.eps, out=self._qkv, workspace=ws.get("gemv"))
                 else:
                     ops.rmsnorm(x, self.ln1[l], s.eps, out=self._h)
                     torch.addmm(self.b_qkv[l], self._h, self.w_qkv[l].t(), out=self._qkv)
@@ -291,15 +361,17 @@ class SagaDecoder:
                                    self.v_cache[l], q_out=self._q)
             K, V = self.k_cache[l], self.v_cache[l]
             if self.mode == "dense" or l in self.exempt:
-                ops.dense_decode(q4, K, V, kv_len=self.kv_len, out=self._attn)
+                ops.dense_decode(q4, K, V, kv_len=self.kv_len, out=self._attn, workspace=ws["dense"])
             elif calibrate:
-                ops.atopn_calibrate(q4, K, V, self.top_n, self.table[l], kv_len=self.kv_len, out=self._attn)
+                ops.atopn_calibrate(q4, K, V, self.top_n, self.table[l], kv_len=self.kv_len, out=self._attn,
+                                    workspace=ws["atopn"])
             else:
-                ops.atopn_decode(q4, K, V, self.table[l], self.top_n, kv_len=self.kv_len, out=self._attn)
+                ops.atopn_decode(q4, K, V, self.table[l], self.top_n, kv_len=self.kv_len, out=self._attn,
+                                 workspace=ws["atopn"], k2_variant=self.k2_variant)
             if self.use_gemv:
-                ops.gemv(self._attn.view(B, s.n_q * d), self.kw_o[l], epilogue="add", out=x)
-                ops.gemv(x, self.kw_gu[l], rms_eps=s.eps, epilogue="silu_pairs", out=self._act)
-                ops.gemv(self._act, self.kw_d[l], epilogue="add", out=x)
+                ops.gemv(self._attn.view(B, s.n_q * d), self.kw_o[l], epilogue="add", out=x, workspace=ws["gemv"])
+                ops.gemv(x, self.kw_gu[l], rms_eps=s.eps, epilogue="silu_pairs", out=self._act, workspace=ws["gemv"])
+                ops.gemv(self._act, self.kw_d[l], epilogue="add", out=x, workspace=ws["gemv"])
             else:
                 x.addmm_(self._attn.view(B, s.n_q * d), self.w_o[l].t())
                 ops.rmsnorm(x, self.ln2[l], s.eps, out=self._h)
@@ -307,8 +379,8 @@ class SagaDecoder:
                 ops.silu_mul(self._gu, out=self._act)
                 x.addmm_(self._act, self.w_d[l].t())
         if self.use_gemv:
-            ops.gemv(x, self.kw_lm, rms_eps=s.eps, out=self._logits)
-            ops.argmax_rows(self._logits, out=self.tokens)
+            ops.gemv(x, self.kw_lm, rms_eps=s.eps, out=self._logits, workspace=ws["gemv"])
+            ops.argmax_rows(self._logits, out=self.tokens, workspace=ws["argmax"])
         else:
             ops.rmsnorm(x, self.ln_f, s.eps, out=self._h)
             torch.mm(self._h, self.lm_head.t(), out=self._logits)

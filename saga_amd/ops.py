@@ -2,10 +2,16 @@
 
 Each function validates torch tensors, makes sure they live on a ROCm device,
 and calls one C-ABI entry point of libsaga_amd.so on the current stream.
-Nothing here computes on the CPU.  Workspaces are allocated once per
-(device, kind), zero-filled, grown when needed and reused (the counterpart of
-the reference's _BUFFER_CACHE, attention/triton_atopn.py:56, 73-84), so calls
-are capturable in a HIP graph after a warm-up call.
+Nothing here computes on the CPU.
+
+Workspaces: a caller may pass its own (`workspace=`, a uint8 device tensor of
+at least the entry point's *_workspace_bytes); otherwise one is taken from a
+cache keyed by (device, stream, kind), grown when needed and reused (the
+counterpart of the reference's _BUFFER_CACHE, attention/triton_atopn.py:56,
+73-84), so calls are capturable in a HIP graph after a warm-up call on the
+same stream.  Calls on different streams never share a cached workspace, and
+a workspace replaced by a larger one is kept alive until clear_workspaces(),
+because a graph captured earlier still holds its address.
 """
 from __future__ import annotations
 
@@ -16,7 +22,8 @@ import torch
 
 from . import _lib
 
-_WORKSPACES: dict = {}
+_WORKSPACES: dict = {}  # (device, stream handle, kind) -> uint8 tensor
+_RETIRED: list = []     # replaced cached workspaces, alive until clear_workspaces()
 
 
 def _need_gpu(*ts: Optional[torch.Tensor]) -> torch.device:
@@ -34,18 +41,46 @@ def _need_gpu(*ts: Optional[torch.Tensor]) -> torch.device:
     return dev
 
 
-def workspace(device: torch.device, kind: str, nbytes: int) -> torch.Tensor:
-    """Zero-filled uint8 workspace of at least nbytes, cached per (device, kind)."""
-    key = (device, kind)
+def _device(device) -> torch.device:
+    dev = torch.device(device)
+    if dev.type == "cuda" and dev.index is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    return dev
+
+
+def workspace(device: torch.device, kind: str, nbytes: int, stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+    """uint8 workspace of at least nbytes for calls on `stream` (default: the
+    device's current stream), cached per (device, stream, kind).  A cached
+    workspace too small for a call is replaced; the old one stays allocated
+    until clear_workspaces()."""
+    dev = _device(device)
+    if stream is None:
+        stream = torch.cuda.current_stream(dev)
+    key = (dev, stream.cuda_stream, kind)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+        if ws is not None:
+            _RETIRED.append(ws)
+        ws = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=dev)
         _WORKSPACES[key] = ws
     return ws
 
 
 def clear_workspaces() -> None:
+    """Free every cached workspace (speedup.py:427-428 clears the reference's
+    _BUFFER_CACHE between configurations).  A HIP graph captured with cached
+    workspaces must not be replayed afterwards."""
     _WORKSPACES.clear()
+    _RETIRED.clear()
+
+
+def _take_workspace(given: Optional[torch.Tensor], device, kind: str, nbytes: int) -> torch.Tensor:
+    if given is None:
+        return workspace(device, kind, nbytes)
+    if given.device != device or given.dtype != torch.uint8 or not given.is_contiguous() or given.numel() < nbytes:
+        raise ValueError(f"saga_amd: {kind} workspace must be a contiguous uint8 tensor of >= {nbytes} bytes "
+                         f"on {device}")
+    return given
 
 
 def _scale(query: torch.Tensor, scaling: Optional[float]) -> float:
@@ -166,12 +201,19 @@ def _decode_prep(query, key, value, attention_mask, kv_len):
     return dev, query, key, value, _mask_view(attention_mask, key.shape[2])
 
 
+def atopn_workspace_bytes(b: int, q_h: int, k_h: int, L: int, d: int, top_n: int, calibrate: bool = False) -> int:
+    """Bytes of the workspace of one fast step (or calibration step) call."""
+    buf_k = min(top_n, L) if calibrate else min(2 * top_n, L)
+    return int(_lib.load().saga_atopn_workspace_bytes(b, q_h, k_h, L, d, buf_k))
+
+
 def atopn_decode(query, key, value, softmax_threshold, top_n, attention_mask=None, scaling=None, kv_len=None,
-                 out=None, out_dtype=None):
+                 out=None, out_dtype=None, workspace=None, k2_variant=_lib.K2_AUTO):
     """Atop-N fast step (attention/attention.py:192-209).
 
     softmax_threshold: fp32 [b*q_h] (a row of the threshold table).
-    """
+    k2_variant: the kernels of the selection + softmax.V (results are
+    identical in every variant; see saga_atopn_decode_ex)."""
     dev, query, key, value, mask = _decode_prep(query, key, value, attention_mask, kv_len)
     b, q_h, _, d = query.shape
     L = key.shape[2]
@@ -181,17 +223,16 @@ def atopn_decode(query, key, value, softmax_threshold, top_n, attention_mask=Non
     if out is None:
         out = torch.empty(b, q_h, 1, d, dtype=out_dtype or query.dtype, device=dev)
     lib = _lib.load()
-    buf_k = min(2 * top_n, L)
-    ws = workspace(dev, "atopn", lib.saga_atopn_workspace_bytes(b, q_h, key.shape[1], L, d, buf_k))
-    _lib.check(lib.saga_atopn_decode(_lib.tensor(query), _lib.tensor(key), _lib.tensor(value), _lib.tensor(mask),
-                                     _lib.ptr(_kv_len(kv_len)), _scale(query, scaling), int(top_n),
-                                     _lib.ptr(softmax_threshold), _lib.tensor(out), _lib.ptr(ws), ws.numel(),
-                                     _lib.stream_of(query)), "atopn_decode")
+    ws = _take_workspace(workspace, dev, "atopn", atopn_workspace_bytes(b, q_h, key.shape[1], L, d, top_n))
+    _lib.check(lib.saga_atopn_decode_ex(_lib.tensor(query), _lib.tensor(key), _lib.tensor(value), _lib.tensor(mask),
+                                        _lib.ptr(_kv_len(kv_len)), _scale(query, scaling), int(top_n),
+                                        _lib.ptr(softmax_threshold), _lib.tensor(out), int(k2_variant), _lib.ptr(ws),
+                                        ws.numel(), _lib.stream_of(query)), "atopn_decode")
     return out
 
 
 def atopn_calibrate(query, key, value, top_n, threshold_out, attention_mask=None, scaling=None, kv_len=None,
-                    out=None, out_dtype=None):
+                    out=None, out_dtype=None, workspace=None):
     """Atop-N calibration step (attention/attention.py:173-189).
 
     threshold_out: fp32 [b*q_h], receives the k-th largest probability per row.
@@ -204,8 +245,7 @@ def atopn_calibrate(query, key, value, top_n, threshold_out, attention_mask=None
     if out is None:
         out = torch.empty(b, q_h, 1, d, dtype=out_dtype or query.dtype, device=dev)
     lib = _lib.load()
-    buf_k = min(top_n, L)
-    ws = workspace(dev, "atopn", lib.saga_atopn_workspace_bytes(b, q_h, key.shape[1], L, d, buf_k))
+    ws = _take_workspace(workspace, dev, "atopn", atopn_workspace_bytes(b, q_h, key.shape[1], L, d, top_n, True))
     _lib.check(lib.saga_atopn_calibrate(_lib.tensor(query), _lib.tensor(key), _lib.tensor(value), _lib.tensor(mask),
                                         _lib.ptr(_kv_len(kv_len)), _scale(query, scaling), int(top_n),
                                         _lib.ptr(threshold_out), _lib.tensor(out), _lib.ptr(ws), ws.numel(),
@@ -213,7 +253,8 @@ def atopn_calibrate(query, key, value, top_n, threshold_out, attention_mask=None
     return out
 
 
-def dense_decode(query, key, value, attention_mask=None, scaling=None, kv_len=None, out=None, out_dtype=None):
+def dense_decode(query, key, value, attention_mask=None, scaling=None, kv_len=None, out=None, out_dtype=None,
+                 workspace=None):
     """Dense decode attention (attention/attention.py:64-85, l_q == 1)."""
     dev, query, key, value, mask = _decode_prep(query, key, value, attention_mask, kv_len)
     b, q_h, _, d = query.shape
@@ -221,7 +262,7 @@ def dense_decode(query, key, value, attention_mask=None, scaling=None, kv_len=No
     if out is None:
         out = torch.empty(b, q_h, 1, d, dtype=out_dtype or query.dtype, device=dev)
     lib = _lib.load()
-    ws = workspace(dev, "dense", lib.saga_dense_workspace_bytes(b, q_h, L, d))
+    ws = _take_workspace(workspace, dev, "dense", lib.saga_dense_workspace_bytes(b, q_h, L, d))
     _lib.check(lib.saga_dense_decode(_lib.tensor(query), _lib.tensor(key), _lib.tensor(value), _lib.tensor(mask),
                                      _lib.ptr(_kv_len(kv_len)), _scale(query, scaling), _lib.tensor(out),
                                      _lib.ptr(ws), ws.numel(), _lib.stream_of(query)), "dense_decode")
@@ -281,39 +322,19 @@ def prefill_attention(query, key, value, attention_mask=None, scaling=None, is_c
     return out
 
 
-def set_fused_fast_step(enable: bool) -> bool:
-    """Process-wide switch of the fused Atop-N fast step (off by default: it
-    measured slower than the three-kernel path); on, shapes whose grid fits
-    the GPU at once run it.  Returns the previous setting."""
-    return bool(_lib.load().saga_set_fused_fast_step(1 if enable else 0))
-
-
-def set_k2_mode(mode: int) -> int:
-    """Process-wide shape of the fast step's selection + softmax.V: 0 by
-    shape (default: one block per row for rows of at most 12 slices of 1024
-    positions with buf_k <= 2048), 1 always one block per row (one launch), 2
-    always slice kernel + row kernel.  Results are identical in every mode.  Returns the
-    previous mode."""
-    prev = _lib.load().saga_set_k2_mode(int(mode))
-    if prev < 0:
-        raise ValueError(f"saga_amd: k2 mode must be 0, 1 or 2, got {mode}")
-    return prev
-
-
-def atopn_workspace_views(b: int, q_h: int, k_h: int, L: int, d: int, buf_k: int, device, fast: bool = True) -> dict:
-    """The cached fused-decode workspace after a call, for inspection (valid
-    until the next call): logit thresholds (fast step), kept / passing counts,
-    the selected positions and logits in ascending order, and the scores.
-    The calibration step (fast=False) writes its list to sel_idx / sel_val;
-    the fast step keeps it in per-slice lists, concatenated here in slice
-    order and cut at buf_k (host copies).  The fused fast step (layout field
-    `fused`) writes no scores; `sync_error` is non-zero if one of its barrier
-    waits gave up."""
+def atopn_workspace_views(b: int, q_h: int, k_h: int, L: int, d: int, buf_k: int, device, fast: bool = True,
+                          workspace=None) -> dict:
+    """An Atop-N workspace after a call, for inspection (valid until the next
+    call on it; default: the cached one of the device's current stream):
+    logit thresholds (fast step), kept / passing counts, the selected
+    positions and logits in ascending order, and the scores.  The calibration
+    step (fast=False) writes its list to sel_idx / sel_val; the fast step
+    keeps it in per-slice lists, concatenated here in slice order and cut at
+    buf_k (host copies)."""
     lay = _lib.atopn_layout(b, q_h, k_h, L, d, buf_k)
-    dev = torch.device(device)
-    if dev.type == "cuda" and dev.index is None:
-        dev = torch.device("cuda", torch.cuda.current_device())
-    ws = _WORKSPACES[(dev, "atopn")]
+    dev = _device(device)
+    ws = workspace if workspace is not None else \
+        _WORKSPACES[(dev, torch.cuda.current_stream(dev).cuda_stream, "atopn")]
     nr = b * q_h
 
     def view(off, n, dt):
@@ -327,8 +348,6 @@ def atopn_workspace_views(b: int, q_h: int, k_h: int, L: int, d: int, buf_k: int
         "sel_idx": view(lay.sel_idx, nr * buf_k, torch.int32).reshape(nr, buf_k),
         "sel_val": view(lay.sel_val, nr * buf_k, torch.float32).reshape(nr, buf_k),
         "scores": view(lay.scores, nr * lay.scores_ld, torch.float32).reshape(nr, lay.scores_ld)[:, :L],
-        "sync_error": view(lay.sync + lay.sync_bytes - 256, 1, torch.int32),
-        "fused": bool(lay.fused),
     }
     if fast:
         ns, cap = lay.nslice, lay.slice_cap
@@ -399,7 +418,7 @@ def _gemv_n(w: torch.Tensor) -> int:
     return w.shape[0] * 16 if w.dim() == 4 else w.shape[0]
 
 
-def gemv(x, w, bias=None, rms_eps=None, epilogue="store", out=None, split_k=True):
+def gemv(x, w, bias=None, rms_eps=None, epilogue="store", out=None, split_k=True, workspace=None):
     """Skinny projection for decode (x [M <= 16, K] bf16, w [N, K] bf16, or
     packed by pack_gemv_weight):
     y = s * x @ w.T (+ bias), s = 1/sqrt(mean(x^2) + rms_eps) per row when
@@ -407,7 +426,8 @@ def gemv(x, w, bias=None, rms_eps=None, epilogue="store", out=None, split_k=True
     epilogue: "store", "add" (out += result, in place) or "silu_pairs" (w rows
     interleaved gate/up; out = silu(gate) * up, [M, N/2]).  split_k: pass
     the cached workspace, so that long-row weights with few tiles are read
-    split over K (deterministic two-kernel reduction)."""
+    split over K (deterministic two-kernel reduction); workspace: a caller's
+    own instead of the cached one."""
     _need_gpu(x, w, bias, out)
     codes = {"store": _lib.GEMV_STORE, "add": _lib.GEMV_ADD, "silu_pairs": _lib.GEMV_SILU_PAIRS}
     code = codes[epilogue]
@@ -419,7 +439,7 @@ def gemv(x, w, bias=None, rms_eps=None, epilogue="store", out=None, split_k=True
     eps = -1.0 if rms_eps is None else float(rms_eps)
     lib = _lib.load()
     need = lib.saga_gemv_workspace_bytes(M, N, x.shape[1]) if split_k else 0
-    ws = workspace(x.device, "gemv", need) if need else None
+    ws = _take_workspace(workspace, x.device, "gemv", need) if need else None
     _lib.check(lib.saga_gemv(_lib.tensor(x), _lib.tensor(w), _lib.tensor(bias), eps, code, _lib.tensor(out),
                              _lib.ptr(ws), ws.numel() if ws is not None else 0, _lib.stream_of(x)), "gemv")
     return out
@@ -457,13 +477,13 @@ def gemv_rope_kv(x, w_pairs, bias_pairs, n_q, n_k, n_v, theta, pos, k_cache, v_c
     return q_out
 
 
-def argmax_rows(x, out=None):
+def argmax_rows(x, out=None, workspace=None):
     """First index of each row's maximum (bf16 [rows, N]) -> int64 [rows]."""
     _need_gpu(x, out)
     out = torch.empty(x.shape[0], dtype=torch.int64, device=x.device) if out is None else out
     lib = _lib.load()
     need = lib.saga_argmax_workspace_bytes(x.shape[0], x.shape[1])
-    ws = workspace(x.device, "argmax", need) if need else None
+    ws = _take_workspace(workspace, x.device, "argmax", need) if need else None
     _lib.check(lib.saga_argmax(_lib.tensor(x), _lib.ptr(out), _lib.ptr(ws), ws.numel() if ws is not None else 0,
                                _lib.stream_of(x)), "argmax")
     return out

@@ -231,8 +231,13 @@ int main(int argc, char** argv) {
       case 14: rc = saga_argmax(maybe(a), fake<int64_t>(p1), fake<void>(p2), size_t(rnd_size()), nullptr); break;
       case 15: rc = saga_prefill_attention(maybe(a), maybe(b), maybe(c), next() % 2 ? nullptr : &d, rnd_float(),
                                            int32_t(next() % 3), rnd_size(), &e, nullptr); break;
-      case 16: rc = saga_set_k2_mode(int(next() % 5) - 1); if (rc >= 0) saga_set_k2_mode(0); rc = -1; break;
-      case 17: rc = saga_set_fused_fast_step(int(next() % 3)); saga_set_fused_fast_step(0); rc = -1; break;
+      case 16: rc = saga_atopn_decode_ex(maybe(a), maybe(b), maybe(c), next() % 2 ? nullptr : &d, fake<int32_t>(p1),
+                                         rnd_float(), rnd_size(), fake<float>(p2), &e, int32_t(next() % 5) - 1,
+                                         fake<void>(p3), size_t(rnd_size()), nullptr); break;
+      case 17: (void)saga_atopn_workspace_bytes(rnd_size(), rnd_size(), rnd_size(), rnd_size(), rnd_size(),
+                                                rnd_size());
+        rc = -1;
+        break;
       case 18: rc = saga_atopn_decode(nullptr, nullptr, nullptr, nullptr, nullptr, 0.f, 0, nullptr, nullptr,
                                       nullptr, 0, nullptr); break;
       case 19: rc = saga_qk_scores(&a, &b, nullptr, nullptr, rnd_float(), maybe(c) ? &c : nullptr, nullptr,

@@ -29,21 +29,19 @@ pytestmark = pytest.mark.gpu
 
 def _views(b, q_h, k_h, L, d, buf_k, fast=True, scores_of=None):
     """Workspace views as numpy.  scores_of = (query, key, mask, scale,
-    kv_len): the fast step's fp32 scores, recomputed by the score kernel (the
-    fused fast step keeps them in registers; both run the same tile code, so
-    the values are bit-identical)."""
+    kv_len): the fast step's fp32 scores, recomputed by the score kernel
+    (the same tile code, so the values are bit-identical)."""
     raw = ops.atopn_workspace_views(b, q_h, k_h, L, d, buf_k, "cuda:0", fast=fast)
     views = {k: (v.cpu().numpy() if isinstance(v, torch.Tensor) else v) for k, v in raw.items()}
     if scores_of is not None:
         qd, kd, mask, scale, kv_len = scores_of
         views["scores"] = host(ops.qk_scores(qd, kd, mask, scale, kv_len)).reshape(b * q_h, L)
-    if fast:
-        assert int(views["sync_error"][0]) == 0
     return views
 
 
-def _run_fast(qd, kd, vd, table_row, N, mask=None, scale=None, out_dtype=torch.float32, kv_len=None):
-    out = ops.atopn_decode(qd, kd, vd, table_row, N, mask, scale, kv_len=kv_len, out_dtype=out_dtype)
+def _run_fast(qd, kd, vd, table_row, N, mask=None, scale=None, out_dtype=torch.float32, kv_len=None, k2_variant=0):
+    out = ops.atopn_decode(qd, kd, vd, table_row, N, mask, scale, kv_len=kv_len, out_dtype=out_dtype,
+                           k2_variant=k2_variant)
     torch.cuda.synchronize()
     return out
 
@@ -90,8 +88,14 @@ def test_against_reference_golden(name, golden):
     for r in range(nr):
         assert views["sel_cnt"][r] == kk
         got = np.sort(views["sel_idx"][r, :kk])
-        assert np.array_equal(got, g["cal_idx_sorted" + sfx][r]) or \
-            len(set(got) ^ set(g["cal_idx_sorted" + sfx][r])) <= 2  # a swap at the k-th boundary
+        ref_set = g["cal_idx_sorted" + sfx][r]
+        diff = set(got.tolist()) ^ set(ref_set.tolist())
+        if bf:  # bf16 logits: at most one swap at the k-th boundary
+            assert len(diff) <= 2
+        elif diff:  # fp32: only an exact tie at the k-th value may swap (equal GPU logits)
+            x = views["scores"][r]
+            kth = np.sort(x[:L])[::-1][kk - 1]
+            assert all(abs(float(x[i]) - float(kth)) <= 2e-7 * max(1.0, abs(float(kth))) for i in diff), diff
     assert rel_l2(cal, g["cal_out" + sfx]) < (1e-3 if bf else 1e-5)
 
     buf_k = min(2 * N, L)
@@ -123,6 +127,21 @@ def test_against_reference_golden(name, golden):
         ok = ~np.isnan(o_ref)
         if flips == 0:
             assert rel_l2(out[ok], o_ref[ok]) < (1e-3 if bf else 1e-5)
+        # always: the reference's fp32 gather . V on the GPU's own selection
+        # (the golden inputs, the oracle's logits at the GPU's positions)
+        rnd = O.round_bf16 if bf else (lambda a: a)
+        logits = O.qk_scores(rnd(inp["q2"]), rnd(inp["key"]), sc, inp.get("mask")).reshape(nr, L)
+        vals = np.full((nr, buf_k), -np.inf, np.float32)
+        idx = np.zeros((nr, buf_k), np.int64)
+        for r in range(nr):
+            n = int(views["sel_cnt"][r])
+            idx[r, :n] = views["sel_idx"][r, :n]
+            vals[r, :n] = logits[r, idx[r, :n]]
+        same_sel = O.gather_output(vals.reshape(b, q_h, 1, buf_k), idx.reshape(b, q_h, 1, buf_k), rnd(inp["value"]),
+                                   (b, q_h, 1, d), input_is_logits=True)
+        ok = ~np.isnan(same_sel)
+        np.testing.assert_array_equal(np.isnan(out), ~ok)
+        assert rel_l2(out[ok], same_sel[ok]) < (1e-3 if bf else 1e-5), (tag, flips)
 
 
 BENCH_SHAPES = {  # name: b, q_h, k_h, v_h, d, L, N
@@ -250,18 +269,9 @@ def test_reference_api_module_end_to_end(monkeypatch):
     assert B.EXEMPT_LAYERS == {0}
 
 
-@pytest.fixture
-def k2_mode(request):
-    """Force one shape of the fast step's K2 (1: one block per row, 2: slice
-    kernel + row kernel) for the test, restoring the default after it."""
-    prev = ops.set_k2_mode(request.param)
-    yield request.param
-    ops.set_k2_mode(prev)
-
-
-@pytest.mark.parametrize("k2_mode", [1, 2], indirect=True)
+@pytest.mark.parametrize("k2_variant", [1, 2])
 @pytest.mark.parametrize("cut_pos", [2500, 5200])
-def test_fast_overflow_cut_inside_a_later_slice(cut_pos, k2_mode):
+def test_fast_overflow_cut_inside_a_later_slice(cut_pos, k2_variant):
     """More than buf_k positions pass and rank buf_k falls inside a slice
     after the first: the earlier slices count whole, the straddling one over
     its first entries, later ones not at all (the ordered cap of the oracle).
@@ -276,7 +286,7 @@ def test_fast_overflow_cut_inside_a_later_slice(cut_pos, k2_mode):
     v = O.round_bf16(rng.standard_normal((b, v_h, L, d), dtype=np.float32))
     table = np.full(b * q_h, 1e-7, dtype=np.float32)
     out = host(ops.atopn_decode(dev(q, "bf16"), dev(k, "bf16"), dev(v, "bf16"), torch.from_numpy(table).cuda(), N,
-                                out_dtype=torch.float32))
+                                out_dtype=torch.float32, k2_variant=k2_variant))
     views = _views(b, q_h, k_h, L, d, 2 * N)
     ref_out, t_ref, idx_ref, cnt_ref = O.fast(q, k, v, table, None, N, None)
     buf_k = 2 * N
@@ -287,7 +297,7 @@ def test_fast_overflow_cut_inside_a_later_slice(cut_pos, k2_mode):
     assert np.max(np.abs(out - ref_out)) < 2e-3 and rel_l2(out, ref_out) < 1e-4
 
 
-FUSED_SHAPES = {  # name: b, q_h, k_h, v_h, d, L, N, dtype
+K2_BASE_SHAPES = {  # name: b, q_h, k_h, v_h, d, L, N, dtype
     "qwen1.5b_32k_b8": (8, 12, 1, 2, 128, 33024, 512, "bf16"),
     "b32_4k_g12": (32, 12, 1, 2, 128, 4096, 256, "bf16"),
     "b2_k2_v8_16h": (2, 16, 2, 8, 128, 6000, 64, "f16"),
@@ -296,91 +306,7 @@ FUSED_SHAPES = {  # name: b, q_h, k_h, v_h, d, L, N, dtype
 }
 
 
-@pytest.mark.parametrize("name", list(FUSED_SHAPES))
-def test_fused_fast_step_matches_three_kernel_path(name):
-    """The fused fast step (scores kept on chip, a flag barrier per (batch,
-    key head)) against the three-kernel path on the same inputs: identical
-    thresholds, counts and ordered lists; outputs equal to fp32 rounding (the
-    merge order differs); the selection rule on the recomputed scores."""
-    b, q_h, k_h, v_h, d, L, N, dt = FUSED_SHAPES[name]
-    print(f"atopn fused vs split shape={name}", flush=True)
-    rng = np.random.default_rng(zlib.crc32(name.encode()))
-    (q, k, v), (qd, kd, vd) = qkv(rng, b, q_h, k_h, v_h, d, L, dt, outliers=0.01)
-    lens = None
-    if name == "b3_ragged":
-        lens = torch.tensor([777, 300, 1], dtype=torch.int32, device="cuda")
-    table = torch.zeros(b * q_h, device="cuda")
-    ops.atopn_calibrate(qd, kd, vd, N, table, kv_len=lens)
-    q2 = O.round_bf16(q + np.float32(0.3) * rng.standard_normal(q.shape, dtype=np.float32))
-    q2d = dev(q2, dt)
-    buf_k = min(2 * N, L)
-    res = {}
-    prev = ops.set_fused_fast_step(True)
-    try:
-        for fused in (True, False):
-            ops.set_fused_fast_step(fused)
-            out = host(_run_fast(q2d, kd, vd, table, N, out_dtype=torch.float32, kv_len=lens))
-            views = _views(b, q_h, k_h, L, d, buf_k, scores_of=(q2d, kd, None, None, lens))
-            assert views["fused"] == fused, "shape expected on the fused path"
-            _check_selection_rule(views, b * q_h, L, buf_k, kv_len=None if lens is None else host(lens), q_h=q_h)
-            res[fused] = (out, views)
-    finally:
-        ops.set_fused_fast_step(prev)
-    (of, vf), (os_, vs) = res[True], res[False]
-    np.testing.assert_array_equal(vf["sel_cnt"], vs["sel_cnt"])
-    np.testing.assert_array_equal(vf["sel_total"], vs["sel_total"])
-    np.testing.assert_array_equal(vf["sel_idx"], vs["sel_idx"])
-    np.testing.assert_allclose(vf["thresh"], vs["thresh"], rtol=2e-6, atol=2e-6)
-    nan = np.isnan(os_)
-    np.testing.assert_array_equal(np.isnan(of), nan)
-    assert rel_l2(of[~nan], os_[~nan]) < 1e-5
-    print(f"  mean_count={vf['sel_cnt'].mean():.1f}", flush=True)
-
-
-def test_fused_fast_step_overflow_and_repeated_calls():
-    """An overflowing row through the fused path (cut at buf_k inside a
-    block's list), then calls of other shapes sharing the workspace's
-    barrier state, then the first shape again: same results each time."""
-    rng = np.random.default_rng(31)
-    b, q_h, k_h, v_h, d, L, N = 8, 4, 1, 2, 128, 6000, 256
-    q = O.round_bf16(rng.standard_normal((b, q_h, 1, d), dtype=np.float32))
-    k = O.round_bf16(rng.standard_normal((b, k_h, L, d), dtype=np.float32) * np.float32(0.2))
-    k[:, :, 2500:, :] += O.round_bf16(q.mean(axis=1, keepdims=True)[:, :, 0:1, :] * np.float32(0.3))
-    k = O.round_bf16(k)
-    v = O.round_bf16(rng.standard_normal((b, v_h, L, d), dtype=np.float32))
-    table = np.full(b * q_h, 1e-7, dtype=np.float32)
-    args = (dev(q, "bf16"), dev(k, "bf16"), dev(v, "bf16"), torch.from_numpy(table).cuda(), N)
-    ref_out, _, idx_ref, _ = O.fast(q, k, v, table, None, N, None)
-    prev = ops.set_fused_fast_step(True)
-    try:
-        _fused_overflow_reps(args, b, q_h, k_h, L, d, N, ref_out, idx_ref, rng)
-    finally:
-        ops.set_fused_fast_step(prev)
-
-
-def _fused_overflow_reps(args, b, q_h, k_h, L, d, N, ref_out, idx_ref, rng):
-    first = None
-    for rep in range(3):
-        out = host(ops.atopn_decode(*args, out_dtype=torch.float32))
-        views = _views(b, q_h, k_h, L, d, 2 * N)
-        assert views["fused"]
-        assert (views["sel_total"] > 2 * N).all(), "the case must overflow"
-        for r in range(b * q_h):
-            np.testing.assert_array_equal(views["sel_idx"][r], idx_ref.reshape(b * q_h, 2 * N)[r])
-        assert np.max(np.abs(out - ref_out)) < 2e-3 and rel_l2(out, ref_out) < 1e-4
-        if first is None:
-            first = out
-        np.testing.assert_array_equal(out, first)
-        # other shapes (other unit and block counts) in between
-        for bb, LL in ((1, 3000), (16, 2048)):
-            (_, _, _), (q3, k3, v3) = qkv(rng, bb, 12, 1, 2, 128, LL, "bf16")
-            t3 = torch.full((bb * 12,), 1e-3, device="cuda")
-            ops.atopn_decode(q3, k3, v3, t3, 64)
-            torch.cuda.synchronize()
-            assert int(_views(bb, 12, 1, LL, 128, 128)["sync_error"][0]) == 0
-
-
-K2_SHAPES = dict(FUSED_SHAPES, **{  # + long slice lists; lists past one LDS batch; rows past 64 slices
+K2_SHAPES = dict(K2_BASE_SHAPES, **{  # + long slice lists; lists past one LDS batch; rows past 64 slices
     "b4_long_lists": (4, 12, 1, 2, 128, 20000, 1024, "bf16"),
     "b2_buf4096": (2, 12, 1, 2, 128, 20000, 2048, "bf16"),
     "b1_70k": (1, 12, 1, 2, 128, 70000, 256, "bf16"),
@@ -406,16 +332,11 @@ def test_row_block_k2_matches_slice_and_row_kernels(name):
     q2d = dev(q2, dt)
     buf_k = min(2 * N, L)
     res = {}
-    prev = ops.set_k2_mode(0)
-    try:
-        for mode in (1, 2):
-            ops.set_k2_mode(mode)
-            out = host(_run_fast(q2d, kd, vd, table, N, out_dtype=torch.float32, kv_len=lens))
-            views = _views(b, q_h, k_h, L, d, buf_k, scores_of=(q2d, kd, None, None, lens))
-            _check_selection_rule(views, b * q_h, L, buf_k, kv_len=None if lens is None else host(lens), q_h=q_h)
-            res[mode] = (out, views)
-    finally:
-        ops.set_k2_mode(prev)
+    for variant in (1, 2):
+        out = host(_run_fast(q2d, kd, vd, table, N, out_dtype=torch.float32, kv_len=lens, k2_variant=variant))
+        views = _views(b, q_h, k_h, L, d, buf_k, scores_of=(q2d, kd, None, None, lens))
+        _check_selection_rule(views, b * q_h, L, buf_k, kv_len=None if lens is None else host(lens), q_h=q_h)
+        res[variant] = (out, views)
     (o1, v1), (o2, v2) = res[1], res[2]
     for key in ("sel_cnt", "sel_total", "sel_idx", "thresh"):
         np.testing.assert_array_equal(v1[key], v2[key])
@@ -425,9 +346,11 @@ def test_row_block_k2_matches_slice_and_row_kernels(name):
     print(f"  mean_count={v1['sel_cnt'].mean():.1f} max={v1['sel_cnt'].max()}", flush=True)
 
 
-def test_k2_mode_switch_rejects_other_values():
-    with pytest.raises(ValueError):
-        ops.set_k2_mode(3)
+def test_k2_variant_rejects_other_values():
+    rng = np.random.default_rng(5)
+    (_, _, _), (qd, kd, vd) = qkv(rng, 1, 12, 1, 2, 128, 256, "bf16")
+    with pytest.raises(RuntimeError, match="k2_variant"):
+        ops.atopn_decode(qd, kd, vd, torch.zeros(12, device="cuda"), 16, k2_variant=3)
 
 
 def _random_case(seed):

@@ -58,11 +58,12 @@ def test_rmsnorm_and_silu_mul_match_oracle():
     assert rel_l2(a, O.silu_mul(gu)) < 4e-3
 
 
-def _tiny_model(mode, top_n=16):
+def _tiny_model(mode, top_n=16, keep_source_weights=False):
     from saga_amd.decoder import DecoderShape, SagaDecoder
     shape = DecoderShape(layers=3, hidden=256, n_q=4, n_k=1, n_v=2, head_dim=64, intermediate=512, vocab=1024,
                          rope_theta=1e4, eps=1e-6, qkv_bias=True)
-    m = SagaDecoder(shape, batch=2, max_len=600, mode=mode, top_n=top_n, exempt_layers=(0,) if mode == "atopn" else ())
+    m = SagaDecoder(shape, batch=2, max_len=600, mode=mode, top_n=top_n, exempt_layers=(0,) if mode == "atopn" else (),
+                    keep_source_weights=keep_source_weights)
     return m
 
 
@@ -91,7 +92,7 @@ def test_one_decode_step_vs_float64_reference():
     embed, rmsnorm, projections, RoPE, cache append, attention, MLP, LM head.
     (Dense attention: an Atop-N top-k boundary could flip under the bf16
     rounding of the intermediates; selection is checked by its own tests.)"""
-    m = _tiny_model("dense")
+    m = _tiny_model("dense", keep_source_weights=True)
     g = torch.Generator(device="cuda").manual_seed(5)
     for t in m.ln1 + m.ln2 + [m.ln_f]:  # non-trivial norm weights: exercises their folding
         t.copy_((1 + 0.3 * torch.randn(t.shape, generator=g, device="cuda")).to(t.dtype))

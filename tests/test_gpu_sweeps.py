@@ -181,7 +181,7 @@ def test_small_decoder_step_sweep(seed):
           flush=True)
     shape = DecoderShape(layers=layers, hidden=hidden, n_q=n_q, n_k=n_k, n_v=n_v, head_dim=d, intermediate=inter,
                          vocab=vocab, rope_theta=1e4, eps=1e-6, qkv_bias=bool(seed % 2))
-    m = SagaDecoder(shape, batch=B, max_len=max_len, mode="dense")
+    m = SagaDecoder(shape, batch=B, max_len=max_len, mode="dense", keep_source_weights=True)
     g = torch.Generator(device="cuda").manual_seed(seed)
     for t in m.ln1 + m.ln2 + [m.ln_f]:
         t.copy_((1 + 0.3 * torch.randn(t.shape, generator=g, device="cuda")).to(t.dtype))

@@ -1,0 +1,117 @@
+"""Workspace lifetime under HIP graph capture.
+
+A captured graph keeps raw device addresses.  The decoder owns its
+workspaces; the ops-level cache is keyed by (device, stream, kind) and keeps
+a replaced workspace alive until clear_workspaces().  So growing the cache
+with a larger call after a capture, and churning the allocator with fresh
+tensors, must leave every replay's output unchanged."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import qkv
+from saga_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _churn():
+    """A few hundred MB of fresh NaN-filled tensors: freed workspace memory
+    would be handed out to them.  Kept alive over a replay, they must come
+    out untouched (a replay writing into freed memory would overwrite them)."""
+    bufs = [torch.full((32 << 20,), float("nan"), device="cuda") for _ in range(4)]
+    torch.cuda.synchronize()
+    return bufs
+
+
+def _untouched(bufs):
+    torch.cuda.synchronize()
+    return all(bool(torch.isnan(b).all()) for b in bufs)
+
+
+def test_decoder_graph_survives_cache_growth():
+    from saga_amd.decoder import DecoderShape, SagaDecoder
+    shape = DecoderShape(layers=2, hidden=256, n_q=4, n_k=1, n_v=2, head_dim=64, intermediate=512, vocab=1024,
+                         rope_theta=1e4, eps=1e-6, qkv_bias=True)
+    m = SagaDecoder(shape, batch=2, max_len=700, mode="atopn", top_n=16)
+    m.prefill(torch.randint(0, 1024, (600,)))
+    m.capture()
+
+    def run():
+        m.reset()
+        toks = []
+        for i in range(4):
+            m.replay(i)
+            toks.append(m.tokens.clone())
+        torch.cuda.synchronize()
+        return torch.stack(toks), m._logits.clone()
+
+    toks0, logits0 = run()
+    # a much larger call through the shared cache on the same (default) stream
+    rng = np.random.default_rng(3)
+    (_, _, _), (qd, kd, vd) = qkv(rng, 8, 12, 1, 2, 128, 20000, "bf16")
+    ops.atopn_decode(qd, kd, vd, torch.full((96,), 1e-4, device="cuda"), 512)
+    ops.dense_decode(qd, kd, vd)
+    torch.cuda.synchronize()
+    del qd, kd, vd
+    ops.clear_workspaces()  # the decoder's own workspaces are not the cache's
+    bufs = _churn()
+    toks1, logits1 = run()
+    assert _untouched(bufs)
+    assert torch.equal(toks0, toks1)
+    assert torch.equal(logits0, logits1)
+
+
+def test_cached_workspace_replaced_under_a_captured_graph_stays_alive():
+    """A graph captured with the cache's workspace of its capture stream; a
+    larger call on that stream replaces the cached workspace; the replay
+    still reads and writes the old one, which must not have been freed."""
+    rng = np.random.default_rng(4)
+    (_, _, _), (qd, kd, vd) = qkv(rng, 2, 12, 1, 2, 128, 3000, "bf16")
+    table = torch.full((24,), 1e-3, device="cuda")
+    out = torch.empty(2, 12, 1, 128, device="cuda", dtype=torch.bfloat16)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.atopn_decode(qd, kd, vd, table, 64, out=out)  # warm-up: allocates the cached workspace of s
+    torch.cuda.synchronize()
+    small = ops.workspace(qd.device, "atopn", 1, stream=s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        ops.atopn_decode(qd, kd, vd, table, 64, out=out)
+    g.replay()
+    torch.cuda.synchronize()
+    ref = out.clone()
+    (_, _, _), (q2, k2, v2) = qkv(rng, 8, 12, 1, 2, 128, 30000, "bf16")
+    with torch.cuda.stream(s):
+        ops.atopn_decode(q2, k2, v2, torch.full((96,), 1e-4, device="cuda"), 512)
+    torch.cuda.synchronize()
+    assert ops.workspace(qd.device, "atopn", 1, stream=s).data_ptr() != small.data_ptr(), "cache must have grown"
+    del q2, k2, v2, small
+    bufs = _churn()
+    out.zero_()
+    g.replay()
+    assert _untouched(bufs)
+    assert torch.equal(out, ref)
+    del g
+
+
+def test_streams_get_separate_cached_workspaces():
+    dev = torch.device("cuda", torch.cuda.current_device())
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    a = ops.workspace(dev, "atopn", 4096, stream=s1)
+    b = ops.workspace(dev, "atopn", 4096, stream=s2)
+    assert a.data_ptr() != b.data_ptr()
+    assert ops.workspace(dev, "atopn", 1024, stream=s1).data_ptr() == a.data_ptr()
+    # an explicit workspace is used as given; a too small one is refused
+    rng = np.random.default_rng(5)
+    (_, _, _), (qd, kd, vd) = qkv(rng, 1, 12, 1, 2, 128, 512, "bf16")
+    need = ops.atopn_workspace_bytes(1, 12, 1, 512, 128, 16)
+    own = torch.empty(need, dtype=torch.uint8, device="cuda")
+    t = torch.full((12,), 1e-3, device="cuda")
+    o1 = ops.atopn_decode(qd, kd, vd, t, 16, workspace=own)
+    o2 = ops.atopn_decode(qd, kd, vd, t, 16)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+    with pytest.raises(ValueError, match="workspace"):
+        ops.atopn_decode(qd, kd, vd, t, 16, workspace=own[: need - 256])
