@@ -13,9 +13,21 @@ Also reported on the same line:
                 algorithmic bytes per launch / its average duration, timed
                 with HIP events over a graph of launches on the stream they
                 run on, against the 8 TB/s HBM peak;
+  attention_call_roofline
+                the whole Atop-N fast step (every kernel of one call) at the
+                decoder's state: K + the distinct V rows it selects (per batch
+                row and value head, counted from the workspace) + Q/O +
+                thresholds, over the call's average duration;
+  hbm_copy_GBs  a measured device-to-device copy (bytes read + written /
+                time), beside the 8 TB/s spec;
+  c5            the 128k comparison: batch 4, 131072 positions, SAGA 1K/2V
+                with Atop-N N=1024 against dense GQA 2K/2V, attention alone on
+                the same seeded N(0,1) caches, microseconds per call and ratio;
   cpu_baseline  the CPU oracle (the reference's fp32 path restated in numpy)
-                on a bounded sample: one decode step of attention over the
-                28 layers at the same shapes, as attention tokens/s;
+                on all host cores: per-layer decode-attention latency at the
+                C1 (b1, 15/1/5 heads, d64, 4096 positions, N=128), C3 (this
+                workload) and C5 (b4, 128k, N=1024) shapes, and attention
+                tokens/s at C3; the CPU model is printed;
   dense_gqa     the same harness with 2 key / 2 value heads and the dense
                 split-L decode kernel (the in-house dense-GQA comparator).
 
@@ -105,72 +117,275 @@ def decode_rate(model, steps, warmup):
     return ms / steps, model.batch * steps / (ms / 1000.0), wall
 
 
-def cpu_baseline(batch, ctx, shape, top_n, layers, min_secs=10.0, max_steps=30):
-    """The oracle (reference fp32 path) on one decode step of attention."""
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+# decode-attention shapes of the CPU baseline: b, q_h, k_h, v_h, d, L, N
+CPU_SHAPES = {
+    "C1": (1, 15, 1, 5, 64, 4096, 128),
+    "C5": (4, 12, 1, 2, 128, 131072, 1024),
+}
+
+
+def _cpu_layer_ms(b, q_h, k_h, v_h, d, L, N, budget_s, max_calls=20):
+    """Per-layer latency (ms) of the oracle's fast step on N(0,1) fp32 inputs
+    after one calibration, as many calls as fit budget_s (at least 2)."""
     from oracle import saga_oracle as O
+    rng = np.random.default_rng(0)
+    q = rng.standard_normal((b, q_h, 1, d), dtype=np.float32)
+    k = rng.standard_normal((b, k_h, L, d), dtype=np.float32)
+    v = rng.standard_normal((b, v_h, L, d), dtype=np.float32)
+    q2 = q + np.float32(0.3) * rng.standard_normal(q.shape, dtype=np.float32)
+    t0 = time.perf_counter()
+    _, thr, _ = O.calibrate(q, k, v, None, N, None)
+    cal_ms = (time.perf_counter() - t0) * 1e3
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 2 or (time.perf_counter() - t_start < budget_s and len(times) < max_calls):
+        t0 = time.perf_counter()
+        O.fast(q2, k, v, thr, None, N, None)
+        times.append((time.perf_counter() - t0) * 1e3)
+    a = np.asarray(times)
+    return {"fast_ms_mean": round(float(a.mean()), 3), "fast_ms_p50": round(float(np.percentile(a, 50)), 3),
+            "fast_ms_p90": round(float(np.percentile(a, 90)), 3), "calibration_ms": round(cal_ms, 3),
+            "calls": len(times)}
+
+
+def cpu_baseline(batch, ctx, shape, top_n, layers, budget_s=6.0):
+    """The oracle (the reference's fp32 path restated in numpy) on every host
+    core: per-layer decode-attention latency at C1, C3 (this workload) and C5,
+    and attention tokens/s at C3 (batch / (layers x per-layer fast step))."""
     try:
         from threadpoolctl import threadpool_limits
     except ImportError:  # pragma: no cover
         threadpool_limits = None
-    cores = min(16, os.cpu_count() or 1)
-    rng = np.random.default_rng(0)
-    L = ctx + 1
-    q = rng.standard_normal((batch, shape.n_q, 1, shape.head_dim), dtype=np.float32)
-    k = rng.standard_normal((batch, shape.n_k, L, shape.head_dim), dtype=np.float32)
-    v = rng.standard_normal((batch, shape.n_v, L, shape.head_dim), dtype=np.float32)
-    q2 = q + np.float32(0.3) * rng.standard_normal(q.shape, dtype=np.float32)
+    cores = os.cpu_count() or 1
+    shapes = dict(CPU_SHAPES)
+    shapes["C3"] = (batch, shape.n_q, shape.n_k, shape.n_v, shape.head_dim, ctx + 1, top_n)
+    t0 = time.perf_counter()
+    per_layer = {}
 
     def run():
-        # whole decode steps (a calibration layer + fast layers) until about
-        # min_secs of CPU work, at most max_steps
-        steps, t0 = 0, time.perf_counter()
-        while True:
-            _, thr, _ = O.calibrate(q, k, v, None, top_n, None)
-            for _ in range(layers - 1):
-                O.fast(q2, k, v, thr, None, top_n, None)
-            steps += 1
-            secs = time.perf_counter() - t0
-            if secs >= min_secs or steps >= max_steps:
-                return steps, secs
+        for name in ("C1", "C3", "C5"):
+            per_layer[name] = dict(_cpu_layer_ms(*shapes[name], budget_s), shape=list(shapes[name]))
 
     if threadpool_limits is not None:
         with threadpool_limits(limits=cores):
-            steps, secs = run()
+            run()
     else:
-        steps, secs = run()
+        run()
+    c3 = per_layer["C3"]["fast_ms_p50"]
     return {
-        "value": round(batch * steps / secs, 3),
-        "unit": f"tokens/s (attention only, {layers} layers)",
+        "value": round(batch / (layers * c3 * 1e-3), 3),
+        "unit": f"tokens/s (attention only, {layers} layers of the fast step)",
         "cores": cores,
         "kind": "port",
-        "sample": (f"{steps} decode steps of attention, each {layers} layers (1 calibration + {layers - 1} fast), "
-                   f"b{batch} q{shape.n_q}/k{shape.n_k}/v{shape.n_v} d{shape.head_dim} ctx {L}, N={top_n}, fp32, "
-                   f"numpy oracle, {secs:.1f} s"),
+        "cpu_model": cpu_model(),
+        "per_layer": per_layer,
+        "sample": (f"numpy oracle in fp32 on {cores} threads: after one calibration, repeated fast steps per shape "
+                   f"[b, q_h, k_h, v_h, d, L, N] for ~{budget_s:.0f} s each ({time.perf_counter() - t0:.1f} s); "
+                   f"value = batch / ({layers} x C3 per-layer median)"),
     }
 
 
-def profile_kernels(batch, ctx, shape, launches=8):
-    """K1 alone at the decode shape (K cache of ctx + 1 positions), then a
-    plain 1 GiB device-to-device copy: per-dispatch hardware counters of the
-    copy (2 GiB of known traffic) scale those of K1."""
+def hbm_copy_gbs(nbytes=1 << 30, reps=10):
+    """A plain device-to-device copy of nbytes: (read + written bytes) / time."""
+    src = torch.empty(nbytes // 2, dtype=torch.int16, device="cuda")
+    src.fill_(1)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / reps
+    del src, dst
+    return round(2 * nbytes / us / 1e3, 1)
+
+
+def atopn_call_bytes(model, top_n, kvl):
+    """Algorithmic bytes of one fast-step call at the decoder's state,
+    averaged over its layers: K (b * k_h * kv_len * d * 2) + the distinct V
+    rows selected per (batch row, value head) * d * 2 + Q and O + the
+    thresholds.  Returns (bytes, distinct V rows per call)."""
+    from saga_amd import ops
+    s, B = model.shape, model.batch
+    q4 = model._q.view(B, s.n_q, 1, s.head_dim)
+    L = model.k_cache.shape[3]
+    buf_k = min(2 * top_n, L)
+    kv = int(kvl[0])
+    ws = model.ws["atopn"]
+    rows = 0
+    for l in range(s.layers):
+        ops.atopn_decode(q4, model.k_cache[l], model.v_cache[l], model.table[l], top_n, kv_len=kvl, out=model._attn,
+                         workspace=ws)
+        kept = ops.atopn_kept_positions(B, s.n_q, s.n_k, L, s.head_dim, buf_k, ws)
+        rows += ops.atopn_distinct_value_rows(kept, B, s.n_q, s.n_v, L)
+    torch.cuda.synchronize()
+    vrows = rows / s.layers
+    d2 = s.head_dim * 2
+    return B * s.n_k * kv * d2 + vrows * d2 + 2 * B * s.n_q * d2 + 4 * B * s.n_q, vrows
+
+
+def c5_leg(copies=4, b=4, q_h=12, L=131072, N=1024, d=128):
+    """Attention alone at the 128k comparison shape: SAGA (1 key / 2 value
+    heads, Atop-N N=1024: calibrated on q, timed on a nearby q2) against
+    dense GQA (2 key / 2 value heads) on the same seeded N(0,1) caches,
+    `copies` distinct caches cycled (the Infinity Cache would hold one)."""
+    from saga_amd import _lib, ops
+    g = torch.Generator(device="cuda").manual_seed(5)
+    q = torch.randn(b, q_h, 1, d, device="cuda", generator=g).to(torch.bfloat16)
+    q2 = (q.float() + 0.3 * torch.randn(q.shape, device="cuda", generator=g)).to(torch.bfloat16)
+    out = torch.empty(b, q_h, 1, d, device="cuda", dtype=torch.bfloat16)
+    kd = [torch.randn(b, 2, L, d, device="cuda", generator=g).to(torch.bfloat16) for _ in range(copies)]
+    vd = [torch.randn(b, 2, L, d, device="cuda", generator=g).to(torch.bfloat16) for _ in range(copies)]
+    ks = [x[:, :1].contiguous() for x in kd]   # SAGA: the first key head, the same two value heads
+    lib = _lib.load()
+    wsd = torch.empty(max(lib.saga_dense_workspace_bytes(b, q_h, L, d), 256), dtype=torch.uint8, device="cuda")
+    wsa = torch.empty(max(ops.atopn_workspace_bytes(b, q_h, 1, L, d, N, c) for c in (False, True)),
+                      dtype=torch.uint8, device="cuda")
+    tabs = [torch.zeros(b * q_h, device="cuda") for _ in range(copies)]
+    for i in range(copies):
+        ops.atopn_calibrate(q, ks[i], vd[i], N, tabs[i], out=out, workspace=wsa)
+    saga_us = timed_graph(lambda i: ops.atopn_decode(q2, ks[i % copies], vd[i % copies], tabs[i % copies], N, out=out,
+                                                     workspace=wsa), 2 * copies)
+    dense_us = timed_graph(lambda i: ops.dense_decode(q2, kd[i % copies], vd[i % copies], out=out, workspace=wsd),
+                           2 * copies)
+    ops.atopn_decode(q2, ks[0], vd[0], tabs[0], N, out=out, workspace=wsa)
+    kept = ops.atopn_kept_positions(b, q_h, 1, L, d, min(2 * N, L), wsa)
+    vrows = ops.atopn_distinct_value_rows(kept, b, q_h, 2, L)
+    torch.cuda.synchronize()
+    qo = 2 * b * q_h * d * 2
+    saga_bytes = b * L * d * 2 + vrows * d * 2 + qo + 4 * b * q_h
+    dense_bytes = 2 * b * 2 * L * d * 2 + qo
+    del kd, vd, ks
+    torch.cuda.empty_cache()
+    return {"workload": f"attention alone, batch {b}, {L} positions, {q_h} query heads, d{d}: SAGA 1K/2V Atop-N "
+                        f"N={N} vs dense GQA 2K/2V, N(0,1) bf16 caches",
+            "saga_us": round(saga_us, 2), "dense_us": round(dense_us, 2), "speedup": round(dense_us / saga_us, 3),
+            "saga_GBs": round(saga_bytes / saga_us / 1e3, 1), "dense_GBs": round(dense_bytes / dense_us / 1e3, 1),
+            "saga_frac": round(saga_bytes / saga_us / 1e3 / HBM_PEAK_GBS, 4),
+            "dense_frac": round(dense_bytes / dense_us / 1e3 / HBM_PEAK_GBS, 4),
+            "saga_bytes": int(saga_bytes), "dense_bytes": int(dense_bytes), "saga_value_rows": vrows}
+
+
+def c1_gpu_us(reps=20):
+    """The fast step at the C1 shape (b1, 15/1/5 heads, d64, 4096 positions,
+    fp32, N=128) on the GPU, microseconds per call (graph of calls)."""
+    from saga_amd import ops
+    b, q_h, k_h, v_h, d, L, N = CPU_SHAPES["C1"]
+    g = torch.Generator(device="cuda").manual_seed(1)
+    q = torch.randn(b, q_h, 1, d, device="cuda", generator=g)
+    k = torch.randn(b, k_h, L, d, device="cuda", generator=g)
+    v = torch.randn(b, v_h, L, d, device="cuda", generator=g)
+    tab = torch.zeros(b * q_h, device="cuda")
+    ops.atopn_calibrate(q, k, v, N, tab)
+    out = torch.empty(b, q_h, 1, d, device="cuda")
+    ws = torch.empty(ops.atopn_workspace_bytes(b, q_h, k_h, L, d, N), dtype=torch.uint8, device="cuda")
+    return round(timed_graph(lambda i: ops.atopn_decode(q, k, v, tab, N, out=out, workspace=ws), reps), 2)
+
+
+def profile_kernels(batch, ctx, shape, top_n, launches=8):
+    """Kernels alone at the decode shape, for hardware-counter runs: K1
+    (qk_scores) `launches` times, the whole Atop-N fast step (after one
+    calibration) `launches` times, the dense decode at the dense-GQA
+    comparator's heads `launches` times, then a plain 1 GiB device-to-device
+    copy 3 times, whose counters (2 GiB of known traffic per dispatch) scale
+    the others'.  Inputs: N(0,1) bf16 caches of ctx + 1 positions."""
     from saga_amd import ops
     L = ctx + 1
+    d = shape.head_dim
     g = torch.Generator(device="cuda").manual_seed(0)
-    q = torch.randn(batch, shape.n_q, 1, shape.head_dim, device="cuda", generator=g).to(torch.bfloat16)
-    k = torch.randn(batch, shape.n_k, L, shape.head_dim, device="cuda", generator=g).to(torch.bfloat16)
+    q = torch.randn(batch, shape.n_q, 1, d, device="cuda", generator=g).to(torch.bfloat16)
+    q2 = (q.float() + 0.3 * torch.randn(q.shape, device="cuda", generator=g)).to(torch.bfloat16)
+    k = torch.randn(batch, shape.n_k, L, d, device="cuda", generator=g).to(torch.bfloat16)
+    v = torch.randn(batch, shape.n_v, L, d, device="cuda", generator=g).to(torch.bfloat16)
     kvl = torch.full((batch,), L, dtype=torch.int32, device="cuda")
     for _ in range(launches):
         ops.qk_scores(q, k, kv_len=kvl, with_partials=True)
+    tab = torch.zeros(batch * shape.n_q, device="cuda")
+    ops.atopn_calibrate(q, k, v, top_n, tab, kv_len=kvl)
+    ws = torch.empty(ops.atopn_workspace_bytes(batch, shape.n_q, shape.n_k, L, d, top_n), dtype=torch.uint8,
+                     device="cuda")
+    for _ in range(launches):
+        ops.atopn_decode(q2, k, v, tab, top_n, kv_len=kvl, workspace=ws)
+    kept = ops.atopn_kept_positions(batch, shape.n_q, shape.n_k, L, d, min(2 * top_n, L), ws)
+    vrows = ops.atopn_distinct_value_rows(kept, batch, shape.n_q, shape.n_v, L)
+    kd = torch.randn(batch, 2, L, d, device="cuda", generator=g).to(torch.bfloat16)
+    vd = torch.randn(batch, 2, L, d, device="cuda", generator=g).to(torch.bfloat16)
+    for _ in range(launches):
+        ops.dense_decode(q, kd, vd, kv_len=kvl)
     src = torch.empty(1 << 29, dtype=torch.int16, device="cuda")
     src.fill_(1)
     dst = torch.empty_like(src)
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    k1_bytes = batch * shape.n_k * L * shape.head_dim * 2 + batch * shape.n_q * shape.head_dim * 2
-    print(json.dumps({"k1_launches": launches, "k1_algorithmic_bytes": k1_bytes,
-                      "copy_launches": 3, "copy_bytes_read": src.numel() * 2, "copy_bytes_written": dst.numel() * 2}),
-          flush=True)
+    d2 = d * 2
+    qo = 2 * batch * shape.n_q * d2
+    print(json.dumps({
+        "launches": launches, "batch": batch, "kv_len": L, "n_q": shape.n_q, "n_k": shape.n_k, "n_v": shape.n_v,
+        "head_dim": d, "top_n": top_n,
+        "k1_algorithmic_bytes": batch * shape.n_k * L * d2 + batch * shape.n_q * d2,
+        "atopn_call_algorithmic_bytes": batch * shape.n_k * L * d2 + vrows * d2 + qo + 4 * batch * shape.n_q,
+        "atopn_distinct_value_rows": vrows,
+        "dense_algorithmic_bytes": batch * 4 * L * d2 + qo,
+        "copy_launches": 3, "copy_bytes_read": src.numel() * 2, "copy_bytes_written": dst.numel() * 2}), flush=True)
+    return 0
+
+
+def summarize_counters(paths):
+    """Per-kernel averages of the rocprofv3 counter CSVs (*counter_collection.csv)
+    under `paths`, each counter scaled by the known bytes of the 1 GiB copy
+    dispatches in the same run (FETCH_SIZE / WRITE_SIZE are in KiB)."""
+    import csv
+    import glob
+    from collections import defaultdict
+    vals = defaultdict(lambda: defaultdict(list))  # kernel -> counter -> per-dispatch values
+    for p in paths:
+        files = glob.glob(os.path.join(p, "**", "*counter_collection.csv"), recursive=True) if os.path.isdir(p) else [p]
+        for f in files:
+            per = defaultdict(float)
+            names = {}
+            with open(f) as fh:
+                for row in csv.DictReader(fh):
+                    key = (row["Dispatch_Id"], row["Counter_Name"])
+                    per[key] += float(row["Counter_Value"])
+                    names[row["Dispatch_Id"]] = row["Kernel_Name"]
+            for (disp, ctr), v in per.items():
+                vals[names[disp]][ctr].append(v)
+    copy = next((k for k in vals if "copyBuffer" in k or "copy" in k.lower() and "saga" not in k), None)
+    scale = {}
+    if copy:
+        for ctr, xs in vals[copy].items():
+            avg = sum(xs) / len(xs)
+            if ctr.startswith("FETCH_SIZE") and avg > 0:
+                scale[ctr] = (1 << 30) / (avg * 1024)
+            elif ctr.startswith("WRITE_SIZE") and avg > 0:
+                scale[ctr] = (1 << 30) / (avg * 1024)
+    out = {"copy_kernel": copy, "scale_bytes_per_kib": {k: round(v * 1024, 3) for k, v in scale.items()},
+           "kernels": {}}
+    for kern, ctrs in vals.items():
+        ent = {}
+        for ctr, xs in ctrs.items():
+            avg = sum(xs) / len(xs)
+            ent[ctr] = {"dispatches": len(xs), "avg": round(avg, 3), "min": min(xs), "max": max(xs)}
+            if ctr in scale:
+                ent[ctr]["bytes"] = int(avg * 1024 * scale[ctr])
+        out["kernels"][kern] = ent
+    print(json.dumps(out, indent=1), flush=True)
     return 0
 
 
@@ -278,8 +493,7 @@ def sweep(copies=8):
     grid = []
     for L in (4096, 16384, 65536, 131072):          # lengths x batches, 12Q / 1K / 2V, N = 256
         for b in (1, 8, 32):
-            if b * L <= 32 * 65536:
-                grid.append(("len-batch", b, 12, 1, 2, L, 256))
+            grid.append(("len-batch", b, 12, 1, 2, L, 256))
     for k_h, v_h, q_h in ((1, 2, 12), (1, 4, 12), (2, 2, 12), (2, 4, 12), (1, 8, 16), (2, 8, 16)):
         grid.append(("heads", 8, q_h, k_h, v_h, 16384, 256))   # head groupings
     for N in (64, 256, 1024):
@@ -356,6 +570,7 @@ def main():
     ap.add_argument("--top-n", type=int, default=None)
     ap.add_argument("--no-dense", action="store_true", help="skip the dense-GQA comparator")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-c5", action="store_true", help="skip the 128k SAGA vs dense-GQA attention comparison")
     ap.add_argument("--synthetic-kv", action="store_true", help="fill the caches with N(0,1) instead of a prefill")
     ap.add_argument("--sweep", action="store_true",
                     help="attention kernels alone over a grid of shapes (lengths, batches, head groupings, N) "
@@ -369,9 +584,14 @@ def main():
     ap.add_argument("--prefill", action="store_true",
                     help="measure the prefill attention kernel alone (its own JSON line) instead of decode")
     ap.add_argument("--profile-kernels", action="store_true",
-                    help="only launch K1 (qk_scores) at the workload shape and a 1 GiB device copy, "
-                         "for hardware-counter runs")
+                    help="only launch K1 (qk_scores), the whole Atop-N fast step and the dense decode at the "
+                         "workload shape, then a 1 GiB device copy: for hardware-counter runs")
+    ap.add_argument("--summarize-counters", nargs="+", metavar="DIR",
+                    help="summarize rocprofv3 counter CSVs under DIR(s) per kernel, bytes scaled by the copy "
+                         "dispatches of the same run (no GPU needed)")
     args = ap.parse_args()
+    if args.summarize_counters:
+        return summarize_counters(args.summarize_counters)
     if args.gpus != 1:
         print("bench.py measures one GPU: there is no multi-GPU path (the design shards the "
               "caches by sequence, not built); run with --gpus 1", file=sys.stderr)
@@ -391,7 +611,7 @@ def main():
 
     B, ctx, K, W = args.batch, args.ctx, args.steps, args.warmup
     if args.profile_kernels:
-        return profile_kernels(B, ctx, SAGA_SHAPE)
+        return profile_kernels(B, ctx, SAGA_SHAPE, args.top_n)
     if args.prefill:
         return prefill_bench(ctx, SAGA_SHAPE, no_cpu=args.no_cpu)
     if args.sweep:
@@ -431,11 +651,17 @@ def main():
     k1_gbs = k1_bytes / (k1_us * 1e-6) / 1e9
     attn_us = timed_graph(lambda i: ops.atopn_decode(q4, saga.k_cache[i % s.layers], saga.v_cache[i % s.layers],
                                                      saga.table[i % s.layers], args.top_n, kv_len=kvl,
-                                                     out=saga._attn, k2_variant=args.k2_variant), nlaunch)
-    log(f"K1 qk_scores: {k1_us:.2f} us/launch, {k1_gbs:.0f} GB/s; Atop-N fast attention {attn_us:.2f} us/layer")
+                                                     out=saga._attn, k2_variant=args.k2_variant,
+                                                     workspace=saga.ws["atopn"]), nlaunch)
+    call_bytes, call_vrows = atopn_call_bytes(saga, args.top_n, kvl)
+    call_gbs = call_bytes / (attn_us * 1e-6) / 1e9
+    log(f"K1 qk_scores: {k1_us:.2f} us/launch, {k1_gbs:.0f} GB/s; Atop-N fast attention {attn_us:.2f} us/layer, "
+        f"{call_bytes / 1e6:.1f} MB algorithmic ({call_vrows:.0f} distinct V rows), {call_gbs:.0f} GB/s")
     saga_cache = saga.k_cache.shape, saga.v_cache.shape
     del saga
     torch.cuda.empty_cache()
+    copy_gbs = hbm_copy_gbs()
+    log(f"device copy: {copy_gbs:.0f} GB/s (read + written)")
 
     dense = None
     if not args.no_dense:
@@ -453,11 +679,22 @@ def main():
         del gqa
         torch.cuda.empty_cache()
 
+    c5 = None
+    if not args.no_c5 and args.model == "qwen2.5-1.5b":
+        log("C5: batch 4, 131072 positions, SAGA 1K/2V N=1024 vs dense GQA 2K/2V (attention alone)")
+        c5 = c5_leg()
+        log(f"C5: SAGA {c5['saga_us']} us, dense {c5['dense_us']} us per call -> {c5['speedup']}x")
+
     cpu = None
     if not args.no_cpu:
         log("CPU baseline (oracle, fp32)")
         cpu = cpu_baseline(B, ctx, SAGA_SHAPE, args.top_n, SAGA_SHAPE.layers)
-        log(f"CPU: {cpu['value']} attention tokens/s on {cpu['cores']} cores")
+        gpu_layer = {"C1": c1_gpu_us(), "C3": round(attn_us, 2)}
+        if c5 is not None:
+            gpu_layer["C5"] = c5["saga_us"]
+        cpu["gpu_per_layer_us"] = gpu_layer
+        log(f"CPU: {cpu['value']} attention tokens/s on {cpu['cores']} cores ({cpu['cpu_model']}); per layer "
+            + ", ".join(f"{k} {v['fast_ms_mean']} ms" for k, v in cpu["per_layer"].items()))
 
     traffic, traffic_src = k1_traffic(B, ctx, SAGA_SHAPE)
     out = {
@@ -495,9 +732,22 @@ def main():
             "us_per_launch": round(k1_us, 3),
             "algorithmic_bytes_per_launch": k1_bytes,
         },
+        "attention_call_roofline": {
+            "kernel": "Atop-N fast step, every kernel of one call (saga_atopn_decode)",
+            "bound": "hbm",
+            "achieved": round(call_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(call_gbs / HBM_PEAK_GBS, 4),
+            "us_per_call": round(attn_us, 3),
+            "algorithmic_bytes_per_call": int(call_bytes),
+            "distinct_value_rows_per_call": round(call_vrows, 1),
+        },
+        "hbm_copy_GBs": copy_gbs,
         "attention_us_per_layer": round(attn_us, 2),
         "attention_tokens_per_s_gpu": round(B / (attn_us * 1e-6 * SAGA_SHAPE.layers), 1),
         "dense_gqa": dense,
+        "c5": c5,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -322,15 +322,46 @@ def prefill_attention(query, key, value, attention_mask=None, scaling=None, is_c
     return out
 
 
+def atopn_kept_positions(b: int, q_h: int, k_h: int, L: int, d: int, buf_k: int, workspace: torch.Tensor):
+    """The fast step's kept positions of every row after a call on
+    `workspace`, on the device: int32 [b*q_h, buf_k] in ascending order,
+    padded with -1 past each row's count."""
+    lay = _lib.atopn_layout(b, q_h, k_h, L, d, buf_k)
+    nr, ns, cap = b * q_h, lay.nslice, lay.slice_cap
+    ws = workspace
+    cnt = ws[lay.slice_cnt:lay.slice_cnt + nr * ns * 4].view(torch.int32).reshape(nr, ns).clamp(max=cap)
+    sidx = ws[lay.slice_idx:lay.slice_idx + nr * ns * cap * 4].view(torch.int32).reshape(nr, ns, cap)
+    valid = torch.arange(cap, device=ws.device)[None, None, :] < cnt[:, :, None]
+    rank = torch.cumsum(valid.reshape(nr, -1).to(torch.int32), dim=1).reshape(nr, ns, cap)
+    valid &= rank <= buf_k  # the ordered cap: the first buf_k by position
+    out = torch.full((nr, buf_k), -1, dtype=torch.int32, device=ws.device)
+    dest = (rank - 1).clamp(min=0)
+    rows = torch.arange(nr, device=ws.device)[:, None, None].expand(nr, ns, cap)
+    out[rows[valid], dest[valid]] = sidx[valid]
+    return out
+
+
+def atopn_distinct_value_rows(kept: torch.Tensor, b: int, q_h: int, v_h: int, L: int) -> int:
+    """Distinct V rows a fast step reads: the union of kept positions over the
+    query heads sharing each (batch, value head)."""
+    nr = b * q_h
+    r = torch.arange(nr, device=kept.device)[:, None].expand_as(kept)
+    group = (r // q_h) * v_h + (r % q_h) // (q_h // v_h)
+    valid = kept >= 0
+    key = group[valid].to(torch.int64) * L + kept[valid].to(torch.int64)
+    return int(torch.unique(key).numel())
+
+
 def atopn_workspace_views(b: int, q_h: int, k_h: int, L: int, d: int, buf_k: int, device, fast: bool = True,
-                          workspace=None) -> dict:
+                          workspace=None, rows=None) -> dict:
     """An Atop-N workspace after a call, for inspection (valid until the next
     call on it; default: the cached one of the device's current stream):
     logit thresholds (fast step), kept / passing counts, the selected
     positions and logits in ascending order, and the scores.  The calibration
     step (fast=False) writes its list to sel_idx / sel_val; the fast step
     keeps it in per-slice lists, concatenated here in slice order and cut at
-    buf_k (host copies)."""
+    buf_k (host copies).  rows: only these score rows, as host tensors (for
+    large shapes)."""
     lay = _lib.atopn_layout(b, q_h, k_h, L, d, buf_k)
     dev = _device(device)
     ws = workspace if workspace is not None else \
@@ -349,19 +380,24 @@ def atopn_workspace_views(b: int, q_h: int, k_h: int, L: int, d: int, buf_k: int
         "sel_val": view(lay.sel_val, nr * buf_k, torch.float32).reshape(nr, buf_k),
         "scores": view(lay.scores, nr * lay.scores_ld, torch.float32).reshape(nr, lay.scores_ld)[:, :L],
     }
+    sel = list(range(nr)) if rows is None else [int(r) for r in rows]
+    if rows is not None:
+        ri = torch.tensor(sel, device=ws.device, dtype=torch.int64)
+        out = {k: v.index_select(0, ri).cpu() for k, v in out.items()}
     if fast:
         ns, cap = lay.nslice, lay.slice_cap
-        cnt = view(lay.slice_cnt, nr * ns, torch.int32).reshape(nr, ns).cpu()
-        sidx = view(lay.slice_idx, nr * ns * cap, torch.int32).reshape(nr, ns, cap).cpu()
-        sval = view(lay.slice_val, nr * ns * cap, torch.float32).reshape(nr, ns, cap).cpu()
-        idx = torch.full((nr, buf_k), -1, dtype=torch.int32)
-        val = torch.full((nr, buf_k), float("nan"))
-        for r in range(nr):
-            keep = [min(int(cnt[r, s]), cap) for s in range(ns)]
-            ri = torch.cat([sidx[r, s, :keep[s]] for s in range(ns)])[:buf_k]
-            rv = torch.cat([sval[r, s, :keep[s]] for s in range(ns)])[:buf_k]
-            idx[r, :ri.numel()] = ri
-            val[r, :rv.numel()] = rv
+        ri = torch.tensor(sel, device=ws.device, dtype=torch.int64)
+        cnt = view(lay.slice_cnt, nr * ns, torch.int32).reshape(nr, ns).index_select(0, ri).cpu()
+        sidx = view(lay.slice_idx, nr * ns * cap, torch.int32).reshape(nr, ns, cap).index_select(0, ri).cpu()
+        sval = view(lay.slice_val, nr * ns * cap, torch.float32).reshape(nr, ns, cap).index_select(0, ri).cpu()
+        idx = torch.full((len(sel), buf_k), -1, dtype=torch.int32)
+        val = torch.full((len(sel), buf_k), float("nan"))
+        for j in range(len(sel)):
+            keep = [min(int(cnt[j, s]), cap) for s in range(ns)]
+            rj = torch.cat([sidx[j, s, :keep[s]] for s in range(ns)])[:buf_k]
+            rv = torch.cat([sval[j, s, :keep[s]] for s in range(ns)])[:buf_k]
+            idx[j, :rj.numel()] = rj
+            val[j, :rv.numel()] = rv
         out["sel_idx"], out["sel_val"] = idx, val
     return out
 
