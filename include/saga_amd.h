@@ -192,6 +192,24 @@ int saga_atopn_decode_ex(const saga_tensor* query, const saga_tensor* key, const
                          const float* softmax_threshold, saga_tensor* out, int32_t k2_variant,
                          void* workspace, size_t workspace_bytes, saga_stream_t stream);
 
+/* saga_atopn_decode without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * workspace is a static device array of SAGA_NOALLOC_SCRATCH_BYTES (64 MiB)
+ * inside the library's code object, one copy per GPU, held until the
+ * process ends; its address is looked up once per device (the stream must
+ * be on the current device).  Nothing is allocated or freed.  Shapes whose
+ * saga_atopn_workspace_bytes(b, q_h, k_h, L, d, min(2*top_n, L)) exceed the
+ * scratch return SAGA_ERR_WORKSPACE (the 12/1/2-head d128 decode at batch 8
+ * and 33024 cached positions needs about 41 MB).  Every call on a GPU uses
+ * that GPU's one scratch: calls that may overlap on one GPU (other streams,
+ * other threads) race and give wrong results; order them on one stream.
+ * Results equal saga_atopn_decode's. */
+#define SAGA_NOALLOC_SCRATCH_BYTES (64ull << 20)
+int saga_atopn_decode_noalloc(const saga_tensor* query, const saga_tensor* key, const saga_tensor* value,
+                              const saga_tensor* mask, const int32_t* kv_len, float scale, int64_t top_n,
+                              const float* softmax_threshold, saga_tensor* out, saga_stream_t stream);
+
 /* Atop-N calibration step: full softmax statistics, exact top-k
  * (k = min(top_n, L), radix select; equal values: lower index first),
  * stores the k-th largest probability per row into softmax_threshold_out

@@ -64,6 +64,7 @@ _SIGS = {
     "saga_atopn_decode": (ctypes.c_int, [_T, _T, _T, _T, _P, ctypes.c_float, _I64, _P, _T, _P, ctypes.c_size_t, _P]),
     "saga_atopn_decode_ex": (ctypes.c_int, [_T, _T, _T, _T, _P, ctypes.c_float, _I64, _P, _T, ctypes.c_int32, _P,
                                             ctypes.c_size_t, _P]),
+    "saga_atopn_decode_noalloc": (ctypes.c_int, [_T, _T, _T, _T, _P, ctypes.c_float, _I64, _P, _T, _P]),
     "saga_atopn_calibrate": (ctypes.c_int, [_T, _T, _T, _T, _P, ctypes.c_float, _I64, _P, _T, _P, ctypes.c_size_t, _P]),
     "saga_dense_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I64]),
     "saga_dense_decode": (ctypes.c_int, [_T, _T, _T, _T, _P, ctypes.c_float, _T, _P, ctypes.c_size_t, _P]),
@@ -80,6 +81,7 @@ _SIGS = {
 }
 GEMV_STORE, GEMV_ADD, GEMV_SILU_PAIRS = 0, 1, 2
 K2_AUTO, K2_ROW_BLOCK, K2_SLICE_ROW = 0, 1, 2
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 _lock = threading.Lock()
 _lib = None

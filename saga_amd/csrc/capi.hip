@@ -6,11 +6,18 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <mutex>
 
 #include "../../include/saga_amd.h"
 #include "kernels.h"
 
 using namespace saga;
+
+// Scratch of saga_atopn_decode_noalloc: one copy per GPU, part of the code
+// object, held until the process ends.  On the host this name is only a
+// stand-in for the device copy: kernels and copies use the device address
+// from hipGetSymbolAddress (scratch_ptr below), never the name itself.
+static __device__ __align__(256) unsigned char scratch[SAGA_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -358,6 +365,36 @@ int rows_of(const saga_tensor* t, const char* name, int64_t* rows, int64_t* ld) 
   return SAGA_OK;
 }
 
+// Device address of `scratch` on the current device, looked up once per
+// device with that device current (each GPU holds its own copy at its own
+// address).  Returns SAGA_OK and sets *out, or an error code.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_ptr(hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(SAGA_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(SAGA_ERR_UNSUPPORTED, "device %d out of range", dev);
+  if (stream) {
+    int sdev = -1;
+    e = hipStreamGetDevice(stream, &sdev);
+    if (e != hipSuccess) return fail(SAGA_ERR_HIP, "hipStreamGetDevice: %s", hipGetErrorString(e));
+    if (sdev != dev)
+      return fail(SAGA_ERR_INVALID, "stream is on device %d, the current device is %d: make it current", sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return fail(SAGA_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SAGA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -523,6 +560,28 @@ int saga_atopn_decode_ex(const saga_tensor* query, const saga_tensor* key, const
                          size_t workspace_bytes, saga_stream_t stream) {
   return atopn_run(false, query, key, value, mask, kv_len, scale, top_n, softmax_threshold, nullptr, out, k2_variant,
                    workspace, workspace_bytes, stream);
+}
+
+int saga_atopn_decode_noalloc(const saga_tensor* query, const saga_tensor* key, const saga_tensor* value,
+                              const saga_tensor* mask, const int32_t* kv_len, float scale, int64_t top_n,
+                              const float* softmax_threshold, saga_tensor* out, saga_stream_t stream) {
+  // the scratch bound first: a shape whose workspace exceeds it is refused
+  // before anything is looked up or launched
+  Shape s{};
+  int rc;
+  if ((rc = check_qk(query, key, mask, &s)) || (rc = check_v(value, &s)) || (rc = check_out(out, s))) return rc;
+  if (top_n < 1) return fail(SAGA_ERR_INVALID, "top_n must be >= 1, got %lld", (long long)top_n);
+  const int64_t buf_k = top_n < (s.L + 1) / 2 ? 2 * top_n : s.L;
+  if (!atopn_sizes_ok(s.b, s.q_h, s.k_h, s.L, s.d, buf_k)) return fail(SAGA_ERR_UNSUPPORTED, "workspace too large");
+  saga_atopn_layout lay;
+  atopn_layout(s.b, s.q_h, s.k_h, s.L, s.d, buf_k, &lay);
+  if (lay.total_bytes > static_cast<int64_t>(SAGA_NOALLOC_SCRATCH_BYTES))
+    return fail(SAGA_ERR_WORKSPACE, "this shape needs %lld bytes of scratch; the static scratch holds %lld",
+                (long long)lay.total_bytes, (long long)SAGA_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if ((rc = scratch_ptr(static_cast<hipStream_t>(stream), &ws))) return rc;
+  return atopn_run(false, query, key, value, mask, kv_len, scale, top_n, softmax_threshold, nullptr, out, kK2Auto, ws,
+                   SAGA_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int saga_atopn_calibrate(const saga_tensor* query, const saga_tensor* key, const saga_tensor* value,

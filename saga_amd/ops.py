@@ -231,6 +231,26 @@ def atopn_decode(query, key, value, softmax_threshold, top_n, attention_mask=Non
     return out
 
 
+def atopn_decode_noalloc(query, key, value, softmax_threshold, top_n, attention_mask=None, scaling=None, kv_len=None,
+                         out=None):
+    """atopn_decode on the library's static per-GPU scratch
+    (saga_atopn_decode_noalloc): no workspace is allocated or passed, so the
+    call allocates nothing when `out` is given.  Calls that may overlap on
+    one GPU race on that scratch; shapes whose workspace exceeds it raise."""
+    dev, query, key, value, mask = _decode_prep(query, key, value, attention_mask, kv_len)
+    b, q_h, _, d = query.shape
+    if softmax_threshold.dtype != torch.float32 or not softmax_threshold.is_contiguous() \
+            or softmax_threshold.numel() < b * q_h:
+        raise ValueError("saga_amd: softmax_threshold must be contiguous fp32 with b*q_h entries")
+    if out is None:
+        out = torch.empty(b, q_h, 1, d, dtype=query.dtype, device=dev)
+    _lib.check(_lib.load().saga_atopn_decode_noalloc(
+        _lib.tensor(query), _lib.tensor(key), _lib.tensor(value), _lib.tensor(mask), _lib.ptr(_kv_len(kv_len)),
+        _scale(query, scaling), int(top_n), _lib.ptr(softmax_threshold), _lib.tensor(out), _lib.stream_of(query)),
+        "atopn_decode_noalloc")
+    return out
+
+
 def atopn_calibrate(query, key, value, top_n, threshold_out, attention_mask=None, scaling=None, kv_len=None,
                     out=None, out_dtype=None, workspace=None):
     """Atop-N calibration step (attention/attention.py:173-189).
