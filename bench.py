@@ -215,7 +215,7 @@ def hbm_copy_gbs(nbytes=1 << 30, reps=10):
     return round(2 * nbytes / us / 1e3, 1)
 
 
-def atopn_call_bytes(model, top_n, kvl):
+def atopn_call_bytes(model, top_n, kvl, k2_variant=0):
     """Algorithmic bytes of one fast-step call at the decoder's state,
     averaged over its layers: K (b * k_h * kv_len * d * 2) + the distinct V
     rows selected per (batch row, value head) * d * 2 + Q and O + the
@@ -230,7 +230,7 @@ def atopn_call_bytes(model, top_n, kvl):
     rows = 0
     for l in range(s.layers):
         ops.atopn_decode(q4, model.k_cache[l], model.v_cache[l], model.table[l], top_n, kv_len=kvl, out=model._attn,
-                         workspace=ws)
+                         workspace=ws, k2_variant=k2_variant)
         kept = ops.atopn_kept_positions(B, s.n_q, s.n_k, L, s.head_dim, buf_k, ws)
         rows += ops.atopn_distinct_value_rows(kept, B, s.n_q, s.n_v, L)
     torch.cuda.synchronize()
@@ -239,7 +239,7 @@ def atopn_call_bytes(model, top_n, kvl):
     return B * s.n_k * kv * d2 + vrows * d2 + 2 * B * s.n_q * d2 + 4 * B * s.n_q, vrows
 
 
-def c5_leg(copies=4, b=4, q_h=12, L=131072, N=1024, d=128):
+def c5_leg(copies=4, b=4, q_h=12, L=131072, N=1024, d=128, k2_variant=0):
     """Attention alone at the 128k comparison shape: SAGA (1 key / 2 value
     heads, Atop-N N=1024: calibrated on q, timed on a nearby q2) against
     dense GQA (2 key / 2 value heads) on the same seeded N(0,1) caches,
@@ -260,10 +260,10 @@ def c5_leg(copies=4, b=4, q_h=12, L=131072, N=1024, d=128):
     for i in range(copies):
         ops.atopn_calibrate(q, ks[i], vd[i], N, tabs[i], out=out, workspace=wsa)
     saga_us = timed_graph(lambda i: ops.atopn_decode(q2, ks[i % copies], vd[i % copies], tabs[i % copies], N, out=out,
-                                                     workspace=wsa), 2 * copies)
+                                                     workspace=wsa, k2_variant=k2_variant), 2 * copies)
     dense_us = timed_graph(lambda i: ops.dense_decode(q2, kd[i % copies], vd[i % copies], out=out, workspace=wsd),
                            2 * copies)
-    ops.atopn_decode(q2, ks[0], vd[0], tabs[0], N, out=out, workspace=wsa)
+    ops.atopn_decode(q2, ks[0], vd[0], tabs[0], N, out=out, workspace=wsa, k2_variant=k2_variant)
     kept = ops.atopn_kept_positions(b, q_h, 1, L, d, min(2 * N, L), wsa)
     vrows = ops.atopn_distinct_value_rows(kept, b, q_h, 2, L)
     torch.cuda.synchronize()
@@ -480,7 +480,7 @@ def prefill_bench(ctx, shape, reps=10, no_cpu=False):
     return 0
 
 
-def sweep(copies=8):
+def sweep(copies=8, k2_variant=0):
     """Attention-only timings on synthetic bf16 caches: every shape is timed
     as a graph of 2 x `copies` launches cycling over `copies` distinct K/V
     caches (the same cache in a row would sit in the 256 MB Infinity Cache).
@@ -522,17 +522,20 @@ def sweep(copies=8):
             tabs = [torch.zeros(b * q_h, device=dev) for _ in range(ncp)]
             for i in range(ncp):
                 ops.atopn_calibrate(q, ks[i], vs[i], N, tabs[i])
-            us = timed_graph(lambda i: ops.atopn_decode(q2, ks[i % ncp], vs[i % ncp], tabs[i % ncp], N, out=out),
-                             2 * ncp)
+            us = timed_graph(lambda i: ops.atopn_decode(q2, ks[i % ncp], vs[i % ncp], tabs[i % ncp], N, out=out,
+                                                        k2_variant=k2_variant), 2 * ncp)
             k1 = timed_graph(lambda i: ops.qk_scores(q2, ks[i % ncp], with_partials=True), 2 * ncp)
-            ops.atopn_decode(q2, ks[0], vs[0], tabs[0], N, out=out)
-            torch.cuda.synchronize()
-            cnt = ops.atopn_workspace_views(b, q_h, k_h, L, 128, min(2 * N, L), dev)["sel_cnt"]
-            sel = int(cnt.sum())
-            byts = kv_bytes + sel * 256
+            ws = ops.workspace(torch.device(dev, torch.cuda.current_device()), "atopn",
+                               ops.atopn_workspace_bytes(b, q_h, k_h, L, 128, N))
+            ops.atopn_decode(q2, ks[0], vs[0], tabs[0], N, out=out, k2_variant=k2_variant, workspace=ws)
+            kept = ops.atopn_kept_positions(b, q_h, k_h, L, 128, min(2 * N, L), ws)
+            sel = int((kept >= 0).sum())
+            vrows = ops.atopn_distinct_value_rows(kept, b, q_h, v_h, L)
+            byts = kv_bytes + vrows * 256 + 2 * b * q_h * 256 + 4 * b * q_h
             line = {"sweep": tag, "b": b, "q_h": q_h, "k_h": k_h, "v_h": v_h, "L": L, "N": N, "kernel": "atopn",
                     "us": round(us, 2), "k1_us": round(k1, 2), "k1_GBs": round(kv_bytes / k1 / 1e3, 1),
-                    "selected_per_row": round(sel / (b * q_h), 1), "GBs": round(byts / us / 1e3, 1)}
+                    "selected_per_row": round(sel / (b * q_h), 1), "distinct_value_rows": vrows,
+                    "GBs": round(byts / us / 1e3, 1), "frac": round(byts / us / 1e3 / HBM_PEAK_GBS, 4)}
         print(json.dumps(line), flush=True)
         del ks, vs
         torch.cuda.empty_cache()
@@ -615,7 +618,7 @@ def main():
     if args.prefill:
         return prefill_bench(ctx, SAGA_SHAPE, no_cpu=args.no_cpu)
     if args.sweep:
-        return sweep()
+        return sweep(k2_variant=args.k2_variant)
     max_len = ctx + K
     torch.manual_seed(0)
     prompt = torch.randint(0, SAGA_SHAPE.vocab, (ctx,), dtype=torch.int64)
@@ -653,7 +656,7 @@ def main():
                                                      saga.table[i % s.layers], args.top_n, kv_len=kvl,
                                                      out=saga._attn, k2_variant=args.k2_variant,
                                                      workspace=saga.ws["atopn"]), nlaunch)
-    call_bytes, call_vrows = atopn_call_bytes(saga, args.top_n, kvl)
+    call_bytes, call_vrows = atopn_call_bytes(saga, args.top_n, kvl, args.k2_variant)
     call_gbs = call_bytes / (attn_us * 1e-6) / 1e9
     log(f"K1 qk_scores: {k1_us:.2f} us/launch, {k1_gbs:.0f} GB/s; Atop-N fast attention {attn_us:.2f} us/layer, "
         f"{call_bytes / 1e6:.1f} MB algorithmic ({call_vrows:.0f} distinct V rows), {call_gbs:.0f} GB/s")
@@ -682,7 +685,7 @@ def main():
     c5 = None
     if not args.no_c5 and args.model == "qwen2.5-1.5b":
         log("C5: batch 4, 131072 positions, SAGA 1K/2V N=1024 vs dense GQA 2K/2V (attention alone)")
-        c5 = c5_leg()
+        c5 = c5_leg(k2_variant=args.k2_variant)
         log(f"C5: SAGA {c5['saga_us']} us, dense {c5['dense_us']} us per call -> {c5['speedup']}x")
 
     cpu = None

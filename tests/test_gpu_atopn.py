@@ -346,6 +346,55 @@ def test_row_block_k2_matches_slice_and_row_kernels(name):
     print(f"  mean_count={v1['sel_cnt'].mean():.1f} max={v1['sel_cnt'].max()}", flush=True)
 
 
+@pytest.mark.parametrize("L", [700, 2048, 5000])
+def test_recency_heavy_rows(L):
+    """Rows whose last slice keeps hundreds of positions (keys of the last
+    600 positions aligned with the queries; at L = 700 every row overflows
+    buf_k inside its only slice): the long lists go to the row kernel's
+    gathers.  Both K2 shapes give identical lists, counts and thresholds,
+    outputs equal to fp32 rounding and to the oracle on the same selection,
+    and the same bits twice in a row."""
+    rng = np.random.default_rng(L)
+    b, q_h, k_h, v_h, d, N = 4, 12, 1, 2, 128, 256
+    q = O.round_bf16(rng.standard_normal((b, q_h, 1, d), dtype=np.float32))
+    k = O.round_bf16(rng.standard_normal((b, k_h, L, d), dtype=np.float32) * np.float32(0.3))
+    k[:, :, max(0, L - 600):, :] += O.round_bf16(q.mean(axis=1, keepdims=True)[:, :, 0:1, :] * np.float32(1.0))
+    k = O.round_bf16(k)
+    v = O.round_bf16(rng.standard_normal((b, v_h, L, d), dtype=np.float32))
+    qd, kd, vd = dev(q, "bf16"), dev(k, "bf16"), dev(v, "bf16")
+    table = torch.full((b * q_h,), 5e-4, device="cuda")
+    buf_k = min(2 * N, L)
+    res = {}
+    for variant in (2, 1, 1):
+        out = host(_run_fast(qd, kd, vd, table, N, k2_variant=variant))
+        views = _views(b, q_h, k_h, L, d, buf_k, scores_of=(qd, kd, None, None, None))
+        _check_selection_rule(views, b * q_h, L, buf_k)
+        if variant in res:
+            np.testing.assert_array_equal(out, res[variant][0])  # deterministic
+        res[variant] = (out, views)
+    (o2, v2), (o1, v1) = res[2], res[1]
+    for key in ("sel_cnt", "sel_total", "sel_idx", "thresh"):
+        np.testing.assert_array_equal(v1[key], v2[key])
+    nan = np.isnan(o2)
+    np.testing.assert_array_equal(np.isnan(o1), nan)
+    assert rel_l2(o1[~nan], o2[~nan]) < 1e-6
+    last = (L - 1) // 1024
+    heavy = sum(int((v1["sel_idx"][r, :v1["sel_cnt"][r]] >= 1024 * last).sum()) > 64 for r in range(b * q_h))
+    assert heavy > 0, "the case must have rows whose last slice keeps more than 64 positions"
+    logits = O.qk_scores(q, k).reshape(b * q_h, L)
+    for r in range(b * q_h):
+        n = v1["sel_cnt"][r]
+        if n == 0:
+            assert np.isnan(o1.reshape(b * q_h, d)[r]).all()
+            continue
+        sel = v1["sel_idx"][r, :n]
+        vh = (r % q_h) // (q_h // v_h)
+        ref = O.gather_output(logits[r, sel][None, None, None, :], sel[None, None, None, :].astype(np.int64),
+                              v[r // q_h:r // q_h + 1, vh:vh + 1], (1, 1, 1, d), input_is_logits=True)
+        assert rel_l2(o1.reshape(b * q_h, d)[r], ref.reshape(d)) < 1e-5, r
+    print(f"  rows with a heavy last slice: {heavy}, mean kept {v1['sel_cnt'].mean():.1f}", flush=True)
+
+
 def test_k2_variant_rejects_other_values():
     rng = np.random.default_rng(5)
     (_, _, _), (qd, kd, vd) = qkv(rng, 1, 12, 1, 2, 128, 256, "bf16")
