@@ -84,16 +84,19 @@ def timed_graph(fn, n_launch, repeats=3):
 
 def k1_traffic(batch, ctx, shape):
     """HBM bytes per K1 launch from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE passes (profiles/k1_qk_scores_*_traffic.json), when they were
-    taken at this workload; else None."""
+    WRITE_SIZE passes (profiles/*_counters.json, written by
+    --summarize-counters), when they were taken at this workload; else None."""
     import glob
-    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "k1_qk_scores_*_traffic.json"))):
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*_counters.json"))):
         with open(path) as f:
             d = json.load(f)
-        w = d.get("workload", {})
-        if (w.get("batch"), w.get("ctx"), w.get("n_q"), w.get("n_k"), w.get("head_dim")) == \
+        w = d.get("workload") or {}
+        if (w.get("batch"), w.get("ctx"), w.get("n_q"), w.get("n_k"), w.get("head_dim")) != \
                 (batch, ctx, shape.n_q, shape.n_k, shape.head_dim):
-            return int(d["traffic_bytes_per_launch"]), os.path.relpath(path, ROOT)
+            continue
+        for kern, ent in d["kernels"].items():
+            if kern.startswith("void saga::qk_scores_kernel<1, %d>" % shape.head_dim) and "traffic_bytes_per_launch" in ent:
+                return int(ent["traffic_bytes_per_launch"]), os.path.relpath(path, ROOT)
     return None, None
 
 
@@ -346,15 +349,29 @@ def profile_kernels(batch, ctx, shape, top_n, launches=8):
     return 0
 
 
-def summarize_counters(paths):
+def summarize_counters(paths, workload=None):
     """Per-kernel averages of the rocprofv3 counter CSVs (*counter_collection.csv)
-    under `paths`, each counter scaled by the known bytes of the 1 GiB copy
-    dispatches in the same run (FETCH_SIZE / WRITE_SIZE are in KiB)."""
+    under `paths` (one directory per --pmc pass of `bench.py --profile-kernels`;
+    a path ending in .log is that run's output, whose JSON line names the
+    workload and its algorithmic bytes).
+    FETCH_SIZE and WRITE_SIZE (KiB per dispatch) are scaled by what the same
+    counter reads on the 1 GiB device-to-device copies of the same run (the
+    __amd_rocclr_copyBuffer dispatches of at least half the largest reading):
+    bytes = KiB * 1024 * (2^30 B / (copy reading * 1024)).  traffic = scaled
+    FETCH + scaled WRITE.  Other counters are averaged as read."""
     import csv
     import glob
     from collections import defaultdict
     vals = defaultdict(lambda: defaultdict(list))  # kernel -> counter -> per-dispatch values
     for p in paths:
+        if p.endswith(".log"):  # the --profile-kernels output: its JSON line names the workload
+            with open(p) as fh:
+                for line in fh:
+                    if line.startswith('{"launches"'):
+                        w = json.loads(line)
+                        workload = {"batch": w["batch"], "ctx": w["kv_len"] - 1, **{k: w[k] for k in w if k not in (
+                            "batch", "launches", "copy_launches", "copy_bytes_read", "copy_bytes_written")}}
+            continue
         files = glob.glob(os.path.join(p, "**", "*counter_collection.csv"), recursive=True) if os.path.isdir(p) else [p]
         for f in files:
             per = defaultdict(float)
@@ -366,24 +383,25 @@ def summarize_counters(paths):
                     names[row["Dispatch_Id"]] = row["Kernel_Name"]
             for (disp, ctr), v in per.items():
                 vals[names[disp]][ctr].append(v)
-    copy = next((k for k in vals if "copyBuffer" in k or "copy" in k.lower() and "saga" not in k), None)
+    copy = "__amd_rocclr_copyBuffer"
     scale = {}
-    if copy:
-        for ctr, xs in vals[copy].items():
-            avg = sum(xs) / len(xs)
-            if ctr.startswith("FETCH_SIZE") and avg > 0:
-                scale[ctr] = (1 << 30) / (avg * 1024)
-            elif ctr.startswith("WRITE_SIZE") and avg > 0:
-                scale[ctr] = (1 << 30) / (avg * 1024)
-    out = {"copy_kernel": copy, "scale_bytes_per_kib": {k: round(v * 1024, 3) for k, v in scale.items()},
-           "kernels": {}}
-    for kern, ctrs in vals.items():
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        xs = vals.get(copy, {}).get(ctr, [])
+        big = [x for x in xs if xs and x >= 0.5 * max(xs)]
+        if big and max(big) > 0:
+            scale[ctr] = (1 << 30) / (sum(big) / len(big) * 1024)
+    out = {"workload": workload, "copy_kernel": f"{copy}, 1 GiB read + 1 GiB written per dispatch",
+           "bytes_per_counter_kib": {k: round(v * 1024, 3) for k, v in scale.items()}, "kernels": {}}
+    for kern, ctrs in sorted(vals.items()):
+        if "saga::" not in kern:
+            continue
         ent = {}
-        for ctr, xs in ctrs.items():
-            avg = sum(xs) / len(xs)
-            ent[ctr] = {"dispatches": len(xs), "avg": round(avg, 3), "min": min(xs), "max": max(xs)}
-            if ctr in scale:
-                ent[ctr]["bytes"] = int(avg * 1024 * scale[ctr])
+        for ctr, xs in sorted(ctrs.items()):
+            ent[ctr] = {"dispatches": len(xs), "avg": round(sum(xs) / len(xs), 3), "min": min(xs), "max": max(xs)}
+        if all(c in ent and c in scale for c in ("FETCH_SIZE", "WRITE_SIZE")):
+            ent["fetch_bytes"] = int(ent["FETCH_SIZE"]["avg"] * 1024 * scale["FETCH_SIZE"])
+            ent["write_bytes"] = int(ent["WRITE_SIZE"]["avg"] * 1024 * scale["WRITE_SIZE"])
+            ent["traffic_bytes_per_launch"] = ent["fetch_bytes"] + ent["write_bytes"]
         out["kernels"][kern] = ent
     print(json.dumps(out, indent=1), flush=True)
     return 0

@@ -310,6 +310,8 @@ K2_SHAPES = dict(K2_BASE_SHAPES, **{  # + long slice lists; lists past one LDS b
     "b4_long_lists": (4, 12, 1, 2, 128, 20000, 1024, "bf16"),
     "b2_buf4096": (2, 12, 1, 2, 128, 20000, 2048, "bf16"),
     "b1_70k": (1, 12, 1, 2, 128, 70000, 256, "bf16"),
+    "b2_g1": (2, 4, 4, 2, 128, 5000, 128, "bf16"),  # one query head per key head
+    "b3_g2_d64": (3, 8, 4, 4, 64, 3000, 64, "f16"),
 })
 
 
