@@ -34,7 +34,9 @@ def test_decoder_graph_survives_cache_growth():
     shape = DecoderShape(layers=2, hidden=256, n_q=4, n_k=1, n_v=2, head_dim=64, intermediate=512, vocab=1024,
                          rope_theta=1e4, eps=1e-6, qkv_bias=True)
     m = SagaDecoder(shape, batch=2, max_len=700, mode="atopn", top_n=16)
-    m.prefill(torch.randint(0, 1024, (600,)))
+    # a seeded prompt: the test does not depend on the global RNG state that
+    # earlier tests leave behind
+    m.prefill(torch.randint(0, 1024, (600,), generator=torch.Generator().manual_seed(11)))
     m.capture()
 
     def run():
@@ -59,7 +61,9 @@ def test_decoder_graph_survives_cache_growth():
     toks1, logits1 = run()
     assert _untouched(bufs)
     assert torch.equal(toks0, toks1)
-    assert torch.equal(logits0, logits1)
+    # bit-identical replays (a step whose rows pass no position gives NaN, as
+    # the reference's softmax over an empty selection does)
+    torch.testing.assert_close(logits0, logits1, rtol=0, atol=0, equal_nan=True)
 
 
 def test_cached_workspace_replaced_under_a_captured_graph_stays_alive():
