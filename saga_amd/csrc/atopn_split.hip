@@ -128,12 +128,18 @@ __device__ __forceinline__ void load_row_partials(const FusedSelParams& p, int r
   const float* prow_m = p.pmax + static_cast<int64_t>(r) * p.nparts;
   const float* prow_s = p.psum + static_cast<int64_t>(r) * p.nparts;
   const float* prow_t = p.ptail + static_cast<int64_t>(r) * p.nparts;
+  // unconditional loads (index clamped into the row, nparts >= 1), selected
+  // after they return: a load under a branch is waited for at the branch's
+  // join, which would hold back every later load of the wave (the scores)
+  // by one round trip
 #pragma unroll
   for (int k = 0; k < kSlicePrefetch; ++k) {
     const int c = lane + k * kWave;
-    rp.pm[k] = c < p.nparts ? prow_m[c] : kNegInf;
-    rp.ps[k] = c < p.nparts ? prow_s[c] : 0.f;
-    rp.pt[k] = c < p.nparts ? prow_t[c] : kNegInf;
+    const int cc = min(c, p.nparts - 1);
+    const float vm = prow_m[cc], vs = prow_s[cc], vt = prow_t[cc];
+    rp.pm[k] = c < p.nparts ? vm : kNegInf;
+    rp.ps[k] = c < p.nparts ? vs : 0.f;
+    rp.pt[k] = c < p.nparts ? vt : kNegInf;
   }
   rp.pstar = p.pstar[r];
 }

@@ -25,8 +25,9 @@ namespace saga {
 constexpr int kGemvUnroll = 12;  // 32-wide k steps in flight per wave (K = 1536 over 4 waves: one burst)
 constexpr int kSplitBatch = 8;   // split-K partial sums in flight per epilogue thread
 
-// Epilogue inputs of one lane, loaded before the weight burst (as loads they
-// return with it; after the reduction each would cost one more round trip):
+// Epilogue inputs of one lane, loaded right behind the first weight burst (as
+// loads they return with it; after the reduction each would cost one more
+// round trip):
 // the residual of output rows n..n+3 of token row m (SAGA_GEMV_ADD), and the
 // bias, position and batch row of the fused q/k/v projection (kGemvRopeKV).
 // Absent inputs read a valid dummy address instead of branching (a load under
@@ -83,7 +84,6 @@ gemv_kernel(GemvParams p) {
   // the tile this wave finishes (waves 0..TPW-1) and its epilogue inputs
   const int tf = w < TPW ? w : TPW - 1;
   const int nf = n0 + 16 * tf + 4 * s;
-  const GemvPre pre = gemv_prefetch<EPI>(p, m, nf, wrow[0]);
   const int steps = p.K / 32;
   // this workgroup's k steps [k0, k1), dealt to its waves round robin (wave
   // w: k0 + w, k0 + w + WAVES, ...): at any moment the workgroup's waves
@@ -98,16 +98,19 @@ gemv_kernel(GemvParams p) {
 #pragma unroll
   for (int t = 0; t < TPW; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   float ssq = 0.f;
-  for (int i0 = 0; i0 < nmine; i0 += UNROLL) {
-    u32x4 a[UNROLL][TPW], b[UNROLL];
+  // one burst: every k step of [i0, i0 + UNROLL) of the wave (steps past its
+  // share repeat its last one, clamped into the workgroup's range: a wave
+  // with no step loads valid addresses it never uses)
+  auto load_burst = [&](int i0, u32x4 (&a)[UNROLL][TPW], u32x4 (&b)[UNROLL]) {
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
-      const int jj = jbase + jstride * min(i0 + u, nmine - 1);
+      const int jj = min(max(jbase + jstride * min(i0 + u, nmine - 1), k0), k1 - 1);
 #pragma unroll
       for (int t = 0; t < TPW; ++t) a[u][t] = ld16(wrow[t] + static_cast<int64_t>(jj) * wstep);
       b[u] = mvalid ? ld16(xrow + static_cast<int64_t>(jj) * 64) : u32x4{0u, 0u, 0u, 0u};
     }
-    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto use_burst = [&](int i0, const u32x4 (&a)[UNROLL][TPW], const u32x4 (&b)[UNROLL]) {
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
       if (i0 + u < nmine) {
@@ -121,6 +124,25 @@ gemv_kernel(GemvParams p) {
         }
       }
     }
+  };
+  // The first burst (the only one for waves of at most UNROLL k steps: every
+  // decode projection of K <= 1536 and every split-K range), then the
+  // epilogue inputs.  Issued behind the burst they return right after it
+  // (loads return in order); issued ahead of a loop they would be waited for
+  // at its header, before the burst.
+  GemvPre pre;
+  {
+    u32x4 a[UNROLL][TPW], b[UNROLL];
+    load_burst(0, a, b);
+    pre = gemv_prefetch<EPI>(p, m, nf, wrow[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    use_burst(0, a, b);
+  }
+  for (int i0 = UNROLL; i0 < nmine; i0 += UNROLL) {
+    u32x4 a[UNROLL][TPW], b[UNROLL];
+    load_burst(i0, a, b);
+    __builtin_amdgcn_sched_barrier(0);
+    use_burst(i0, a, b);
   }
   // lane (col, s): rows n0 + 16t + 4s + r of tile t for token row m = col
 #pragma unroll
