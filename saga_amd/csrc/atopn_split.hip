@@ -19,7 +19,8 @@
 //      ballots and mbcnt put every passing element at its rank in ascending
 //      position order; the slice's list and count go to the workspace;
 //   3. a list of at most kSliceSmall entries (the usual case) is gathered by
-//      the wave itself in one burst: its (m, l, o) softmax . V partial.
+//      the wave itself, 48 V rows per burst (a second burst only for the
+//      slices of a peaked head): its (m, l, o) softmax . V partial.
 // Row blocks (atopn_gather_kernel), one block per row (256 threads when buf_k
 // <= 1024, else 1024): a block scan
 // of the slice counts ranks the slices; exactly the first n = min(total,
@@ -49,7 +50,7 @@ constexpr int kRowSmallCap = 1024;
 constexpr int kRowBatch = 2048;                       // list entries per LDS batch
 constexpr int kRowMaxSlices = 2048;                   // slice ranks kept in LDS
 constexpr int kRowUnroll = 16;                        // V rows in flight per lane group
-constexpr int kWaveUnroll = 16;                       // slice wave: 4 groups x 16 = 64 V rows in flight
+constexpr int kWaveUnroll = 12;                       // slice wave: 4 groups x 12 = 48 V rows in flight
 constexpr int kRowMergeSlices = 8;                    // slice partials per merge thread in one burst
 // auto mode: one block per row when a row has at most this many slices and
 // its list fits one LDS batch (measured on MI355X, attention call at b1-b32,
@@ -59,7 +60,8 @@ constexpr int kRowMergeSlices = 8;                    // slice partials per merg
 constexpr int kRowBlockAutoSlices = 12;
 
 static_assert(kSliceLen == kSliceLoads * 4 * kWave, "slice = whole f32x4 loads of every lane");
-static_assert(kSliceSmall == 4 * kWaveUnroll, "a small slice list is one gather burst of its wave");
+static_assert(kSliceSmall % (4 * kWaveUnroll) == 0 && kSliceSmall <= 2 * kWave,
+              "a short slice list is whole gather bursts of its wave, at most two entries per lane");
 
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -67,41 +69,50 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// One wave's softmax . V over n <= kSliceSmall entries (one burst): 4 lane
+// One wave's softmax . V over n <= kSliceSmall entries, in bursts of 48 V
+// rows (one for the usual short list, two for a peaked head's): 4 lane
 // groups of 16 lanes, lane c of group G owns dims [c*DPL, c*DPL + DPL) and
 // loads the rows G, G+4, ...; weights are relative to the list's max m.
-// Writes o (unnormalised, D floats) and returns (m, l) in every lane.
+// The bursts reuse the same registers (a second burst costs a round trip,
+// not occupancy: 7 waves per SIMD at d128).  Writes o (unnormalised, D floats) and returns (m, l) in
+// every lane.
 template <int DT, int D>
 __device__ void wave_pv_small(int n, const int* sidx, const float* sval, const char* vbase, int64_t vrow,
                               float* scratch, float* o, float& m, float& l) {
   using PV = BlockPV<DT, D>;
   constexpr int DPL = D / 16;
+  constexpr int BURST = 4 * kWaveUnroll;
   const int lane = threadIdx.x & 63, G = lane >> 4, c = lane & 15;
-  const float xv = lane < n ? sval[lane] : kNegInf;
-  m = wave_max(xv);
-  l = wave_sum(lane < n ? __expf(xv - m) : 0.f);
+  const float x0 = lane < n ? sval[lane] : kNegInf;
+  const float x1 = lane + kWave < n ? sval[lane + kWave] : kNegInf;
+  m = wave_max(fmaxf(x0, x1));
+  l = wave_sum((lane < n ? __expf(x0 - m) : 0.f) + (lane + kWave < n ? __expf(x1 - m) : 0.f));
   float acc[DPL];
 #pragma unroll
   for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
   const char* vb = vbase + static_cast<int64_t>(c) * PV::BYTES;
-  u32x4 raw[kWaveUnroll][PV::NV];
+  auto burst = [&](int e0) {
+    u32x4 raw[kWaveUnroll][PV::NV];
 #pragma unroll
-  for (int u = 0; u < kWaveUnroll; ++u) {
-    const int e = G + 4 * u;
-    if (e < n) PV::load_raw(vb + static_cast<int64_t>(sidx[e]) * vrow, raw[u]);
-  }
-  __builtin_amdgcn_sched_barrier(0);  // all gathers in flight before the FMAs
-#pragma unroll
-  for (int u = 0; u < kWaveUnroll; ++u) {
-    const int e = G + 4 * u;
-    if (e < n) {
-      const float w = __expf(sval[e] - m);
-      float f[DPL];
-      PV::unpack(raw[u], f);
-#pragma unroll
-      for (int i = 0; i < DPL; ++i) acc[i] += w * f[i];
+    for (int u = 0; u < kWaveUnroll; ++u) {
+      const int e = e0 + G + 4 * u;
+      if (e < n) PV::load_raw(vb + static_cast<int64_t>(sidx[e]) * vrow, raw[u]);
     }
-  }
+    __builtin_amdgcn_sched_barrier(0);  // all gathers of the burst in flight before the FMAs
+#pragma unroll
+    for (int u = 0; u < kWaveUnroll; ++u) {
+      const int e = e0 + G + 4 * u;
+      if (e < n) {
+        const float w = __expf(sval[e] - m);
+        float f[DPL];
+        PV::unpack(raw[u], f);
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) acc[i] += w * f[i];
+      }
+    }
+  };
+  burst(0);
+  if (n > BURST) burst(BURST);  // wave-uniform
   // the 4 groups summed through the wave's LDS scratch (>= 4 * D floats)
   wave_lds_sync();
 #pragma unroll
@@ -276,15 +287,16 @@ __device__ __forceinline__ void slice_wave(const FusedSelParams& p, const PVPara
     p.sl_cnt[gw] = n;
     if (sl == 0 && p.t_out) p.t_out[r] = t;
   }
-  if (n > 0 && n <= kSliceSmall) {  // the list is in LDS: one coalesced store per lane
+  if (n > 0 && n <= kSliceSmall) {  // the list is in LDS: coalesced stores, one or two per lane
     wave_lds_sync();
-    if (lane < min(n, p.slice_cap)) {
-      p.sl_idx[gw * p.slice_cap + lane] = sh.sidx[lane];
-      p.sl_val[gw * p.slice_cap + lane] = sh.sval[lane];
+    for (int i = lane; i < min(n, p.slice_cap); i += kWave) {
+      p.sl_idx[gw * p.slice_cap + i] = sh.sidx[i];
+      p.sl_val[gw * p.slice_cap + i] = sh.sval[i];
     }
   }
-  // 3. a short list is gathered here, in one burst: (m, l, o) partial of the
-  //    slice (its count tells the row kernel that the partial exists)
+  // 3. a short list is gathered here (one burst, two for a peaked head):
+  //    (m, l, o) partial of the slice (its count tells the row kernel that
+  //    the partial exists)
   if (n > 0 && n <= kSliceSmall) {
     wave_lds_sync();
     const int h = r - bi * p.q_h;

@@ -104,7 +104,7 @@ struct FusedSelParams {
 // calibrate: one block per row; fast step: slice kernel + per-row gather kernel
 hipError_t launch_atopn_select_pv(bool calibrate, const FusedSelParams& p, const PVParams& v, hipStream_t st);
 constexpr int kSliceLen = 1024;  // score positions per slice wave of the fast step
-constexpr int kSliceSmall = 64;  // slice lists this short are gathered by their slice wave
+constexpr int kSliceSmall = 96;  // slice lists this short are gathered by their slice wave (<= 2 bursts)
 hipError_t launch_atopn_fast(const FusedSelParams& p, const PVParams& v, hipStream_t st);
 // The per-row kernel of the fast step alone (ranks, cut at buf_k, merge, long gathers).
 hipError_t launch_atopn_rows(const FusedSelParams& p, const PVParams& v, hipStream_t st);

@@ -397,6 +397,36 @@ def test_recency_heavy_rows(L):
     print(f"  rows with a heavy last slice: {heavy}, mean kept {v1['sel_cnt'].mean():.1f}", flush=True)
 
 
+@pytest.mark.parametrize("k2_variant", [2, 1])
+def test_slice_lists_at_the_in_wave_gather_sizes(k2_variant):
+    """Slices passing 1, 47, 48, 49, 95, 96, 97 and 200 positions (batch row
+    b's slice 1 holds the b-th count): one in-wave gather burst (<= 48),
+    two bursts (<= 96), or the row kernel's gather (> 96).  Output equals
+    the oracle on the same inputs; lists, counts and thresholds equal
+    between the two K2 shapes."""
+    counts = [1, 47, 48, 49, 95, 96, 97, 200]
+    b, q_h, k_h, v_h, d, L, N = len(counts), 4, 1, 2, 128, 4096, 256
+    rng = np.random.default_rng(97)
+    q = np.zeros((b, q_h, 1, d), dtype=np.float32)
+    q[..., 0] = 8.0
+    q = O.round_bf16(q + np.float32(0.01) * rng.standard_normal(q.shape, dtype=np.float32))
+    k = O.round_bf16(rng.standard_normal((b, k_h, L, d), dtype=np.float32) * np.float32(0.02))
+    for bi, c in enumerate(counts):
+        pos = 1024 + rng.choice(1024, size=c, replace=False)
+        k[bi, 0, pos, 0] = 8.0  # logit 8 * 8 / sqrt(128) = 5.7, the others within 0.1 of 0
+    k = O.round_bf16(k)
+    v = O.round_bf16(rng.standard_normal((b, v_h, L, d), dtype=np.float32))
+    qd, kd, vd = dev(q, "bf16"), dev(k, "bf16"), dev(v, "bf16")
+    table = np.full(b * q_h, 1e-3, dtype=np.float32)
+    out = host(_run_fast(qd, kd, vd, torch.from_numpy(table).cuda(), N, k2_variant=k2_variant))
+    views = _views(b, q_h, k_h, L, d, 2 * N, scores_of=(qd, kd, None, None, None))
+    _check_selection_rule(views, b * q_h, L, 2 * N)
+    got = views["sel_cnt"].reshape(b, q_h)
+    np.testing.assert_array_equal(got, np.repeat(np.array(counts)[:, None], q_h, axis=1))
+    ref_out, _, _, _ = O.fast(q, k, v, table, None, N, None)
+    assert np.max(np.abs(out - ref_out)) < 2e-3 and rel_l2(out, ref_out) < 1e-4
+
+
 def test_k2_variant_rejects_other_values():
     rng = np.random.default_rng(5)
     (_, _, _), (qd, kd, vd) = qkv(rng, 1, 12, 1, 2, 128, 256, "bf16")
