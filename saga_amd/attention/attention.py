@@ -98,11 +98,30 @@ def register_sdpa():
 
 def full_einsum_forward(query, key, value, attention_mask=None, is_causal=False, scaling=None):
     """attention/attention.py:64-85: softmax(Q K^T * scaling + mask) V with
-    separate key / value head grouping; one HIP split-L kernel (l_q == 1).
-    Returns [b, q_h, 1, d] in the input dtype."""
-    if query.shape[2] != 1:
-        raise NotImplementedError("full_einsum_forward: the MI355X build implements the decode case (l_q == 1)")
-    return _saga.dense_decode(query, key, value, attention_mask, scaling)
+    separate key / value head grouping (query head h reads key head
+    h // (q_h / k_h) and value head h // (q_h / v_h)), on the HIP split-L
+    dense kernel.  Returns [b, q_h, l_q, d] in the input dtype.
+
+    l_q > 1: every query attends to all l_kv keys (the reference adds only
+    the mask, :75-77, and ignores is_causal).  Each batch row runs the
+    kernel once with its l_q queries as the kernel's batch and the row's
+    keys and values as stride-0 views (nothing is copied); the mask slice of
+    the row is passed the same way."""
+    b, q_h, l_q, d = query.shape
+    if l_q == 1:
+        return _saga.dense_decode(query, key, value, attention_mask, scaling)
+    out = torch.empty(b, q_h, l_q, d, dtype=query.dtype, device=query.device)
+    k_h, v_h = key.shape[1], value.shape[1]
+    for i in range(b):
+        qi = query[i].permute(1, 0, 2).unsqueeze(2)                     # [l_q, q_h, 1, d]
+        ki = key[i:i + 1].expand(l_q, k_h, key.shape[2], d)             # stride 0 over the queries
+        vi = value[i:i + 1].expand(l_q, v_h, value.shape[2], d)
+        mi = None
+        if attention_mask is not None:
+            m = attention_mask[min(i, attention_mask.shape[0] - 1)]     # [1 | q_h, l_q, L']
+            mi = m.permute(1, 0, 2).unsqueeze(2)                        # [l_q, 1 | q_h, 1, L']
+        out[i] = ops.dense_decode(qi, ki, vi, mi, scaling)[:, :, 0].permute(1, 0, 2)
+    return out
 
 
 # =============================================================================

@@ -69,9 +69,14 @@ class SagaDecoder:
     """Qwen2 / Llama-shaped decoder with SAGA attention on MI355X: random-init
     weights, or a checkpoint's (weights=..., from_pretrained).
 
-    mode: "atopn" (calibration + fast Atop-N steps) or "dense" (every layer
-    dense; with n_k == n_v this is plain GQA).  exempt_layers run dense in
-    "atopn" mode (attention/attention.py:94, speedup.py:65-66).
+    mode: "atopn" (calibration + fast Atop-N steps), "dense" (every layer on
+    the split-L dense decode kernel; with n_k == n_v this is plain GQA) or
+    "vanilla" (every layer through sdpa_attention_forward, the drop-in for
+    the model's own SDPA function that the reference's vanilla mode calls
+    for decode, speedup.py:76-83: the flash prefill kernel over the
+    unexpanded caches with one query per row and a kv_len mask, built on the
+    device).  exempt_layers run dense in "atopn" mode
+    (attention/attention.py:94, speedup.py:65-66).
     With packed decode weights (pack_weights) the row-major projection
     weights are released after packing unless keep_source_weights: the
     prefill then unpacks one layer's weights at a time.  k2_variant picks the
@@ -82,8 +87,8 @@ class SagaDecoder:
                  exempt_layers=(), device="cuda", dtype=torch.bfloat16, seed: int = 0, fuse_rope: bool = True,
                  pack_weights: bool = True, weights: Optional[dict] = None, keep_source_weights: bool = False,
                  k2_variant: int = 0):
-        if mode not in ("atopn", "dense"):
-            raise ValueError(f"mode must be 'atopn' or 'dense', got {mode!r}")
+        if mode not in ("atopn", "dense", "vanilla"):
+            raise ValueError(f"mode must be 'atopn', 'dense' or 'vanilla', got {mode!r}")
         self.shape, self.batch, self.max_len, self.mode, self.top_n = shape, batch, max_len, mode, top_n
         self.exempt = set(exempt_layers)
         self.device, self.dtype = torch.device(device), dtype
@@ -116,6 +121,7 @@ class SagaDecoder:
         self.tokens = torch.zeros(batch, dtype=torch.int64, device=self.device)
         self.pos = torch.zeros(batch, dtype=torch.int32, device=self.device)
         self.kv_len = torch.zeros(batch, dtype=torch.int32, device=self.device)
+        self._positions = torch.arange(max_len, dtype=torch.int32, device=self.device)  # vanilla mode's mask
         self._x = torch.empty(batch, s.hidden, device=self.device, dtype=dtype)
         self._h = torch.empty(batch, s.hidden, device=self.device, dtype=dtype)
         self._qkv = torch.empty(batch, s.qkv_width, device=self.device, dtype=dtype)
@@ -360,7 +366,9 @@ class SagaDecoder:
                 ops.rope_kv_append(self._qkv, s.n_q, s.n_k, s.n_v, s.rope_theta, self.pos, self.k_cache[l],
                                    self.v_cache[l], q_out=self._q)
             K, V = self.k_cache[l], self.v_cache[l]
-            if self.mode == "dense" or l in self.exempt:
+            if self.mode == "vanilla":
+                self._vanilla_attention(q4, K, V)
+            elif self.mode == "dense" or l in self.exempt:
                 ops.dense_decode(q4, K, V, kv_len=self.kv_len, out=self._attn, workspace=ws["dense"])
             elif calibrate:
                 ops.atopn_calibrate(q4, K, V, self.top_n, self.table[l], kv_len=self.kv_len, out=self._attn,
@@ -387,6 +395,15 @@ class SagaDecoder:
             torch.argmax(self._logits, dim=-1, out=self.tokens)
         self.pos.add_(1)
         self.kv_len.add_(1)
+
+    def _vanilla_attention(self, q4: torch.Tensor, K: torch.Tensor, V: torch.Tensor) -> None:
+        """speedup.py:76-83, vanilla mode: the decode step through the base
+        SDPA function (sdpa_attention_forward), the cache's unfilled slots
+        masked off (position < kv_len[b], built on the device)."""
+        B, s = self.batch, self.shape
+        keep = (self._positions[None, :] < self.kv_len[:, None])[:, None, None, :]
+        o, _ = sdpa_attention_forward(_HeadGroups(), q4, K, V, keep, is_causal=False)  # [B, 1, n_q, d]
+        self._attn.view(B, s.n_q, s.head_dim).copy_(o.view(B, s.n_q, s.head_dim))
 
     def capture(self) -> None:
         """Capture the calibration and fast steps as HIP graphs (after an eager

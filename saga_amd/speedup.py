@@ -4,7 +4,9 @@
         --batch_sizes 1,8 --seq_lengths 4096,32768 --num_new_tokens 256
 
 What it mirrors (speedup.py:447-700):
-  * attention modes: `full` / `vanilla` (dense decode), `atopn:N` and
+  * attention modes: `full` (the split-L dense decode kernel), `vanilla`
+    (the base SDPA function for decode: the flash kernel with one query per
+    row, speedup.py:76-83), `atopn:N` and
     `atopn_amortized:N` (calibration on the first generated token, fast
     Atop-N steps after it: the amortized schedule of speedup.py:56-75);
   * the grid of batch sizes x sequence lengths x attention modes x merge
@@ -65,7 +67,7 @@ def build_decoder(model_path: str, merge: bool, new_heads: int, batch: int, max_
     checkpoint directory)."""
     from saga_amd.decoder import (QWEN25_15B_GQA, QWEN25_15B_SAGA, SMOLLM2_360M_GQA, SMOLLM2_360M_SAGA,
                                   SagaDecoder)
-    dmode = "dense" if mode in ("full", "vanilla") else "atopn"
+    dmode = {"full": "dense", "vanilla": "vanilla"}.get(mode, "atopn")
     if model_path in BUILTIN:
         saga, gqa = ((QWEN25_15B_SAGA, QWEN25_15B_GQA) if model_path == "qwen2.5-1.5b"
                      else (SMOLLM2_360M_SAGA, SMOLLM2_360M_GQA))

@@ -67,7 +67,7 @@ def _tiny_model(mode, top_n=16, keep_source_weights=False):
     return m
 
 
-@pytest.mark.parametrize("mode", ["atopn", "dense"])
+@pytest.mark.parametrize("mode", ["atopn", "dense", "vanilla"])
 def test_graph_replay_equals_eager_steps(mode):
     m = _tiny_model(mode)
     m.prefill(torch.randint(0, 1024, (500,), generator=torch.Generator().manual_seed(7)))
@@ -164,3 +164,21 @@ def test_packed_weights_decode_step_identical():
     torch.cuda.synchronize()
     for a, b in ((ms[0].k_cache, ms[1].k_cache), (ms[0].v_cache, ms[1].v_cache), (ms[0]._logits, ms[1]._logits)):
         assert torch.equal(a, b)
+
+
+def test_vanilla_mode_matches_dense_mode():
+    """The harness's vanilla mode (speedup.py:76-83: decode through the base
+    SDPA function, here the flash kernel with one query per row and a
+    device-built kv_len mask) and its full mode (the split-L dense decode
+    kernel) compute the same attention: one decode step of the same
+    weights and prompt gives the same logits to bf16 rounding."""
+    prompt = torch.randint(0, 1024, (400,), generator=torch.Generator().manual_seed(3))
+    logits = {}
+    for mode in ("dense", "vanilla"):
+        m = _tiny_model(mode)
+        m.prefill(prompt)
+        m.step(calibrate=False)
+        m.step(calibrate=False)
+        torch.cuda.synchronize()
+        logits[mode] = m._logits.float().cpu().numpy()
+    assert rel_l2(logits["vanilla"], logits["dense"]) < 2e-2

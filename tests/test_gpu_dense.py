@@ -5,7 +5,7 @@ import pytest
 import torch
 
 from conftest import rel_l2
-from gpu_util import host, qkv
+from gpu_util import host, qkv, randn
 from oracle import saga_oracle as O
 from saga_amd import ops
 
@@ -63,3 +63,30 @@ def test_workspace_reuse_across_shapes():
         fast = host(ops.atopn_decode(qd, kd, vd, table, 128, out_dtype=torch.float32))
         ref, _, _, _ = O.fast(q, k, v, host(table), None, 128, None)
         assert rel_l2(fast, ref) < 1e-3, shape
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("mask_kind", [None, "bool", "float"])
+def test_full_einsum_forward_several_queries(dt, mask_kind):
+    """full_einsum_forward with l_q > 1 (attention/attention.py:64-85): every
+    query attends to all keys plus the mask (is_causal is ignored, as in the
+    reference), query head h reading key head h // (q_h / k_h) and value
+    head h // (q_h / v_h); a bool mask adds 1.0 where true."""
+    from saga_amd.attention import attention as A
+    rng = np.random.default_rng(17 + (mask_kind is not None))
+    b, q_h, k_h, v_h, d, L, l_q = 3, 12, 1, 2, 128, 700, 5
+    q, qd = randn(rng, (b, q_h, l_q, d), dt)
+    (_, k, v), (_, kd, vd) = qkv(rng, b, q_h, k_h, v_h, d, L, dt)
+    m = None
+    if mask_kind == "bool":
+        m = rng.random((b, 1, l_q, L + 4)) > 0.4
+    elif mask_kind == "float":
+        m = rng.standard_normal((1, q_h, l_q, L), dtype=np.float32)
+    md = None if m is None else torch.from_numpy(m).cuda()
+    out = A.full_einsum_forward(qd, kd, vd, md, is_causal=True, scaling=0.09)
+    assert tuple(out.shape) == (b, q_h, l_q, d) and out.dtype == qd.dtype
+    ref = O.dense(q.astype(np.float64), k.astype(np.float64), v.astype(np.float64), m, 0.09)
+    got = host(out)
+    assert rel_l2(got, ref) < (1e-5 if dt == "f32" else 5e-3)
+    if dt != "f32":
+        assert np.max(np.abs(got - ref)) < 2e-2
