@@ -92,18 +92,31 @@ __device__ void wave_pv_small(int n, const int* sidx, const float* sval, const c
   for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
   const char* vb = vbase + static_cast<int64_t>(c) * PV::BYTES;
   auto burst = [&](int e0) {
+    // the burst's positions first (LDS reads issued back to back and waited
+    // for once), then every gather: each load would otherwise wait for its
+    // own LDS read
+    int id[kWaveUnroll];
+#pragma unroll
+    for (int u = 0; u < kWaveUnroll; ++u) {
+      const int e = e0 + G + 4 * u;
+      id[u] = sidx[min(e, kSliceSmall - 1)];
+    }
     u32x4 raw[kWaveUnroll][PV::NV];
 #pragma unroll
     for (int u = 0; u < kWaveUnroll; ++u) {
       const int e = e0 + G + 4 * u;
-      if (e < n) PV::load_raw(vb + static_cast<int64_t>(sidx[e]) * vrow, raw[u]);
+      if (e < n) PV::load_raw(vb + static_cast<int64_t>(id[u]) * vrow, raw[u]);
     }
+    // the entries' logits, read while the rows are in flight
+    float xs[kWaveUnroll];
+#pragma unroll
+    for (int u = 0; u < kWaveUnroll; ++u) xs[u] = sval[min(e0 + G + 4 * u, kSliceSmall - 1)];
     __builtin_amdgcn_sched_barrier(0);  // all gathers of the burst in flight before the FMAs
 #pragma unroll
     for (int u = 0; u < kWaveUnroll; ++u) {
       const int e = e0 + G + 4 * u;
       if (e < n) {
-        const float w = __expf(sval[e] - m);
+        const float w = __expf(xs[u] - m);
         float f[DPL];
         PV::unpack(raw[u], f);
 #pragma unroll
