@@ -448,7 +448,11 @@ struct RowShared {
 
 // The row merge of row r by the NT threads of a block (see the file comment).
 // ALL_GATHER: the slices carry no partials; every kept entry is gathered here.
-template <int DT, int D, int NT, bool ALL_GATHER = false>
+// LONG: rows of more than kRowMaxSlices slices, whose slice ranks live in the
+// workspace instead of LDS (a host-side choice: with the address space known
+// at compile time the ranks are LDS reads, not flat loads that wait on both
+// the LDS and the memory counters at every use).
+template <int DT, int D, int NT, bool ALL_GATHER = false, bool LONG = false>
 __device__ __forceinline__ void row_merge(const FusedSelParams& p, const PVParams& v, int r, RowShared<NT>& sh) {
   constexpr int NW = NT / kWave;
   float* red = sh.red;
@@ -466,9 +470,8 @@ __device__ __forceinline__ void row_merge(const FusedSelParams& p, const PVParam
   const int64_t row0 = static_cast<int64_t>(r) * ns;
   const int bi = r / p.q_h, h = r - bi * p.q_h;
   // the row's slice ranks: LDS, or the workspace for very long rows
-  const bool in_lds = ns <= kRowMaxSlices;
-  int* pre = in_lds ? spre : p.sl_pre + static_cast<int64_t>(r) * 2 * (ns + 1);
-  int* gpre = in_lds ? sgpre : pre + (ns + 1);
+  int* pre = LONG ? p.sl_pre + static_cast<int64_t>(r) * 2 * (ns + 1) : spre;
+  int* gpre = LONG ? pre + (ns + 1) : sgpre;
 
   // 0. the first merge batch's slice partials, loaded before the counts
   //    (whether a slice's partial counts is known only after the scan; the
@@ -616,10 +619,10 @@ __device__ __forceinline__ void row_merge(const FusedSelParams& p, const PVParam
   }
 }
 
-template <int DT, int D, int NT>
+template <int DT, int D, int NT, bool LONG>
 __global__ void __launch_bounds__(NT) atopn_gather_kernel(FusedSelParams p, PVParams v) {
   __shared__ RowShared<NT> sh;
-  row_merge<DT, D, NT>(p, v, blockIdx.x, sh);
+  row_merge<DT, D, NT, false, LONG>(p, v, blockIdx.x, sh);
 }
 
 // One block per row: its waves compact the row's slices (t once per wave,
@@ -627,14 +630,14 @@ __global__ void __launch_bounds__(NT) atopn_gather_kernel(FusedSelParams p, PVPa
 // barrier (which orders their workspace writes before the reads), the whole
 // block gathers every kept entry and computes softmax . V -- one launch, no
 // kernel boundary and no per-slice partials.
-template <int DT, int D, int NT>
+template <int DT, int D, int NT, bool LONG>
 __global__ void __launch_bounds__(NT) atopn_rowblock_kernel(FusedSelParams p, PVParams v) {
   __shared__ RowShared<NT> sh;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = blockIdx.x;
   rowblock_slices(p, r, w, NT / kWave);
   __syncthreads();
-  row_merge<DT, D, NT, true>(p, v, r, sh);
+  row_merge<DT, D, NT, true, LONG>(p, v, r, sh);
 }
 
 // One block per row with the whole selection in LDS (rows of at most
@@ -744,12 +747,22 @@ __global__ void __launch_bounds__(NT) atopn_rowlds_kernel(FusedSelParams p, PVPa
 
 template <int DT, int D>
 static hipError_t launch_rows_typed(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
-  if (p.cap <= kRowSmallCap)
-    hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsSmall>), dim3(p.nrows), dim3(kRowThreadsSmall), 0, st, p,
-                       v);
-  else
-    hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsLarge>), dim3(p.nrows), dim3(kRowThreadsLarge), 0, st, p,
-                       v);
+  const bool lng = p.nslice > kRowMaxSlices;
+  if (p.cap <= kRowSmallCap) {
+    if (lng)
+      hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsSmall, true>), dim3(p.nrows), dim3(kRowThreadsSmall), 0,
+                         st, p, v);
+    else
+      hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsSmall, false>), dim3(p.nrows), dim3(kRowThreadsSmall),
+                         0, st, p, v);
+  } else {
+    if (lng)
+      hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsLarge, true>), dim3(p.nrows), dim3(kRowThreadsLarge), 0,
+                         st, p, v);
+    else
+      hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsLarge, false>), dim3(p.nrows), dim3(kRowThreadsLarge),
+                         0, st, p, v);
+  }
   return hipGetLastError();
 }
 
@@ -766,8 +779,10 @@ static hipError_t launch_split(const FusedSelParams& p, const PVParams& v, hipSt
       hipLaunchKernelGGL((atopn_rowlds_kernel<DT, D, 256>), dim3(p.nrows), dim3(256), 0, st, p, v);
     else if (p.cap <= kRowBatch && p.nslice <= 16 * kRowBlockBurst)
       hipLaunchKernelGGL((atopn_rowlds_kernel<DT, D, 1024>), dim3(p.nrows), dim3(1024), 0, st, p, v);
+    else if (p.nslice <= kRowMaxSlices)
+      hipLaunchKernelGGL((atopn_rowblock_kernel<DT, D, 1024, false>), dim3(p.nrows), dim3(1024), 0, st, p, v);
     else
-      hipLaunchKernelGGL((atopn_rowblock_kernel<DT, D, 1024>), dim3(p.nrows), dim3(1024), 0, st, p, v);
+      hipLaunchKernelGGL((atopn_rowblock_kernel<DT, D, 1024, true>), dim3(p.nrows), dim3(1024), 0, st, p, v);
     return hipGetLastError();
   }
   const int64_t waves = static_cast<int64_t>(p.nslice) * p.nrows;

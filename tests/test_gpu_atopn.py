@@ -427,6 +427,44 @@ def test_slice_lists_at_the_in_wave_gather_sizes(k2_variant):
     assert np.max(np.abs(out - ref_out)) < 2e-3 and rel_l2(out, ref_out) < 1e-4
 
 
+@pytest.mark.parametrize("k2_variant", [2, 1])
+def test_rows_of_more_than_2048_slices(k2_variant):
+    """Rows of 2051 slices (L = 2050 * 1024 + 300): the row merge keeps its
+    slice ranks in the workspace instead of LDS.  Batch row 0 passes 300
+    positions in slices 5, 1000, 2047, 2048 and 2049 (buf_k = 256: the cut
+    falls inside slice 2049; slice 1000's 120 entries are gathered by the
+    row merge); batch row 1 passes 112 (97 in the short last slice), none cut.  Keys and values are zero
+    outside the passing positions, so the selection has a wide margin (logit
+    32 against 0).  Counts, lists and outputs against the oracle."""
+    b, q_h, k_h, v_h, d, N = 2, 2, 1, 1, 64, 128
+    L = 2050 * 1024 + 300
+    plan = [{5: 40, 1000: 120, 2047: 60, 2048: 30, 2049: 50}, {3: 10, 2048: 5, 2050: 97}]
+    rng = np.random.default_rng(2049)
+    q = np.zeros((b, q_h, 1, d), dtype=np.float32)
+    q[..., 0] = 16.0
+    k = np.zeros((b, k_h, L, d), dtype=np.float32)
+    v = np.zeros((b, v_h, L, d), dtype=np.float32)
+    for bi, slices in enumerate(plan):
+        for s, c in slices.items():
+            pos = s * 1024 + np.sort(rng.choice(min(1024, L - s * 1024), size=c, replace=False))
+            k[bi, 0, pos, 0] = 16.0  # logit 16 * 16 / sqrt(64) = 32
+            v[bi, 0, pos] = O.round_bf16(rng.standard_normal((c, d), dtype=np.float32))
+    print(f"atopn rows of 2051 slices k2_variant={k2_variant} L={L}", flush=True)
+    qd, kd, vd = dev(q, "bf16"), dev(k, "bf16"), dev(v, "bf16")
+    table = np.full(b * q_h, 1e-3, dtype=np.float32)
+    out = host(_run_fast(qd, kd, vd, torch.from_numpy(table).cuda(), N, k2_variant=k2_variant))
+    views = _views(b, q_h, k_h, L, d, 2 * N)
+    ref_out, _, idx_ref, cnt_ref = O.fast(q, k, v, table, None, N, None)
+    np.testing.assert_array_equal(views["sel_total"], np.repeat([300, 112], q_h))
+    np.testing.assert_array_equal(views["sel_total"], cnt_ref)
+    np.testing.assert_array_equal(views["sel_cnt"], np.repeat([256, 112], q_h))
+    idx_ref = idx_ref.reshape(b * q_h, 2 * N)
+    for r in range(b * q_h):
+        kept = views["sel_cnt"][r]
+        np.testing.assert_array_equal(views["sel_idx"][r, :kept], idx_ref[r, :kept])
+    assert np.max(np.abs(out - ref_out)) < 2e-3 and rel_l2(out, ref_out) < 1e-4
+
+
 def test_k2_variant_rejects_other_values():
     rng = np.random.default_rng(5)
     (_, _, _), (qd, kd, vd) = qkv(rng, 1, 12, 1, 2, 128, 256, "bf16")
