@@ -291,11 +291,22 @@ int saga_gemv(const saga_tensor* x, const saga_tensor* w, const saga_tensor* bia
  * so results equal saga_gemv into an unpermuted qkv followed by
  * saga_rope_kv_append.  Replaces q/k/v_proj + apply_rotary_pos_emb + the
  * cache update (transformers models/qwen2/modeling_qwen2.py:205-214,
- * cache_utils.py:455-487).  d % 16 == 0. */
+ * cache_utils.py:455-487).  d % 16 == 0.  rope_table: NULL (the rotations
+ * are computed in the epilogue), or the token rows' rotations from
+ * saga_rope_table for the same pos, d and theta (16-byte aligned): a decode
+ * step computes them once for all its layers, with identical results. */
 int saga_gemv_rope_kv(const saga_tensor* x, const saga_tensor* w, const saga_tensor* bias, float rms_eps,
                       int64_t n_q, int64_t n_k, int64_t n_v, float theta, const int32_t* pos,
                       const int32_t* batch, saga_tensor* q_out, saga_tensor* k_cache,
-                      saga_tensor* v_cache, saga_stream_t stream);
+                      saga_tensor* v_cache, const float* rope_table, saga_stream_t stream);
+
+/* Rotations of N token rows: table [N][d/2][2] fp32 (16-byte aligned) with
+ * table[n][i] = (cos, sin)(pos[n] * theta^(-2i/d)), the angles of
+ * saga_rope_kv_append.  The cos / sin tables of transformers'
+ * Qwen2RotaryEmbedding (models/qwen2/modeling_qwen2.py:51-104), kept in fp32,
+ * for saga_gemv_rope_kv's rope_table. */
+int saga_rope_table(const int32_t* pos, int64_t N, int64_t d, float theta, float* table,
+                    saga_stream_t stream);
 
 /* out[r] = first index of the maximum of row r of x [rows, N] (bf16); the
  * greedy next token of speedup.py:169/193 (logits.argmax(dim=-1)).  NaN is

@@ -771,15 +771,34 @@ int saga_rope_kv_append(const saga_tensor* qkv, int64_t n_q, int64_t n_k, int64_
   return ok();
 }
 
+int saga_rope_table(const int32_t* pos, int64_t N, int64_t d, float theta, float* table, saga_stream_t stream) {
+  if (N < 0 || d < 2 || d % 2) return fail(SAGA_ERR_INVALID, "rope_table: N >= 0 and an even head_dim >= 2 required");
+  if (N > 0 && (!pos || !table)) return fail(SAGA_ERR_INVALID, "rope_table: null pos or table");
+  if (N >= (1LL << 31) || d > 65536 || N * (d / 2) >= (1LL << 31))
+    return fail(SAGA_ERR_UNSUPPORTED, "rope_table: sizes too large");
+  if (reinterpret_cast<uintptr_t>(table) % 16) return fail(SAGA_ERR_INVALID, "rope_table: table must be 16-byte aligned");
+  if (N == 0) return ok();
+  int rc;
+  if ((rc = hip_status(launch_rope_table(pos, static_cast<int>(N), static_cast<int>(d), theta, table,
+                                         static_cast<hipStream_t>(stream)),
+                       "rope_table launch")))
+    return rc;
+  return ok();
+}
+
 int saga_gemv_rope_kv(const saga_tensor* x, const saga_tensor* w, const saga_tensor* bias, float rms_eps,
                       int64_t n_q, int64_t n_k, int64_t n_v, float theta, const int32_t* pos, const int32_t* batch,
-                      saga_tensor* q_out, saga_tensor* k_cache, saga_tensor* v_cache, saga_stream_t stream) {
+                      saga_tensor* q_out, saga_tensor* k_cache, saga_tensor* v_cache, const float* rope_table,
+                      saga_stream_t stream) {
   int rc;
   GemvParams p;
   if ((rc = make_gemv(x, w, bias, rms_eps, p))) return rc;
   if ((rc = make_rope(p.M, SAGA_DTYPE_BF16, n_q, n_k, n_v, theta, pos, batch, q_out, k_cache, v_cache, p.rope)))
     return rc;
   if (p.rope.d % 16) return fail(SAGA_ERR_UNSUPPORTED, "gemv_rope_kv: head_dim %% 16 == 0 required");
+  if (reinterpret_cast<uintptr_t>(rope_table) % 16)
+    return fail(SAGA_ERR_INVALID, "gemv_rope_kv: rope_table must be 16-byte aligned");
+  p.rope.table = rope_table;
   if (p.N != (n_q + n_k + n_v) * p.rope.d) return fail(SAGA_ERR_INVALID, "gemv_rope_kv: w must have (n_q + n_k + n_v) * d rows");
   if (p.M == 0) return ok();
   p.epilogue = kGemvRopeKV;

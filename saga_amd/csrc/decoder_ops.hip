@@ -53,6 +53,26 @@ hipError_t launch_rope_kv_append(const RopeParams& p, hipStream_t st) {
   return hipGetLastError();
 }
 
+// The rotations of a decode step's token rows, computed once per step for
+// every layer's fused q/k/v projection (the same rope_cos_sin as the kernels
+// that compute them in place: identical values).
+__global__ void __launch_bounds__(256) rope_table_kernel(const int32_t* pos, int N, int d, float theta,
+                                                         float* table) {
+  const int half = d / 2;
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= N * half) return;
+  const int n = t / half, i = t - n * half;
+  float cs, sn;
+  rope_cos_sin(pos[n], i, d, theta, cs, sn);
+  *reinterpret_cast<f32x2*>(table + 2 * static_cast<int64_t>(t)) = f32x2{cs, sn};
+}
+
+hipError_t launch_rope_table(const int32_t* pos, int N, int d, float theta, float* table, hipStream_t st) {
+  const int total = N * (d / 2);
+  hipLaunchKernelGGL(rope_table_kernel, dim3((total + 255) / 256), dim3(256), 0, st, pos, N, d, theta, table);
+  return hipGetLastError();
+}
+
 __global__ void __launch_bounds__(256) rmsnorm_kernel(RowParams p) {
   __shared__ float red[4];
   const int n = blockIdx.x;

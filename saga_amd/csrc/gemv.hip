@@ -29,13 +29,15 @@ constexpr int kSplitBatch = 8;   // split-K partial sums in flight per epilogue 
 // loads they return with it; after the reduction each would cost one more
 // round trip):
 // the residual of output rows n..n+3 of token row m (SAGA_GEMV_ADD), and the
-// bias, position and batch row of the fused q/k/v projection (kGemvRopeKV).
+// bias, position, batch row and rotations (with a rotation table) of the
+// fused q/k/v projection (kGemvRopeKV).
 // Absent inputs read a valid dummy address instead of branching (a load under
 // a branch is waited for at the join, ahead of the burst).  Other epilogues
 // load their (rare) bias after the reduction, keeping registers for the burst.
 struct GemvPre {
   uint16_t bias[4], y[4];
   int pos, batch;
+  f32x4 rot;  // (cos, sin) of the rotary pairs j/2 and j/2 + 1, j = n mod d
 };
 
 template <int EPI>
@@ -53,6 +55,11 @@ __device__ __forceinline__ GemvPre gemv_prefetch(const GemvParams& p, int m, int
     e.pos = p.rope.pos[m];
     e.batch = *(p.rope.batch ? p.rope.batch + m : p.rope.pos + m);
     if (!p.rope.batch) e.batch = m;
+    // rows n..n+3 hold the pairs j/2, j/2 + 1 (j % 4 == 0): 16 aligned bytes
+    const int j = n % p.rope.d;
+    const float* rt = p.rope.table ? p.rope.table + (static_cast<int64_t>(m) * (p.rope.d / 2) + j / 2) * 2
+                                   : static_cast<const float*>(dummy);
+    e.rot = *reinterpret_cast<const f32x4*>(rt);
   }
   return e;
 }
@@ -203,8 +210,8 @@ gemv_kernel(GemvParams p) {
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         const int i = j / 2 + q;
-        float cs, sn;
-        rope_cos_sin(pos, i, rp.d, rp.theta, cs, sn);
+        float cs = pre.rot[2 * q], sn = pre.rot[2 * q + 1];
+        if (!rp.table) rope_cos_sin(pos, i, rp.d, rp.theta, cs, sn);
         const float x1 = o[2 * q], x2 = o[2 * q + 1];
         const float y1 = x1 * cs - x2 * sn;
         const float y2 = x2 * cs + x1 * sn;

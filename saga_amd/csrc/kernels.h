@@ -170,8 +170,13 @@ struct RopeParams {
   void* v_cache;  // [B, n_v, Lmax, d]
   int64_t v_sb, v_sh, v_sl;
   int32_t B, Lmax;
+  // [N][d/2][2] fp32 (cos, sin) of the token rows' rotations (launch_rope_table),
+  // or null: computed where they are used
+  const float* table;
 };
 hipError_t launch_rope_kv_append(const RopeParams& p, hipStream_t st);
+// table[n][i] = (cos, sin)(pos[n] * theta^(-2i/d)), i < d/2, n < N
+hipError_t launch_rope_table(const int32_t* pos, int N, int d, float theta, float* table, hipStream_t st);
 
 // Row-wise ops: rmsnorm (y = w * x * rsqrt(mean(x^2) + eps)) and silu_mul.
 struct RowParams {

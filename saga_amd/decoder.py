@@ -126,6 +126,7 @@ class SagaDecoder:
         self._h = torch.empty(batch, s.hidden, device=self.device, dtype=dtype)
         self._qkv = torch.empty(batch, s.qkv_width, device=self.device, dtype=dtype)
         self._q = torch.empty(batch, s.n_q, d, device=self.device, dtype=dtype)
+        self._rope = torch.empty(batch, d // 2, 2, device=self.device, dtype=torch.float32)  # the step's rotations
         self._attn = torch.empty(batch, s.n_q, 1, d, device=self.device, dtype=dtype)
         self._gu = torch.empty(batch, 2 * s.intermediate, device=self.device, dtype=dtype)
         self._act = torch.empty(batch, s.intermediate, device=self.device, dtype=dtype)
@@ -353,10 +354,13 @@ class SagaDecoder:
         x = self._x
         torch.index_select(self.embed, 0, self.tokens, out=x)
         q4 = self._q.view(B, s.n_q, 1, d)
+        if self.fuse_rope:
+            ops.rope_table(self.pos, d, s.rope_theta, out=self._rope)  # once for all layers
         for l in range(s.layers):
             if self.fuse_rope:
                 ops.gemv_rope_kv(x, self.kw_qkv[l], self.kb_qkv[l], s.n_q, s.n_k, s.n_v, s.rope_theta, self.pos,
-                                 self.k_cache[l], self.v_cache[l], rms_eps=s.eps, q_out=self._q)
+                                 self.k_cache[l], self.v_cache[l], rms_eps=s.eps, q_out=self._q,
+                                 rope_table=self._rope)
             else:
                 if self.use_gemv:
                     ops.gemv(x, self.kw_qkv[l], bias=self.b_qkv[l], rms_eps=s.eps, out=self._qkv, workspace=ws.get("gemv"))

@@ -514,23 +514,44 @@ def rope_pair_order(n_q, n_k, n_v, d, device=None):
 
 
 def gemv_rope_kv(x, w_pairs, bias_pairs, n_q, n_k, n_v, theta, pos, k_cache, v_cache, rms_eps=None, batch=None,
-                 q_out=None):
+                 q_out=None, rope_table=None):
     """Fused q/k/v projection + RoPE + KV-cache append for M <= 16 new tokens:
     the same results as gemv(x, w, bias) followed by rope_kv_append, with w
-    and bias given in rope_pair_order.  Returns q_out [M, n_q, d]."""
-    dev = _need_gpu(x, w_pairs, bias_pairs, pos, k_cache, v_cache, batch, q_out)
+    and bias given in rope_pair_order.  rope_table: rope_table(pos, d, theta)
+    of the same positions (the rotations computed once for several layers),
+    or None.  Returns q_out [M, n_q, d]."""
+    dev = _need_gpu(x, w_pairs, bias_pairs, pos, k_cache, v_cache, batch, q_out, rope_table)
     d = k_cache.shape[-1]
     if q_out is None:
         q_out = torch.empty(x.shape[0], n_q, d, dtype=x.dtype, device=dev)
     for t, name in ((pos, "pos"), (batch, "batch")):
         if t is not None and (t.dtype != torch.int32 or not t.is_contiguous()):
             raise ValueError(f"saga_amd: {name} must be a contiguous int32 tensor")
+    if rope_table is not None and (rope_table.dtype != torch.float32 or not rope_table.is_contiguous()
+                                   or tuple(rope_table.shape) != (x.shape[0], d // 2, 2)):
+        raise ValueError("saga_amd: rope_table must be a contiguous float32 [M, d/2, 2] tensor")
     eps = -1.0 if rms_eps is None else float(rms_eps)
     _lib.check(_lib.load().saga_gemv_rope_kv(_lib.tensor(x), _lib.tensor(w_pairs), _lib.tensor(bias_pairs), eps,
                                              n_q, n_k, n_v, float(theta), _lib.ptr(pos), _lib.ptr(batch),
                                              _lib.tensor(q_out), _lib.tensor(k_cache), _lib.tensor(v_cache),
-                                             _lib.stream_of(x)), "gemv_rope_kv")
+                                             _lib.ptr(rope_table), _lib.stream_of(x)), "gemv_rope_kv")
     return q_out
+
+
+def rope_table(pos, d, theta, out=None):
+    """Rotations of the token rows at positions pos (int32 [M]): fp32
+    [M, d/2, 2] with out[n, i] = (cos, sin)(pos[n] * theta^(-2i/d)), the
+    angles rope_kv_append and gemv_rope_kv use."""
+    dev = _need_gpu(pos, out)
+    if pos.dtype != torch.int32 or not pos.is_contiguous() or pos.dim() != 1:
+        raise ValueError("saga_amd: pos must be a contiguous int32 [M] tensor")
+    if out is None:
+        out = torch.empty(pos.shape[0], d // 2, 2, dtype=torch.float32, device=dev)
+    elif out.dtype != torch.float32 or not out.is_contiguous() or tuple(out.shape) != (pos.shape[0], d // 2, 2):
+        raise ValueError("saga_amd: out must be a contiguous float32 [M, d/2, 2] tensor")
+    _lib.check(_lib.load().saga_rope_table(_lib.ptr(pos), pos.shape[0], d, float(theta), _lib.ptr(out),
+                                           _lib.stream_of(pos)), "rope_table")
+    return out
 
 
 def argmax_rows(x, out=None, workspace=None):

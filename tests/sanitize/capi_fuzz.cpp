@@ -227,17 +227,15 @@ int main(int argc, char** argv) {
                               fake<void>(p1), size_t(rnd_size()), nullptr); break;
       case 13: rc = saga_gemv_rope_kv(maybe(a), maybe(b), next() % 2 ? nullptr : &c, rnd_float(), rnd_size(),
                                       rnd_size(), rnd_size(), rnd_float(), fake<int32_t>(p1), fake<int32_t>(p2), &d,
-                                      &e, &f, nullptr); break;
+                                      &e, &f, next() % 2 ? nullptr : fake<float>(p3), nullptr); break;
       case 14: rc = saga_argmax(maybe(a), fake<int64_t>(p1), fake<void>(p2), size_t(rnd_size()), nullptr); break;
       case 15: rc = saga_prefill_attention(maybe(a), maybe(b), maybe(c), next() % 2 ? nullptr : &d, rnd_float(),
                                            int32_t(next() % 3), rnd_size(), &e, nullptr); break;
       case 16: rc = saga_atopn_decode_ex(maybe(a), maybe(b), maybe(c), next() % 2 ? nullptr : &d, fake<int32_t>(p1),
                                          rnd_float(), rnd_size(), fake<float>(p2), &e, int32_t(next() % 5) - 1,
                                          fake<void>(p3), size_t(rnd_size()), nullptr); break;
-      case 17: (void)saga_atopn_workspace_bytes(rnd_size(), rnd_size(), rnd_size(), rnd_size(), rnd_size(),
-                                                rnd_size());
-        rc = -1;
-        break;
+      case 17: rc = saga_rope_table(next() % 2 ? nullptr : fake<int32_t>(p1), rnd_size(), rnd_size(), rnd_float(),
+                                    next() % 2 ? nullptr : fake<float>(p2), nullptr); break;
       case 18: rc = saga_atopn_decode(nullptr, nullptr, nullptr, nullptr, nullptr, 0.f, 0, nullptr, nullptr,
                                       nullptr, 0, nullptr); break;
       case 19: rc = saga_qk_scores(&a, &b, nullptr, nullptr, rnd_float(), maybe(c) ? &c : nullptr, nullptr,

@@ -110,6 +110,56 @@ def test_gemv_rope_kv_matches_unfused(M, K, n_q, n_k, n_v, d):
         assert rel_l2(vh[bt[m], :, p[m]], proj[m, n_q + n_k:]) < 4e-3
 
 
+@pytest.mark.parametrize("d,theta", [(128, 1e6), (64, 1e5)])
+def test_rope_table_against_float64(d, theta):
+    """table[n, i] = (cos, sin) of the fp32 angle pos[n] * theta^(-2i/d)
+    (transformers computes the angle in fp32 the same way), against float64
+    cos / sin of that angle: positions 0 .. 131071 and a negative one."""
+    pos = np.array([0, 1, 7, 4095, 32767, 32768, 65536 + 3, 131071, -5], dtype=np.int32)
+    got = host(ops.rope_table(torch.from_numpy(pos).cuda(), d, theta))
+    assert got.shape == (pos.size, d // 2, 2)
+    inv = (1.0 / np.power(np.float32(theta), np.arange(0, d, 2, dtype=np.float32) / np.float32(d))).astype(np.float32)
+    ang = (pos[:, None].astype(np.float32) * inv[None, :]).astype(np.float64)
+    # the angles of pos <= 2^17 are within 2^-7 rad of representable: a one-ulp
+    # difference in theta^(-2i/d) moves them by at most 2^17 * 2^-24 = 2^-7
+    tol = 2.0 ** -7 + 1e-6
+    np.testing.assert_allclose(got[..., 0], np.cos(ang), atol=tol)
+    np.testing.assert_allclose(got[..., 1], np.sin(ang), atol=tol)
+    small = np.abs(pos) <= 64  # angles below 64 rad: no room for the ulp argument
+    np.testing.assert_allclose(got[small, :, 0], np.cos(ang[small]), atol=2e-6)
+    np.testing.assert_allclose(got[small, :, 1], np.sin(ang[small]), atol=2e-6)
+
+
+@pytest.mark.parametrize("M,K,n_q,n_k,n_v,d", [(8, 1536, 12, 1, 2, 128), (1, 960, 15, 1, 5, 64)])
+def test_gemv_rope_kv_with_table_identical(M, K, n_q, n_k, n_v, d):
+    """The fused projection with the step's rotation table (computed once for
+    all layers) writes the same bits as with the rotations computed in its
+    epilogue; positions past 32k included."""
+    rng = np.random.default_rng(M * 13 + K)
+    N = (n_q + n_k + n_v) * d
+    x, w, b = _data(rng, M, K, N)
+    B, Lmax = 16, 40000
+    pos = torch.from_numpy(rng.integers(0, Lmax, M).astype(np.int32)).cuda()
+    pos[0] = Lmax - 1
+    batch = torch.from_numpy(rng.permutation(B)[:M].astype(np.int32)).cuda()
+    order = ops.rope_pair_order(n_q, n_k, n_v, d, device="cuda")
+    wd, bd = dev(w, "bf16")[order].contiguous(), dev(b, "bf16")[order].contiguous()
+    xd = dev(x, "bf16")
+    table = ops.rope_table(pos, d, 1e6)
+    outs = []
+    for tab in (None, table):
+        caches = [torch.zeros(B, h, Lmax, d, device="cuda", dtype=torch.bfloat16) for h in (n_k, n_v)]
+        q = ops.gemv_rope_kv(xd, wd, bd, n_q, n_k, n_v, 1e6, pos, caches[0], caches[1], rms_eps=1e-6, batch=batch,
+                             rope_table=tab)
+        torch.cuda.synchronize()
+        outs.append([q] + caches)
+    for a, r in zip(outs[0], outs[1]):
+        assert torch.equal(a.view(torch.int16), r.view(torch.int16))
+    with pytest.raises(ValueError, match="rope_table"):
+        ops.gemv_rope_kv(xd, wd, bd, n_q, n_k, n_v, 1e6, pos, caches[0], caches[1], rms_eps=1e-6, batch=batch,
+                         rope_table=table[:, :-1].contiguous())
+
+
 def test_rope_pair_order_is_a_permutation():
     order = ops.rope_pair_order(3, 1, 2, 8)
     assert sorted(order.tolist()) == list(range(6 * 8))
