@@ -266,7 +266,12 @@ int saga_silu_mul(const saga_tensor* gate_up, saga_tensor* y, saga_stream_t stre
  * w is [N, K] (unit column stride), or packed: a contiguous 16-byte aligned
  * 4-D [N/16, K/32, 16, 32] with packed[t][j][r][c] = w[16t + r][32j + c],
  * each MFMA fragment 1 KB contiguous (measured faster: one DRAM region per
- * load instruction); results are bit-identical.
+ * load instruction); results are bit-identical.  Or, for at most 8 rows of
+ * x, packed in 8-row tiles: a contiguous 16-byte aligned 3-D [N/8, K/64, 512]
+ * with packed[t][j][32r + c] = w[8t + r % 8][64j + 32 (r / 8) + c] (K % 64 ==
+ * 0): one fragment holds 8 rows over 64 columns, so weights of few 16-row
+ * tiles are read by twice the workgroups (equal to rounding: the sums run
+ * in another order); never split over K.
  * workspace (optional, 256-byte aligned, saga_gemv_workspace_bytes(M, N, K)
  * bytes, no initial contents needed): with it, weights with few 16-row
  * tiles and long rows (the MLP down projection) are read by workgroups over

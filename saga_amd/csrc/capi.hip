@@ -710,17 +710,25 @@ int make_rope(int64_t N, int32_t dt, int64_t n_q, int64_t n_k, int64_t n_v, floa
 int make_gemv(const saga_tensor* x, const saga_tensor* w, const saga_tensor* bias, float rms_eps, GemvParams& p) {
   int rc;
   if ((rc = check_tensor(x, "x", 2))) return rc;
-  const bool packed = w && w->ndim == 4;
-  if ((rc = check_tensor(w, "w", packed ? 4 : 2))) return rc;
+  const bool packed = w && w->ndim == 4;   // 16-row tiles
+  const bool packed8 = w && w->ndim == 3;  // 8-row tiles
+  if ((rc = check_tensor(w, "w", packed ? 4 : packed8 ? 3 : 2))) return rc;
   if (x->dtype != SAGA_DTYPE_BF16 || w->dtype != SAGA_DTYPE_BF16) return fail(SAGA_ERR_UNSUPPORTED, "gemv: bf16 only");
   const int64_t M = x->shape[0], K = x->shape[1];
-  const int64_t N = packed ? w->shape[0] * 16 : w->shape[0];
+  const int64_t N = packed ? w->shape[0] * 16 : packed8 ? w->shape[0] * 8 : w->shape[0];
   if (packed) {
     // [N/16][K/32][16][32], contiguous (the stride of a size-1 dim is immaterial)
     if (w->shape[2] != 16 || w->shape[3] != 32 || w->shape[1] * 32 != K || w->stride[3] != 1 || w->stride[2] != 32 ||
         (w->shape[1] > 1 && w->stride[1] != 512) || (w->shape[0] > 1 && w->stride[0] != w->shape[1] * 512))
       return fail(SAGA_ERR_INVALID, "gemv: packed w must be contiguous [N/16, K/32, 16, 32] with K = x.shape[1]");
     if (reinterpret_cast<uintptr_t>(w->data) % 16) return fail(SAGA_ERR_INVALID, "gemv: packed w must be 16-byte aligned");
+  } else if (packed8) {
+    // [N/8][K/64][512], contiguous
+    if (w->shape[2] != 512 || w->shape[1] * 64 != K || w->stride[2] != 1 ||
+        (w->shape[1] > 1 && w->stride[1] != 512) || (w->shape[0] > 1 && w->stride[0] != w->shape[1] * 512))
+      return fail(SAGA_ERR_INVALID, "gemv: 8-row packed w must be contiguous [N/8, K/64, 512] with K = x.shape[1]");
+    if (reinterpret_cast<uintptr_t>(w->data) % 16) return fail(SAGA_ERR_INVALID, "gemv: packed w must be 16-byte aligned");
+    if (M > 8) return fail(SAGA_ERR_UNSUPPORTED, "gemv: 8-row packed w takes at most 8 rows of x");
   } else if (w->shape[1] != K) {
     return fail(SAGA_ERR_INVALID, "gemv: w must be [N, K] with K = x.shape[1]");
   }
@@ -737,8 +745,8 @@ int make_gemv(const saga_tensor* x, const saga_tensor* w, const saga_tensor* bia
   p.x = x->data;
   p.x_ld = x->stride[0];
   p.w = w->data;
-  p.w_ld = packed ? 0 : w->stride[0];
-  p.w_packed = packed ? 1 : 0;
+  p.w_ld = packed || packed8 ? 0 : w->stride[0];
+  p.w_packed = packed ? 1 : packed8 ? 2 : 0;
   p.bias = bias ? bias->data : nullptr;
   p.M = static_cast<int32_t>(M);
   p.N = static_cast<int32_t>(N);
@@ -868,7 +876,7 @@ int saga_gemv(const saga_tensor* x, const saga_tensor* w, const saga_tensor* bia
   p.epilogue = epilogue;
   const int splits = gemv_splits(p.N, p.K);
   const size_t need = saga_gemv_workspace_bytes(p.M, p.N, p.K);
-  if (workspace && splits > 1 && workspace_bytes >= need) {
+  if (workspace && splits > 1 && workspace_bytes >= need && p.w_packed != 2) {
     if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(SAGA_ERR_WORKSPACE, "workspace must be 256-byte aligned");
     p.splits = splits;
     p.part = static_cast<float*>(workspace);

@@ -67,31 +67,49 @@ __device__ __forceinline__ GemvPre gemv_prefetch(const GemvParams& p, int m, int
 // TPW tiles of 16 W rows per workgroup (rows n0 .. n0 + 16*TPW): each k step
 // loads one x fragment and TPW W fragments, so a wave keeps TPW x more weight
 // bytes in flight per register of x.
-template <int WAVES, int EPI, int TPW>
+//
+// HALF (at most 8 token rows, W packed in 8-row tiles): a tile is 8 W rows
+// and a k step 64 wide.  A fragment rows 0-7 are the tile's rows at k
+// [64j, 64j + 32) and rows 8-15 the same rows at [64j + 32, 64j + 64); the B
+// columns 0-7 are the token rows at the first half and 8-15 at the second.
+// Output rows i < 8 of columns c < 8 and rows 8 + i of columns 8 + c then
+// hold the two halves of y[c, n0 + i] (the other two quarters are unused
+// products), added across lanes before the reduction: lane l = 16s + c
+// (s < 2, c < 8) and lane l + 40.  Weights of few 16-row tiles (a 1536-row projection: 96) so
+// spread over twice the workgroups, each CU streaming half the bytes, with no
+// split over K.  UNROLL: k steps per wave and burst.
+template <int WAVES, int EPI, int TPW, bool HALF = false, int UNROLL = kGemvUnroll>
 __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(TPW == 2 ? 3 : 4, 8)))
 gemv_kernel(GemvParams p) {
+  static_assert(!HALF || TPW == 1, "8-row tiles: one per wave");
+  constexpr int TR = HALF ? 8 : 16;  // W rows per tile
   __shared__ float red[WAVES][TPW][64][4];
   __shared__ float rsq[WAVES][64];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int col = lane & 15, s = lane >> 4;
-  const int n0 = blockIdx.x * 16 * TPW;
+  const int n0 = blockIdx.x * TR * TPW;
   const int split = blockIdx.y;  // K range of this workgroup (split-K: partial sums out)
-  const bool mvalid = col < p.M;
-  const int m = mvalid ? col : 0;
+  const int mrow = HALF ? (col & 7) : col;  // token row of this lane's x fragments
+  const bool mvalid = mrow < p.M;
+  const int m = mvalid ? mrow : 0;
   // A fragment of tile t at k step j: wrow[t] + j * wstep.  Row-major W:
   // 16 rows x 64 B, one row per W row stride; packed W: 1 KB contiguous
   const int64_t wstep = p.w_packed ? 1024 : 64;
+  const int steps = p.K / (HALF ? 64 : 32);
   const char* wrow[TPW];
 #pragma unroll
   for (int t = 0; t < TPW; ++t)
     wrow[t] = static_cast<const char*>(p.w) +
-              (p.w_packed ? static_cast<int64_t>(n0 / 16 + t) * (p.K / 32) * 1024 + col * 64 + s * 16
+              (p.w_packed ? static_cast<int64_t>(n0 / TR + t) * steps * 1024 + col * 64 + s * 16
                           : (static_cast<int64_t>(n0 + 16 * t + col) * p.w_ld + 8 * s) * 2);
-  const char* xrow = static_cast<const char*>(p.x) + (static_cast<int64_t>(m) * p.x_ld + 8 * s) * 2;
+  // x fragment: 8 k values of token row m (HALF: of the k half of column col)
+  const int64_t xstep = HALF ? 128 : 64;
+  const char* xrow = static_cast<const char*>(p.x) +
+                     (static_cast<int64_t>(m) * p.x_ld + 8 * s + (HALF ? 32 * (col >> 3) : 0)) * 2;
   // the tile this wave finishes (waves 0..TPW-1) and its epilogue inputs
+  // (HALF: lanes s < 2 own rows n0 + 4s .. + 3; lanes s >= 2 load the same)
   const int tf = w < TPW ? w : TPW - 1;
-  const int nf = n0 + 16 * tf + 4 * s;
-  const int steps = p.K / 32;
+  const int nf = n0 + TR * tf + 4 * (HALF ? (s & 1) : s);
   // this workgroup's k steps [k0, k1), dealt to its waves round robin (wave
   // w: k0 + w, k0 + w + WAVES, ...): at any moment the workgroup's waves
   // read neighbouring fragments of its tiles (measured faster than a
@@ -100,7 +118,6 @@ gemv_kernel(GemvParams p) {
   const int nmine = (k1 - k0 - w + WAVES - 1) / WAVES;
   const int jstride = WAVES;
   const int jbase = k0 + w;
-  constexpr int UNROLL = kGemvUnroll;
   f32x4 acc[TPW];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -114,7 +131,7 @@ gemv_kernel(GemvParams p) {
       const int jj = min(max(jbase + jstride * min(i0 + u, nmine - 1), k0), k1 - 1);
 #pragma unroll
       for (int t = 0; t < TPW; ++t) a[u][t] = ld16(wrow[t] + static_cast<int64_t>(jj) * wstep);
-      b[u] = mvalid ? ld16(xrow + static_cast<int64_t>(jj) * 64) : u32x4{0u, 0u, 0u, 0u};
+      b[u] = mvalid ? ld16(xrow + static_cast<int64_t>(jj) * xstep) : u32x4{0u, 0u, 0u, 0u};
     }
   };
   auto use_burst = [&](int i0, const u32x4 (&a)[UNROLL][TPW], const u32x4 (&b)[UNROLL]) {
@@ -151,7 +168,16 @@ gemv_kernel(GemvParams p) {
     __builtin_amdgcn_sched_barrier(0);
     use_burst(i0, a, b);
   }
+  if constexpr (HALF) {
+    // fold the second k half into lanes l = 16s + c (s < 2, c < 8): + lane l + 40
+    // (rows 8 + 4s + r, column 8 + c); the x^2 sums of the two halves of token
+    // row c & 7 meet in lanes c and c ^ 8
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[0][r] += __shfl(acc[0][r], (lane + 40) & 63);
+    ssq += __shfl_xor(ssq, 8);
+  }
   // lane (col, s): rows n0 + 16t + 4s + r of tile t for token row m = col
+  // (HALF: rows n0 + 4s + r, s < 2, col < 8)
 #pragma unroll
   for (int t = 0; t < TPW; ++t)
 #pragma unroll
@@ -159,6 +185,7 @@ gemv_kernel(GemvParams p) {
   rsq[w][lane] = ssq;
   lds_sync();
   if (w >= TPW) return;
+  if (HALF && (s >= 2 || col >= 8)) return;  // folded into the lanes above
   const int t = w;
   float v[4] = {0.f, 0.f, 0.f, 0.f};
   float sq = 0.f;
@@ -314,6 +341,23 @@ __global__ void __launch_bounds__(64) gemv_splitk_epilogue(GemvParams p) {
 
 template <int EPI>
 static hipError_t launch_gemv_epi(const GemvParams& p, hipStream_t st) {
+  if (p.w_packed == 2) {
+    // 8-row tiles: 16 waves for long rows (the MLP down projection: 140 k steps
+    // of 64, 9 per wave), else 4; the burst sized to the wave's share
+    const unsigned tiles8 = static_cast<unsigned>(p.N / 8);
+    const int steps = p.K / 64;
+    if (steps >= 64) {
+      if ((steps + 15) / 16 <= 9)
+        hipLaunchKernelGGL((gemv_kernel<16, EPI, 1, true, 9>), dim3(tiles8, 1), dim3(1024), 0, st, p);
+      else
+        hipLaunchKernelGGL((gemv_kernel<16, EPI, 1, true, 12>), dim3(tiles8, 1), dim3(1024), 0, st, p);
+    } else if ((steps + 3) / 4 <= 6) {
+      hipLaunchKernelGGL((gemv_kernel<4, EPI, 1, true, 6>), dim3(tiles8, 1), dim3(256), 0, st, p);
+    } else {
+      hipLaunchKernelGGL((gemv_kernel<4, EPI, 1, true, 12>), dim3(tiles8, 1), dim3(256), 0, st, p);
+    }
+    return hipGetLastError();
+  }
   const unsigned tiles = static_cast<unsigned>(p.N / 16);
   if (p.part) {
     hipLaunchKernelGGL((gemv_kernel<4, EPI, 1>), dim3(tiles, p.splits), dim3(256), 0, st, p);

@@ -198,7 +198,9 @@ struct GemvParams {
   int64_t x_ld;
   const void* w;  // bf16 [N, K] (row stride w_ld), or packed [N/16][K/32][16][32]
   int64_t w_ld;
-  int32_t w_packed;  // packed: every MFMA A fragment (16 rows x 32 k) is 1 KB contiguous
+  // 1: packed [N/16][K/32][16][32], every MFMA A fragment (16 rows x 32 k) 1 KB
+  // contiguous; 2: packed [N/8][K/64][512] in 8-row tiles (at most 8 token rows)
+  int32_t w_packed;
   const void* bias;  // bf16 [N] or null
   void* y;           // bf16 [M, N] (SILU_PAIRS: [M, N / 2])
   int64_t y_ld;

@@ -225,12 +225,16 @@ class SagaDecoder:
             self.kw_o = list(self.w_o)
             self.kw_d = list(self.w_d)
             if self.pack_weights:
-                # MFMA-fragment order: every 16 x 32 fragment 1 KB contiguous
+                # MFMA-fragment order: every fragment 1 KB contiguous.  The
+                # projections of few 16-row tiles (q/k/v, o, down: 96-120 at
+                # the 1.5B shape) in 8-row tiles when the batch allows (<= 8
+                # rows: twice the workgroups, no split over K)
                 pk = ops.pack_gemv_weight
-                self.kw_qkv = [pk(w) for w in self.kw_qkv]
+                rows8 = 8 if self.batch <= 8 and s.hidden % 64 == 0 and s.intermediate % 64 == 0 else 16
+                self.kw_qkv = [pk(w, rows8) for w in self.kw_qkv]
                 self.kw_gu = [pk(w) for w in self.kw_gu]
-                self.kw_o = [pk(w) for w in self.w_o]
-                self.kw_d = [pk(w) for w in self.w_d]
+                self.kw_o = [pk(w, rows8) for w in self.w_o]
+                self.kw_d = [pk(w, rows8) for w in self.w_d]
                 self.kw_lm = pk(self.kw_lm)
                 if not self.keep_source_weights:
                     self.w_qkv = self.w_o = self.w_gu = self.w_d = None
@@ -261,9 +265,13 @@ class SagaDecoder:
 
     @staticmethod
     def _unpack(w: torch.Tensor) -> torch.Tensor:
-        """Row-major [N, K] of a packed [N/16, K/32, 16, 32] weight."""
+        """Row-major [N, K] of a packed weight: [N/16, K/32, 16, 32] or, in
+        8-row tiles, [N/8, K/64, 512] (ops.pack_gemv_weight)."""
         if w.dim() == 2:
             return w
+        if w.dim() == 3:
+            n8, k64 = w.shape[0], w.shape[1]
+            return w.reshape(n8, k64, 2, 8, 32).permute(0, 3, 1, 2, 4).reshape(n8 * 8, k64 * 64)
         n16, k32 = w.shape[0], w.shape[1]
         return w.permute(0, 2, 1, 3).reshape(n16 * 16, k32 * 32)
 

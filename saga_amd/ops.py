@@ -460,18 +460,28 @@ def silu_mul(gate_up, out=None):
     return out
 
 
-def pack_gemv_weight(w: torch.Tensor) -> torch.Tensor:
-    """W [N, K] -> the packed layout [N/16, K/32, 16, 32] that gemv and
-    gemv_rope_kv also accept: every 16-row x 32-column MFMA fragment is 1 KB
-    contiguous (one DRAM region per load instruction)."""
+def pack_gemv_weight(w: torch.Tensor, tile_rows: int = 16) -> torch.Tensor:
+    """W [N, K] -> a packed layout that gemv and gemv_rope_kv also accept:
+    every MFMA fragment is 1 KB contiguous (one DRAM region per load).
+    tile_rows 16: [N/16, K/32, 16, 32], fragment = 16 rows x 32 columns.
+    tile_rows 8: [N/8, K/64, 512], fragment row 8h + r = W row 8t + r at
+    columns [64j + 32h, 64j + 32h + 32): weights of few 16-row tiles (the
+    1536-row projections) spread over twice the workgroups, for at most 8
+    rows of x."""
     N, K = w.shape
     if N % 16 or K % 32:
         raise ValueError("saga_amd: packing needs N % 16 == 0 and K % 32 == 0")
-    return w.reshape(N // 16, 16, K // 32, 32).permute(0, 2, 1, 3).contiguous()
+    if tile_rows == 16:
+        return w.reshape(N // 16, 16, K // 32, 32).permute(0, 2, 1, 3).contiguous()
+    if tile_rows != 8:
+        raise ValueError("saga_amd: tile_rows must be 16 or 8")
+    if K % 64:
+        raise ValueError("saga_amd: 8-row packing needs K % 64 == 0")
+    return w.reshape(N // 8, 8, K // 64, 2, 32).permute(0, 2, 3, 1, 4).reshape(N // 8, K // 64, 512).contiguous()
 
 
 def _gemv_n(w: torch.Tensor) -> int:
-    return w.shape[0] * 16 if w.dim() == 4 else w.shape[0]
+    return w.shape[0] * {4: 16, 3: 8}.get(w.dim(), 1)
 
 
 def gemv(x, w, bias=None, rms_eps=None, epilogue="store", out=None, split_k=True, workspace=None):

@@ -215,3 +215,37 @@ def test_gemv_packed_weight_layout_checks():
     assert call(bad) == -1 and "packed" in _err()
     assert call(_t((120, 48, 16, 32), data=0x100008)) == -1 and "aligned" in _err()
     assert call(_t((120, 48, 16, 16))) == -1
+
+
+def test_gemv_packed8_weight_layout_checks():
+    """A 3-D w is the 8-row-tile layout [N/8, K/64, 512]: K must match x, the
+    tensor must be contiguous and 16-byte aligned, x at most 8 rows; errors
+    come back before any launch."""
+    lib = _lib.load()
+    y = _t((8, 1920))
+
+    def call(w, x=_t((8, 1536))):
+        return lib.saga_gemv(ctypes.byref(x), ctypes.byref(w), None, -1.0, 0, ctypes.byref(y), None, 0, None)
+
+    assert call(_t((240, 23, 512))) == -1 and "8-row" in _err()                    # K / 64 = 24 expected
+    assert call(_t((240, 24, 256))) == -1 and "8-row" in _err()                    # fragment of 512
+    assert call(_t((240, 24, 512), strides=(24 * 512, 1, 24))) == -1 and "8-row" in _err()
+    assert call(_t((240, 24, 512), data=0x100008)) == -1 and "aligned" in _err()
+    assert call(_t((240, 24, 512)), x=_t((9, 1536))) == -2 and "at most 8 rows" in _err()
+
+
+def test_pack_gemv_weight_8_row_tiles_on_cpu():
+    """pack_gemv_weight(w, 8)[t, j, 32 r + c] = w[8t + r % 8, 64j + 32 (r // 8) + c],
+    and the decoder's unpacking inverts both layouts."""
+    import torch
+    from saga_amd import ops
+    from saga_amd.decoder import SagaDecoder
+    w = torch.arange(32 * 192, dtype=torch.float32).reshape(32, 192)
+    p = ops.pack_gemv_weight(w, 8)
+    assert p.shape == (4, 3, 512)
+    for t, j, r, c in [(0, 0, 0, 0), (3, 2, 15, 31), (1, 1, 8, 5), (2, 0, 7, 30)]:
+        assert p[t, j, 32 * r + c] == w[8 * t + r % 8, 64 * j + 32 * (r // 8) + c]
+    for rows in (16, 8):
+        assert torch.equal(SagaDecoder._unpack(ops.pack_gemv_weight(w, rows)), w)
+    with pytest.raises(ValueError, match="K % 64"):
+        ops.pack_gemv_weight(torch.zeros(16, 96), 8)

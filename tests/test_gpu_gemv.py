@@ -213,6 +213,68 @@ def test_packed_weights_give_identical_results(M, K, N, epilogue):
         assert torch.equal(ya, yb)
 
 
+@pytest.mark.parametrize("M,K,N", [(8, 1536, 1536), (8, 8960, 1536), (8, 1536, 1920), (5, 960, 2560), (1, 64, 32),
+                                   (7, 2560, 960)])
+@pytest.mark.parametrize("epilogue", ["store", "add", "silu_pairs"])
+def test_packed8_weights_match_float64(M, K, N, epilogue):
+    """W in 8-row tiles [N/8, K/64, 512] (the two 32-column halves of a
+    64-column step in one MFMA, folded across lanes): every epilogue, with
+    and without the fused RMS scale, agrees with the float64 product as the
+    16-row layout does (its sums run in another order: equal to rounding,
+    not bit-identical), and repeats bit for bit."""
+    rng = np.random.default_rng(M * 11 + N + K)
+    x, w, b = _data(rng, M, K, N)
+    xd, wd = dev(x, "bf16"), dev(w, "bf16")
+    w8 = ops.pack_gemv_weight(wd, 8)
+    assert w8.shape == (N // 8, K // 64, 512)
+    y0 = O.round_bf16(rng.standard_normal((M, N // 2 if epilogue == "silu_pairs" else N), dtype=np.float32))
+    bias = dev(b, "bf16") if epilogue == "store" else None
+    for rms in (None, 1e-6):
+        xs = x.astype(np.float64)
+        if rms:
+            xs = xs / np.sqrt((xs ** 2).mean(-1, keepdims=True) + rms)
+        prod = xs @ w.astype(np.float64).T
+        if epilogue == "store":
+            ref = prod + b
+        elif epilogue == "add":
+            ref = prod + y0
+        else:
+            g, u = prod[:, 0::2], prod[:, 1::2]
+            ref = g / (1 + np.exp(-g)) * u
+        outs = [ops.gemv(xd, w8, bias=bias, rms_eps=rms, epilogue=epilogue, out=dev(y0, "bf16")) for _ in range(2)]
+        y16 = ops.gemv(xd, ops.pack_gemv_weight(wd), bias=bias, rms_eps=rms, epilogue=epilogue, out=dev(y0, "bf16"))
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0], outs[1])
+        got = host(outs[0])
+        assert rel_l2(got, ref) < 4e-3 and rel_l2(host(y16), ref) < 4e-3
+        assert np.max(np.abs(got - ref)) <= 2 ** -7 * np.max(np.abs(ref)) + 1e-3
+        assert torch.allclose(outs[0].float(), y16.float(), rtol=2 ** -7, atol=2e-3)
+
+
+def test_packed8_rope_kv_and_row_limit():
+    """The fused q/k/v projection + RoPE + cache append on 8-row tiles equals
+    the 16-row layout to rounding; more than 8 rows of x are refused."""
+    rng = np.random.default_rng(83)
+    M, K, n_q, n_k, n_v, d = 8, 1536, 12, 1, 2, 128
+    x, w, b = _data(rng, M, K, (n_q + n_k + n_v) * d)
+    xd, wd, bd = dev(x, "bf16"), dev(w, "bf16"), dev(b, "bf16")
+    pos = torch.arange(M, dtype=torch.int32, device="cuda") * 3 + 1
+    outs = []
+    for rows in (16, 8):
+        kc = torch.zeros(M, n_k, 64, d, dtype=torch.bfloat16, device="cuda")
+        vc = torch.zeros(M, n_v, 64, d, dtype=torch.bfloat16, device="cuda")
+        q = ops.gemv_rope_kv(xd, ops.pack_gemv_weight(wd, rows), bd, n_q, n_k, n_v, 1e6, pos, kc, vc, rms_eps=1e-6,
+                             rope_table=ops.rope_table(pos, d, 1e6))
+        outs.append((q, kc, vc))
+    torch.cuda.synchronize()
+    for a, c in zip(outs[0], outs[1]):
+        assert torch.allclose(a.float(), c.float(), rtol=2 ** -7, atol=2e-3)
+        assert a.float().abs().sum() > 0
+    x9 = dev(O.round_bf16(rng.standard_normal((9, 64), dtype=np.float32)), "bf16")
+    with pytest.raises(RuntimeError, match="at most 8 rows"):
+        ops.gemv(x9, ops.pack_gemv_weight(wd[:32, :64].contiguous(), 8))
+
+
 def test_packed_rope_kv_projection_identical():
     rng = np.random.default_rng(81)
     M, K, n_q, n_k, n_v, d = 8, 1536, 12, 1, 2, 128
