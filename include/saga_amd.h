@@ -313,6 +313,22 @@ int saga_gemv_rope_kv(const saga_tensor* x, const saga_tensor* w, const saga_ten
 int saga_rope_table(const int32_t* pos, int64_t N, int64_t d, float theta, float* table,
                     saga_stream_t stream);
 
+/* The opening of a decode step in one launch: x[b, :] = embed[tokens[b], :]
+ * for the B = x.shape[0] token rows (embed [V, H], x [B, H], one float
+ * dtype; a token id outside [0, V) writes a NaN row), and, when rope_table
+ * is given, the rows' rotations for positions pos as saga_rope_table
+ * writes them (d even).  Replaces Qwen2Model.forward's embed_tokens and
+ * rotary_emb calls (transformers models/qwen2/modeling_qwen2.py:356, 385). */
+int saga_embed_rope(const int64_t* tokens, const saga_tensor* embed, saga_tensor* x, const int32_t* pos,
+                    int64_t d, float theta, float* rope_table, saga_stream_t stream);
+
+/* The close of a decode step: pos[i] += 1 and kv_len[i] += 1 for i < n
+ * (either may be NULL): the one-token growth of the cache that the
+ * reference's decode loop gets from past_key_values (speedup.py:164-169;
+ * transformers models/qwen2/modeling_qwen2.py:361-364 derives the next
+ * position from the cache length). */
+int saga_advance_positions(int32_t* pos, int32_t* kv_len, int64_t n, saga_stream_t stream);
+
 /* out[r] = first index of the maximum of row r of x [rows, N] (bf16); the
  * greedy next token of speedup.py:169/193 (logits.argmax(dim=-1)).  NaN is
  * never the maximum.  workspace (optional, 256-byte aligned,

@@ -76,6 +76,8 @@ _SIGS = {
     "saga_gemv_rope_kv": (ctypes.c_int, [_T, _T, _T, ctypes.c_float, _I64, _I64, _I64, ctypes.c_float, _P, _P,
                                          _T, _T, _T, _P, _P]),
     "saga_rope_table": (ctypes.c_int, [_P, _I64, _I64, ctypes.c_float, _P, _P]),
+    "saga_embed_rope": (ctypes.c_int, [_P, _T, _T, _P, _I64, ctypes.c_float, _P, _P]),
+    "saga_advance_positions": (ctypes.c_int, [_P, _P, _I64, _P]),
     "saga_argmax_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
     "saga_argmax": (ctypes.c_int, [_T, _P, _P, ctypes.c_size_t, _P]),
     "saga_prefill_attention": (ctypes.c_int, [_T, _T, _T, _T, ctypes.c_float, ctypes.c_int32, ctypes.c_int64, _T, _P]),

@@ -794,6 +794,53 @@ int saga_rope_table(const int32_t* pos, int64_t N, int64_t d, float theta, float
   return ok();
 }
 
+int saga_embed_rope(const int64_t* tokens, const saga_tensor* embed, saga_tensor* x, const int32_t* pos, int64_t d,
+                    float theta, float* rope_table, saga_stream_t stream) {
+  int rc;
+  if ((rc = check_tensor(embed, "embed", 2)) || (rc = check_tensor(x, "x", 2))) return rc;
+  if (!is_float(embed->dtype) || x->dtype != embed->dtype)
+    return fail(SAGA_ERR_INVALID, "embed_rope: embed and x must share one float dtype");
+  if (x->shape[1] != embed->shape[1]) return fail(SAGA_ERR_INVALID, "embed_rope: x must be [B, H] of embed [V, H]");
+  if (embed->stride[1] != 1 || x->stride[1] != 1) return fail(SAGA_ERR_INVALID, "innermost strides must be 1");
+  if (!tokens) return fail(SAGA_ERR_INVALID, "embed_rope: null tokens");
+  if (rope_table) {
+    if (!pos) return fail(SAGA_ERR_INVALID, "embed_rope: a rope_table needs pos");
+    if (d < 2 || d % 2 || d > 65536) return fail(SAGA_ERR_INVALID, "embed_rope: an even head_dim >= 2 required");
+    if (reinterpret_cast<uintptr_t>(rope_table) % 16)
+      return fail(SAGA_ERR_INVALID, "embed_rope: rope_table must be 16-byte aligned");
+  }
+  EmbedParams p{};
+  p.tokens = tokens;
+  p.embed = embed->data;
+  p.e_ld = embed->stride[0];
+  p.x = x->data;
+  p.x_ld = x->stride[0];
+  p.B = static_cast<int32_t>(x->shape[0]);
+  p.H = static_cast<int32_t>(x->shape[1]);
+  p.dt = x->dtype;
+  p.V = embed->shape[0];
+  const int64_t es = elt_size(x->dtype);
+  p.vec = (p.H * es) % 16 == 0 && reinterpret_cast<uintptr_t>(embed->data) % 16 == 0 &&
+          reinterpret_cast<uintptr_t>(x->data) % 16 == 0 && (p.e_ld * es) % 16 == 0 && (p.x_ld * es) % 16 == 0;
+  p.pos = pos;
+  p.d = static_cast<int32_t>(d);
+  p.theta = theta;
+  p.table = rope_table;
+  if ((rc = hip_status(launch_embed_rope(p, static_cast<hipStream_t>(stream)), "embed_rope launch"))) return rc;
+  return ok();
+}
+
+int saga_advance_positions(int32_t* pos, int32_t* kv_len, int64_t n, saga_stream_t stream) {
+  if (n < 0 || n >= (1LL << 31)) return fail(SAGA_ERR_INVALID, "advance_positions: 0 <= n < 2^31 required");
+  if (n > 0 && !pos && !kv_len) return fail(SAGA_ERR_INVALID, "advance_positions: null pos and kv_len");
+  if (n == 0) return ok();
+  int rc;
+  if ((rc = hip_status(launch_advance(pos, kv_len, static_cast<int>(n), static_cast<hipStream_t>(stream)),
+                       "advance_positions launch")))
+    return rc;
+  return ok();
+}
+
 int saga_gemv_rope_kv(const saga_tensor* x, const saga_tensor* w, const saga_tensor* bias, float rms_eps,
                       int64_t n_q, int64_t n_k, int64_t n_v, float theta, const int32_t* pos, const int32_t* batch,
                       saga_tensor* q_out, saga_tensor* k_cache, saga_tensor* v_cache, const float* rope_table,

@@ -73,6 +73,54 @@ hipError_t launch_rope_table(const int32_t* pos, int N, int d, float theta, floa
   return hipGetLastError();
 }
 
+// The opening of a decode step, one block per token row b: x[b] =
+// embed[tokens[b]] (16-byte chunks when rows allow, else element by element,
+// exact for every float dtype; a token id outside [0, V) writes a NaN row)
+// and, with a table, the row's rotations as rope_table_kernel computes them.
+__global__ void __launch_bounds__(256) embed_rope_kernel(EmbedParams p) {
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const int64_t tok = p.tokens[b];
+  const bool ok = tok >= 0 && tok < p.V;
+  if (ok && p.vec) {
+    const int64_t es = p.dt == SAGA_DTYPE_F32 ? 4 : 2;
+    const char* src = static_cast<const char*>(p.embed) + tok * p.e_ld * es;
+    char* dst = static_cast<char*>(p.x) + static_cast<int64_t>(b) * p.x_ld * es;
+    const int chunks = static_cast<int>(p.H * es / 16);
+    for (int c = tid; c < chunks; c += 256) *reinterpret_cast<u32x4*>(dst + 16 * c) = ld16(src + 16 * c);
+  } else {
+    for (int i = tid; i < p.H; i += 256)
+      store_from_f32(p.x, p.dt, static_cast<int64_t>(b) * p.x_ld + i,
+                     ok ? load_as_f32(p.embed, p.dt, tok * p.e_ld + i) : __builtin_nanf(""));
+  }
+  if (p.table) {
+    const int half = p.d / 2;
+    const int pos = p.pos[b];
+    for (int i = tid; i < half; i += 256) {
+      float cs, sn;
+      rope_cos_sin(pos, i, p.d, p.theta, cs, sn);
+      *reinterpret_cast<f32x2*>(p.table + 2 * (static_cast<int64_t>(b) * half + i)) = f32x2{cs, sn};
+    }
+  }
+}
+
+hipError_t launch_embed_rope(const EmbedParams& p, hipStream_t st) {
+  hipLaunchKernelGGL(embed_rope_kernel, dim3(p.B), dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
+// The close of a decode step: every row's position and cache length + 1.
+__global__ void __launch_bounds__(256) advance_kernel(int32_t* pos, int32_t* kv_len, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  if (pos) pos[i] += 1;
+  if (kv_len) kv_len[i] += 1;
+}
+
+hipError_t launch_advance(int32_t* pos, int32_t* kv_len, int n, hipStream_t st) {
+  hipLaunchKernelGGL(advance_kernel, dim3((n + 255) / 256), dim3(256), 0, st, pos, kv_len, n);
+  return hipGetLastError();
+}
+
 __global__ void __launch_bounds__(256) rmsnorm_kernel(RowParams p) {
   __shared__ float red[4];
   const int n = blockIdx.x;

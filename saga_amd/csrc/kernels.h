@@ -178,6 +178,23 @@ hipError_t launch_rope_kv_append(const RopeParams& p, hipStream_t st);
 // table[n][i] = (cos, sin)(pos[n] * theta^(-2i/d)), i < d/2, n < N
 hipError_t launch_rope_table(const int32_t* pos, int N, int d, float theta, float* table, hipStream_t st);
 
+// x[b] = embed[tokens[b]] for b < B (+ the rows' rotations into table when given)
+struct EmbedParams {
+  const int64_t* tokens;
+  const void* embed;  // [V, H], row stride e_ld
+  int64_t e_ld;
+  void* x;  // [B, H], row stride x_ld, dtype dt
+  int64_t x_ld;
+  int32_t B, H, dt, vec;  // vec: rows copied in 16-byte chunks
+  int64_t V;
+  const int32_t* pos;  // [B] (with table)
+  int32_t d;
+  float theta;
+  float* table;  // [B][d/2][2] or null
+};
+hipError_t launch_embed_rope(const EmbedParams& p, hipStream_t st);
+hipError_t launch_advance(int32_t* pos, int32_t* kv_len, int n, hipStream_t st);
+
 // Row-wise ops: rmsnorm (y = w * x * rsqrt(mean(x^2) + eps)) and silu_mul.
 struct RowParams {
   const void* x;

@@ -360,10 +360,10 @@ class SagaDecoder:
         s, d, B = self.shape, self.shape.head_dim, self.batch
         ws = self.ws
         x = self._x
-        torch.index_select(self.embed, 0, self.tokens, out=x)
+        # the token rows' embeddings and their rotations (once for all layers)
+        ops.embed_rope(self.tokens, self.embed, x, self.pos, d, s.rope_theta,
+                       rope_table=self._rope if self.fuse_rope else None)
         q4 = self._q.view(B, s.n_q, 1, d)
-        if self.fuse_rope:
-            ops.rope_table(self.pos, d, s.rope_theta, out=self._rope)  # once for all layers
         for l in range(s.layers):
             if self.fuse_rope:
                 ops.gemv_rope_kv(x, self.kw_qkv[l], self.kb_qkv[l], s.n_q, s.n_k, s.n_v, s.rope_theta, self.pos,
@@ -405,8 +405,7 @@ class SagaDecoder:
             ops.rmsnorm(x, self.ln_f, s.eps, out=self._h)
             torch.mm(self._h, self.lm_head.t(), out=self._logits)
             torch.argmax(self._logits, dim=-1, out=self.tokens)
-        self.pos.add_(1)
-        self.kv_len.add_(1)
+        ops.advance_positions(self.pos, self.kv_len)
 
     def _vanilla_attention(self, q4: torch.Tensor, K: torch.Tensor, V: torch.Tensor) -> None:
         """speedup.py:76-83, vanilla mode: the decode step through the base

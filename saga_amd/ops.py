@@ -564,6 +564,37 @@ def rope_table(pos, d, theta, out=None):
     return out
 
 
+def embed_rope(tokens, embed, out, pos=None, d=None, theta=None, rope_table=None):
+    """The opening of a decode step in one launch: out[b] = embed[tokens[b]]
+    (tokens int64 [B], embed [V, H], out [B, H]; an id outside [0, V) gives
+    a NaN row) and, when rope_table (fp32 [B, d/2, 2]) is given, the rows'
+    rotations at positions pos (int32 [B]) as rope_table() computes them."""
+    _need_gpu(tokens, embed, out, pos, rope_table)
+    if tokens.dtype != torch.int64 or not tokens.is_contiguous() or tokens.shape != (out.shape[0],):
+        raise ValueError("saga_amd: tokens must be a contiguous int64 [B] tensor")
+    if rope_table is not None:
+        if pos is None or pos.dtype != torch.int32 or not pos.is_contiguous() or pos.shape != tokens.shape:
+            raise ValueError("saga_amd: pos must be a contiguous int32 [B] tensor")
+        if (rope_table.dtype != torch.float32 or not rope_table.is_contiguous()
+                or tuple(rope_table.shape) != (out.shape[0], d // 2, 2)):
+            raise ValueError("saga_amd: rope_table must be a contiguous float32 [B, d/2, 2] tensor")
+    _lib.check(_lib.load().saga_embed_rope(_lib.ptr(tokens), _lib.tensor(embed), _lib.tensor(out), _lib.ptr(pos),
+                                           int(d or 0), float(theta or 0.0), _lib.ptr(rope_table),
+                                           _lib.stream_of(out)), "embed_rope")
+    return out
+
+
+def advance_positions(pos, kv_len=None):
+    """pos += 1 and kv_len += 1 (int32 [B] tensors) in one launch: the close
+    of a decode step."""
+    _need_gpu(pos, kv_len)
+    for t in (pos, kv_len):
+        if t is not None and (t.dtype != torch.int32 or not t.is_contiguous() or t.shape != pos.shape):
+            raise ValueError("saga_amd: pos and kv_len must be contiguous int32 tensors of one shape")
+    _lib.check(_lib.load().saga_advance_positions(_lib.ptr(pos), _lib.ptr(kv_len), pos.numel(), _lib.stream_of(pos)),
+               "advance_positions")
+
+
 def argmax_rows(x, out=None, workspace=None):
     """First index of each row's maximum (bf16 [rows, N]) -> int64 [rows]."""
     _need_gpu(x, out)

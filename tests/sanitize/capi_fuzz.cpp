@@ -192,7 +192,7 @@ int main(int argc, char** argv) {
                 f = rnd_tensor();
     const uintptr_t p1 = rnd_ptr(), p2 = rnd_ptr(), p3 = rnd_ptr(), p4 = rnd_ptr();
     int rc = 0;
-    switch (next() % 30) {
+    switch (next() % 32) {
       case 0: rc = saga_qk_scores(maybe(a), maybe(b), maybe(c), fake<int32_t>(p1), rnd_float(), &d,
                                   fake<float>(p2), fake<float>(p3), nullptr); break;
       case 1: rc = saga_logit_threshold(maybe(a), fake<int32_t>(p1), fake<float>(p2), fake<float>(p3), nullptr); break;
@@ -244,6 +244,11 @@ int main(int argc, char** argv) {
       case 21: case 22: case 23: case 24: case 25: case 26: case 27: case 28:
         rc = structured(int(next() % 8));
         break;
+      case 29: rc = saga_embed_rope(next() % 2 ? nullptr : fake<int64_t>(p1), maybe(a), &b,
+                                    next() % 2 ? nullptr : fake<int32_t>(p2), rnd_size(), rnd_float(),
+                                    next() % 2 ? nullptr : fake<float>(p3), nullptr); break;
+      case 30: rc = saga_advance_positions(next() % 2 ? nullptr : fake<int32_t>(p1),
+                                           next() % 2 ? nullptr : fake<int32_t>(p2), rnd_size(), nullptr); break;
       default: rc = saga_version() == 100 ? -1 : 0; break;
     }
     if (rc == SAGA_ERR_HIP) ++reached_hip;  // validated: the launch itself found no device

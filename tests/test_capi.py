@@ -249,3 +249,25 @@ def test_pack_gemv_weight_8_row_tiles_on_cpu():
         assert torch.equal(SagaDecoder._unpack(ops.pack_gemv_weight(w, rows)), w)
     with pytest.raises(ValueError, match="K % 64"):
         ops.pack_gemv_weight(torch.zeros(16, 96), 8)
+
+
+def test_embed_rope_and_advance_argument_errors():
+    """The step's opening and close check their operands before any launch."""
+    lib = _lib.load()
+    emb, x = _t((5000, 1536)), _t((8, 1536))
+    tok = ctypes.c_void_p(0x100000)
+    assert lib.saga_embed_rope(None, ctypes.byref(emb), ctypes.byref(x), None, 0, 0.0, None, None) == -1
+    assert "tokens" in _err()
+    assert lib.saga_embed_rope(tok, ctypes.byref(emb), ctypes.byref(_t((8, 1024))), None, 0, 0.0, None, None) == -1
+    assert "[B, H]" in _err()
+    assert lib.saga_embed_rope(tok, ctypes.byref(emb), ctypes.byref(_t((8, 1536), dtype=_lib.DTYPE_F32)), None, 0,
+                               0.0, None, None) == -1
+    tab = ctypes.c_void_p(0x200000)
+    assert lib.saga_embed_rope(tok, ctypes.byref(emb), ctypes.byref(x), None, 128, 1e6, tab, None) == -1
+    assert "pos" in _err()
+    assert lib.saga_embed_rope(tok, ctypes.byref(emb), ctypes.byref(x), tok, 127, 1e6, tab, None) == -1
+    assert lib.saga_embed_rope(tok, ctypes.byref(emb), ctypes.byref(x), tok, 128, 1e6, ctypes.c_void_p(0x200008),
+                               None) == -1 and "aligned" in _err()
+    assert lib.saga_advance_positions(None, None, 4, None) == -1
+    assert lib.saga_advance_positions(None, None, -1, None) == -1
+    assert lib.saga_advance_positions(None, None, 0, None) == 0

@@ -17,6 +17,34 @@ from saga_amd import ops
 pytestmark = pytest.mark.gpu
 
 
+@pytest.mark.parametrize("dt,H", [(torch.bfloat16, 1536), (torch.float32, 960), (torch.float16, 100)])
+def test_embed_rope_and_advance(dt, H):
+    """The step's opening (embedding rows + rotation table in one launch)
+    equals index_select and rope_table bit for bit (16-byte and element
+    copies); an id outside the vocabulary gives a NaN row; the step's close
+    adds one to every position and cache length."""
+    V, B, d = 5000, 4, 128
+    g = torch.Generator(device="cuda").manual_seed(3)
+    emb = torch.randn(V, H, device="cuda", generator=g).to(dt)
+    toks = torch.tensor([0, 4999, 17, 2500], device="cuda", dtype=torch.int64)
+    pos = torch.tensor([0, 32767, 5, 131071], device="cuda", dtype=torch.int32)
+    x = torch.empty(B, H, device="cuda", dtype=dt)
+    table = torch.empty(B, d // 2, 2, device="cuda", dtype=torch.float32)
+    ops.embed_rope(toks, emb, x, pos, d, 1e6, rope_table=table)
+    torch.cuda.synchronize()
+    assert torch.equal(x, emb.index_select(0, toks))
+    assert torch.equal(table, ops.rope_table(pos, d, 1e6))
+    ops.embed_rope(torch.tensor([1, -1, 5000, 2], device="cuda"), emb, x)  # no table
+    torch.cuda.synchronize()
+    assert torch.equal(x[0], emb[1]) and torch.equal(x[3], emb[2])
+    assert torch.isnan(x[1].float()).all() and torch.isnan(x[2].float()).all()
+    kv = pos + 1
+    ops.advance_positions(pos, kv)
+    ops.advance_positions(pos)
+    torch.cuda.synchronize()
+    assert pos.tolist() == [2, 32769, 7, 131073] and kv.tolist() == [2, 32769, 7, 131073]
+
+
 def test_rope_kv_append_matches_oracle():
     rng = np.random.default_rng(40)
     N, n_q, n_k, n_v, d, B, Lmax = 5, 12, 1, 2, 128, 3, 4096
