@@ -95,6 +95,8 @@ typedef struct saga_atopn_layout {
   int64_t slice_pre; /* i32 [b*q_h, 2, nslice + 1] slice ranks (rows of > 2048 slices) */
   int64_t slice_o;   /* f32 [b*q_h, nslice, d] partial sum_e exp(x_e - m) V[e] of short slices */
   int64_t slice_ml;  /* f32 [b*q_h, nslice, 2] partial (m, sum_e exp(x_e - m)) of short slices */
+  int64_t row_part;  /* f32 [b*q_h, 4, d + 4] partials (m, l, -, -, o) of a row's gather split over blocks */
+  int64_t row_cnt;   /* i32 [b*q_h] blocks of a split row done (zeroed by the slice kernel) */
   int64_t total_bytes;
 } saga_atopn_layout;
 
@@ -172,8 +174,10 @@ int saga_atopn_decode(const saga_tensor* query, const saga_tensor* key, const sa
                       size_t workspace_bytes, saga_stream_t stream);
 
 /* saga_atopn_decode with the kernels of its selection and softmax . V chosen
- * per call (no counterpart in the reference; results are identical in every
- * variant, so this only serves A/B measurement and tests):
+ * per call (no counterpart in the reference; every variant selects the same
+ * lists, counts and thresholds and its outputs agree to fp32 rounding -- the
+ * sums are grouped by other block shapes -- so this only serves A/B
+ * measurement and tests):
  *   SAGA_K2_AUTO       by shape, as saga_atopn_decode;
  *   SAGA_K2_ROW_BLOCK  one block per (batch, head) row: its waves run the
  *                      row's 1024-position slices, the row's list is kept in

@@ -43,7 +43,7 @@ class AtopnLayout(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int64) for n in (
         "scores", "scores_ld", "part_max", "part_sum", "part_tail", "nparts", "thresh",
         "sel_idx", "sel_val", "sel_cnt", "sel_total", "nslice", "slice_cap", "slice_idx", "slice_val",
-        "slice_cnt", "slice_pre", "slice_o", "slice_ml", "total_bytes")]
+        "slice_cnt", "slice_pre", "slice_o", "slice_ml", "row_part", "row_cnt", "total_bytes")]
 
 
 # Every symbol include/saga_amd.h declares, with its ctypes signature.

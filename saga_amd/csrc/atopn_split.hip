@@ -52,6 +52,10 @@ constexpr int kRowMaxSlices = 2048;                   // slice ranks kept in LDS
 constexpr int kRowUnroll = 16;                        // V rows in flight per lane group
 constexpr int kWaveUnroll = 12;                       // slice wave: 4 groups x 12 = 48 V rows in flight
 constexpr int kRowMergeSlices = 8;                    // slice partials per merge thread in one burst
+// rows with more entries to gather than this split them over the row
+// kernel's kRowSplit blocks (one CU draws ~28 GB/s of V rows: an overflowing
+// row's 1024 kept rows took 9 us in one block)
+constexpr int kRowSplitMin = 384;
 // auto mode: one block per row when a row has at most this many slices and
 // its list fits one LDS batch (measured on MI355X, attention call at b1-b32,
 // d 64 and 128: 1.02-1.48x at 4k-12k positions; from 16k positions a row's
@@ -299,6 +303,7 @@ __device__ __forceinline__ void slice_wave(const FusedSelParams& p, const PVPara
   if (lane == 0) {
     p.sl_cnt[gw] = n;
     if (sl == 0 && p.t_out) p.t_out[r] = t;
+    if (sl == 0) p.row_cnt[r] = 0;  // the row kernel's split count starts at zero
   }
   if (n > 0 && n <= kSliceSmall) {  // the list is in LDS: coalesced stores, one or two per lane
     wave_lds_sync();
@@ -444,6 +449,7 @@ struct RowShared {
   int sgpre[kRowMaxSlices + 1];
   int sidx[kRowBatch];
   float sval[kRowBatch];
+  int last;  // this block merges the row's split partials
 };
 
 // The row merge of row r by the NT threads of a block (see the file comment).
@@ -452,8 +458,16 @@ struct RowShared {
 // workspace instead of LDS (a host-side choice: with the address space known
 // at compile time the ranks are LDS reads, not flat loads that wait on both
 // the LDS and the memory counters at every use).
+// piece / pieces: this block's share of the row (pieces blocks per row, the
+// row kernel's grid y).  Every block ranks the row's slices; a row with more
+// than kRowSplitMin entries to gather splits them in contiguous rank ranges
+// over the blocks (block 0 also merges the slice partials), each block writes
+// its (m, l, o) partial, and the last block to finish -- counted with an
+// agent-scope atomic after a release fence, no block waits for another --
+// merges the partials in block order.  Other rows are merged by block 0 alone.
 template <int DT, int D, int NT, bool ALL_GATHER = false, bool LONG = false>
-__device__ __forceinline__ void row_merge(const FusedSelParams& p, const PVParams& v, int r, RowShared<NT>& sh) {
+__device__ __forceinline__ void row_merge(const FusedSelParams& p, const PVParams& v, int r, RowShared<NT>& sh,
+                                          int piece = 0, int pieces = 1) {
   constexpr int NW = NT / kWave;
   float* red = sh.red;
   int2* wsum = sh.wsum;
@@ -484,7 +498,7 @@ __device__ __forceinline__ void row_merge(const FusedSelParams& p, const PVParam
 #pragma unroll
   for (int u = 0; u < kRowMergeSlices; ++u) {
     const int s = g + G * u;
-    const bool in = kPrefetch && s < ns;
+    const bool in = kPrefetch && s < ns && piece == 0;
     ms0[u] = in ? p.sl_ml[2 * (row0 + s)] : kNegInf;
     ls0[u] = in ? p.sl_ml[2 * (row0 + s) + 1] : 0.f;
     ov0[u] = in ? *reinterpret_cast<const f32x4*>(p.sl_o + (row0 + s) * D + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
@@ -516,11 +530,16 @@ __device__ __forceinline__ void row_merge(const FusedSelParams& p, const PVParam
     ng = block_scan_slices<NT>(ns, static_cast<int*>(nullptr), gpre, wsum, cnt_of,
                            [&](int s) { return has_partial(s) ? 0 : take(s); }).y;
   }
+  const bool split = pieces > 1 && ng > kRowSplitMin;  // the same in every block of the row
+  if (!split && piece > 0) return;
+  // this block's gather ranks [j0, j1)
+  const int j0 = split ? static_cast<int>(static_cast<int64_t>(ng) * piece / pieces) : 0;
+  const int j1 = split ? static_cast<int>(static_cast<int64_t>(ng) * (piece + 1) / pieces) : ng;
 
-  // 2. log-sum-exp merge of the slice partials
+  // 2. log-sum-exp merge of the slice partials (block 0)
   float M = kNegInf, lsum = 0.f;
   f32x4 on = {0.f, 0.f, 0.f, 0.f};
-  for (int b0 = 0; b0 < (ALL_GATHER ? 0 : ns); b0 += G * kRowMergeSlices) {
+  for (int b0 = 0; b0 < (ALL_GATHER || piece > 0 ? 0 : ns); b0 += G * kRowMergeSlices) {
     float ms[kRowMergeSlices], lsv[kRowMergeSlices];
     f32x4 ov[kRowMergeSlices];
 #pragma unroll
@@ -573,13 +592,13 @@ __device__ __forceinline__ void row_merge(const FusedSelParams& p, const PVParam
 
   // 3. the remaining entries (long slices, the slice cut at rank buf_k), batch
   //    by batch through softmax . V (block-uniform branch)
-  if (ng > 0) {
+  if (j1 > j0) {
     const int vh = h / (v.q_h / v.v_h);
     const char* vbase = v.v + (bi * v.v_sb + static_cast<int64_t>(vh) * v.v_sh) * Elt<DT>::kBytes;
     BlockPV<DT, D, NT, kRowUnroll> pv;
     pv.init();
-    for (int b0 = 0; b0 < ng; b0 += kRowBatch) {
-      const int nb = min(kRowBatch, ng - b0);
+    for (int b0 = j0; b0 < j1; b0 += kRowBatch) {
+      const int nb = min(kRowBatch, j1 - b0);
       __syncthreads();  // the LDS list of the previous batch (or accs) is free
       for (int i = tid; i < nb; i += NT) {
         const int j = b0 + i;
@@ -605,6 +624,41 @@ __device__ __forceinline__ void row_merge(const FusedSelParams& p, const PVParam
 #pragma unroll
       for (int i = 0; i < 4; ++i) o[i] = o[i] * a + accs_f[4 * tid + i] * bw;
     }
+    M = Mn;
+  }
+  if (split) {
+    // this block's partial out; the last block of the row merges all of them
+    constexpr int PW = D + 4;  // floats per partial: m, l, two unused, o
+    float* part = p.row_part + static_cast<int64_t>(r) * pieces * PW;
+    if (tid < C) *reinterpret_cast<f32x4*>(part + piece * PW + 4 + 4 * tid) = o;
+    if (tid == 0) *reinterpret_cast<f32x2*>(part + piece * PW) = f32x2{M, L};
+    // the block's stores complete at the barrier; one agent-scope release
+    // fence (an L2 write-back) then orders them before the count, and one
+    // acquire fence in the last block (the block's waves share its CU's
+    // caches) makes the other blocks' partials visible
+    __syncthreads();
+    if (tid == 0) {
+      __threadfence();
+      sh.last = atomicAdd(p.row_cnt + r, 1) == pieces - 1;
+      if (sh.last) __threadfence();
+    }
+    __syncthreads();
+    if (!sh.last) return;
+    if (tid < C) {
+      float Mx = kNegInf;
+      for (int q = 0; q < pieces; ++q) Mx = fmaxf(Mx, part[q * PW]);
+      L = 0.f;
+      o = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int q = 0; q < pieces; ++q) {
+        const f32x2 ml = *reinterpret_cast<const f32x2*>(part + q * PW);
+        const f32x4 oq = *reinterpret_cast<const f32x4*>(part + q * PW + 4 + 4 * tid);
+        const float w = ml.x == kNegInf ? 0.f : __expf(ml.x - Mx);
+        L += ml.y * w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] += oq[i] * w;
+      }
+    }
+    if (tid == 0) p.row_cnt[r] = 0;  // ready for the next call
   }
   if (tid < C) {
     const int64_t ooff = bi * v.o_sb + static_cast<int64_t>(h) * v.o_sh;
@@ -622,7 +676,7 @@ __device__ __forceinline__ void row_merge(const FusedSelParams& p, const PVParam
 template <int DT, int D, int NT, bool LONG>
 __global__ void __launch_bounds__(NT) atopn_gather_kernel(FusedSelParams p, PVParams v) {
   __shared__ RowShared<NT> sh;
-  row_merge<DT, D, NT, false, LONG>(p, v, blockIdx.x, sh);
+  row_merge<DT, D, NT, false, LONG>(p, v, blockIdx.x, sh, blockIdx.y, gridDim.y);
 }
 
 // One block per row: its waves compact the row's slices (t once per wave,
@@ -747,21 +801,23 @@ __global__ void __launch_bounds__(NT) atopn_rowlds_kernel(FusedSelParams p, PVPa
 
 template <int DT, int D>
 static hipError_t launch_rows_typed(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
+  // rows of more than kRowMaxSlices slices keep their ranks in the workspace,
+  // shared by a row's blocks: one block per row (no split)
   const bool lng = p.nslice > kRowMaxSlices;
   if (p.cap <= kRowSmallCap) {
     if (lng)
-      hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsSmall, true>), dim3(p.nrows), dim3(kRowThreadsSmall), 0,
-                         st, p, v);
+      hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsSmall, true>), dim3(p.nrows, 1),
+                         dim3(kRowThreadsSmall), 0, st, p, v);
     else
-      hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsSmall, false>), dim3(p.nrows), dim3(kRowThreadsSmall),
-                         0, st, p, v);
+      hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsSmall, false>), dim3(p.nrows, kRowSplit),
+                         dim3(kRowThreadsSmall), 0, st, p, v);
   } else {
     if (lng)
-      hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsLarge, true>), dim3(p.nrows), dim3(kRowThreadsLarge), 0,
-                         st, p, v);
+      hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsLarge, true>), dim3(p.nrows, 1),
+                         dim3(kRowThreadsLarge), 0, st, p, v);
     else
-      hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsLarge, false>), dim3(p.nrows), dim3(kRowThreadsLarge),
-                         0, st, p, v);
+      hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsLarge, false>), dim3(p.nrows, kRowSplit),
+                         dim3(kRowThreadsLarge), 0, st, p, v);
   }
   return hipGetLastError();
 }

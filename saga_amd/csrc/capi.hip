@@ -240,6 +240,8 @@ void atopn_layout(int64_t b, int64_t q_h, int64_t k_h, int64_t L, int64_t d, int
   o->slice_pre = take(nr * 2 * (ns_max + 1) * 4);
   o->slice_o = take(nr * ns_max * d * 4);
   o->slice_ml = take(nr * ns_max * 2 * 4);
+  o->row_part = take(nr * kRowSplit * (d + 4) * 4);
+  o->row_cnt = take(nr * 4);
   o->total_bytes = off;
 }
 
@@ -323,6 +325,8 @@ int atopn_run(bool calibrate, const saga_tensor* query, const saga_tensor* key, 
   sp.sl_pre = reinterpret_cast<int32_t*>(ws + lay.slice_pre);
   sp.sl_o = reinterpret_cast<float*>(ws + lay.slice_o);
   sp.sl_ml = reinterpret_cast<float*>(ws + lay.slice_ml);
+  sp.row_part = reinterpret_cast<float*>(ws + lay.row_part);
+  sp.row_cnt = reinterpret_cast<int32_t*>(ws + lay.row_cnt);
   sp.k2_variant = k2_variant;
   // calibration: softmax over the top-k logits == renormalised top-k probabilities
   const PVParams pp = make_pv(value, out, s);

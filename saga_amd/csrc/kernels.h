@@ -99,11 +99,16 @@ struct FusedSelParams {
   float* sl_o;      // [row][slice][d] unnormalised sum_e w_e V[e] of short slices
   float* sl_ml;     // [row][slice][2] (max logit, sum of weights) of short slices
   int32_t* sl_pre;  // [row][2][nslice + 1] slice ranks (rows of > 2048 slices)
+  // a row's gather split over kRowSplit blocks: their (m, l, -, -, o[d])
+  // partials and the count of blocks done (zeroed by the slice kernel)
+  float* row_part;   // [row][kRowSplit][d + 4]
+  int32_t* row_cnt;  // [row]
   int32_t k2_variant;  // fast step: kK2Auto / kK2RowBlock / kK2SliceRow
 };
 // calibrate: one block per row; fast step: slice kernel + per-row gather kernel
 hipError_t launch_atopn_select_pv(bool calibrate, const FusedSelParams& p, const PVParams& v, hipStream_t st);
 constexpr int kSliceLen = 1024;  // score positions per slice wave of the fast step
+constexpr int kRowSplit = 4;     // blocks of the row kernel per row (a heavy row's gather is split over them)
 constexpr int kSliceSmall = 96;  // slice lists this short are gathered by their slice wave (<= 2 bursts)
 hipError_t launch_atopn_fast(const FusedSelParams& p, const PVParams& v, hipStream_t st);
 // The per-row kernel of the fast step alone (ranks, cut at buf_k, merge, long gathers).

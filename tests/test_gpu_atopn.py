@@ -465,6 +465,47 @@ def test_rows_of_more_than_2048_slices(k2_variant):
     assert np.max(np.abs(out - ref_out)) < 2e-3 and rel_l2(out, ref_out) < 1e-4
 
 
+def test_overflowing_rows_split_over_blocks():
+    """Batch 8, 32769 positions, N = 512 with 1 % of the keys scaled x8: a
+    quarter of the rows pass thousands of positions and gather 1024 kept
+    entries, split over the row kernel's blocks (the last block to finish
+    merges their partials).  Twice in a row bit for bit; lists, counts and
+    thresholds equal to one block per row, outputs equal to fp32 rounding,
+    and equal to the oracle's softmax . V on the GPU's own selection."""
+    b, q_h, k_h, v_h, d, L, N = 8, 12, 1, 2, 128, 32769, 512
+    rng = np.random.default_rng(2024)
+    print(f"atopn overflowing rows split b={b} L={L} N={N}", flush=True)
+    (q, k, v), (qd, kd, vd) = qkv(rng, b, q_h, k_h, v_h, d, L, "bf16", outliers=0.01)
+    table = torch.zeros(b * q_h, device="cuda")
+    ops.atopn_calibrate(qd, kd, vd, N, table)
+    q2 = O.round_bf16(q + np.float32(0.3) * rng.standard_normal(q.shape, dtype=np.float32))
+    q2d = dev(q2, "bf16")
+    buf_k = 2 * N
+    outs, views = [], []
+    for variant in (2, 2, 1):
+        outs.append(_run_fast(q2d, kd, vd, table, N, k2_variant=variant))
+        views.append(_views(b, q_h, k_h, L, d, buf_k, scores_of=(q2d, kd, None, None, None)))
+    assert torch.equal(outs[0], outs[1])
+    heavy = views[0]["sel_total"] > buf_k
+    assert heavy.sum() >= 8, "the case must overflow"
+    for key in ("sel_cnt", "sel_total", "sel_idx", "thresh"):
+        np.testing.assert_array_equal(views[0][key], views[2][key])
+    _check_selection_rule(views[0], b * q_h, L, buf_k)
+    o_split, o_block = host(outs[0]), host(outs[2])
+    assert rel_l2(o_split, o_block) < 1e-6
+    # the oracle's softmax . V on the GPU's selection (its own fp32 scores)
+    nr = b * q_h
+    vals = np.full((nr, buf_k), -np.inf, np.float32)
+    idx = np.zeros((nr, buf_k), np.int64)
+    for r in range(nr):
+        c = int(views[0]["sel_cnt"][r])
+        idx[r, :c] = views[0]["sel_idx"][r, :c]
+        vals[r, :c] = views[0]["scores"][r, idx[r, :c]]
+    ref = O.gather_output(vals.reshape(b, q_h, 1, buf_k), idx.reshape(b, q_h, 1, buf_k), v, (b, q_h, 1, d),
+                          input_is_logits=True)
+    assert rel_l2(o_split, ref) < 1e-5
+
+
 def test_k2_variant_rejects_other_values():
     rng = np.random.default_rng(5)
     (_, _, _), (qd, kd, vd) = qkv(rng, 1, 12, 1, 2, 128, 256, "bf16")
