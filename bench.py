@@ -598,7 +598,7 @@ def main():
                          "and the 128k dense-GQA vs SAGA comparison; one JSON line per shape")
     ap.add_argument("--k2-variant", type=int, choices=(0, 1, 2), default=0,
                     help="fast-step selection + softmax.V kernels: 0 by shape (default), 1 one block per row, "
-                         "2 slice kernel + row kernel (results are identical)")
+                         "2 slice kernel + row kernel (identical selections, outputs equal to fp32 rounding)")
     ap.add_argument("--exempt", default="",
                     help="comma-separated layers that run dense attention in the SAGA model (speedup.py:65-66), "
                          "e.g. 0,14 for Qwen2.5-1.5B")
