@@ -854,17 +854,6 @@ static hipError_t launch_split_d(const FusedSelParams& p, const PVParams& v, hip
   return v.d == 128 ? launch_split<DT, 128>(p, v, st) : launch_split<DT, 64>(p, v, st);
 }
 
-template <int DT>
-static hipError_t launch_rows_d(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
-  return v.d == 128 ? launch_rows_typed<DT, 128>(p, v, st) : launch_rows_typed<DT, 64>(p, v, st);
-}
-
-hipError_t launch_atopn_rows(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
-  if (v.v_dt == SAGA_DTYPE_BF16) return launch_rows_d<SAGA_DTYPE_BF16>(p, v, st);
-  if (v.v_dt == SAGA_DTYPE_F16) return launch_rows_d<SAGA_DTYPE_F16>(p, v, st);
-  return launch_rows_d<SAGA_DTYPE_F32>(p, v, st);
-}
-
 hipError_t launch_atopn_fast(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
   if (v.v_dt == SAGA_DTYPE_BF16) return launch_split_d<SAGA_DTYPE_BF16>(p, v, st);
   if (v.v_dt == SAGA_DTYPE_F16) return launch_split_d<SAGA_DTYPE_F16>(p, v, st);

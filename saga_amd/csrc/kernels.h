@@ -111,8 +111,6 @@ constexpr int kSliceLen = 1024;  // score positions per slice wave of the fast s
 constexpr int kRowSplit = 4;     // blocks of the row kernel per row (a heavy row's gather is split over them)
 constexpr int kSliceSmall = 96;  // slice lists this short are gathered by their slice wave (<= 2 bursts)
 hipError_t launch_atopn_fast(const FusedSelParams& p, const PVParams& v, hipStream_t st);
-// The per-row kernel of the fast step alone (ranks, cut at buf_k, merge, long gathers).
-hipError_t launch_atopn_rows(const FusedSelParams& p, const PVParams& v, hipStream_t st);
 // Fast-step K2 shape (FusedSelParams::k2_variant): 0 by shape (one block per
 // row for rows of few slices), 1 always one block per row, 2 always slice
 // kernel + row kernel.  Results are identical in every variant.
