@@ -480,11 +480,15 @@ def test_overflowing_rows_split_over_blocks():
     ops.atopn_calibrate(qd, kd, vd, N, table)
     q2 = O.round_bf16(q + np.float32(0.3) * rng.standard_normal(q.shape, dtype=np.float32))
     q2d = dev(q2, "bf16")
+    q3d = dev(O.round_bf16(q + np.float32(0.3) * rng.standard_normal(q.shape, dtype=np.float32)), "bf16")
     buf_k = 2 * N
     outs, views = [], []
     for variant in (2, 2, 1):
         outs.append(_run_fast(q2d, kd, vd, table, N, k2_variant=variant))
         views.append(_views(b, q_h, k_h, L, d, buf_k, scores_of=(q2d, kd, None, None, None)))
+        if len(outs) == 1:  # other queries in between: a partial left from them would show
+            other = _run_fast(q3d, kd, vd, table, N, k2_variant=2)
+    assert not torch.equal(other, outs[0])
     assert torch.equal(outs[0], outs[1])
     heavy = views[0]["sel_total"] > buf_k
     assert heavy.sum() >= 8, "the case must overflow"
