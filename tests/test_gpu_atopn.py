@@ -510,6 +510,46 @@ def test_overflowing_rows_split_over_blocks():
     assert rel_l2(o_split, ref) < 1e-5
 
 
+@pytest.mark.parametrize("seed", range(4))
+def test_split_rows_sweep(seed):
+    """Overflowing rows split over the row kernel's blocks at seeded dtypes,
+    head dims, N and head groupings (2 % outlier keys): lists equal to one
+    block per row, outputs equal to fp32 rounding and to the oracle on the
+    GPU's own selection."""
+    rng = np.random.default_rng(7700 + seed)
+    dt = ("bf16", "f16", "f32", "bf16")[seed]
+    d = (128, 64)[seed % 2]
+    N = (512, 256, 512, 384)[seed]
+    q_h, k_h, v_h = [(12, 1, 2), (8, 2, 4), (6, 1, 3), (16, 2, 8)][seed]
+    b, L = 2, int(rng.integers(9000, 20000))
+    print(f"atopn split rows sweep seed={seed} {dt} d={d} N={N} q/k/v={q_h}/{k_h}/{v_h} L={L}", flush=True)
+    (q, k, v), (qd, kd, vd) = qkv(rng, b, q_h, k_h, v_h, d, L, dt, outliers=0.02)
+    table = torch.zeros(b * q_h, device="cuda")
+    ops.atopn_calibrate(qd, kd, vd, N, table)
+    q2 = round_to(q + np.float32(0.3) * rng.standard_normal(q.shape, dtype=np.float32), dt)
+    q2d = dev(q2, dt)
+    buf_k = min(2 * N, L)
+    res = []
+    for variant in (2, 1):
+        out = host(_run_fast(q2d, kd, vd, table, N, k2_variant=variant))
+        res.append((out, _views(b, q_h, k_h, L, d, buf_k, scores_of=(q2d, kd, None, None, None))))
+    (o2, v2), (o1, v1) = res
+    assert (v2["sel_total"] > buf_k).any(), "the case must overflow"
+    for key in ("sel_cnt", "sel_total", "sel_idx", "thresh"):
+        np.testing.assert_array_equal(v2[key], v1[key])
+    assert rel_l2(o2, o1) < 1e-6
+    nr = b * q_h
+    vals = np.full((nr, buf_k), -np.inf, np.float32)
+    idx = np.zeros((nr, buf_k), np.int64)
+    for r in range(nr):
+        c = int(v2["sel_cnt"][r])
+        idx[r, :c] = v2["sel_idx"][r, :c]
+        vals[r, :c] = v2["scores"][r, idx[r, :c]]
+    ref = O.gather_output(vals.reshape(b, q_h, 1, buf_k), idx.reshape(b, q_h, 1, buf_k), v, (b, q_h, 1, d),
+                          input_is_logits=True)
+    assert rel_l2(o2, ref) < 1e-5
+
+
 def test_k2_variant_rejects_other_values():
     rng = np.random.default_rng(5)
     (_, _, _), (qd, kd, vd) = qkv(rng, 1, 12, 1, 2, 128, 256, "bf16")

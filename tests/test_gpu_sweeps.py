@@ -91,8 +91,10 @@ def test_calibration_sweep(seed):
         assert len(set(idx[r, :kk].tolist()) ^ set(ridx[r, :kk].tolist())) <= 2  # a swap at the k-th boundary
 
 
-@pytest.mark.parametrize("seed", range(12))
+@pytest.mark.parametrize("seed", range(18))
 def test_gemv_sweep(seed):
+    """Seeded shapes, epilogues and W layouts (row-major, 16-row packed, and
+    8-row packed for at most 8 token rows) against the float64 product."""
     rng = np.random.default_rng(90000 + seed)
     M = int(rng.integers(1, 17))
     K = 32 * int(rng.choice([1, 2, 5, 48, 63, 280]))
@@ -100,13 +102,19 @@ def test_gemv_sweep(seed):
     epi = ("store", "add", "silu_pairs")[seed % 3]
     if epi == "silu_pairs" and N % 32:
         N += 16
-    rms, packed, split = bool(seed % 2), bool((seed // 2) % 2), seed % 5 != 0
+    rms, split = bool(seed % 2), seed % 5 != 0
+    layout = ("rows", "packed16", "packed8")[(seed // 2) % 3]
+    if layout == "packed8":
+        M = min(M, 8)
+        K += K % 64
     use_bias = epi != "silu_pairs" and seed % 4 == 1
-    print(f"gemv sweep seed={seed} M={M} K={K} N={N} {epi} rms={rms} packed={packed} split={split}", flush=True)
+    print(f"gemv sweep seed={seed} M={M} K={K} N={N} {epi} rms={rms} {layout} split={split}", flush=True)
     x = O.round_bf16(rng.standard_normal((M, K), dtype=np.float32))
     w = O.round_bf16(rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.05))
     b = O.round_bf16(rng.standard_normal(N, dtype=np.float32))
-    wd = ops.pack_gemv_weight(dev(w, "bf16")) if packed else dev(w, "bf16")
+    wd = dev(w, "bf16")
+    if layout != "rows":
+        wd = ops.pack_gemv_weight(wd, 8 if layout == "packed8" else 16)
     xs = x.astype(np.float64)
     if rms:
         xs = xs / np.sqrt((xs ** 2).mean(-1, keepdims=True) + 1e-6)
@@ -127,10 +135,12 @@ def test_gemv_sweep(seed):
     assert np.isfinite(y).all() and rel_l2(y, ref) < 4e-3
 
 
-@pytest.mark.parametrize("seed", range(6))
+@pytest.mark.parametrize("seed", range(9))
 def test_rope_kv_projection_sweep(seed):
     rng = np.random.default_rng(110000 + seed)
     M = int(rng.integers(1, 17))
+    if seed % 3 == 1:  # 8-row packed weights take at most 8 token rows
+        M = min(M, 8)
     n_q, n_k, n_v = GROUPS[seed % len(GROUPS)]
     d = (64, 128)[seed % 2]
     K = 32 * int(rng.choice([5, 30, 48]))
@@ -147,9 +157,14 @@ def test_rope_kv_projection_sweep(seed):
     kc = torch.zeros(B, n_k, Lmax, d, device="cuda", dtype=torch.bfloat16)
     vc = torch.zeros(B, n_v, Lmax, d, device="cuda", dtype=torch.bfloat16)
     order = ops.rope_pair_order(n_q, n_k, n_v, d, device="cuda")
-    wo = ops.pack_gemv_weight(wd[order].contiguous()) if seed % 3 == 0 else wd[order].contiguous()
+    wo = wd[order].contiguous()
+    if seed % 3 == 0:
+        wo = ops.pack_gemv_weight(wo)
+    elif seed % 3 == 1 and M <= 8 and K % 64 == 0:
+        wo = ops.pack_gemv_weight(wo, 8)
+    table = ops.rope_table(pos, d, theta) if seed % 2 == 0 else None
     q = ops.gemv_rope_kv(xd, wo, bd[order].contiguous(), n_q, n_k, n_v, theta, pos, kc, vc, rms_eps=1e-6,
-                         batch=batch)
+                         batch=batch, rope_table=table)
     torch.cuda.synchronize()
     xs = x.astype(np.float64)
     xs = xs / np.sqrt((xs ** 2).mean(-1, keepdims=True) + 1e-6)
