@@ -92,7 +92,7 @@ def k1_traffic(batch, ctx, shape):
             d = json.load(f)
         w = d.get("workload") or {}
         if (w.get("batch"), w.get("ctx"), w.get("n_q"), w.get("n_k"), w.get("head_dim")) != \
-                (batch, ctx, shape.n_q, shape.n_k, shape.head_dim):
+                (batch, ctx, shape.n_q, shape.n_k, shape.head_dim) or w.get("outlier_keys"):
             continue
         for kern, ent in d["kernels"].items():
             if kern.startswith("void saga::qk_scores_kernel<1, %d>" % shape.head_dim) and "traffic_bytes_per_launch" in ent:
@@ -300,20 +300,26 @@ def c1_gpu_us(reps=20):
     return round(timed_graph(lambda i: ops.atopn_decode(q, k, v, tab, N, out=out, workspace=ws), reps), 2)
 
 
-def profile_kernels(batch, ctx, shape, top_n, launches=8):
+def profile_kernels(batch, ctx, shape, top_n, launches=8, outlier_keys=0.0):
     """Kernels alone at the decode shape, for hardware-counter runs: K1
     (qk_scores) `launches` times, the whole Atop-N fast step (after one
     calibration) `launches` times, the dense decode at the dense-GQA
     comparator's heads `launches` times, then a plain 1 GiB device-to-device
     copy 3 times, whose counters (2 GiB of known traffic per dispatch) scale
-    the others'.  Inputs: N(0,1) bf16 caches of ctx + 1 positions."""
+    the others'.  Inputs: N(0,1) bf16 caches of ctx + 1 positions; with
+    outlier_keys, that fraction of the key rows scaled x8 (the kernel
+    sweep's stress case: rows pass far more than buf_k positions)."""
     from saga_amd import ops
     L = ctx + 1
     d = shape.head_dim
     g = torch.Generator(device="cuda").manual_seed(0)
     q = torch.randn(batch, shape.n_q, 1, d, device="cuda", generator=g).to(torch.bfloat16)
     q2 = (q.float() + 0.3 * torch.randn(q.shape, device="cuda", generator=g)).to(torch.bfloat16)
-    k = torch.randn(batch, shape.n_k, L, d, device="cuda", generator=g).to(torch.bfloat16)
+    kf = torch.randn(batch, shape.n_k, L, d, device="cuda", generator=g)
+    if outlier_keys > 0:
+        kf[torch.rand(batch, shape.n_k, L, device="cuda", generator=g) < outlier_keys] *= 8.0
+    k = kf.to(torch.bfloat16)
+    del kf
     v = torch.randn(batch, shape.n_v, L, d, device="cuda", generator=g).to(torch.bfloat16)
     kvl = torch.full((batch,), L, dtype=torch.int32, device="cuda")
     for _ in range(launches):
@@ -326,6 +332,9 @@ def profile_kernels(batch, ctx, shape, top_n, launches=8):
         ops.atopn_decode(q2, k, v, tab, top_n, kv_len=kvl, workspace=ws)
     kept = ops.atopn_kept_positions(batch, shape.n_q, shape.n_k, L, d, min(2 * top_n, L), ws)
     vrows = ops.atopn_distinct_value_rows(kept, batch, shape.n_q, shape.n_v, L)
+    views = ops.atopn_workspace_views(batch, shape.n_q, shape.n_k, L, d, min(2 * top_n, L), "cuda", fast=True,
+                                      workspace=ws)
+    over = int((views["sel_total"] > min(2 * top_n, L)).sum())
     kd = torch.randn(batch, 2, L, d, device="cuda", generator=g).to(torch.bfloat16)
     vd = torch.randn(batch, 2, L, d, device="cuda", generator=g).to(torch.bfloat16)
     for _ in range(launches):
@@ -340,7 +349,7 @@ def profile_kernels(batch, ctx, shape, top_n, launches=8):
     qo = 2 * batch * shape.n_q * d2
     print(json.dumps({
         "launches": launches, "batch": batch, "kv_len": L, "n_q": shape.n_q, "n_k": shape.n_k, "n_v": shape.n_v,
-        "head_dim": d, "top_n": top_n,
+        "head_dim": d, "top_n": top_n, "outlier_keys": outlier_keys, "rows_over_buf_k": over,
         "k1_algorithmic_bytes": batch * shape.n_k * L * d2 + batch * shape.n_q * d2,
         "atopn_call_algorithmic_bytes": batch * shape.n_k * L * d2 + vrows * d2 + qo + 4 * batch * shape.n_q,
         "atopn_distinct_value_rows": vrows,
@@ -607,6 +616,8 @@ def main():
     ap.add_argument("--profile-kernels", action="store_true",
                     help="only launch K1 (qk_scores), the whole Atop-N fast step and the dense decode at the "
                          "workload shape, then a 1 GiB device copy: for hardware-counter runs")
+    ap.add_argument("--outlier-keys", type=float, default=0.0, metavar="FRAC",
+                    help="with --profile-kernels: scale this fraction of the key rows x8 (rows overflow buf_k)")
     ap.add_argument("--summarize-counters", nargs="+", metavar="DIR",
                     help="summarize rocprofv3 counter CSVs under DIR(s) per kernel, bytes scaled by the copy "
                          "dispatches of the same run (no GPU needed)")
@@ -632,7 +643,7 @@ def main():
 
     B, ctx, K, W = args.batch, args.ctx, args.steps, args.warmup
     if args.profile_kernels:
-        return profile_kernels(B, ctx, SAGA_SHAPE, args.top_n)
+        return profile_kernels(B, ctx, SAGA_SHAPE, args.top_n, outlier_keys=args.outlier_keys)
     if args.prefill:
         return prefill_bench(ctx, SAGA_SHAPE, no_cpu=args.no_cpu)
     if args.sweep:
