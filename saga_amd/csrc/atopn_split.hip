@@ -54,8 +54,14 @@ constexpr int kWaveUnroll = 12;                       // slice wave: 4 groups x 
 constexpr int kRowMergeSlices = 8;                    // slice partials per merge thread in one burst
 // rows with more entries to gather than this split them over the row
 // kernel's kRowSplit blocks (one CU draws ~28 GB/s of V rows: an overflowing
-// row's 1024 kept rows took 9 us in one block)
+// row's 1024 kept rows took 9 us in one block) -- when the unsplit kernel
+// holds at most kRowSplitThreads threads: with more rows the blocks already
+// spread over the chip and every split block's release fence costs more than
+// the split gains (b32 16k N 256: 74.5 against 62.3 us; b8 16k N 1024 with
+// 1024-thread blocks: 50.3 against 44.6; b8 32k N 512: 44.5 against 50.0;
+// b4 128k N 1024: 63.7 against 68.0)
 constexpr int kRowSplitMin = 384;
+constexpr int64_t kRowSplitThreads = 65536;
 // auto mode: one block per row when a row has at most this many slices and
 // its list fits one LDS batch (measured on MI355X, attention call at b1-b32,
 // d 64 and 128: 1.02-1.48x at 4k-12k positions; from 16k positions a row's
@@ -804,20 +810,23 @@ static hipError_t launch_rows_typed(const FusedSelParams& p, const PVParams& v, 
   // rows of more than kRowMaxSlices slices keep their ranks in the workspace,
   // shared by a row's blocks: one block per row (no split)
   const bool lng = p.nslice > kRowMaxSlices;
+  auto pieces = [&](int nt) {
+    return lng || static_cast<int64_t>(p.nrows) * nt > kRowSplitThreads ? 1u : static_cast<unsigned>(kRowSplit);
+  };
   if (p.cap <= kRowSmallCap) {
     if (lng)
       hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsSmall, true>), dim3(p.nrows, 1),
                          dim3(kRowThreadsSmall), 0, st, p, v);
     else
-      hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsSmall, false>), dim3(p.nrows, kRowSplit),
-                         dim3(kRowThreadsSmall), 0, st, p, v);
+      hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsSmall, false>),
+                         dim3(p.nrows, pieces(kRowThreadsSmall)), dim3(kRowThreadsSmall), 0, st, p, v);
   } else {
     if (lng)
       hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsLarge, true>), dim3(p.nrows, 1),
                          dim3(kRowThreadsLarge), 0, st, p, v);
     else
-      hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsLarge, false>), dim3(p.nrows, kRowSplit),
-                         dim3(kRowThreadsLarge), 0, st, p, v);
+      hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsLarge, false>),
+                         dim3(p.nrows, pieces(kRowThreadsLarge)), dim3(kRowThreadsLarge), 0, st, p, v);
   }
   return hipGetLastError();
 }
