@@ -52,16 +52,18 @@ constexpr int kRowMaxSlices = 2048;                   // slice ranks kept in LDS
 constexpr int kRowUnroll = 16;                        // V rows in flight per lane group
 constexpr int kWaveUnroll = 12;                       // slice wave: 4 groups x 12 = 48 V rows in flight
 constexpr int kRowMergeSlices = 8;                    // slice partials per merge thread in one burst
-// rows with more entries to gather than this split them over the row
-// kernel's kRowSplit blocks (one CU draws ~28 GB/s of V rows: an overflowing
-// row's 1024 kept rows took 9 us in one block) -- when the unsplit kernel
-// holds at most kRowSplitThreads threads: with more rows the blocks already
-// spread over the chip and every split block's release fence costs more than
-// the split gains (b32 16k N 256: 74.5 against 62.3 us; b8 16k N 1024 with
-// 1024-thread blocks: 50.3 against 44.6; b8 32k N 512: 44.5 against 50.0;
-// b4 128k N 1024: 63.7 against 68.0)
-constexpr int kRowSplitMin = 384;
+// A row kernel of at most kRowSplitThreads threads (unsplit) splits the
+// gathers of rows with more than split_min entries over its kRowSplit blocks
+// per row (one CU draws ~28 GB/s of V rows: an overflowing row's 1024 kept
+// rows took 9 us in one block).  With more rows the blocks already spread
+// over the chip and the split blocks' release fences cost more than the split
+// gains (b32 16k N 256: 74.5 against 62.3 us; b8 16k N 1024 on 1024-thread
+// blocks: 50.3 against 44.6); with few, split (b8 32k N 512: 44.5 against
+// 50.0; b4 128k N 1024: 63.7 against 68.0).  split_min: 384 for kernels of at
+// most kRowSplitSmallThreads threads (b1 16k N 256: 23.9 against 24.8 us),
+// else 768 (b8 16k N 256, lists of <= 512: 34.6 against 35.1 us).
 constexpr int64_t kRowSplitThreads = 65536;
+constexpr int64_t kRowSplitSmallThreads = 16384;
 // auto mode: one block per row when a row has at most this many slices and
 // its list fits one LDS batch (measured on MI355X, attention call at b1-b32,
 // d 64 and 128: 1.02-1.48x at 4k-12k positions; from 16k positions a row's
@@ -466,7 +468,7 @@ struct RowShared {
 // the LDS and the memory counters at every use).
 // piece / pieces: this block's share of the row (pieces blocks per row, the
 // row kernel's grid y).  Every block ranks the row's slices; a row with more
-// than kRowSplitMin entries to gather splits them in contiguous rank ranges
+// than p.split_min entries to gather splits them in contiguous rank ranges
 // over the blocks (block 0 also merges the slice partials), each block writes
 // its (m, l, o) partial, and the last block to finish -- counted with an
 // agent-scope atomic after a release fence, no block waits for another --
@@ -536,7 +538,7 @@ __device__ __forceinline__ void row_merge(const FusedSelParams& p, const PVParam
     ng = block_scan_slices<NT>(ns, static_cast<int*>(nullptr), gpre, wsum, cnt_of,
                            [&](int s) { return has_partial(s) ? 0 : take(s); }).y;
   }
-  const bool split = pieces > 1 && ng > kRowSplitMin;  // the same in every block of the row
+  const bool split = pieces > 1 && ng > p.split_min;  // the same in every block of the row
   if (!split && piece > 0) return;
   // this block's gather ranks [j0, j1)
   const int j0 = split ? static_cast<int>(static_cast<int64_t>(ng) * piece / pieces) : 0;
@@ -810,23 +812,25 @@ static hipError_t launch_rows_typed(const FusedSelParams& p, const PVParams& v, 
   // rows of more than kRowMaxSlices slices keep their ranks in the workspace,
   // shared by a row's blocks: one block per row (no split)
   const bool lng = p.nslice > kRowMaxSlices;
-  auto pieces = [&](int nt) {
-    return lng || static_cast<int64_t>(p.nrows) * nt > kRowSplitThreads ? 1u : static_cast<unsigned>(kRowSplit);
-  };
-  if (p.cap <= kRowSmallCap) {
+  const int nt = p.cap <= kRowSmallCap ? kRowThreadsSmall : kRowThreadsLarge;
+  const int64_t threads = static_cast<int64_t>(p.nrows) * nt;
+  const unsigned pieces = lng || threads > kRowSplitThreads ? 1u : static_cast<unsigned>(kRowSplit);
+  FusedSelParams q = p;
+  q.split_min = threads <= kRowSplitSmallThreads ? 384 : 768;
+  if (nt == kRowThreadsSmall) {
     if (lng)
-      hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsSmall, true>), dim3(p.nrows, 1),
-                         dim3(kRowThreadsSmall), 0, st, p, v);
+      hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsSmall, true>), dim3(q.nrows, 1),
+                         dim3(kRowThreadsSmall), 0, st, q, v);
     else
-      hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsSmall, false>),
-                         dim3(p.nrows, pieces(kRowThreadsSmall)), dim3(kRowThreadsSmall), 0, st, p, v);
+      hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsSmall, false>), dim3(q.nrows, pieces),
+                         dim3(kRowThreadsSmall), 0, st, q, v);
   } else {
     if (lng)
-      hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsLarge, true>), dim3(p.nrows, 1),
-                         dim3(kRowThreadsLarge), 0, st, p, v);
+      hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsLarge, true>), dim3(q.nrows, 1),
+                         dim3(kRowThreadsLarge), 0, st, q, v);
     else
-      hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsLarge, false>),
-                         dim3(p.nrows, pieces(kRowThreadsLarge)), dim3(kRowThreadsLarge), 0, st, p, v);
+      hipLaunchKernelGGL((atopn_gather_kernel<DT, D, kRowThreadsLarge, false>), dim3(q.nrows, pieces),
+                         dim3(kRowThreadsLarge), 0, st, q, v);
   }
   return hipGetLastError();
 }

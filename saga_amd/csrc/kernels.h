@@ -103,6 +103,7 @@ struct FusedSelParams {
   // partials and the count of blocks done (zeroed by the slice kernel)
   float* row_part;   // [row][kRowSplit][d + 4]
   int32_t* row_cnt;  // [row]
+  int32_t split_min;  // rows gathering more entries than this split (set by the row kernel's launcher)
   int32_t k2_variant;  // fast step: kK2Auto / kK2RowBlock / kK2SliceRow
 };
 // calibrate: one block per row; fast step: slice kernel + per-row gather kernel

@@ -519,7 +519,7 @@ def test_split_rows_sweep(seed):
     rng = np.random.default_rng(7700 + seed)
     dt = ("bf16", "f16", "f32", "bf16")[seed]
     d = (128, 64)[seed % 2]
-    N = (512, 256, 512, 384)[seed]
+    N = (512, 512, 512, 1024)[seed]
     q_h, k_h, v_h = [(12, 1, 2), (8, 2, 4), (6, 1, 3), (16, 2, 8)][seed]
     b, L = 2, int(rng.integers(9000, 20000))
     print(f"atopn split rows sweep seed={seed} {dt} d={d} N={N} q/k/v={q_h}/{k_h}/{v_h} L={L}", flush=True)
