@@ -257,7 +257,7 @@ int saga_rmsnorm(const saga_tensor* x, const saga_tensor* weight, float eps, sag
 /* y[n, i] = silu(x[n, i]) * x[n, H + i]; x [N, 2H] = [gate | up], y [N, H]. */
 int saga_silu_mul(const saga_tensor* gate_up, saga_tensor* y, saga_stream_t stream);
 
-/* Skinny GEMM for decode projections (M <= 16 token rows, bf16):
+/* Skinny GEMM for decode projections (M <= 32 token rows, bf16):
  *   y[m, n] (op)= s[m] * sum_k x[m, k] * w[n, k]  (+ bias[n])
  * s[m] = 1 / sqrt(mean_k x[m, k]^2 + eps) when rms_eps >= 0 (RMSNorm of x
  * fused; its weight is expected folded into w), else 1.  epilogue:
@@ -292,7 +292,7 @@ int saga_gemv(const saga_tensor* x, const saga_tensor* w, const saga_tensor* bia
 
 /* saga_gemv (STORE, bias, fused RMSNorm) of the fused q/k/v projection with
  * saga_rope_kv_append applied in its epilogue: one launch per layer for
- * projection + RoPE + cache append.  x [M, K] (M <= 16 new tokens), w bf16
+ * projection + RoPE + cache append.  x [M, K] (M <= 32 new tokens), w bf16
  * [(n_q + n_k + n_v) * d, K] and bias [(n_q + n_k + n_v) * d] hold the q, k
  * and v heads in that order, with the rows of every q and k head permuted to
  * rotary-pair order [0, d/2, 1, d/2 + 1, ..., d/2 - 1, d - 1] (v heads

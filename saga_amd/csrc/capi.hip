@@ -736,7 +736,7 @@ int make_gemv(const saga_tensor* x, const saga_tensor* w, const saga_tensor* bia
   } else if (w->shape[1] != K) {
     return fail(SAGA_ERR_INVALID, "gemv: w must be [N, K] with K = x.shape[1]");
   }
-  if (M > 16) return fail(SAGA_ERR_UNSUPPORTED, "gemv: at most 16 rows");
+  if (M > 32) return fail(SAGA_ERR_UNSUPPORTED, "gemv: at most 32 rows");
   if (N % 16 || K % 32 || K >= (1LL << 30) || N >= (1LL << 30))
     return fail(SAGA_ERR_UNSUPPORTED, "gemv: N %% 16 == 0 and K %% 32 == 0 required");
   if ((rc = check_vec_rows(x, "x")) || (!packed && (rc = check_vec_rows(w, "w")))) return rc;
@@ -902,7 +902,7 @@ int saga_silu_mul(const saga_tensor* gate_up, saga_tensor* y, saga_stream_t stre
 }
 
 size_t saga_gemv_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-  if (M < 1 || M > 16 || N < 16 || K < 32 || N >= (1LL << 31) || K >= (1LL << 31)) return 0;
+  if (M < 1 || M > 32 || N < 16 || K < 32 || N >= (1LL << 31) || K >= (1LL << 31)) return 0;
   const int s = gemv_splits(N, K);
   if (s <= 1) return 0;
   return static_cast<size_t>(align256(s * M * N * 4) + align256(s * M * 4));

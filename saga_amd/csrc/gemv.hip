@@ -1,4 +1,4 @@
-// Skinny GEMM for decode projections: y[m, n] = sum_k x[m, k] * W[n, k], m < 16.
+// Skinny GEMM for decode projections: y[m, n] = sum_k x[m, k] * W[n, k], m < 32.
 //
 // W is row-major [N, K], or packed [N/16][K/32][16][32] (each 16-row x 32-k
 // MFMA A fragment 1 KB contiguous: a load instruction reads 1 KB of one
@@ -78,20 +78,29 @@ __device__ __forceinline__ GemvPre gemv_prefetch(const GemvParams& p, int m, int
 // (s < 2, c < 8) and lane l + 40.  Weights of few 16-row tiles (a 1536-row projection: 96) so
 // spread over twice the workgroups, each CU streaming half the bytes, with no
 // split over K.  UNROLL: k steps per wave and burst.
-template <int WAVES, int EPI, int TPW, bool HALF = false, int UNROLL = kGemvUnroll>
+//
+// MT = 2 (17 to 32 token rows): every W fragment meets two B fragments, token
+// rows c and 16 + c of lane column c, into two accumulators; the epilogue
+// waves split over (tile, token tile).
+template <int WAVES, int EPI, int TPW, bool HALF = false, int UNROLL = kGemvUnroll, int MT = 1>
 __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(TPW == 2 ? 3 : 4, 8)))
 gemv_kernel(GemvParams p) {
-  static_assert(!HALF || TPW == 1, "8-row tiles: one per wave");
+  static_assert(!HALF || (TPW == 1 && MT == 1), "8-row tiles: one per wave, at most 8 token rows");
+  static_assert(WAVES >= TPW * MT, "one epilogue wave per (tile, token tile)");
   constexpr int TR = HALF ? 8 : 16;  // W rows per tile
-  __shared__ float red[WAVES][TPW][64][4];
-  __shared__ float rsq[WAVES][64];
+  __shared__ float red[WAVES][TPW * MT][64][4];
+  __shared__ float rsq[WAVES][MT][64];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int col = lane & 15, s = lane >> 4;
   const int n0 = blockIdx.x * TR * TPW;
   const int split = blockIdx.y;  // K range of this workgroup (split-K: partial sums out)
-  const int mrow = HALF ? (col & 7) : col;  // token row of this lane's x fragments
-  const bool mvalid = mrow < p.M;
-  const int m = mvalid ? mrow : 0;
+  const int mrow = HALF ? (col & 7) : col;  // token row of this lane's x fragments (+ 16 per token tile)
+  // the (tile, token tile) this wave finishes (waves 0 .. TPW*MT - 1) and
+  // its token row m: the epilogue inputs are loaded for it
+  const int tf = w < TPW * MT ? (MT == 1 ? w : w % TPW) : TPW - 1;
+  const int mte = MT == 1 ? 0 : (w < TPW * MT ? w / TPW : 0);
+  const int tme = mrow + 16 * mte;
+  const int m = tme < p.M ? tme : 0;
   // A fragment of tile t at k step j: wrow[t] + j * wstep.  Row-major W:
   // 16 rows x 64 B, one row per W row stride; packed W: 1 KB contiguous
   const int64_t wstep = p.w_packed ? 1024 : 64;
@@ -102,13 +111,18 @@ gemv_kernel(GemvParams p) {
     wrow[t] = static_cast<const char*>(p.w) +
               (p.w_packed ? static_cast<int64_t>(n0 / TR + t) * steps * 1024 + col * 64 + s * 16
                           : (static_cast<int64_t>(n0 + 16 * t + col) * p.w_ld + 8 * s) * 2);
-  // x fragment: 8 k values of token row m (HALF: of the k half of column col)
+  // x fragments: 8 k values of token row mrow + 16 mt (HALF: of the k half of column col)
   const int64_t xstep = HALF ? 128 : 64;
-  const char* xrow = static_cast<const char*>(p.x) +
-                     (static_cast<int64_t>(m) * p.x_ld + 8 * s + (HALF ? 32 * (col >> 3) : 0)) * 2;
-  // the tile this wave finishes (waves 0..TPW-1) and its epilogue inputs
+  bool xvalid[MT];
+  const char* xrow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int mm = mrow + 16 * mt;
+    xvalid[mt] = mm < p.M;
+    xrow[mt] = static_cast<const char*>(p.x) +
+               (static_cast<int64_t>(xvalid[mt] ? mm : 0) * p.x_ld + 8 * s + (HALF ? 32 * (col >> 3) : 0)) * 2;
+  }
   // (HALF: lanes s < 2 own rows n0 + 4s .. + 3; lanes s >= 2 load the same)
-  const int tf = w < TPW ? w : TPW - 1;
   const int nf = n0 + TR * tf + 4 * (HALF ? (s & 1) : s);
   // this workgroup's k steps [k0, k1), dealt to its waves round robin (wave
   // w: k0 + w, k0 + w + WAVES, ...): at any moment the workgroup's waves
@@ -118,33 +132,44 @@ gemv_kernel(GemvParams p) {
   const int nmine = (k1 - k0 - w + WAVES - 1) / WAVES;
   const int jstride = WAVES;
   const int jbase = k0 + w;
-  f32x4 acc[TPW];
+  f32x4 acc[TPW][MT];
 #pragma unroll
-  for (int t = 0; t < TPW; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float ssq = 0.f;
+  for (int t = 0; t < TPW; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float ssq[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) ssq[mt] = 0.f;
   // one burst: every k step of [i0, i0 + UNROLL) of the wave (steps past its
   // share repeat its last one, clamped into the workgroup's range: a wave
   // with no step loads valid addresses it never uses)
-  auto load_burst = [&](int i0, u32x4 (&a)[UNROLL][TPW], u32x4 (&b)[UNROLL]) {
+  auto load_burst = [&](int i0, u32x4 (&a)[UNROLL][TPW], u32x4 (&b)[UNROLL][MT]) {
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
       const int jj = min(max(jbase + jstride * min(i0 + u, nmine - 1), k0), k1 - 1);
 #pragma unroll
       for (int t = 0; t < TPW; ++t) a[u][t] = ld16(wrow[t] + static_cast<int64_t>(jj) * wstep);
-      b[u] = mvalid ? ld16(xrow + static_cast<int64_t>(jj) * xstep) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        b[u][mt] = xvalid[mt] ? ld16(xrow[mt] + static_cast<int64_t>(jj) * xstep) : u32x4{0u, 0u, 0u, 0u};
     }
   };
-  auto use_burst = [&](int i0, const u32x4 (&a)[UNROLL][TPW], const u32x4 (&b)[UNROLL]) {
+  auto use_burst = [&](int i0, const u32x4 (&a)[UNROLL][TPW], const u32x4 (&b)[UNROLL][MT]) {
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
       if (i0 + u < nmine) {
 #pragma unroll
-        for (int t = 0; t < TPW; ++t) acc[t] = mfma_16b<SAGA_DTYPE_BF16>(a[u][t], b[u], acc[t]);
-        if (p.rms) {
-          float f[8];
-          unpack16<SAGA_DTYPE_BF16>(b[u], f);
+        for (int t = 0; t < TPW; ++t)
 #pragma unroll
-          for (int i = 0; i < 8; ++i) ssq += f[i] * f[i];
+          for (int mt = 0; mt < MT; ++mt) acc[t][mt] = mfma_16b<SAGA_DTYPE_BF16>(a[u][t], b[u][mt], acc[t][mt]);
+        if (p.rms) {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            float f[8];
+            unpack16<SAGA_DTYPE_BF16>(b[u][mt], f);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ssq[mt] += f[i] * f[i];
+          }
         }
       }
     }
@@ -156,14 +181,14 @@ gemv_kernel(GemvParams p) {
   // at its header, before the burst.
   GemvPre pre;
   {
-    u32x4 a[UNROLL][TPW], b[UNROLL];
+    u32x4 a[UNROLL][TPW], b[UNROLL][MT];
     load_burst(0, a, b);
     pre = gemv_prefetch<EPI>(p, m, nf, wrow[0]);
     __builtin_amdgcn_sched_barrier(0);
     use_burst(0, a, b);
   }
   for (int i0 = UNROLL; i0 < nmine; i0 += UNROLL) {
-    u32x4 a[UNROLL][TPW], b[UNROLL];
+    u32x4 a[UNROLL][TPW], b[UNROLL][MT];
     load_burst(i0, a, b);
     __builtin_amdgcn_sched_barrier(0);
     use_burst(i0, a, b);
@@ -173,38 +198,42 @@ gemv_kernel(GemvParams p) {
     // (rows 8 + 4s + r, column 8 + c); the x^2 sums of the two halves of token
     // row c & 7 meet in lanes c and c ^ 8
 #pragma unroll
-    for (int r = 0; r < 4; ++r) acc[0][r] += __shfl(acc[0][r], (lane + 40) & 63);
-    ssq += __shfl_xor(ssq, 8);
+    for (int r = 0; r < 4; ++r) acc[0][0][r] += __shfl(acc[0][0][r], (lane + 40) & 63);
+    ssq[0] += __shfl_xor(ssq[0], 8);
   }
-  // lane (col, s): rows n0 + 16t + 4s + r of tile t for token row m = col
+  // lane (col, s): rows n0 + 16t + 4s + r of tile t for token row col + 16 mt
   // (HALF: rows n0 + 4s + r, s < 2, col < 8)
 #pragma unroll
   for (int t = 0; t < TPW; ++t)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) red[w][t][lane][r] = acc[t][r];
-  rsq[w][lane] = ssq;
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[w][t + TPW * mt][lane][r] = acc[t][mt][r];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) rsq[w][mt][lane] = ssq[mt];
   lds_sync();
-  if (w >= TPW) return;
+  if (w >= TPW * MT) return;
   if (HALF && (s >= 2 || col >= 8)) return;  // folded into the lanes above
-  const int t = w;
+  const int t = tf;
+  const int tm = tme;  // this lane's output token row
   float v[4] = {0.f, 0.f, 0.f, 0.f};
   float sq = 0.f;
 #pragma unroll
   for (int q = 0; q < WAVES; ++q) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) v[r] += red[q][t][lane][r];
+    for (int r = 0; r < 4; ++r) v[r] += red[q][t + TPW * mte][lane][r];
     if (p.rms) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) sq += rsq[q][col + 16 * g];  // all k-slot groups of row m
+      for (int g = 0; g < 4; ++g) sq += rsq[q][mte][col + 16 * g];  // all k-slot groups of row tm
     }
   }
-  if (!mvalid) return;
+  if (tm >= p.M) return;
   const int n = nf;
   if (p.part) {
     // split-K: this K range's sums; gemv_splitk_epilogue finishes the rows
-    *reinterpret_cast<f32x4*>(p.part + (static_cast<int64_t>(split) * p.M + col) * p.N + n) =
+    *reinterpret_cast<f32x4*>(p.part + (static_cast<int64_t>(split) * p.M + tm) * p.N + n) =
         f32x4{v[0], v[1], v[2], v[3]};
-    if (s == 0 && blockIdx.x == 0 && t == 0) p.part_ssq[split * p.M + col] = sq;
+    if (s == 0 && blockIdx.x == 0 && t == 0) p.part_ssq[split * p.M + tm] = sq;
     return;
   }
   const float scale = p.rms ? rsqrtf(sq / static_cast<float>(p.K) + p.eps) : 1.f;
@@ -217,7 +246,7 @@ gemv_kernel(GemvParams p) {
     for (int r = 0; r < 4; ++r) bias[r] = bf16_bits_to_f32(static_cast<const uint16_t*>(p.bias)[nf + r]);
   }
   if constexpr (EPI == kGemvRopeKV) {
-    // token row m = col; the 4 rows n..n+3 lie in one head (d % 16 == 0).  q/k
+    // token row tm; the 4 rows n..n+3 lie in one head (d % 16 == 0).  q/k
     // heads are stored in rotary-pair order [0, d/2, 1, d/2 + 1, ...], so rows
     // (n, n+1) and (n+2, n+3) are the pairs (i, i + d/2) of i = j/2, j/2 + 1.
     const RopeParams& rp = p.rope;
@@ -243,7 +272,7 @@ gemv_kernel(GemvParams p) {
         const float y1 = x1 * cs - x2 * sn;
         const float y2 = x2 * cs + x1 * sn;
         if (hh < rp.n_q) {
-          uint16_t* qo = static_cast<uint16_t*>(rp.q_out) + static_cast<int64_t>(col) * rp.q_sn +
+          uint16_t* qo = static_cast<uint16_t*>(rp.q_out) + static_cast<int64_t>(tm) * rp.q_sn +
                          static_cast<int64_t>(hh) * rp.q_sh;
           qo[i] = f32_to_bf16_bits(ok ? y1 : __builtin_nanf(""));
           qo[i + half] = f32_to_bf16_bits(ok ? y2 : __builtin_nanf(""));
@@ -262,7 +291,7 @@ gemv_kernel(GemvParams p) {
     }
     return;
   }
-  uint16_t* y = static_cast<uint16_t*>(p.y) + static_cast<int64_t>(col) * p.y_ld;
+  uint16_t* y = static_cast<uint16_t*>(p.y) + static_cast<int64_t>(tm) * p.y_ld;
   if constexpr (EPI == SAGA_GEMV_SILU_PAIRS) {
     // rows (n, n+1) and (n+2, n+3) are (gate, up) pairs -> outputs n/2, n/2 + 1
 #pragma unroll
@@ -359,6 +388,24 @@ static hipError_t launch_gemv_epi(const GemvParams& p, hipStream_t st) {
     return hipGetLastError();
   }
   const unsigned tiles = static_cast<unsigned>(p.N / 16);
+  if (p.M > 16) {
+    // 17-32 token rows: two token tiles per W fragment, 6 k steps per burst
+    // (12 registers of fragments per step), 8 waves per workgroup so that a
+    // K = 1536 row or a split-K range is one burst
+    if (p.part) {
+      hipLaunchKernelGGL((gemv_kernel<8, EPI, 1, false, 6, 2>), dim3(tiles, p.splits), dim3(512), 0, st, p);
+      const hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      const int64_t pairs = static_cast<int64_t>(p.M) * (p.N / 2);
+      hipLaunchKernelGGL((gemv_splitk_epilogue<EPI>), dim3(static_cast<unsigned>((pairs + 63) / 64)), dim3(64), 0,
+                         st, p);
+    } else if (p.K >= 4096) {
+      hipLaunchKernelGGL((gemv_kernel<16, EPI, 1, false, 6, 2>), dim3(tiles, 1), dim3(1024), 0, st, p);
+    } else {
+      hipLaunchKernelGGL((gemv_kernel<8, EPI, 1, false, 6, 2>), dim3(tiles, 1), dim3(512), 0, st, p);
+    }
+    return hipGetLastError();
+  }
   if (p.part) {
     hipLaunchKernelGGL((gemv_kernel<4, EPI, 1>), dim3(tiles, p.splits), dim3(256), 0, st, p);
     const hipError_t e = hipGetLastError();

@@ -213,7 +213,7 @@ struct RowParams {
 hipError_t launch_rmsnorm(const RowParams& p, hipStream_t st);
 hipError_t launch_silu_mul(const RowParams& p, hipStream_t st);
 
-// Skinny GEMM y[m, n] = rms(x)[m] * sum_k x[m, k] W[n, k] (+ epilogue), m < 16.
+// Skinny GEMM y[m, n] = rms(x)[m] * sum_k x[m, k] W[n, k] (+ epilogue), m < 32.
 struct GemvParams {
   const void* x;  // bf16 [M, K]
   int64_t x_ld;

@@ -14,7 +14,7 @@ fused -> RoPE + cache append -> attention (Atop-N: scores, then
 select + softmax.V; or dense) -> o_proj accumulated into the residual stream
 -> [gate, up] projection with the RMSNorm and silu(gate)*up fused -> down
 projection accumulated into the residual stream.  Projections use the
-saga_amd skinny GEMM (batch <= 16; hipBLASLt otherwise), the LM head is
+saga_amd skinny GEMM (batch <= 32; hipBLASLt otherwise), the LM head is
 followed by a row argmax kernel.  Positions advance on the device, so one
 captured graph serves every step.
 """
@@ -131,8 +131,8 @@ class SagaDecoder:
         self._gu = torch.empty(batch, 2 * s.intermediate, device=self.device, dtype=dtype)
         self._act = torch.empty(batch, s.intermediate, device=self.device, dtype=dtype)
         self._logits = torch.empty(batch, s.vocab, device=self.device, dtype=dtype)
-        # decode projections: the skinny-GEMM kernel for up to 16 token rows
-        self.use_gemv = (batch <= 16 and dtype == torch.bfloat16 and s.hidden % 32 == 0 and s.intermediate % 32 == 0
+        # decode projections: the skinny-GEMM kernel for up to 32 token rows
+        self.use_gemv = (batch <= 32 and dtype == torch.bfloat16 and s.hidden % 32 == 0 and s.intermediate % 32 == 0
                          and (s.n_q * d) % 32 == 0 and s.qkv_width % 16 == 0 and s.vocab % 16 == 0)
         # q/k/v projection, RoPE and cache append in one launch (pair-ordered rows)
         self.fuse_rope = fuse_rope and self.use_gemv and d % 16 == 0

@@ -485,7 +485,7 @@ def _gemv_n(w: torch.Tensor) -> int:
 
 
 def gemv(x, w, bias=None, rms_eps=None, epilogue="store", out=None, split_k=True, workspace=None):
-    """Skinny projection for decode (x [M <= 16, K] bf16, w [N, K] bf16, or
+    """Skinny projection for decode (x [M <= 32, K] bf16, w [N, K] bf16, or
     packed by pack_gemv_weight):
     y = s * x @ w.T (+ bias), s = 1/sqrt(mean(x^2) + rms_eps) per row when
     rms_eps is given (RMSNorm fused, norm weight folded into w).
@@ -525,7 +525,7 @@ def rope_pair_order(n_q, n_k, n_v, d, device=None):
 
 def gemv_rope_kv(x, w_pairs, bias_pairs, n_q, n_k, n_v, theta, pos, k_cache, v_cache, rms_eps=None, batch=None,
                  q_out=None, rope_table=None):
-    """Fused q/k/v projection + RoPE + KV-cache append for M <= 16 new tokens:
+    """Fused q/k/v projection + RoPE + KV-cache append for M <= 32 new tokens:
     the same results as gemv(x, w, bias) followed by rope_kv_append, with w
     and bias given in rope_pair_order.  rope_table: rope_table(pos, d, theta)
     of the same positions (the rotations computed once for several layers),

@@ -11,6 +11,7 @@ from saga_amd import _lib, ops
 pytestmark = pytest.mark.gpu
 
 SHAPES = [(8, 1536, 1792), (8, 1536, 1536), (8, 1536, 17920), (8, 8960, 1536), (1, 960, 1344), (16, 1536, 4096),
+          (32, 1536, 1920), (17, 8960, 1536), (24, 4096, 64), (32, 64, 32),
           (3, 64, 32), (8, 2560, 960)]
 
 
@@ -45,7 +46,7 @@ def test_gemv_add_in_place(M, K, N):
     assert rel_l2(host(out), ref) < 4e-3
 
 
-@pytest.mark.parametrize("M,K,N", [(8, 1536, 17920), (1, 960, 5120), (4, 64, 64)])
+@pytest.mark.parametrize("M,K,N", [(8, 1536, 17920), (1, 960, 5120), (4, 64, 64), (32, 1536, 17920)])
 def test_gemv_silu_pairs(M, K, N):
     rng = np.random.default_rng(7 + N)
     x, w, _ = _data(rng, M, K, N)
@@ -58,9 +59,9 @@ def test_gemv_silu_pairs(M, K, N):
 
 
 def test_gemv_rejects_bad_shapes():
-    x = torch.zeros(17, 64, device="cuda", dtype=torch.bfloat16)
+    x = torch.zeros(33, 64, device="cuda", dtype=torch.bfloat16)
     w = torch.zeros(32, 64, device="cuda", dtype=torch.bfloat16)
-    with pytest.raises(RuntimeError, match="16 rows"):
+    with pytest.raises(RuntimeError, match="32 rows"):
         ops.gemv(x, w)
     with pytest.raises(RuntimeError, match="N % 16"):
         ops.gemv(x[:4], torch.zeros(20, 64, device="cuda", dtype=torch.bfloat16))
@@ -76,7 +77,8 @@ def test_argmax_rows_first_max(N):
     np.testing.assert_array_equal(got, np.argmax(x, axis=1))
 
 
-@pytest.mark.parametrize("M,K,n_q,n_k,n_v,d", [(8, 1536, 12, 1, 2, 128), (1, 960, 15, 1, 5, 64), (16, 512, 4, 2, 2, 64)])
+@pytest.mark.parametrize("M,K,n_q,n_k,n_v,d", [(8, 1536, 12, 1, 2, 128), (1, 960, 15, 1, 5, 64), (16, 512, 4, 2, 2, 64),
+                                             (32, 1536, 12, 1, 2, 128), (19, 960, 15, 1, 5, 64)])
 def test_gemv_rope_kv_matches_unfused(M, K, n_q, n_k, n_v, d):
     """Projection + RoPE + cache append in one launch == gemv then
     rope_kv_append (the projection is rounded to bf16 before the rotation in
@@ -84,7 +86,7 @@ def test_gemv_rope_kv_matches_unfused(M, K, n_q, n_k, n_v, d):
     rng = np.random.default_rng(M * 7 + K)
     N = (n_q + n_k + n_v) * d
     x, w, b = _data(rng, M, K, N)
-    B, Lmax = 16, 2048
+    B, Lmax = max(16, M), 2048
     pos = torch.from_numpy(rng.integers(0, Lmax, M).astype(np.int32)).cuda()
     batch = torch.from_numpy(rng.permutation(B)[:M].astype(np.int32)).cuda()
     xd, wd, bd = dev(x, "bf16"), dev(w, "bf16"), dev(b, "bf16")
@@ -130,7 +132,7 @@ def test_rope_table_against_float64(d, theta):
     np.testing.assert_allclose(got[small, :, 1], np.sin(ang[small]), atol=2e-6)
 
 
-@pytest.mark.parametrize("M,K,n_q,n_k,n_v,d", [(8, 1536, 12, 1, 2, 128), (1, 960, 15, 1, 5, 64)])
+@pytest.mark.parametrize("M,K,n_q,n_k,n_v,d", [(8, 1536, 12, 1, 2, 128), (1, 960, 15, 1, 5, 64), (32, 1536, 12, 1, 2, 128)])
 def test_gemv_rope_kv_with_table_identical(M, K, n_q, n_k, n_v, d):
     """The fused projection with the step's rotation table (computed once for
     all layers) writes the same bits as with the rotations computed in its
@@ -138,7 +140,7 @@ def test_gemv_rope_kv_with_table_identical(M, K, n_q, n_k, n_v, d):
     rng = np.random.default_rng(M * 13 + K)
     N = (n_q + n_k + n_v) * d
     x, w, b = _data(rng, M, K, N)
-    B, Lmax = 16, 40000
+    B, Lmax = max(16, M), 40000
     pos = torch.from_numpy(rng.integers(0, Lmax, M).astype(np.int32)).cuda()
     pos[0] = Lmax - 1
     batch = torch.from_numpy(rng.permutation(B)[:M].astype(np.int32)).cuda()
@@ -166,14 +168,15 @@ def test_rope_pair_order_is_a_permutation():
     assert order[:8].tolist() == [0, 4, 1, 5, 2, 6, 3, 7] and order[32:].tolist() == list(range(32, 48))
 
 
+@pytest.mark.parametrize("M", [8, 32, 23])
 @pytest.mark.parametrize("epilogue", ["store", "add", "silu_pairs"])
 @pytest.mark.parametrize("rms", [False, True])
-def test_gemv_split_k_matches_single_pass_and_is_deterministic(epilogue, rms):
+def test_gemv_split_k_matches_single_pass_and_is_deterministic(M, epilogue, rms):
     """Long rows with few tiles (the down projection shape) go through the
     split-K path; it agrees with the one-workgroup-per-tile path and repeats
     bit for bit."""
-    rng = np.random.default_rng(77)
-    M, K, N = 8, 8960, 1536
+    rng = np.random.default_rng(77 + M)
+    K, N = 8960, 1536
     x, w, _ = _data(rng, M, K, N)
     xd, wd = dev(x, "bf16"), dev(w, "bf16")
     assert _lib.load().saga_gemv_workspace_bytes(M, N, K) > 0
@@ -190,7 +193,7 @@ def test_gemv_split_k_matches_single_pass_and_is_deterministic(epilogue, rms):
 
 # (5, 32, 64): one 32-column block, whose size-1 dim keeps torch's stride
 @pytest.mark.parametrize("M,K,N", [(8, 1536, 1920), (8, 1536, 17920), (8, 8960, 1536), (3, 64, 32), (8, 1536, 151936),
-                                   (5, 32, 64)])
+                                   (5, 32, 64), (32, 1536, 1920), (29, 8960, 1536), (32, 1536, 151936)])
 @pytest.mark.parametrize("epilogue", ["store", "add", "silu_pairs"])
 def test_packed_weights_give_identical_results(M, K, N, epilogue):
     """W in the packed MFMA-fragment layout [N/16, K/32, 16, 32] feeds the same
@@ -317,7 +320,8 @@ def test_split_k_shapes_share_one_workspace():
     workspace (the tile counters sit at a fixed offset and are left at zero):
     each matches its single-pass result."""
     rng = np.random.default_rng(90)
-    for M, K, N in [(8, 2560, 960), (8, 8960, 1536), (4, 2560, 960), (8, 8960, 1536), (2, 4096, 256)]:
+    for M, K, N in [(8, 2560, 960), (8, 8960, 1536), (32, 8960, 1536), (4, 2560, 960), (8, 8960, 1536), (2, 4096, 256),
+                    (17, 2560, 960)]:
         x, w, _ = _data(rng, M, K, N)
         xd, wd = dev(x, "bf16"), dev(w, "bf16")
         for rms in (None, 1e-6):

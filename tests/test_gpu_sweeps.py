@@ -96,7 +96,7 @@ def test_gemv_sweep(seed):
     """Seeded shapes, epilogues and W layouts (row-major, 16-row packed, and
     8-row packed for at most 8 token rows) against the float64 product."""
     rng = np.random.default_rng(90000 + seed)
-    M = int(rng.integers(1, 17))
+    M = int(rng.integers(1, 33))
     K = 32 * int(rng.choice([1, 2, 5, 48, 63, 280]))
     N = 16 * int(rng.choice([1, 2, 7, 96, 120, 560, 1120]))
     epi = ("store", "add", "silu_pairs")[seed % 3]
@@ -138,7 +138,7 @@ def test_gemv_sweep(seed):
 @pytest.mark.parametrize("seed", range(9))
 def test_rope_kv_projection_sweep(seed):
     rng = np.random.default_rng(110000 + seed)
-    M = int(rng.integers(1, 17))
+    M = int(rng.integers(1, 33))
     if seed % 3 == 1:  # 8-row packed weights take at most 8 token rows
         M = min(M, 8)
     n_q, n_k, n_v = GROUPS[seed % len(GROUPS)]
