@@ -86,12 +86,12 @@ def test_rmsnorm_and_silu_mul_match_oracle():
     assert rel_l2(a, O.silu_mul(gu)) < 4e-3
 
 
-def _tiny_model(mode, top_n=16, keep_source_weights=False):
+def _tiny_model(mode, top_n=16, keep_source_weights=False, batch=2):
     from saga_amd.decoder import DecoderShape, SagaDecoder
     shape = DecoderShape(layers=3, hidden=256, n_q=4, n_k=1, n_v=2, head_dim=64, intermediate=512, vocab=1024,
                          rope_theta=1e4, eps=1e-6, qkv_bias=True)
-    m = SagaDecoder(shape, batch=2, max_len=600, mode=mode, top_n=top_n, exempt_layers=(0,) if mode == "atopn" else (),
-                    keep_source_weights=keep_source_weights)
+    m = SagaDecoder(shape, batch=batch, max_len=600, mode=mode, top_n=top_n,
+                    exempt_layers=(0,) if mode == "atopn" else (), keep_source_weights=keep_source_weights)
     return m
 
 
@@ -115,12 +115,15 @@ def test_graph_replay_equals_eager_steps(mode):
     assert int(m.pos[0]) == 504 and int(m.kv_len[0]) == 505
 
 
-def test_one_decode_step_vs_float64_reference():
+@pytest.mark.parametrize("batch", [2, 24])
+def test_one_decode_step_vs_float64_reference(batch):
     """One dense decode step of the harness recomputed on the host in float64:
     embed, rmsnorm, projections, RoPE, cache append, attention, MLP, LM head.
     (Dense attention: an Atop-N top-k boundary could flip under the bf16
-    rounding of the intermediates; selection is checked by its own tests.)"""
-    m = _tiny_model("dense", keep_source_weights=True)
+    rounding of the intermediates; selection is checked by its own tests.)
+    Batch 24: the projections' 17-32-row kernels (two token tiles per weight
+    fragment) and 16-row weight tiles."""
+    m = _tiny_model("dense", keep_source_weights=True, batch=batch)
     g = torch.Generator(device="cuda").manual_seed(5)
     for t in m.ln1 + m.ln2 + [m.ln_f]:  # non-trivial norm weights: exercises their folding
         t.copy_((1 + 0.3 * torch.randn(t.shape, generator=g, device="cuda")).to(t.dtype))
@@ -128,17 +131,18 @@ def test_one_decode_step_vs_float64_reference():
     assert m.use_gemv
     prompt_len = 400
     m.fill_synthetic(prompt_len)
-    m.tokens.copy_(torch.tensor([3, 1023], device="cuda"))
+    toks = [3, 1023] + [(37 * i + 11) % 1024 for i in range(batch - 2)]
+    m.tokens.copy_(torch.tensor(toks, device="cuda"))
     s = m.shape
     f = lambda t: t.detach().to(torch.float64).cpu().numpy()
     kc0, vc0 = f(m.k_cache), f(m.v_cache)
     m.step(calibrate=True)
     torch.cuda.synchronize()
-    x = f(m.embed)[[3, 1023]]
+    x = f(m.embed)[toks]
     for l in range(s.layers):
         h = O.rmsnorm(x, f(m.ln1[l]), s.eps)
         qkv = h @ f(m.w_qkv[l]).T + f(m.b_qkv[l])
-        qkv = qkv.reshape(2, s.n_q + s.n_k + s.n_v, s.head_dim)
+        qkv = qkv.reshape(batch, s.n_q + s.n_k + s.n_v, s.head_dim)
         q = O.rope(qkv[:, :s.n_q], prompt_len, s.rope_theta)
         k_new = O.rope(qkv[:, s.n_q:s.n_q + s.n_k], prompt_len, s.rope_theta)
         K, V = kc0[l][:, :, :prompt_len + 1].copy(), vc0[l][:, :, :prompt_len + 1].copy()
@@ -146,14 +150,14 @@ def test_one_decode_step_vs_float64_reference():
         V[:, :, prompt_len] = qkv[:, s.n_q + s.n_k:]
         q4 = q[:, :, None, :]
         attn = O.dense(q4, K, V)
-        x = x + attn.reshape(2, -1) @ f(m.w_o[l]).T
+        x = x + attn.reshape(batch, -1) @ f(m.w_o[l]).T
         h = O.rmsnorm(x, f(m.ln2[l]), s.eps)
         x = x + O.silu_mul(h @ f(m.w_gu[l]).T) @ f(m.w_d[l]).T
     logits = O.rmsnorm(x, f(m.ln_f), s.eps) @ f(m.embed).T
     got = f(m._logits)
     assert rel_l2(got, logits) < 3e-2
     # bf16 rounding of intermediates may flip a near-tie argmax; compare when the margin is clear
-    for r in range(2):
+    for r in range(batch):
         top2 = np.sort(logits[r])[-2:]
         if top2[1] - top2[0] > 0.05:
             assert int(m.tokens[r]) == int(np.argmax(logits[r]))
