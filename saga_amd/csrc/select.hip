@@ -79,10 +79,143 @@ __device__ void row_pv(SelShared& sh, float* accs, int n, const int32_t* gidx, c
   pv.finish(accs, v.out, v.out_dt, bi * v.o_sb + static_cast<int64_t>(h) * v.o_sh, probs);
 }
 
+// Bin holding the krem-th largest element of sh.hist[0..nb) (bin nb - 1 holds
+// the largest) and the count in the bins above it; bin -1 if fewer than krem
+// elements are counted.  Every thread of the block calls it.
+__device__ __forceinline__ void hist_pick(SelShared& sh, int nb, int krem, int& bin, int& above) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  if (tid == 0) sh.sel_bin = -1;
+  // bins scanned from the top: thread t owns bins nb-1-2t and nb-2-2t
+  const int b0 = nb - 1 - 2 * tid, b1 = b0 - 1;
+  const int c0 = b0 >= 0 ? sh.hist[b0] : 0;
+  const int c1 = b1 >= 0 ? sh.hist[b1] : 0;
+  const int tsum = c0 + c1;
+  const int incl = wave_incl_scan(tsum, lane);
+  if (lane == kWave - 1) sh.cnt[w] = incl;
+  __syncthreads();
+  int woff = 0;
+  for (int i = 0; i < w; ++i) woff += sh.cnt[i];
+  const int ex = woff + incl - tsum;
+  if (c0 > 0 && ex < krem && krem <= ex + c0) {
+    sh.sel_bin = b0;
+    sh.sel_above = ex;
+  } else if (c1 > 0 && ex + c0 < krem && krem <= ex + tsum) {
+    sh.sel_bin = b1;
+    sh.sel_above = ex + c0;
+  }
+  __syncthreads();
+  bin = sh.sel_bin;
+  above = sh.sel_above;
+  __syncthreads();
+}
+
+// f(x[i]) for every i < n of a score row (ld floats, 16-byte aligned, n <= ld),
+// in tiles of 16 elements per thread whose four 16-byte loads are in flight
+// together (one load per element and step would wait out a round trip each).
+template <class F>
+__device__ __forceinline__ void row_tiles(const float* x, int64_t ld, int n, F f) {
+  const int tid = threadIdx.x;
+  for (int st = 0; st < n; st += 16 * kBlkThreads) {
+    f32x4 v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t e = st + 4 * (q * kBlkThreads + tid);
+      v[q] = e < ld ? *reinterpret_cast<const f32x4*>(x + e) : f32x4{kNegInf, kNegInf, kNegInf, kNegInf};
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (st + 4 * (q * kBlkThreads + tid) + j < n) f(v[q][j]);
+  }
+}
+
+// The krem-th largest of n keys -- of the score row x (ROW) or of the LDS
+// candidates sh.sval -- by a 3-pass radix select (11/11/10 bits of the
+// order-preserving uint32 key) over 2048-bin LDS histograms; krem is left at
+// the count of elements equal to it that are among the krem largest.
+template <bool ROW>
+__device__ __forceinline__ uint32_t radix_select(SelShared& sh, const float* x, int64_t ld, int n, int& krem) {
+  const int tid = threadIdx.x;
+  uint32_t prefix = 0;
+  const int shifts[3] = {21, 10, 0};
+  const int nbits[3] = {11, 11, 10};
+#pragma unroll
+  for (int pass = 0; pass < 3; ++pass) {
+    const int nb = 1 << nbits[pass];
+    const uint32_t hmask = pass == 0 ? 0u : (0xffffffffu << (shifts[pass] + nbits[pass]));
+    for (int i = tid; i < 2048; i += kBlkThreads) sh.hist[i] = 0;
+    __syncthreads();
+    auto count = [&](float xi) {
+      const uint32_t key = f32_to_key(xi);
+      if ((key & hmask) == prefix) atomicAdd(&sh.hist[(key >> shifts[pass]) & (nb - 1)], 1);
+    };
+    if constexpr (ROW) {
+      row_tiles(x, ld, n, count);
+    } else {
+      for (int i = tid; i < n; i += kBlkThreads) count(sh.sval[i]);
+    }
+    __syncthreads();
+    int bin, above;
+    hist_pick(sh, nb, krem, bin, above);
+    prefix |= static_cast<uint32_t>(bin) << shifts[pass];
+    krem -= above;
+  }
+  return prefix;
+}
+
+constexpr int kNearBins = 2048;      // bins of the distance below the row max
+constexpr float kNearScale = 32.0f;  // bins per unit of logit: the bins span M - 64 .. M
+
+// The krem-th largest score of the row without a radix pass over it: one
+// pass counts every position into its bin of distance (M - x) * 32 below the
+// row max M (the bins are monotone in x, so every element of a nearer bin is
+// strictly larger than every element of a farther one), a second gathers
+// the elements of the bin that holds the krem-th largest into LDS, and the
+// radix select runs over those few.  On N(0,1)-like scores the counts spread
+// over hundreds of bins, where the top bits of the float key put them into a
+// handful (LDS atomics serialised up to 64 ways).  Returns false, leaving the
+// work to the full-row select, for a NaN or non-finite max, a k-th value more
+// than 64 below M, or more candidates than the LDS list holds.  kth and krem
+// as radix_select.
+__device__ __forceinline__ bool near_pick(SelShared& sh, const float* x, int64_t ld, int Leff, float M, int& krem,
+                                          uint32_t& kth) {
+  const int tid = threadIdx.x;
+  if (!(M > -INFINITY && M < INFINITY)) return false;  // block-uniform
+  for (int i = tid; i < kNearBins; i += kBlkThreads) sh.hist[i] = 0;
+  __syncthreads();
+  int odd = 0;
+  row_tiles(x, ld, Leff, [&](float xi) {
+    if (!(xi <= M)) {  // NaN
+      odd = 1;
+      return;
+    }
+    const float dd = (M - xi) * kNearScale;
+    if (dd < kNearBins) atomicAdd(&sh.hist[kNearBins - 1 - static_cast<int>(dd)], 1);
+  });
+  if (__syncthreads_or(odd)) return false;
+  int bin, above;
+  hist_pick(sh, kNearBins, krem, bin, above);
+  if (bin < 0) return false;
+  const int c = sh.hist[bin];
+  if (c > kListLDS) return false;
+  const int want = kNearBins - 1 - bin;  // distance bin of the candidates
+  if (tid == 0) sh.sel_bin = 0;          // candidate count
+  __syncthreads();
+  row_tiles(x, ld, Leff, [&](float xi) {
+    const float dd = (M - xi) * kNearScale;
+    if (dd < kNearBins && static_cast<int>(dd) == want) sh.sval[atomicAdd(&sh.sel_bin, 1)] = xi;
+  });
+  __syncthreads();
+  krem -= above;
+  kth = radix_select<false>(sh, nullptr, 0, c, krem);
+  return true;
+}
+
 // Calibration: exact top-k of the row (k = min(top_n, L)).
 //   1. full-row max M and sum S of exp(x - M) from the K1 partials;
-//   2. the k-th largest value by a 3-pass radix select (11/11/10 bits of the
-//      order-preserving uint32 key) over 2048-bin LDS histograms;
+//   2. the k-th largest value: by a radix select over the few elements of
+//      its bin of distance below M (near_pick), else over the whole row;
 //   3. ordered compaction of the elements above it plus the first (by index)
 //      elements equal to it, exactly k;
 //   4. p* = exp(x_k - M) / S, the k-th largest probability, into the
@@ -125,45 +258,14 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_kernel(FusedSelPa
     return;
   }
 
-  uint32_t prefix = 0;
+  // the k-th largest key: among the few elements of its bin of distance
+  // below M when that is cheap (near_pick), else over the whole row
   int krem = k;
-  const int shifts[3] = {21, 10, 0};
-  const int nbits[3] = {11, 11, 10};
-#pragma unroll
-  for (int pass = 0; pass < 3; ++pass) {
-    const int nb = 1 << nbits[pass];
-    const uint32_t hmask = pass == 0 ? 0u : (0xffffffffu << (shifts[pass] + nbits[pass]));
-    for (int i = tid; i < 2048; i += kBlkThreads) sh.hist[i] = 0;
-    __syncthreads();
-    for (int i = tid; i < Leff; i += kBlkThreads) {
-      const uint32_t key = f32_to_key(x[i]);
-      if ((key & hmask) == prefix) atomicAdd(&sh.hist[(key >> shifts[pass]) & (nb - 1)], 1);
-    }
-    __syncthreads();
-    // bins scanned from the top: thread t owns bins nb-1-2t and nb-2-2t
-    const int b0 = nb - 1 - 2 * tid, b1 = b0 - 1;
-    const int c0 = b0 >= 0 ? sh.hist[b0] : 0;
-    const int c1 = b1 >= 0 ? sh.hist[b1] : 0;
-    const int tsum = c0 + c1;
-    const int incl = wave_incl_scan(tsum, lane);
-    if (lane == kWave - 1) sh.cnt[w] = incl;
-    __syncthreads();
-    int woff = 0;
-    for (int i = 0; i < w; ++i) woff += sh.cnt[i];
-    const int ex = woff + incl - tsum;
-    if (c0 > 0 && ex < krem && krem <= ex + c0) {
-      sh.sel_bin = b0;
-      sh.sel_above = ex;
-    } else if (c1 > 0 && ex + c0 < krem && krem <= ex + tsum) {
-      sh.sel_bin = b1;
-      sh.sel_above = ex + c0;
-    }
-    __syncthreads();
-    prefix |= static_cast<uint32_t>(sh.sel_bin) << shifts[pass];
-    krem -= sh.sel_above;
-    __syncthreads();
+  uint32_t kth = 0;
+  if (!near_pick(sh, x, p.ld, Leff, M, krem, kth)) {
+    krem = k;
+    kth = radix_select<true>(sh, x, p.ld, Leff, krem);
   }
-  const uint32_t kth = prefix;
   const int need = krem;  // elements equal to the k-th value that are taken
 
   int baseG = 0, baseE = 0;
