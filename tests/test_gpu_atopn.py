@@ -636,3 +636,28 @@ def test_fast_step_random_shapes_vs_oracle(seed):
                                   v[i:i + 1, (j // (q_h // v_h)):(j // (q_h // v_h)) + 1], (1, 1, 1, d),
                                   input_is_logits=True)
             assert rel_l2(out.reshape(nr, d)[r], ref.reshape(d)) < tol, (r, cnt)
+
+
+@pytest.mark.parametrize("case", ["constant", "far_outlier", "near_constant", "gaussian"])
+def test_calibration_kth_logit_paths(case):
+    """The calibration kernel finds the N-th logit among the few elements of
+    its distance-below-max bin, or over the whole row when that bin holds more
+    than 4096 elements (all logits equal: ties taken by lowest index; or all
+    within 1/32 of the max) or the N-th logit lies more than 64 below the max
+    (one huge key): every path against the float64 oracle, fp32 inputs."""
+    rng = np.random.default_rng(zlib.crc32(case.encode()))
+    b, q_h, k_h, v_h, d, L, N = 2, 4, 1, 2, 64, 6000, 256
+    q = rng.standard_normal((b, q_h, 1, d), dtype=np.float32)
+    k = rng.standard_normal((b, k_h, L, d), dtype=np.float32)
+    v = rng.standard_normal((b, v_h, L, d), dtype=np.float32)
+    if case == "constant":
+        k[:] = 0.0
+    elif case == "near_constant":
+        k *= np.float32(1e-3)
+    elif case == "far_outlier":
+        k[:, 0, 1234] = q[:, 0, 0] * np.float32(50.0)  # logit ~400 for head 0, ~+-50 for the others
+    table = torch.zeros(b * q_h, device="cuda")
+    cal = host(ops.atopn_calibrate(dev(q, "f32"), dev(k, "f32"), dev(v, "f32"), N, table, out_dtype=torch.float32))
+    ref, thr, _ = O.calibrate(q, k, v, None, N, None)
+    assert rel_l2(cal, ref) < 1e-4, case
+    np.testing.assert_allclose(host(table), thr, rtol=1e-4)
