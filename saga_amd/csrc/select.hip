@@ -4,11 +4,13 @@
 // Replaces torch.topk + the renormalised gather of
 // approx_top_n_attention_amortized_cal (attention/attention.py:173-189) and
 // the Triton stream compaction threshold_select_fast_kernel
-// (attention/triton_atopn.py:6-53).  Ordered, deterministic compaction: a
-// row is read in tiles of 1024 x 16 elements; each wave turns its pass flags
-// into 64-bit ballots, the per-(slot, wave) counts are prefix-summed in LDS in
-// ascending index order, and every passing element goes to
-// base + prefix + popcount(ballot & lanes_below).
+// (attention/triton_atopn.py:6-53).  Ordered, deterministic compactions.
+// API kernel: a row is read in tiles of 1024 x 16 elements; each wave turns
+// its pass flags into 64-bit ballots, the per-(slot, wave) counts are
+// prefix-summed in LDS in ascending index order, and every passing element
+// goes to base + prefix + popcount(ballot & lanes_below).  Calibration: each
+// wave takes 1024 consecutive elements of a tile, so a rank is the lower
+// waves' total + the wave's running count + mbcnt.
 #include <type_traits>
 
 #include "block_pv.cuh"
@@ -268,50 +270,70 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_kernel(FusedSelPa
   }
   const int need = krem;  // elements equal to the k-th value that are taken
 
+  // Ordered compaction, tile by tile: wave w takes the kSelEPT * 64
+  // consecutive elements [st + 1024 w, st + 1024 (w + 1)) of the tile, so the
+  // index order is (tile, wave, step, lane) and an element's rank is its
+  // wave's offset (the totals of the lower waves) + the running count of its
+  // wave + its lane's mbcnt; loads are clamped, not branched (a load under a
+  // branch is waited for at the join).
   int baseG = 0, baseE = 0;
   for (int st = 0; st < Leff; st += kSelTile) {
+    const int w0 = st + w * (kSelEPT * kWave);
     float xv[kSelEPT];
+#pragma unroll
+    for (int kk = 0; kk < kSelEPT; ++kk) xv[kk] = x[min(w0 + kk * kWave + lane, Leff - 1)];
     unsigned long long bg[kSelEPT], be[kSelEPT];
+    int cg = 0, ce = 0;
 #pragma unroll
     for (int kk = 0; kk < kSelEPT; ++kk) {
-      const int i = st + kk * kBlkThreads + tid;
-      xv[kk] = i < Leff ? x[i] : kNegInf;
-    }
-#pragma unroll
-    for (int kk = 0; kk < kSelEPT; ++kk) {
-      const int i = st + kk * kBlkThreads + tid;
+      const bool in = w0 + kk * kWave + lane < Leff;
       const uint32_t key = f32_to_key(xv[kk]);
-      bg[kk] = __ballot(i < Leff && key > kth);
-      be[kk] = __ballot(i < Leff && key == kth);
-      if (lane == 0) {
-        sh.cnt[kk * kBlkWaves + w] = __popcll(bg[kk]);
-        sh.cntE[kk * kBlkWaves + w] = __popcll(be[kk]);
-      }
+      bg[kk] = __ballot(in && key > kth);
+      be[kk] = __ballot(in && key == kth);
+      cg += __popcll(bg[kk]);
+      ce += __popcll(be[kk]);
+    }
+    if (lane == 0) {
+      sh.cnt[w] = cg;
+      sh.cntE[w] = ce;
     }
     __syncthreads();
-    if (w == 0) scan_slots(sh.cnt, sh.pre, lane);
-    if (w == 1) scan_slots(sh.cntE, sh.preE, lane);
-    __syncthreads();
+    int g_off = baseG, e_off = baseE, totG = 0, totE = 0;
+#pragma unroll
+    for (int q = 0; q < kBlkWaves; ++q) {
+      const int a = sh.cnt[q], b = sh.cntE[q];
+      if (q < w) {
+        g_off += a;
+        e_off += b;
+      }
+      totG += a;
+      totE += b;
+    }
 #pragma unroll
     for (int kk = 0; kk < kSelEPT; ++kk) {
-      const int slot = kk * kBlkWaves + w;
-      const int i = st + kk * kBlkThreads + tid;
-      const int g_before = baseG + sh.pre[slot] + __popcll(bg[kk] & lanes_below(lane));
-      const int e_before = baseE + sh.preE[slot] + __popcll(be[kk] & lanes_below(lane));
-      int pos = -1;
-      if ((bg[kk] >> lane) & 1ull) pos = g_before + min(e_before, need);
-      else if (((be[kk] >> lane) & 1ull) && e_before < need) pos = g_before + e_before;
-      if (pos >= 0) {
-        gidx[pos] = i;
-        gval[pos] = xv[kk];
-        if (pos < kListLDS) {
-          sh.sidx[pos] = i;
-          sh.sval[pos] = xv[kk];
+      if ((bg[kk] | be[kk]) != 0ull) {  // wave-uniform: most steps hold no taken element
+        const int g_before = g_off + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+            static_cast<uint32_t>(bg[kk] >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bg[kk]), 0u)));
+        const int e_before = e_off + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+            static_cast<uint32_t>(be[kk] >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(be[kk]), 0u)));
+        int pos = -1;
+        if ((bg[kk] >> lane) & 1ull) pos = g_before + min(e_before, need);
+        else if (((be[kk] >> lane) & 1ull) && e_before < need) pos = g_before + e_before;
+        if (pos >= 0) {
+          const int i = w0 + kk * kWave + lane;
+          gidx[pos] = i;
+          gval[pos] = xv[kk];
+          if (pos < kListLDS) {
+            sh.sidx[pos] = i;
+            sh.sval[pos] = xv[kk];
+          }
         }
       }
+      g_off += __popcll(bg[kk]);
+      e_off += __popcll(be[kk]);
     }
-    baseG += sh.pre[kSelSlots];
-    baseE += sh.preE[kSelSlots];
+    baseG += totG;
+    baseE += totE;
     __syncthreads();
   }
   if (tid == 0) {
