@@ -661,3 +661,41 @@ def test_calibration_kth_logit_paths(case):
     ref, thr, _ = O.calibrate(q, k, v, None, N, None)
     assert rel_l2(cal, ref) < 1e-4, case
     np.testing.assert_allclose(host(table), thr, rtol=1e-4)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_calibration_random_shapes_exact_topk(seed):
+    """The calibration step at the seeded shapes of the fast-step test: its
+    kept list is exactly the top min(N, kv_len) of the GPU's own fp32 scores
+    (equal scores taken by lowest index), in ascending position order; the
+    stored p* and the output follow from that list in float64."""
+    b, q_h, k_h, v_h, d, L, N, dt, lens, rng = _random_case(seed)
+    print(f"calibration random seed={seed} b={b} q/k/v={q_h}/{k_h}/{v_h} d={d} L={L} N={N} {dt} kv_len={lens}",
+          flush=True)
+    (q, k, v), (qd, kd, vd) = qkv(rng, b, q_h, k_h, v_h, d, L, dt, outliers=0.01 * (seed % 2))
+    kvl = None if lens is None else torch.from_numpy(lens).cuda()
+    nr, cap = b * q_h, min(N, L)
+    table = torch.zeros(nr, device="cuda")
+    out = host(ops.atopn_calibrate(qd, kd, vd, N, table, kv_len=kvl, out_dtype=torch.float32)).reshape(nr, d)
+    torch.cuda.synchronize()
+    views = _views(b, q_h, k_h, L, d, cap, fast=False)
+    x = views["scores"]
+    thr = host(table)
+    tol = 1e-5 if dt == "f32" else 1e-3
+    for r in range(nr):
+        i, j = divmod(r, q_h)
+        n = L if lens is None else int(lens[i])
+        kk = min(cap, n)
+        assert views["sel_cnt"][r] == kk
+        xr = x[r, :n].astype(np.float64)
+        top = np.sort(np.argsort(-x[r, :n], kind="stable")[:kk])
+        np.testing.assert_array_equal(views["sel_idx"][r, :kk], top)
+        if kk == 0:
+            continue
+        m = xr.max()
+        kth = xr[np.argsort(-x[r, :n], kind="stable")[kk - 1]]
+        np.testing.assert_allclose(thr[r], np.exp(kth - m) / np.exp(xr - m).sum(), rtol=1e-4)
+        w = np.exp(xr[top] - xr[top].max())
+        vv = v[i, j // (q_h // v_h), top].astype(np.float64)
+        ref = (w[:, None] * vv).sum(0) / w.sum()
+        assert rel_l2(out[r], ref) < tol, (r, kk)
