@@ -60,6 +60,15 @@ SMOLLM2_360M_SAGA = DecoderShape(32, 960, 15, 1, 5, 64, 2560, 49152, 1e5, 1e-5, 
 SMOLLM2_360M_GQA = replace(SMOLLM2_360M_SAGA, n_k=5)
 
 
+def gemv_tile_rows(shape: DecoderShape, batch: int) -> int:
+    """Weight tile rows of the q/k/v, o and down projections: 8-row tiles
+    (packed [N/8, K/64, 512]: twice the workgroups of 16-row tiles) when the
+    batch is at most 8 rows and every one of those weights has K % 64 == 0
+    (q/k/v: hidden, o: n_q * head_dim, down: intermediate), else 16."""
+    ks = (shape.hidden, shape.n_q * shape.head_dim, shape.intermediate)
+    return 8 if batch <= 8 and all(k % 64 == 0 for k in ks) else 16
+
+
 class _HeadGroups(torch.nn.Module):
     """Stand-in for the HF attention module passed to sdpa_attention_forward."""
     num_key_value_groups = 1
@@ -230,7 +239,7 @@ class SagaDecoder:
                 # the 1.5B shape) in 8-row tiles when the batch allows (<= 8
                 # rows: twice the workgroups, no split over K)
                 pk = ops.pack_gemv_weight
-                rows8 = 8 if self.batch <= 8 and s.hidden % 64 == 0 and s.intermediate % 64 == 0 else 16
+                rows8 = gemv_tile_rows(s, self.batch)
                 self.kw_qkv = [pk(w, rows8) for w in self.kw_qkv]
                 self.kw_gu = [pk(w) for w in self.kw_gu]
                 self.kw_o = [pk(w, rows8) for w in self.w_o]

@@ -9,9 +9,12 @@ at least the entry point's *_workspace_bytes); otherwise one is taken from a
 cache keyed by (device, stream, kind), grown when needed and reused (the
 counterpart of the reference's _BUFFER_CACHE, attention/triton_atopn.py:56,
 73-84), so calls are capturable in a HIP graph after a warm-up call on the
-same stream.  Calls on different streams never share a cached workspace, and
-a workspace replaced by a larger one is kept alive until clear_workspaces(),
-because a graph captured earlier still holds its address.
+same stream.  Calls on different streams never share a cached workspace.  A
+cached workspace grows by at least half its size when a call needs more, so
+a need that grows step by step (a decode whose cache length grows with every
+token) reallocates a logarithmic number of times.  A replaced workspace that
+was handed out during a graph capture is kept alive until clear_workspaces(),
+because the graph still holds its address; any other is freed at once.
 """
 from __future__ import annotations
 
@@ -23,7 +26,8 @@ import torch
 from . import _lib
 
 _WORKSPACES: dict = {}  # (device, stream handle, kind) -> uint8 tensor
-_RETIRED: list = []     # replaced cached workspaces, alive until clear_workspaces()
+_CAPTURED: set = set()  # keys whose current workspace was handed out during a graph capture
+_RETIRED: list = []     # replaced workspaces that a captured graph may use, alive until clear_workspaces()
 
 
 def _need_gpu(*ts: Optional[torch.Tensor]) -> torch.device:
@@ -48,21 +52,39 @@ def _device(device) -> torch.device:
     return dev
 
 
+def grown_size(old: int, need: int) -> int:
+    """Bytes of a cached workspace replacing one of `old` bytes for a call
+    needing `need`: at least 1.5x the old size, so that a need growing in
+    small steps replaces the workspace O(log(final / first)) times."""
+    return max(int(need), old + old // 2, 256)
+
+
+def _replace(key, ws: Optional[torch.Tensor], need: int, alloc) -> torch.Tensor:
+    """The cache's policy, without the device: a replaced workspace is kept
+    (in _RETIRED) only if it was handed out while a graph was being captured."""
+    if ws is not None and key in _CAPTURED:
+        _RETIRED.append(ws)
+    _CAPTURED.discard(key)
+    new = alloc(grown_size(0 if ws is None else ws.numel(), need))
+    _WORKSPACES[key] = new
+    return new
+
+
 def workspace(device: torch.device, kind: str, nbytes: int, stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
     """uint8 workspace of at least nbytes for calls on `stream` (default: the
     device's current stream), cached per (device, stream, kind).  A cached
-    workspace too small for a call is replaced; the old one stays allocated
-    until clear_workspaces()."""
+    workspace too small for a call is replaced by one at least 1.5x larger;
+    the old one stays allocated until clear_workspaces() if a graph was
+    captured while it was handed out, else it is freed."""
     dev = _device(device)
     if stream is None:
         stream = torch.cuda.current_stream(dev)
     key = (dev, stream.cuda_stream, kind)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
-        if ws is not None:
-            _RETIRED.append(ws)
-        ws = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=dev)
-        _WORKSPACES[key] = ws
+        ws = _replace(key, ws, nbytes, lambda n: torch.empty(n, dtype=torch.uint8, device=dev))
+    if torch.cuda.is_current_stream_capturing():
+        _CAPTURED.add(key)
     return ws
 
 
@@ -71,6 +93,7 @@ def clear_workspaces() -> None:
     _BUFFER_CACHE between configurations).  A HIP graph captured with cached
     workspaces must not be replayed afterwards."""
     _WORKSPACES.clear()
+    _CAPTURED.clear()
     _RETIRED.clear()
 
 
