@@ -21,7 +21,27 @@ What it mirrors (speedup.py:447-700):
     (speedup.py:434-440);
   * `--exempt_layers` (dense attention in those layers, speedup.py:65-66) and
     `--merge_mode merge|baseline` with `--new_heads`: the SAGA model (key
-    heads merged) or the plain GQA model.
+    heads merged) or the plain GQA model;
+  * the reference's execution flags (speedup.py:447-476), with the same
+    meanings where they apply to this harness:
+      --cuda_graph      replay the decode step as the two captured HIP graphs;
+                        without it every step's kernels are launched eagerly
+                        from Python (the reference's uncompiled/compiled
+                        `decode`, speedup.py:164-177);
+      --compile_mode, --no_compile
+                        accepted and printed; the decode step is hand-written
+                        HIP kernels behind the C ABI, so there is nothing for
+                        torch.compile to fuse (no-op);
+      --calibrate_during_measurement
+                        accepted and printed; every measured generation starts
+                        with the calibration step in any case, as the
+                        reference's measurement loop does (it resets the
+                        amortized step count per iteration, speedup.py:380-405);
+      --profile_decode, --profile_output
+                        torch.profiler around the measured generations only
+                        (not warm-up, prefill or capture), one chrome trace per
+                        configuration named as the reference names them
+                        (speedup.py:640-661).
 
 Models: `--model_path` is a local checkpoint directory (config.json +
 safetensors, loaded by saga_amd.checkpoint; merge mode averages its key heads
@@ -81,6 +101,13 @@ def build_decoder(model_path: str, merge: bool, new_heads: int, batch: int, max_
                        weights=weights)
 
 
+def trace_name(profile_output: str, merge: bool, mode: str, param: Optional[int], batch: int, seq_len: int) -> str:
+    """The decode trace file of one configuration (speedup.py:657-658)."""
+    merge_label = "merged" if merge else "baseline"
+    return (f"{profile_output.replace('.json', '')}_{merge_label}_{_label(mode, param).replace(':', '_')}"
+            f"_bs{batch}_seq{seq_len}.json")
+
+
 def run_config(args, mode: str, param: Optional[int], batch: int, seq_len: int, merge: bool) -> dict:
     """One configuration in this process: per-token latency statistics."""
     import numpy as np
@@ -92,22 +119,41 @@ def run_config(args, mode: str, param: Optional[int], batch: int, seq_len: int, 
                       dtype)
     torch.manual_seed(0)
     m.prefill(torch.randint(0, m.shape.vocab, (seq_len,), dtype=torch.int64))
-    m.capture()
+    graphs = bool(getattr(args, "cuda_graph", True))
+    if graphs:
+        m.capture()
 
     def generate():
         m.reset()
         for i in range(n_new):
-            m.replay(i)
+            if graphs:
+                m.replay(i)
+            else:
+                m.step(calibrate=(m.mode == "atopn" and i == 0))
 
-    for _ in range(args.num_warmup):
-        generate()
-    torch.cuda.synchronize()
-    lat = []
-    for _ in range(args.num_iterations):
-        t0 = time.perf_counter()
-        generate()
+    with torch.no_grad():
+        for _ in range(args.num_warmup):
+            generate()
         torch.cuda.synchronize()
-        lat.append((time.perf_counter() - t0) * 1000.0)
+        prof = None
+        if getattr(args, "profile_decode", False):
+            from torch.profiler import ProfilerActivity, profile
+            prof = profile(activities=[ProfilerActivity.CPU, ProfilerActivity.CUDA])
+        lat = []
+        for _ in range(args.num_iterations):
+            torch.cuda.synchronize()
+            if prof is not None:
+                prof.start()
+            t0 = time.perf_counter()
+            generate()
+            torch.cuda.synchronize()
+            lat.append((time.perf_counter() - t0) * 1000.0)
+            if prof is not None:
+                prof.stop()
+                trace = trace_name(args.profile_output, merge, mode, param, batch, seq_len)
+                prof.export_chrome_trace(trace)
+                prof = None  # the first measured generation is traced (one trace per configuration)
+                print(f"decode trace: {trace}", file=sys.stderr, flush=True)
     lat = np.array(lat) / n_new
     return {"mean_ms": float(np.mean(lat)), "std_ms": float(np.std(lat)), "p50_ms": float(np.percentile(lat, 50)),
             "p90_ms": float(np.percentile(lat, 90)), "tokens_per_s": float(batch * 1000.0 / np.mean(lat))}
@@ -121,14 +167,33 @@ def _sub_cmd(args, mode, param, batch, seq_len, merge_mode) -> List[str]:
            "--merge_mode", merge_mode, "--_subprocess_json"]
     if args.exempt_layers:
         cmd += ["--exempt_layers", args.exempt_layers]
+    if getattr(args, "cuda_graph", False):
+        cmd.append("--cuda_graph")
+    if getattr(args, "profile_decode", False):
+        cmd += ["--profile_decode", "--profile_output", args.profile_output]
     return cmd
+
+
+def describe_flags(args) -> str:
+    """What the reference's execution flags mean in this harness (printed
+    before the grid, as speedup.py:518-528 prints its settings)."""
+    lines = [f"Compile: no-op (hand-written HIP kernels; --compile_mode {args.compile_mode}"
+             f"{', --no_compile' if args.no_compile else ''} accepted)",
+             "CUDA graph: " + ("enabled (HIP graphs: calibration step, fast step)" if args.cuda_graph
+                               else "disabled (kernels launched eagerly per step)")]
+    if args.calibrate_during_measurement:
+        lines.append("Calibration during measurement: on (every measured generation starts with it)")
+    if args.profile_decode:
+        lines.append(f"Profiling decode: output={args.profile_output}")
+    return "\n".join(lines)
 
 
 def _is_oom(text: str) -> bool:
     return "OutOfMemoryError" in text or "out of memory" in text or "OOM" in text
 
 
-def main(argv=None) -> int:
+def build_parser() -> argparse.ArgumentParser:
+    """The reference's command line (speedup.py:447-476) plus --timeout."""
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--model_path", default="qwen2.5-1.5b",
                     help="checkpoint directory, or a built-in shape: " + ", ".join(BUILTIN))
@@ -142,9 +207,25 @@ def main(argv=None) -> int:
     ap.add_argument("--merge_mode", default="merge", help="merge, baseline or both (comma-separated)")
     ap.add_argument("--attention", default="full", help="full, vanilla, atopn:N, atopn_amortized:N (comma-separated)")
     ap.add_argument("--exempt_layers", default="", help="comma-separated layers that keep dense attention")
+    ap.add_argument("--no_compile", action="store_true",
+                    help="accepted (no-op): the decode step is hand-written HIP kernels, not torch.compile output")
+    ap.add_argument("--compile_mode", default="default", choices=["default", "reduce-overhead", "max-autotune"],
+                    help="accepted (no-op), as --no_compile")
+    ap.add_argument("--cuda_graph", action="store_true",
+                    help="replay each decode step as a captured HIP graph (else launch its kernels eagerly)")
+    ap.add_argument("--calibrate_during_measurement", action="store_true",
+                    help="accepted: every measured generation starts with the calibration step in any case")
+    ap.add_argument("--profile_decode", action="store_true",
+                    help="torch.profiler trace of the measured generations only, one file per configuration")
+    ap.add_argument("--profile_output", default="decode_trace.json",
+                    help="trace file stem (default: decode_trace.json)")
     ap.add_argument("--timeout", type=int, default=600, help="seconds per configuration subprocess")
     ap.add_argument("--_subprocess_json", action="store_true", help=argparse.SUPPRESS)
-    args = ap.parse_args(argv)
+    return ap
+
+
+def main(argv=None) -> int:
+    args = build_parser().parse_args(argv)
 
     seq_lengths = [int(x) for x in args.seq_lengths.split(",")]
     batch_sizes = [int(x) for x in args.batch_sizes.split(",")]
@@ -159,6 +240,8 @@ def main(argv=None) -> int:
         stats = run_config(args, mode, param, batch_sizes[0], seq_lengths[0], merge_modes[0] == "merge")
         print(json.dumps(stats), flush=True)
         return 0
+
+    print(describe_flags(args), flush=True)
 
     results, failures = {}, []
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
