@@ -17,7 +17,9 @@ fp32 path within rounding):
     in bf16 runs);
   * Atop-N selection keeps the first buf_k passing positions in index order
     when more pass (the reference keeps a race-dependent subset);
-  * full_einsum_forward is a decode (l_q == 1) kernel.
+  * full_einsum_forward with l_q > 1 runs the decode kernel once per batch
+    row with that row's l_q queries as its batch (all keys visible, the mask
+    added, is_causal ignored, as the reference's einsum does).
 """
 import math
 from typing import Optional, Tuple

@@ -335,14 +335,16 @@ int atopn_run(bool calibrate, const saga_tensor* query, const saga_tensor* key, 
 }
 
 // Dense split plan: about 512 blocks over the (batch, key head) units,
-// splits of >= 512 positions, split length a multiple of the 32-position wave
-// step.  The split count never grows with the number of units, so the
-// workspace bound computed for k_h = 1 covers every k_h.
+// splits of >= 512 positions, or up to 256 splits of >= 64 positions where
+// that gives more (a batch-1 4k decode ran on 8 blocks, 32k on 64), split
+// length a multiple of the 32-position wave step.  The split count never
+// grows with the number of units, so the workspace bound computed for
+// k_h = 1 covers every k_h.
 void dense_plan(int64_t units, int64_t L, int64_t* nsplit, int64_t* split_len) {
   units = std::max<int64_t>(units, 1);
   L = std::max<int64_t>(L, 1);
   int64_t ns = (512 + units - 1) / units;
-  const int64_t by_len = (L + 511) / 512;
+  const int64_t by_len = std::max<int64_t>((L + 511) / 512, std::min<int64_t>((L + 63) / 64, 256));
   if (ns > by_len) ns = by_len;
   if (ns < 1) ns = 1;
   int64_t sl = (L + ns - 1) / ns;

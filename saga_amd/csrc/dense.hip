@@ -252,41 +252,62 @@ __global__ void __launch_bounds__(256) dense_split_kernel(DenseParams p) {
 }
 
 // Merge the split partials of one (batch, head): block of D threads.
+// Kernel 2: one block per head, kMergeGroups x D threads: thread (grp, i)
+// sums dim i of the splits grp, grp + kMergeGroups, ... (all of its loads in
+// one burst for up to kMergeGroups x kMergeBurst splits), then the groups
+// are added in LDS in a fixed order.
+constexpr int kMergeGroups = 8;
+constexpr int kMergeBurst = 8;
+
 template <int D>
-__global__ void __launch_bounds__(D) dense_merge_kernel(DenseParams p) {
+__global__ void __launch_bounds__(kMergeGroups * D) dense_merge_kernel(DenseParams p) {
+  constexpr int NT = kMergeGroups * D;
   __shared__ float fm[1024];
-  __shared__ float red[D / kWave];
+  __shared__ float red[NT / kWave];
+  __shared__ float og[kMergeGroups][D];
   const int unit = blockIdx.x / p.g, hh = blockIdx.x - unit * p.g;
   const int bi = unit / p.k_h, kh = unit - bi * p.k_h;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, grp = tid / D, i = tid - grp * D;
   const int64_t stride = static_cast<int64_t>(p.g) * (2 + D);  // between splits
   const float* base = p.part + static_cast<int64_t>(unit) * p.nsplit * stride + hh * (2 + D);
   // (max, sum) of every split, then the common max
   float mloc = kNegInf;
-  for (int q = tid; q < p.nsplit; q += D) {
+  for (int q = tid; q < p.nsplit; q += NT) {
     const float m = base[q * stride];
     fm[q] = m;
     mloc = fmaxf(mloc, m);
   }
-  const float M = block_max<D / kWave>(mloc, red);
+  const float M = block_max<NT / kWave>(mloc, red);
   float lloc = 0.f;
-  for (int q = tid; q < p.nsplit; q += D) {
+  for (int q = tid; q < p.nsplit; q += NT) {
     const float f = fm[q] == kNegInf ? 0.f : __expf(fm[q] - M);
     lloc += base[q * stride + 1] * f;
     fm[q] = f;
   }
-  const float l = block_sum<D / kWave>(lloc, red);  // orders the fm writes too
-  // o[tid]: independent loads, eight splits in flight
+  const float l = block_sum<NT / kWave>(lloc, red);  // orders the fm writes too
+  // dim i of this group's splits: independent loads, kMergeBurst in flight
   float o = 0.f;
-  for (int q0 = 0; q0 < p.nsplit; q0 += 8) {
-    float ov[8];
+  for (int q0 = grp; q0 < p.nsplit; q0 += kMergeGroups * kMergeBurst) {
+    float ov[kMergeBurst];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) ov[u] = q0 + u < p.nsplit ? base[(q0 + u) * stride + 2 + tid] : 0.f;
+    for (int u = 0; u < kMergeBurst; ++u) {
+      const int q = q0 + u * kMergeGroups;
+      ov[u] = q < p.nsplit ? base[q * stride + 2 + i] : 0.f;
+    }
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
-      if (q0 + u < p.nsplit) o += ov[u] * fm[q0 + u];
+    for (int u = 0; u < kMergeBurst; ++u) {
+      const int q = q0 + u * kMergeGroups;
+      if (q < p.nsplit) o += ov[u] * fm[q];
+    }
   }
-  store_from_f32(p.out, p.out_dt, bi * p.o_sb + static_cast<int64_t>(kh * p.g + hh) * p.o_sh + tid, o / l);
+  og[grp][i] = o;
+  __syncthreads();
+  if (grp == 0) {
+    float t = og[0][i];
+#pragma unroll
+    for (int g2 = 1; g2 < kMergeGroups; ++g2) t += og[g2][i];
+    store_from_f32(p.out, p.out_dt, bi * p.o_sb + static_cast<int64_t>(kh * p.g + hh) * p.o_sh + i, t / l);
+  }
 }
 
 template <int DT>
@@ -295,10 +316,12 @@ static hipError_t launch_dense_typed(int d, const DenseParams& p, hipStream_t st
   const unsigned heads = static_cast<unsigned>(p.b * p.k_h * p.g);
   if (d == 128) {
     hipLaunchKernelGGL((dense_split_kernel<DT, 128, kDenseSubDefault>), dim3(blocks), dim3(256), 0, st, p);
-    if (p.nsplit > 1) hipLaunchKernelGGL((dense_merge_kernel<128>), dim3(heads), dim3(128), 0, st, p);
+    if (p.nsplit > 1)
+      hipLaunchKernelGGL((dense_merge_kernel<128>), dim3(heads), dim3(kMergeGroups * 128), 0, st, p);
   } else {
     hipLaunchKernelGGL((dense_split_kernel<DT, 64, kDenseSubDefault>), dim3(blocks), dim3(256), 0, st, p);
-    if (p.nsplit > 1) hipLaunchKernelGGL((dense_merge_kernel<64>), dim3(heads), dim3(64), 0, st, p);
+    if (p.nsplit > 1)
+      hipLaunchKernelGGL((dense_merge_kernel<64>), dim3(heads), dim3(kMergeGroups * 64), 0, st, p);
   }
   return hipGetLastError();
 }

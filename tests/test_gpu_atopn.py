@@ -125,8 +125,13 @@ def test_against_reference_golden(name, golden):
                 assert not set_diff_outside_band(sel, sel_ref, views["scores"][r], t_ref[r], band)
                 flips += len(set(sel) ^ set(sel_ref))
         ok = ~np.isnan(o_ref)
-        if flips == 0:
-            assert rel_l2(out[ok], o_ref[ok]) < (1e-3 if bf else 1e-5)
+        # the reference's own output, whatever the near-tie flips (a flipped
+        # entry's weight is about p*): the north star's 1e-3 always, fp32's
+        # 1e-5 when both kept the same sets
+        print(f"  golden {name} {tag}: flips={flips}", flush=True)
+        assert rel_l2(out[ok], o_ref[ok]) < 1e-3, (tag, flips)
+        if flips == 0 and not bf:
+            assert rel_l2(out[ok], o_ref[ok]) < 1e-5
         # always: the reference's fp32 gather . V on the GPU's own selection
         # (the golden inputs, the oracle's logits at the GPU's positions)
         rnd = O.round_bf16 if bf else (lambda a: a)
@@ -198,10 +203,13 @@ def test_bf16_benchmark_shapes_vs_fp32_path(name):
                                    input_is_logits=True)
     assert rel_l2(out32, ref_same_sel) < 1e-3
     assert np.max(np.abs(out16 - ref_same_sel)) < 2e-2
-    if flips == 0:
-        assert rel_l2(out32, ref_out) < 1e-3
-        assert np.max(np.abs(out16 - ref_out)) < 2e-2
+    # the reference fp32 path's own output, whatever the near-tie flips, on
+    # the rows whose selection is defined (the reference keeps a
+    # race-dependent subset of an overflowing row)
     print(f"  flips={flips} mean_count={views['sel_cnt'].mean():.1f}", flush=True)
+    rows = (cnt_ref <= buf_k).reshape(b, q_h)
+    assert rel_l2(out32[rows], ref_out[rows]) < 1e-3, flips
+    assert np.max(np.abs(out16[rows] - ref_out[rows])) < 2e-2, flips
 
 
 def test_kv_len_equals_truncated_reference():

@@ -114,6 +114,13 @@ def test_sweep_corner_vs_oracle(name):
             else:
                 assert not set_diff_outside_band(sel, sel_ref, x, t_ref[j], band)
                 flips += len(set(sel.tolist()) ^ set(sel_ref.tolist()))
+                # the reference fp32 path's own output (its own selection), whatever the flips
+                vh = j // g_v
+                direct = O.gather_output(logits[j, sel_ref][None, None, None, :],
+                                         sel_ref[None, None, None, :].astype(np.int64), vi[:, vh:vh + 1],
+                                         (1, 1, 1, D), input_is_logits=True).reshape(D)
+                assert rel_l2(out32[i, j, 0], direct) < 1e-3, (i, j, flips)
+                assert np.max(np.abs(out16[i, j, 0] - direct)) < 2e-2, (i, j, flips)
             # the reference fp32 gather . V on the GPU's own selection
             vh = j // g_v
             ref = O.gather_output(logits[j, sel][None, None, None, :], sel[None, None, None, :].astype(np.int64),

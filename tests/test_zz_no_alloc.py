@@ -74,3 +74,54 @@ def test_noalloc_refuses_shapes_past_the_scratch():
     table = torch.zeros(b * q_h, device="cuda")
     rc = _decode(lib, "saga_atopn_decode_noalloc", q, k, v, table, N, out)
     assert rc == -3 and b"static scratch" in lib.saga_last_error()
+
+
+def test_noalloc_under_hip_graph_capture():
+    """The entry point's purpose: calls inside a captured HIP graph, which
+    cannot allocate.  The graph (two decode calls of different shapes) is
+    replayed several times, with eager calls that reuse the scratch and
+    in-place input changes between replays; every replay must equal the
+    workspace entry point on the inputs of that moment."""
+    lib = _lib.load()
+    cases = [_case(201, 8, 12, 1, 2, 8192, 512), _case(202, 2, 12, 1, 2, 3000, 64, masked=True)]
+    Ns = (512, 64)
+    outs = [torch.empty(c[0].shape[0], 12, 1, 128, device="cuda", dtype=torch.float32) for c in cases]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):  # eager warm-up on the capture stream: the scratch address is looked up here
+        for (qd, kd, vd, table, mask, kv_len), N, out in zip(cases, Ns, outs):
+            assert _decode(lib, "saga_atopn_decode_noalloc", qd, kd, vd, table, N, out, mask, kv_len) == 0
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for (qd, kd, vd, table, mask, kv_len), N, out in zip(cases, Ns, outs):
+            assert _decode(lib, "saga_atopn_decode_noalloc", qd, kd, vd, table, N, out, mask, kv_len) == 0, \
+                lib.saga_last_error()
+    other = _case(203, 4, 12, 1, 2, 20000, 256)
+    other_out = torch.empty(4, 12, 1, 128, device="cuda", dtype=torch.float32)
+    rng = np.random.default_rng(7)
+    for rep in range(4):
+        print(f"noalloc graph replay {rep}", flush=True)
+        if rep >= 2:  # new queries in place: the replay must follow them
+            for qd, *_ in cases:
+                qd.copy_(torch.from_numpy(rng.standard_normal(tuple(qd.shape), dtype=np.float32)).to(qd.dtype).cuda())
+        for o in outs:
+            o.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        for (qd, kd, vd, table, mask, kv_len), N, out in zip(cases, Ns, outs):
+            b, L = qd.shape[0], kd.shape[2]
+            ws = torch.empty(lib.saga_atopn_workspace_bytes(b, 12, 1, L, 128, min(2 * N, L)), dtype=torch.uint8,
+                             device="cuda")
+            ref = torch.full_like(out, float("nan"))
+            assert _decode(lib, "saga_atopn_decode", qd, kd, vd, table, N, ref, mask, kv_len, ws) == 0
+            torch.cuda.synchronize()
+            assert torch.equal(torch.isnan(out), torch.isnan(ref))
+            ok = ~torch.isnan(ref)
+            assert ok.any() and torch.equal(out[ok], ref[ok]), rep
+        # an eager call between replays overwrites the shared scratch
+        qd, kd, vd, table, mask, kv_len = other
+        assert _decode(lib, "saga_atopn_decode_noalloc", qd, kd, vd, table, 256, other_out) == 0
+        torch.cuda.synchronize()
+    del g
