@@ -43,6 +43,7 @@ __device__ __forceinline__ unsigned long long lanes_below(int lane) {
 }
 
 struct SelShared {
+  static constexpr int kList = kListLDS;  // selection entries kept in LDS
   float red[kBlkWaves];
   int cnt[kSelSlots];
   int pre[kSelSlots + 1];
@@ -50,15 +51,16 @@ struct SelShared {
   int preE[kSelSlots + 1];
   int hist[2048];
   int sel_bin, sel_above;
-  int sidx[kListLDS];
-  float sval[kListLDS];
+  int sidx[kList];
+  float sval[kList];
 };
 
 // Run the PV phase over a row's list: from LDS when it fits, otherwise in
 // LDS-sized batches re-read from the workspace copy.
-template <int DT, int D>
-__device__ void row_pv(SelShared& sh, float* accs, int n, const int32_t* gidx, const float* gval, const PVParams& v,
+template <int DT, int D, class SH>
+__device__ void row_pv(SH& sh, float* accs, int n, const int32_t* gidx, const float* gval, const PVParams& v,
                        int bi, int h, bool probs) {
+  constexpr int kListLDS = SH::kList;
   const int vh = h / (v.q_h / v.v_h);
   const char* vbase = v.v + (bi * v.v_sb + static_cast<int64_t>(vh) * v.v_sh) * Elt<DT>::kBytes;
   const int64_t vrow = v.v_sl * Elt<DT>::kBytes;
@@ -84,7 +86,8 @@ __device__ void row_pv(SelShared& sh, float* accs, int n, const int32_t* gidx, c
 // Bin holding the krem-th largest element of sh.hist[0..nb) (bin nb - 1 holds
 // the largest) and the count in the bins above it; bin -1 if fewer than krem
 // elements are counted.  Every thread of the block calls it.
-__device__ __forceinline__ void hist_pick(SelShared& sh, int nb, int krem, int& bin, int& above) {
+template <class SH>
+__device__ __forceinline__ void hist_pick(SH& sh, int nb, int krem, int& bin, int& above) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   if (tid == 0) sh.sel_bin = -1;
   // bins scanned from the top: thread t owns bins nb-1-2t and nb-2-2t
@@ -94,7 +97,7 @@ __device__ __forceinline__ void hist_pick(SelShared& sh, int nb, int krem, int& 
   const int tsum = c0 + c1;
   const int incl = wave_incl_scan(tsum, lane);
   if (lane == kWave - 1) sh.cnt[w] = incl;
-  __syncthreads();
+  lds_sync();
   int woff = 0;
   for (int i = 0; i < w; ++i) woff += sh.cnt[i];
   const int ex = woff + incl - tsum;
@@ -105,10 +108,10 @@ __device__ __forceinline__ void hist_pick(SelShared& sh, int nb, int krem, int& 
     sh.sel_bin = b1;
     sh.sel_above = ex + c0;
   }
-  __syncthreads();
+  lds_sync();
   bin = sh.sel_bin;
   above = sh.sel_above;
-  __syncthreads();
+  lds_sync();
 }
 
 // f(x[i]) for every i < n of a score row (ld floats, 16-byte aligned, n <= ld),
@@ -132,12 +135,13 @@ __device__ __forceinline__ void row_tiles(const float* x, int64_t ld, int n, F f
   }
 }
 
-// The krem-th largest of n keys -- of the score row x (ROW) or of the LDS
-// candidates sh.sval -- by a 3-pass radix select (11/11/10 bits of the
-// order-preserving uint32 key) over 2048-bin LDS histograms; krem is left at
-// the count of elements equal to it that are among the krem largest.
-template <bool ROW>
-__device__ __forceinline__ uint32_t radix_select(SelShared& sh, const float* x, int64_t ld, int n, int& krem) {
+// The krem-th largest of a set of keys, by a 3-pass radix select (11/11/10
+// bits of the order-preserving uint32 key) over 2048-bin LDS histograms;
+// each(f) calls f(x) for every element of the set (in the calling thread's
+// share); krem is left at the count of elements equal to it that are among
+// the krem largest.
+template <class SH, class EACH>
+__device__ __forceinline__ uint32_t radix_select_each(SH& sh, int& krem, EACH each) {
   const int tid = threadIdx.x;
   uint32_t prefix = 0;
   const int shifts[3] = {21, 10, 0};
@@ -147,23 +151,30 @@ __device__ __forceinline__ uint32_t radix_select(SelShared& sh, const float* x, 
     const int nb = 1 << nbits[pass];
     const uint32_t hmask = pass == 0 ? 0u : (0xffffffffu << (shifts[pass] + nbits[pass]));
     for (int i = tid; i < 2048; i += kBlkThreads) sh.hist[i] = 0;
-    __syncthreads();
-    auto count = [&](float xi) {
+    lds_sync();
+    each([&](float xi) {
       const uint32_t key = f32_to_key(xi);
       if ((key & hmask) == prefix) atomicAdd(&sh.hist[(key >> shifts[pass]) & (nb - 1)], 1);
-    };
-    if constexpr (ROW) {
-      row_tiles(x, ld, n, count);
-    } else {
-      for (int i = tid; i < n; i += kBlkThreads) count(sh.sval[i]);
-    }
-    __syncthreads();
+    });
+    lds_sync();
     int bin, above;
     hist_pick(sh, nb, krem, bin, above);
     prefix |= static_cast<uint32_t>(bin) << shifts[pass];
     krem -= above;
   }
   return prefix;
+}
+
+// radix_select_each over the score row x (ROW) or the LDS candidates sh.sval.
+template <bool ROW, class SH>
+__device__ __forceinline__ uint32_t radix_select(SH& sh, const float* x, int64_t ld, int n, int& krem) {
+  if constexpr (ROW) {
+    return radix_select_each(sh, krem, [&](auto f) { row_tiles(x, ld, n, f); });
+  } else {
+    return radix_select_each(sh, krem, [&](auto f) {
+      for (int i = threadIdx.x; i < n; i += kBlkThreads) f(sh.sval[i]);
+    });
+  }
 }
 
 constexpr int kNearBins = 2048;      // bins of the distance below the row max
@@ -180,12 +191,14 @@ constexpr float kNearScale = 32.0f;  // bins per unit of logit: the bins span M 
 // work to the full-row select, for a NaN or non-finite max, a k-th value more
 // than 64 below M, or more candidates than the LDS list holds.  kth and krem
 // as radix_select.
-__device__ __forceinline__ bool near_pick(SelShared& sh, const float* x, int64_t ld, int Leff, float M, int& krem,
-                                          uint32_t& kth) {
+// The distance histogram (pass 1 of near_pick): every position of the row
+// into its bin; false for a NaN or a non-finite max (block-uniform).
+template <class SH>
+__device__ __forceinline__ bool near_hist(SH& sh, const float* x, int64_t ld, int Leff, float M) {
   const int tid = threadIdx.x;
   if (!(M > -INFINITY && M < INFINITY)) return false;  // block-uniform
   for (int i = tid; i < kNearBins; i += kBlkThreads) sh.hist[i] = 0;
-  __syncthreads();
+  lds_sync();
   int odd = 0;
   row_tiles(x, ld, Leff, [&](float xi) {
     if (!(xi <= M)) {  // NaN
@@ -195,26 +208,43 @@ __device__ __forceinline__ bool near_pick(SelShared& sh, const float* x, int64_t
     const float dd = (M - xi) * kNearScale;
     if (dd < kNearBins) atomicAdd(&sh.hist[kNearBins - 1 - static_cast<int>(dd)], 1);
   });
-  if (__syncthreads_or(odd)) return false;
+  return !__syncthreads_or(odd);
+}
+
+// The rest of near_pick, over the histogram of near_hist: the bin holding
+// the krem-th largest, its elements gathered into LDS, the radix select
+// over them.
+template <class SH>
+__device__ __forceinline__ bool near_select(SH& sh, const float* x, int64_t ld, int Leff, float M, int& krem,
+                                            uint32_t& kth) {
+  const int tid = threadIdx.x;
   int bin, above;
   hist_pick(sh, kNearBins, krem, bin, above);
   if (bin < 0) return false;
   const int c = sh.hist[bin];
-  if (c > kListLDS) return false;
+  if (c > SH::kList) return false;
   const int want = kNearBins - 1 - bin;  // distance bin of the candidates
   if (tid == 0) sh.sel_bin = 0;          // candidate count
-  __syncthreads();
+  lds_sync();
   row_tiles(x, ld, Leff, [&](float xi) {
     const float dd = (M - xi) * kNearScale;
     if (dd < kNearBins && static_cast<int>(dd) == want) sh.sval[atomicAdd(&sh.sel_bin, 1)] = xi;
   });
-  __syncthreads();
+  lds_sync();
   krem -= above;
   kth = radix_select<false>(sh, nullptr, 0, c, krem);
   return true;
 }
 
-// Calibration: exact top-k of the row (k = min(top_n, L)).
+template <class SH>
+__device__ __forceinline__ bool near_pick(SH& sh, const float* x, int64_t ld, int Leff, float M, int& krem,
+                                          uint32_t& kth) {
+  return near_hist(sh, x, ld, Leff, M) && near_select(sh, x, ld, Leff, M, krem, kth);
+}
+
+// Calibration: exact top-k of the row (k = min(top_n, L)), for rows past
+// the register-resident kernel below (more than 13 * 4096 positions, or
+// top_n > 4096), the row re-read from memory by each pass.
 //   1. full-row max M and sum S of exp(x - M) from the K1 partials;
 //   2. the k-th largest value: by a radix select over the few elements of
 //      its bin of distance below M (near_pick), else over the whole row;
@@ -270,7 +300,8 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_kernel(FusedSelPa
   }
   const int need = krem;  // elements equal to the k-th value that are taken
 
-  // Ordered compaction, tile by tile: wave w takes the kSelEPT * 64
+  // Ordered compaction, tile by tile (LDS-only barriers: the list's global
+  // copy is read back only by row_pv's batches, after a full barrier): wave w takes the kSelEPT * 64
   // consecutive elements [st + 1024 w, st + 1024 (w + 1)) of the tile, so the
   // index order is (tile, wave, step, lane) and an element's rank is its
   // wave's offset (the totals of the lower waves) + the running count of its
@@ -297,7 +328,7 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_kernel(FusedSelPa
       sh.cnt[w] = cg;
       sh.cntE[w] = ce;
     }
-    __syncthreads();
+    lds_sync();
     int g_off = baseG, e_off = baseE, totG = 0, totE = 0;
 #pragma unroll
     for (int q = 0; q < kBlkWaves; ++q) {
@@ -334,7 +365,7 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_kernel(FusedSelPa
     }
     baseG += totG;
     baseE += totE;
-    __syncthreads();
+    lds_sync();
   }
   if (tid == 0) {
     p.sel_cnt[r] = k;
@@ -344,9 +375,453 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_kernel(FusedSelPa
   row_pv<DT, D>(sh, accs, k, gidx, gval, v, bi, h, false);
 }
 
+// ---------------------------------------------------------------------------
+// Calibration with the score row held in registers: rows of up to
+// CH * 4096 positions are read from HBM once, every later pass runs over the
+// registers.  Wave w holds positions [w * 256 CH, (w + 1) * 256 CH): chunk q
+// of the wave is the 256 positions from w * 256 CH + 256 q, lane l holding
+// its four from 4 l (16-byte loads, 1 KiB per wave and load).  Index order is
+// (wave, chunk, lane, element), so a position's rank among the selected ones
+// is its wave's offset + its chunk's offset in the wave + a wave scan.
+//
+// Selection by classes: with the k-th largest value's distance bin B
+// (elements of nearer bins are all larger than every element of B, as in
+// near_pick), the positions of nearer bins are all kept ("nearer") and the
+// krem largest of bin B's elements ("candidates", by value, then lowest
+// index) complete the k.  The candidates -- a few dozen on N(0,1)-like rows
+// -- go to LDS in index order and are ranked there; a kept position's slot
+// in the list is the nearer positions before it + the kept candidates
+// before it.  When the distance bins cannot be used (a NaN or non-finite
+// max, a k-th value more than 64 below the max, more candidates than LDS
+// holds) the classes are by key: above the k-th key (from a radix select
+// over the registers) and equal to it, the first `need` of which are kept.
+constexpr int kRegList = 4096;   // k <= kRegList: the kept list in LDS
+constexpr int kRegCand = 2048;   // candidates of the distance classes kept in LDS
+constexpr int kRegRank = 128;    // candidates ranked pairwise; more: radix select
+
+struct RegShared {
+  static constexpr int kList = kRegList;
+  float red[kBlkWaves];
+  int cnt[kBlkWaves];      // hist_pick's per-wave totals
+  int wtot[2][kBlkWaves];  // per-wave class totals (nearer, candidates)
+  int scan[kBlkWaves];     // per-wave totals of the taken-flag scan
+  int hist[2048];
+  int sel_bin, sel_above, sel_key;
+  int sidx[kRegList];       // the kept list (key classes) / the nearer positions (distance classes),
+  float sval[kRegList];     //   their values
+  int ncb[kRegList];        //   and the candidates before each nearer position
+  float cval[kRegCand];     // candidates in index order: value,
+  int cidx[kRegCand];       // position,
+  int cnb[kRegCand];        // nearer positions before it,
+  int ctp[kRegCand + 1];    // kept candidates before it (ctp[c] = all kept)
+  int cflag[kRegCand];      // kept?
+};
+
+// Exclusive scan over the block of four values per thread (thread t's four
+// are entries 4t..4t+3 of the sequence); returns thread t's exclusive base.
+__device__ __forceinline__ int block_excl_scan4(int tsum, int* wscan) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int incl = wave_incl_scan(tsum, lane);
+  if (lane == kWave - 1) wscan[w] = incl;
+  lds_sync();
+  int base = incl - tsum;
+#pragma unroll
+  for (int u = 0; u < kBlkWaves; ++u)
+    if (u < w) base += wscan[u];
+  return base;
+}
+
+template <int DT, int D, int CH>
+__global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_reg_kernel(FusedSelParams p, PVParams v) {
+  __shared__ RegShared sh;
+  __shared__ float accs[kBlkWaves * D];
+  const int r = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int bi = r / p.q_h, h = r - bi * p.q_h;
+  int Leff = p.L;
+  if (p.kv_len) Leff = min(Leff, max(p.kv_len[bi], 0));
+  const float* x = p.scores + static_cast<int64_t>(r) * p.ld;
+  const float* prow_m = p.pmax + static_cast<int64_t>(r) * p.nparts;
+  const float* prow_s = p.psum + static_cast<int64_t>(r) * p.nparts;
+  const int nch = p.nparts;  // parts past kv_len hold (-inf, 0)
+
+  // K1's partials first, then the whole row: the row's loads stay in flight
+  // through the max / sum reductions
+  const float pm0 = tid < nch ? prow_m[tid] : kNegInf;
+  const float ps0 = tid < nch ? prow_s[tid] : 0.f;
+  const int wbase = w * (CH * 256) + 4 * lane;  // chunk q: wbase + 256 q + j
+  const int lastq = max(0, (Leff + 3) / 4 * 4 - 4);  // loads past Leff are clamped (and never used)
+  f32x4 xr[CH];
+#pragma unroll
+  for (int q = 0; q < CH; ++q) xr[q] = *reinterpret_cast<const f32x4*>(x + min(wbase + 256 * q, lastq));
+  for (int i = tid; i < 2048; i += kBlkThreads) sh.hist[i] = 0;
+
+  float mloc = pm0;
+  for (int c = tid + kBlkThreads; c < nch; c += kBlkThreads) mloc = fmaxf(mloc, prow_m[c]);
+  const float M = block_max<kBlkWaves>(mloc, sh.red);  // (its barriers also publish the zeroed histogram)
+  float sloc = pm0 != kNegInf ? ps0 * __expf(pm0 - M) : 0.f;
+  for (int c = tid + kBlkThreads; c < nch; c += kBlkThreads) {
+    const float pm = prow_m[c];
+    if (pm != kNegInf) sloc += prow_s[c] * __expf(pm - M);
+  }
+  const float S = block_sum<kBlkWaves>(sloc, sh.red);
+
+  const int k = min(p.cap, Leff);
+  int32_t* gidx = p.sel_idx + static_cast<int64_t>(r) * p.cap;
+  float* gval = p.sel_val + static_cast<int64_t>(r) * p.cap;
+  using PV = BlockPV<DT, D>;
+  const int vh = h / (v.q_h / v.v_h);
+  const char* vbase = v.v + (bi * v.v_sb + static_cast<int64_t>(vh) * v.v_sh) * Elt<DT>::kBytes;
+  const int64_t vrow = v.v_sl * Elt<DT>::kBytes;
+  const int64_t ooff = bi * v.o_sb + static_cast<int64_t>(h) * v.o_sh;
+  if (k <= 0) {
+    if (tid == 0) {
+      p.sel_cnt[r] = 0;
+      if (p.sel_total) p.sel_total[r] = 0;
+      p.pstar_out[r] = 0.f;
+    }
+    PV pv;
+    pv.init();
+    pv.finish(accs, v.out, v.out_dt, ooff, false);  // 0 / 0: an empty row's output is NaN
+    return;
+  }
+
+  // every in-row element of the thread's share: f(value, position)
+  auto each_in = [&](auto f) {
+#pragma unroll
+    for (int q = 0; q < CH; ++q)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (wbase + 256 * q + j < Leff) f(xr[q][j]);
+  };
+
+  // pass 1: distance bins (M - x) * 32 below the max; a NaN, or a max
+  // that is not finite, sends the row to the key classes
+  const float M32 = M * kNearScale;
+  int odd = (M > -INFINITY && M < INFINITY) ? 0 : 1;
+  if (!odd) {
+    each_in([&](float xi) {
+      const float dd = fmaf(-xi, kNearScale, M32);
+      if (!(dd >= 0.f)) odd = 1;
+      else if (dd < static_cast<float>(kNearBins)) atomicAdd(&sh.hist[kNearBins - 1 - static_cast<int>(dd)], 1);
+    });
+  }
+  bool near = !__syncthreads_or(odd);
+  int krem = k, bin = -1, above = 0;
+  if (near) {
+    hist_pick(sh, kNearBins, k, bin, above);
+    near = bin >= 0 && sh.hist[bin] <= kRegCand;  // block-uniform
+  }
+  uint32_t kth = 0;
+  float wantf = 0.f;
+  if (near) {
+    krem = k - above;
+    wantf = static_cast<float>(kNearBins - 1 - bin);
+  } else {
+    krem = k;
+    kth = radix_select_each(sh, krem, each_in);  // krem -> need (keys equal to kth that are kept)
+  }
+  const int need = krem;
+
+  // class pass: per chunk, 4-bit masks of nearer / candidate elements and
+  // one wave scan of both counts (packed: 16 bits each; a wave chunk holds
+  // at most 256 of a class); positions past Leff are masked per chunk
+  // the lane's class masks, 8 bits per chunk (nearer | candidates << 4);
+  // the lane's counts before it in the chunk are re-scanned where needed
+  uint32_t msk[(CH + 3) / 4];
+#pragma unroll
+  for (int u = 0; u < (CH + 3) / 4; ++u) msk[u] = 0u;
+  int base[CH];  // the wave's nearer | candidates << 16 before chunk q (wave-uniform)
+  int wN = 0, wC = 0;
+  auto classify = [&](auto cls) {
+#pragma unroll
+    for (int q = 0; q < CH; ++q) {
+      uint32_t mN = 0, mC = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        bool n, c;
+        cls(xr[q][j], n, c);
+        mN |= static_cast<uint32_t>(n) << j;
+        mC |= static_cast<uint32_t>(c) << j;
+      }
+      const int lim = Leff - (wbase + 256 * q);
+      const uint32_t valid = lim >= 4 ? 15u : (lim > 0 ? (1u << lim) - 1u : 0u);
+      mN &= valid;
+      mC &= valid & ~mN;
+      const int cntv = __popc(mN) | (__popc(mC) << 16);
+      const int inc = wave_incl_scan(cntv, lane);
+      msk[q >> 2] |= (mN | (mC << 4)) << (8 * (q & 3));
+      base[q] = wN | (wC << 16);
+      const int tot = __builtin_amdgcn_readlane(inc, kWave - 1);
+      wN += tot & 0xffff;
+      wC += tot >> 16;
+    }
+  };
+  if (near) {
+    const float wantf1 = wantf + 1.f;
+    classify([&](float xi, bool& n, bool& c) {  // (in-row elements have dd >= 0)
+      const float dd = fmaf(-xi, kNearScale, M32);
+      n = dd < wantf;
+      c = dd < wantf1;  // minus the nearer ones
+    });
+  } else {
+    classify([&](float xi, bool& n, bool& c) {
+      const uint32_t key = f32_to_key(xi);
+      n = key > kth;
+      c = key == kth;
+    });
+  }
+  if (lane == 0) {
+    sh.wtot[0][w] = wN;
+    sh.wtot[1][w] = wC;
+  }
+  lds_sync();
+  int WN = 0, WC = 0, TN = 0, TC = 0;
+#pragma unroll
+  for (int u = 0; u < kBlkWaves; ++u) {
+    const int a = sh.wtot[0][u], b = sh.wtot[1][u];
+    if (u < w) {
+      WN += a;
+      WC += b;
+    }
+    TN += a;
+    TC += b;
+  }
+  // chunk q's masks and the nearer / candidates before the lane's first
+  // element of it (every lane calls it: it holds a wave scan)
+  auto chunk_bases = [&](int q, uint32_t& mN, uint32_t& mC, int& nb0, int& cb0) {
+    const uint32_t m8 = (msk[q >> 2] >> (8 * (q & 3))) & 0xffu;
+    mN = m8 & 15u;
+    mC = m8 >> 4;
+    const int cntv = __popc(mN) | (__popc(mC) << 16);
+    const int ex = wave_incl_scan(cntv, lane) - cntv;
+    nb0 = WN + (base[q] & 0xffff) + (ex & 0xffff);
+    cb0 = WC + (base[q] >> 16) + (ex >> 16);
+  };
+
+  if (!near) {
+    // key classes: every kept position is placed by its owner, the first
+    // need equal ones by their rank among the equal ones
+#pragma unroll
+    for (int q = 0; q < CH; ++q) {
+      uint32_t mN, mC;
+      int nb0, cb0;
+      chunk_bases(q, mN, mC, nb0, cb0);
+      if (mN | mC) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t below = (1u << j) - 1u;
+          const int cb = cb0 + __popc(mC & below);
+          if (((mN >> j) & 1u) || (((mC >> j) & 1u) && cb < need)) {
+            const int pos = nb0 + __popc(mN & below) + min(cb, need);
+            if (pos < k) {
+              sh.sidx[pos] = wbase + 256 * q + j;
+              sh.sval[pos] = xr[q][j];
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+    for (int i = tid; i < k; i += kBlkThreads) {  // the kept list for inspection, coalesced
+      gidx[i] = sh.sidx[i];
+      gval[i] = sh.sval[i];
+    }
+    if (tid == 0) {
+      p.sel_cnt[r] = k;
+      if (p.sel_total) p.sel_total[r] = k;
+      p.pstar_out[r] = expf(key_to_f32(kth) - M) / S;
+    }
+    PV pv;
+    pv.init();
+    pv.add(k, sh.sidx, sh.sval, vbase, vrow, false, sh.red);  // (k <= kRegList: the list is in LDS)
+    pv.finish(accs, v.out, v.out_dt, ooff, false);
+    return;
+  }
+
+  // distance classes: the nearer positions go to LDS at their rank among
+  // the nearer ones (with the candidates before each), the candidates in
+  // index order; the V rows of both are gathered while the candidates are
+  // ranked.  Softmax weights are exp(x - M): the row max is always kept.
+  const int c = TC;  // == the bin's count <= kRegCand
+#pragma unroll
+  for (int q = 0; q < CH; ++q) {
+    uint32_t mN, mC;
+    int nb0, cb0;
+    chunk_bases(q, mN, mC, nb0, cb0);
+    if (mN | mC) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t below = (1u << j) - 1u;
+        const int nb = nb0 + __popc(mN & below), cb = cb0 + __popc(mC & below);
+        if ((mN >> j) & 1u) {
+          if (nb < kRegList) {
+            sh.sidx[nb] = wbase + 256 * q + j;
+            sh.sval[nb] = xr[q][j];
+            sh.ncb[nb] = cb;
+          }
+        } else if ((mC >> j) & 1u) {
+          if (cb < kRegCand) {
+            sh.cval[cb] = xr[q][j];
+            sh.cidx[cb] = wbase + 256 * q + j;
+            sh.cnb[cb] = nb;
+          }
+        }
+      }
+    }
+  }
+  lds_sync();
+
+  // softmax . V entries: the nearer positions, then every candidate
+  const int nE = TN + c;  // TN (== k - krem) nearer positions, all kept
+  const int G = tid >> 4;
+  const char* vb = vbase + static_cast<int64_t>(tid & 15) * PV::BYTES;
+  auto entry_pos = [&](int e) { return e < TN ? sh.sidx[e] : sh.cidx[e - TN]; };
+
+  // which candidates are kept, and the k-th key (block-uniform branches)
+  if (c <= kRegRank) {
+    // pairwise ranks by (value desc, index asc), 8 threads per candidate:
+    // rank < krem is kept, rank krem - 1 is the k-th
+    const int i = tid >> 3, sub = tid & 7;
+    int rank = 0;
+    uint32_t ki = 0;
+    if (i < c) {
+      ki = f32_to_key(sh.cval[i]);
+#pragma unroll 4
+      for (int u = sub; u < c; u += 8) {
+        const uint32_t ku = f32_to_key(sh.cval[u]);
+        rank += (ku > ki || (ku == ki && u < i)) ? 1 : 0;
+      }
+    }
+    rank += __shfl_xor(rank, 1);
+    rank += __shfl_xor(rank, 2);
+    rank += __shfl_xor(rank, 4);
+    if (i < c && sub == 0) {
+      sh.cflag[i] = rank < krem ? 1 : 0;
+      if (rank == krem - 1) sh.sel_key = static_cast<int>(ki);
+    }
+    lds_sync();
+    kth = static_cast<uint32_t>(sh.sel_key);
+    // prefix of the flags, 8 threads per candidate
+    int before = 0;
+    if (i < c) {
+#pragma unroll 4
+      for (int u = sub; u < i; u += 8) before += sh.cflag[u];
+    }
+    before += __shfl_xor(before, 1);
+    before += __shfl_xor(before, 2);
+    before += __shfl_xor(before, 4);
+    if (i < c && sub == 0) sh.ctp[i] = before;
+    if (tid == 0) sh.ctp[c] = krem;
+  } else {
+    int nd = krem;
+    kth = radix_select_each(sh, nd, [&](auto f) {
+      for (int t = tid; t < c; t += kBlkThreads) f(sh.cval[t]);
+    });
+    // kept: above kth, or equal to it and among the first nd equal ones
+    int tflag[4] = {0, 0, 0, 0};  // candidates 4 tid .. 4 tid + 3
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = 4 * tid + j;
+      if (t < c) {
+        const uint32_t kt = f32_to_key(sh.cval[t]);
+        if (kt > kth) {
+          tflag[j] = 1;
+        } else if (kt == kth) {
+          int eq = 0;
+          for (int u = 0; u < t; ++u) eq += f32_to_key(sh.cval[u]) == kth ? 1 : 0;
+          tflag[j] = eq < nd ? 1 : 0;
+        }
+        sh.cflag[t] = tflag[j];
+      }
+    }
+    const int ts = tflag[0] + tflag[1] + tflag[2] + tflag[3];
+    const int tb = block_excl_scan4(ts, sh.scan);
+    if (4 * tid < c) {
+      sh.ctp[4 * tid] = tb;
+      if (4 * tid + 1 <= c) sh.ctp[4 * tid + 1] = tb + tflag[0];
+      if (4 * tid + 2 <= c) sh.ctp[4 * tid + 2] = tb + tflag[0] + tflag[1];
+      if (4 * tid + 3 <= c) sh.ctp[4 * tid + 3] = tb + tflag[0] + tflag[1] + tflag[2];
+      if (4 * tid + 4 <= c) sh.ctp[4 * tid + 4] = ts + tb;
+    }
+  }
+  lds_sync();
+
+  // the kept list, in position order, straight to the workspace: slot =
+  // nearer before + kept candidates before
+  for (int e = tid; e < TN; e += kBlkThreads) {
+    const int pos = e + sh.ctp[min(sh.ncb[e], c)];
+    if (pos < k) {
+      gidx[pos] = sh.sidx[e];
+      gval[pos] = sh.sval[e];
+    }
+  }
+  for (int t = tid; t < c; t += kBlkThreads) {
+    if (sh.cflag[t]) {
+      const int pos = sh.cnb[t] + sh.ctp[t];
+      if (pos < k) {
+        gidx[pos] = sh.cidx[t];
+        gval[pos] = sh.cval[t];
+      }
+    }
+  }
+  if (tid == 0) {
+    p.sel_cnt[r] = k;
+    if (p.sel_total) p.sel_total[r] = k;
+    p.pstar_out[r] = expf(key_to_f32(kth) - M) / S;
+  }
+
+  // softmax . V over the entries: weight exp(x - M) (0 for a candidate not kept)
+  auto weight = [&](int e) {
+    if (e < TN) return __expf(sh.sval[e] - M);
+    return sh.cflag[e - TN] ? __expf(sh.cval[e - TN] - M) : 0.f;
+  };
+  PV pv;
+  pv.init();
+  pv.m = M;
+  u32x4 raw[kPVUnroll][PV::NV];
+  for (int e0 = G; e0 < nE; e0 += kPVUnroll * kBlkGroups) {
+#pragma unroll
+    for (int u = 0; u < kPVUnroll; ++u) {
+      const int e = e0 + u * kBlkGroups;
+      if (e < nE) PV::load_raw(vb + static_cast<int64_t>(entry_pos(e)) * vrow, raw[u]);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // all gathers in flight before the FMAs
+#pragma unroll
+    for (int u = 0; u < kPVUnroll; ++u) {
+      const int e = e0 + u * kBlkGroups;
+      if (e < nE) {
+        const float wt = weight(e);
+        float f[PV::DPL];
+        PV::unpack(raw[u], f);
+#pragma unroll
+        for (int i = 0; i < PV::DPL; ++i) pv.acc[i] += wt * f[i];
+      }
+    }
+  }
+  float ls = 0.f;
+  for (int e = tid; e < nE; e += kBlkThreads) ls += weight(e);
+  pv.l = block_sum<kBlkWaves>(ls, sh.red);
+  pv.finish(accs, v.out, v.out_dt, ooff, false);
+}
+
 template <int DT, int D>
 static hipError_t launch_calibrate(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
-  hipLaunchKernelGGL((atopn_calibrate_kernel<DT, D>), dim3(p.nrows), dim3(kBlkThreads), 0, st, p, v);
+  const dim3 grid(p.nrows), block(kBlkThreads);
+  // the row in registers, chunks of 4096 positions per block: up to 13 (at
+  // 14 and more the compiler spills the row itself)
+  if (p.cap <= kRegList && p.L <= 13 * 4096) {
+    if (p.L <= 2 * 4096)
+      hipLaunchKernelGGL((atopn_calibrate_reg_kernel<DT, D, 2>), grid, block, 0, st, p, v);
+    else if (p.L <= 4 * 4096)
+      hipLaunchKernelGGL((atopn_calibrate_reg_kernel<DT, D, 4>), grid, block, 0, st, p, v);
+    else if (p.L <= 9 * 4096)
+      hipLaunchKernelGGL((atopn_calibrate_reg_kernel<DT, D, 9>), grid, block, 0, st, p, v);
+    else
+      hipLaunchKernelGGL((atopn_calibrate_reg_kernel<DT, D, 13>), grid, block, 0, st, p, v);
+  } else {
+    hipLaunchKernelGGL((atopn_calibrate_kernel<DT, D>), grid, block, 0, st, p, v);
+  }
   return hipGetLastError();
 }
 

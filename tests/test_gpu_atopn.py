@@ -646,15 +646,22 @@ def test_fast_step_random_shapes_vs_oracle(seed):
             assert rel_l2(out.reshape(nr, d)[r], ref.reshape(d)) < tol, (r, cnt)
 
 
-@pytest.mark.parametrize("case", ["constant", "far_outlier", "near_constant", "gaussian"])
+@pytest.mark.parametrize("case", ["constant", "far_outlier", "near_constant", "gaussian", "gaussian_dup",
+                                  "clustered", "clustered_dup", "long_clustered"])
 def test_calibration_kth_logit_paths(case):
     """The calibration kernel finds the N-th logit among the few elements of
-    its distance-below-max bin, or over the whole row when that bin holds more
-    than 4096 elements (all logits equal: ties taken by lowest index; or all
-    within 1/32 of the max) or the N-th logit lies more than 64 below the max
-    (one huge key): every path against the float64 oracle, fp32 inputs."""
+    its distance-below-max bin (ranked pairwise when at most 128, else by a
+    radix select over them: "clustered" puts a few hundred in that bin), or
+    by keys over the whole row when that bin holds more than 4096 elements
+    (all logits equal: ties taken by lowest index; or all within 1/32 of the
+    max) or the N-th logit lies more than 64 below the max (one huge key).
+    "_dup" rows repeat every key once, so the N-th logit is tied and the
+    lower position must win.  Every path against the float64 oracle (fp32
+    inputs), and the kept list exactly the stable top N of the GPU's scores."""
     rng = np.random.default_rng(zlib.crc32(case.encode()))
     b, q_h, k_h, v_h, d, L, N = 2, 4, 1, 2, 64, 6000, 256
+    if case == "long_clustered":
+        L = 50000  # the largest register-resident row class
     q = rng.standard_normal((b, q_h, 1, d), dtype=np.float32)
     k = rng.standard_normal((b, k_h, L, d), dtype=np.float32)
     v = rng.standard_normal((b, v_h, L, d), dtype=np.float32)
@@ -662,10 +669,22 @@ def test_calibration_kth_logit_paths(case):
         k[:] = 0.0
     elif case == "near_constant":
         k *= np.float32(1e-3)
+    elif case in ("clustered", "clustered_dup", "long_clustered"):
+        k *= np.float32(0.05)  # logits of std 0.05: a few hundred per 1/32 bin near the N-th
     elif case == "far_outlier":
         k[:, 0, 1234] = q[:, 0, 0] * np.float32(50.0)  # logit ~400 for head 0, ~+-50 for the others
+    if case.endswith("_dup"):
+        k[:, :, L // 2:] = k[:, :, :L // 2]
     table = torch.zeros(b * q_h, device="cuda")
     cal = host(ops.atopn_calibrate(dev(q, "f32"), dev(k, "f32"), dev(v, "f32"), N, table, out_dtype=torch.float32))
+    torch.cuda.synchronize()
+    views = _views(b, q_h, k_h, L, d, N, fast=False)
+    for r in range(b * q_h):
+        x = views["scores"][r, :L]
+        top = np.sort(np.argsort(-x, kind="stable")[:N])
+        assert views["sel_cnt"][r] == N
+        np.testing.assert_array_equal(views["sel_idx"][r, :N], top, err_msg=f"{case} row {r}")
+        np.testing.assert_array_equal(views["sel_val"][r, :N], x[top])
     ref, thr, _ = O.calibrate(q, k, v, None, N, None)
     assert rel_l2(cal, ref) < 1e-4, case
     np.testing.assert_allclose(host(table), thr, rtol=1e-4)
