@@ -385,16 +385,18 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_kernel(FusedSelPa
 // is its wave's offset + its chunk's offset in the wave + a wave scan.
 //
 // Selection by classes: with the k-th largest value's distance bin B
-// (elements of nearer bins are all larger than every element of B, as in
-// near_pick), the positions of nearer bins are all kept ("nearer") and the
+// (2048 bins of (M - x) * s below the max M, s a power of two fitted to the
+// row's spread; elements of nearer bins are all larger than every element of
+// B, as in near_pick), the positions of nearer bins are all kept ("nearer") and the
 // krem largest of bin B's elements ("candidates", by value, then lowest
 // index) complete the k.  The candidates -- a few dozen on N(0,1)-like rows
 // -- go to LDS in index order and are ranked there; a kept position's slot
 // in the list is the nearer positions before it + the kept candidates
 // before it.  When the distance bins cannot be used (a NaN or non-finite
-// max, a k-th value more than 64 below the max, more candidates than LDS
-// holds) the classes are by key: above the k-th key (from a radix select
-// over the registers) and equal to it, the first `need` of which are kept.
+// max, more candidates than LDS holds: ties, or one bin of a row stretched by
+// a far outlier) the classes are by key: above the k-th key (from a radix
+// select over the registers) and equal to it, the first `need` of which are
+// kept.
 constexpr int kRegList = 4096;   // k <= kRegList: the kept list in LDS
 constexpr int kRegCand = 2048;   // candidates of the distance classes kept in LDS
 constexpr int kRegRank = 128;    // candidates ranked pairwise; more: radix select
@@ -489,19 +491,44 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_reg_kernel(FusedS
   // every in-row element of the thread's share: f(value, position)
   auto each_in = [&](auto f) {
 #pragma unroll
-    for (int q = 0; q < CH; ++q)
+    for (int q = 0; q < CH; ++q) {
+      const int lim = Leff - (wbase + 256 * q);  // elements of this chunk in the row
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        if (wbase + 256 * q + j < Leff) f(xr[q][j]);
+        if (j < lim) f(xr[q][j]);
+    }
   };
 
-  // pass 1: distance bins (M - x) * 32 below the max; a NaN, or a max
+  // the bins' scale s: the largest power of two (at most 2^40) with
+  // (M - mn) * s <= 2047 for the smallest finite score mn, so that every
+  // finite position has a bin whatever the row's spread; a power of two
+  // keeps M * s exact, so the max sits at distance 0
+  float mnl = INFINITY;
+#pragma unroll
+  for (int q = 0; q < CH; ++q) {
+    const int lim = Leff - (wbase + 256 * q);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float xi = xr[q][j];
+      mnl = fminf(mnl, (j < lim && xi > -INFINITY) ? xi : INFINITY);  // (no branch per element)
+    }
+  }
+  const float mn = -block_max<kBlkWaves>(-mnl, sh.red);
+  float scale = kNearScale;
+  const float range = M - mn;
+  if (range > 0.f && range < INFINITY) {
+    int ex;
+    frexpf(fminf(static_cast<float>(kNearBins - 1) / range, 1e30f), &ex);  // in [2^(ex-1), 2^ex)
+    scale = ldexpf(1.f, min(max(ex - 1, -100), 40));
+  }
+
+  // pass 1: distance bins (M - x) * s below the max; a NaN, or a max
   // that is not finite, sends the row to the key classes
-  const float M32 = M * kNearScale;
+  const float Ms = M * scale;
   int odd = (M > -INFINITY && M < INFINITY) ? 0 : 1;
   if (!odd) {
     each_in([&](float xi) {
-      const float dd = fmaf(-xi, kNearScale, M32);
+      const float dd = fmaf(-xi, scale, Ms);
       if (!(dd >= 0.f)) odd = 1;
       else if (dd < static_cast<float>(kNearBins)) atomicAdd(&sh.hist[kNearBins - 1 - static_cast<int>(dd)], 1);
     });
@@ -560,7 +587,7 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_reg_kernel(FusedS
   if (near) {
     const float wantf1 = wantf + 1.f;
     classify([&](float xi, bool& n, bool& c) {  // (in-row elements have dd >= 0)
-      const float dd = fmaf(-xi, kNearScale, M32);
+      const float dd = fmaf(-xi, scale, Ms);
       n = dd < wantf;
       c = dd < wantf1;  // minus the nearer ones
     });

@@ -650,14 +650,15 @@ def test_fast_step_random_shapes_vs_oracle(seed):
                                   "clustered", "clustered_dup", "long_clustered"])
 def test_calibration_kth_logit_paths(case):
     """The calibration kernel finds the N-th logit among the few elements of
-    its distance-below-max bin (ranked pairwise when at most 128, else by a
-    radix select over them: "clustered" puts a few hundred in that bin), or
-    by keys over the whole row when that bin holds more than 4096 elements
-    (all logits equal: ties taken by lowest index; or all within 1/32 of the
-    max) or the N-th logit lies more than 64 below the max (one huge key).
-    "_dup" rows repeat every key once, so the N-th logit is tied and the
-    lower position must win.  Every path against the float64 oracle (fp32
-    inputs), and the kept list exactly the stable top N of the GPU's scores."""
+    its bin of distance below the max (2048 bins scaled to the row's spread:
+    "near_constant" rows span ~0.01, "far_outlier" rows ~450 for head 0),
+    ranked pairwise when at most 128, else by a radix select over them
+    ("clustered" and "far_outlier" put a few hundred in that bin), or by keys
+    over the whole row when that bin holds more than 2048 elements (all
+    logits equal: ties taken by lowest index).  "_dup" rows repeat every key
+    once, so the N-th logit is tied and the lower position must win.  Every
+    path against the float64 oracle (fp32 inputs), and the kept list exactly
+    the stable top N of the GPU's scores."""
     rng = np.random.default_rng(zlib.crc32(case.encode()))
     b, q_h, k_h, v_h, d, L, N = 2, 4, 1, 2, 64, 6000, 256
     if case == "long_clustered":
