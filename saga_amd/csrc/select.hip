@@ -243,8 +243,9 @@ __device__ __forceinline__ bool near_pick(SH& sh, const float* x, int64_t ld, in
 }
 
 // Calibration: exact top-k of the row (k = min(top_n, L)), for rows past
-// the register-resident kernel below (more than 13 * 4096 positions, or
-// top_n > 4096), the row re-read from memory by each pass.
+// the block-resident kernel below (more than 17 * 4096 positions, top_n >
+// 4096, or top_n > 2048 past 13 * 4096 positions), the row re-read from
+// memory by each pass.
 //   1. full-row max M and sum S of exp(x - M) from the K1 partials;
 //   2. the k-th largest value: by a radix select over the few elements of
 //      its bin of distance below M (near_pick), else over the whole row;
@@ -398,25 +399,30 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_kernel(FusedSelPa
 // select over the registers) and equal to it, the first `need` of which are
 // kept.
 constexpr int kRegList = 4096;   // k <= kRegList: the kept list in LDS
+constexpr int kRegChunks = 13;   // chunks kept in registers (more: thread-private LDS slots)
+constexpr int kRegListLong = 2048;  // the 17-chunk rows: kept list (k <= 2048),
+constexpr int kRegCandLong = 1024;  //   candidates in LDS,
+constexpr int kRegChunksLong = 12;  //   chunks in registers (5 in LDS)
 constexpr int kRegCand = 2048;   // candidates of the distance classes kept in LDS
 constexpr int kRegRank = 128;    // candidates ranked pairwise; more: radix select
 
+template <int LIST, int CAND>
 struct RegShared {
-  static constexpr int kList = kRegList;
+  static constexpr int kList = LIST;
   float red[kBlkWaves];
   int cnt[kBlkWaves];      // hist_pick's per-wave totals
   int wtot[2][kBlkWaves];  // per-wave class totals (nearer, candidates)
   int scan[kBlkWaves];     // per-wave totals of the taken-flag scan
   int hist[2048];
   int sel_bin, sel_above, sel_key;
-  int sidx[kRegList];       // the kept list (key classes) / the nearer positions (distance classes),
-  float sval[kRegList];     //   their values
-  int ncb[kRegList];        //   and the candidates before each nearer position
-  float cval[kRegCand];     // candidates in index order: value,
-  int cidx[kRegCand];       // position,
-  int cnb[kRegCand];        // nearer positions before it,
-  int ctp[kRegCand + 1];    // kept candidates before it (ctp[c] = all kept)
-  int cflag[kRegCand];      // kept?
+  int sidx[LIST];           // the kept list (key classes) / the nearer positions (distance classes),
+  float sval[LIST];         //   their values
+  int ncb[LIST];            //   and the candidates before each nearer position
+  float cval[CAND];         // candidates in index order: value,
+  int cidx[CAND];           // position,
+  int cnb[CAND];            // nearer positions before it,
+  int ctp[CAND + 1];        // kept candidates before it (ctp[c] = all kept)
+  int cflag[CAND];          // kept?
 };
 
 // Exclusive scan over the block of four values per thread (thread t's four
@@ -433,10 +439,16 @@ __device__ __forceinline__ int block_excl_scan4(int tsum, int* wscan) {
   return base;
 }
 
-template <int DT, int D, int CH>
+template <int DT, int D, int CH, int LIST>
 __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_reg_kernel(FusedSelParams p, PVParams v) {
-  __shared__ RegShared sh;
+  // chunks [0, CHR) in registers, the rest in thread-private LDS slots (at
+  // 14 register chunks and more the compiler spills the row itself)
+  constexpr int CHR = CH <= kRegChunks ? CH : kRegChunksLong;
+  constexpr int CHL = CH - CHR;
+  constexpr int CAND = CHL > 0 ? kRegCandLong : kRegCand;
+  __shared__ RegShared<LIST, CAND> sh;
   __shared__ float accs[kBlkWaves * D];
+  __shared__ f32x4 rowl[CHL > 0 ? CHL * kBlkThreads : 1];
   const int r = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int bi = r / p.q_h, h = r - bi * p.q_h;
@@ -453,9 +465,13 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_reg_kernel(FusedS
   const float ps0 = tid < nch ? prow_s[tid] : 0.f;
   const int wbase = w * (CH * 256) + 4 * lane;  // chunk q: wbase + 256 q + j
   const int lastq = max(0, (Leff + 3) / 4 * 4 - 4);  // loads past Leff are clamped (and never used)
-  f32x4 xr[CH];
+  f32x4 xr[CHR], xl[CHL > 0 ? CHL : 1];
 #pragma unroll
-  for (int q = 0; q < CH; ++q) xr[q] = *reinterpret_cast<const f32x4*>(x + min(wbase + 256 * q, lastq));
+  for (int q = 0; q < CH; ++q) {
+    const f32x4 v4 = *reinterpret_cast<const f32x4*>(x + min(wbase + 256 * q, lastq));
+    if (q < CHR) xr[q < CHR ? q : 0] = v4;
+    else xl[q >= CHR ? q - CHR : 0] = v4;
+  }
   for (int i = tid; i < 2048; i += kBlkThreads) sh.hist[i] = 0;
 
   float mloc = pm0;
@@ -467,6 +483,13 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_reg_kernel(FusedS
     if (pm != kNegInf) sloc += prow_s[c] * __expf(pm - M);
   }
   const float S = block_sum<kBlkWaves>(sloc, sh.red);
+#pragma unroll
+  for (int q = 0; q < CHL; ++q) rowl[q * kBlkThreads + tid] = xl[q];  // (read back by this thread only)
+  // chunk q of the thread's share of the row
+  auto chunk = [&](int q) -> f32x4 {
+    if (q < CHR) return xr[q < CHR ? q : 0];
+    return rowl[(q >= CHR ? q - CHR : 0) * kBlkThreads + tid];
+  };
 
   const int k = min(p.cap, Leff);
   int32_t* gidx = p.sel_idx + static_cast<int64_t>(r) * p.cap;
@@ -493,9 +516,10 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_reg_kernel(FusedS
 #pragma unroll
     for (int q = 0; q < CH; ++q) {
       const int lim = Leff - (wbase + 256 * q);  // elements of this chunk in the row
+      const f32x4 xq = chunk(q);
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        if (j < lim) f(xr[q][j]);
+        if (j < lim) f(xq[j]);
     }
   };
 
@@ -507,9 +531,10 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_reg_kernel(FusedS
 #pragma unroll
   for (int q = 0; q < CH; ++q) {
     const int lim = Leff - (wbase + 256 * q);
+    const f32x4 xq = chunk(q);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float xi = xr[q][j];
+      const float xi = xq[j];
       mnl = fminf(mnl, (j < lim && xi > -INFINITY) ? xi : INFINITY);  // (no branch per element)
     }
   }
@@ -537,7 +562,7 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_reg_kernel(FusedS
   int krem = k, bin = -1, above = 0;
   if (near) {
     hist_pick(sh, kNearBins, k, bin, above);
-    near = bin >= 0 && sh.hist[bin] <= kRegCand;  // block-uniform
+    near = bin >= 0 && sh.hist[bin] <= CAND;  // block-uniform
   }
   uint32_t kth = 0;
   float wantf = 0.f;
@@ -564,10 +589,11 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_reg_kernel(FusedS
 #pragma unroll
     for (int q = 0; q < CH; ++q) {
       uint32_t mN = 0, mC = 0;
+      const f32x4 xq = chunk(q);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         bool n, c;
-        cls(xr[q][j], n, c);
+        cls(xq[j], n, c);
         mN |= static_cast<uint32_t>(n) << j;
         mC |= static_cast<uint32_t>(c) << j;
       }
@@ -643,7 +669,7 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_reg_kernel(FusedS
             const int pos = nb0 + __popc(mN & below) + min(cb, need);
             if (pos < k) {
               sh.sidx[pos] = wbase + 256 * q + j;
-              sh.sval[pos] = xr[q][j];
+              sh.sval[pos] = chunk(q)[j];
             }
           }
         }
@@ -661,7 +687,7 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_reg_kernel(FusedS
     }
     PV pv;
     pv.init();
-    pv.add(k, sh.sidx, sh.sval, vbase, vrow, false, sh.red);  // (k <= kRegList: the list is in LDS)
+    pv.add(k, sh.sidx, sh.sval, vbase, vrow, false, sh.red);  // (k <= LIST: the list is in LDS)
     pv.finish(accs, v.out, v.out_dt, ooff, false);
     return;
   }
@@ -670,7 +696,7 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_reg_kernel(FusedS
   // the nearer ones (with the candidates before each), the candidates in
   // index order; the V rows of both are gathered while the candidates are
   // ranked.  Softmax weights are exp(x - M): the row max is always kept.
-  const int c = TC;  // == the bin's count <= kRegCand
+  const int c = TC;  // == the bin's count <= CAND
 #pragma unroll
   for (int q = 0; q < CH; ++q) {
     uint32_t mN, mC;
@@ -682,14 +708,14 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_reg_kernel(FusedS
         const uint32_t below = (1u << j) - 1u;
         const int nb = nb0 + __popc(mN & below), cb = cb0 + __popc(mC & below);
         if ((mN >> j) & 1u) {
-          if (nb < kRegList) {
+          if (nb < LIST) {
             sh.sidx[nb] = wbase + 256 * q + j;
-            sh.sval[nb] = xr[q][j];
+            sh.sval[nb] = chunk(q)[j];
             sh.ncb[nb] = cb;
           }
         } else if ((mC >> j) & 1u) {
-          if (cb < kRegCand) {
-            sh.cval[cb] = xr[q][j];
+          if (cb < CAND) {
+            sh.cval[cb] = chunk(q)[j];
             sh.cidx[cb] = wbase + 256 * q + j;
             sh.cnb[cb] = nb;
           }
@@ -835,17 +861,19 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_reg_kernel(FusedS
 template <int DT, int D>
 static hipError_t launch_calibrate(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
   const dim3 grid(p.nrows), block(kBlkThreads);
-  // the row in registers, chunks of 4096 positions per block: up to 13 (at
-  // 14 and more the compiler spills the row itself)
+  // the row resident in the block, chunks of 4096 positions: up to 13 in
+  // registers, 17 with 4 in LDS (a 2048-entry list then leaves room for them)
   if (p.cap <= kRegList && p.L <= 13 * 4096) {
     if (p.L <= 2 * 4096)
-      hipLaunchKernelGGL((atopn_calibrate_reg_kernel<DT, D, 2>), grid, block, 0, st, p, v);
+      hipLaunchKernelGGL((atopn_calibrate_reg_kernel<DT, D, 2, kRegList>), grid, block, 0, st, p, v);
     else if (p.L <= 4 * 4096)
-      hipLaunchKernelGGL((atopn_calibrate_reg_kernel<DT, D, 4>), grid, block, 0, st, p, v);
+      hipLaunchKernelGGL((atopn_calibrate_reg_kernel<DT, D, 4, kRegList>), grid, block, 0, st, p, v);
     else if (p.L <= 9 * 4096)
-      hipLaunchKernelGGL((atopn_calibrate_reg_kernel<DT, D, 9>), grid, block, 0, st, p, v);
+      hipLaunchKernelGGL((atopn_calibrate_reg_kernel<DT, D, 9, kRegList>), grid, block, 0, st, p, v);
     else
-      hipLaunchKernelGGL((atopn_calibrate_reg_kernel<DT, D, 13>), grid, block, 0, st, p, v);
+      hipLaunchKernelGGL((atopn_calibrate_reg_kernel<DT, D, 13, kRegList>), grid, block, 0, st, p, v);
+  } else if (p.cap <= kRegListLong && p.L <= 17 * 4096) {
+    hipLaunchKernelGGL((atopn_calibrate_reg_kernel<DT, D, 17, kRegListLong>), grid, block, 0, st, p, v);
   } else {
     hipLaunchKernelGGL((atopn_calibrate_kernel<DT, D>), grid, block, 0, st, p, v);
   }

@@ -647,7 +647,7 @@ def test_fast_step_random_shapes_vs_oracle(seed):
 
 
 @pytest.mark.parametrize("case", ["constant", "far_outlier", "near_constant", "gaussian", "gaussian_dup",
-                                  "clustered", "clustered_dup", "long_clustered"])
+                                  "clustered", "clustered_dup", "long_clustered", "longest_clustered"])
 def test_calibration_kth_logit_paths(case):
     """The calibration kernel finds the N-th logit among the few elements of
     its bin of distance below the max (2048 bins scaled to the row's spread:
@@ -662,7 +662,9 @@ def test_calibration_kth_logit_paths(case):
     rng = np.random.default_rng(zlib.crc32(case.encode()))
     b, q_h, k_h, v_h, d, L, N = 2, 4, 1, 2, 64, 6000, 256
     if case == "long_clustered":
-        L = 50000  # the largest register-resident row class
+        L = 50000  # the largest all-register row class
+    elif case == "longest_clustered":
+        L = 65537  # a 64k context + 1: 13 chunks in registers, 4 in LDS
     q = rng.standard_normal((b, q_h, 1, d), dtype=np.float32)
     k = rng.standard_normal((b, k_h, L, d), dtype=np.float32)
     v = rng.standard_normal((b, v_h, L, d), dtype=np.float32)
@@ -670,7 +672,7 @@ def test_calibration_kth_logit_paths(case):
         k[:] = 0.0
     elif case == "near_constant":
         k *= np.float32(1e-3)
-    elif case in ("clustered", "clustered_dup", "long_clustered"):
+    elif case in ("clustered", "clustered_dup", "long_clustered", "longest_clustered"):
         k *= np.float32(0.05)  # logits of std 0.05: a few hundred per 1/32 bin near the N-th
     elif case == "far_outlier":
         k[:, 0, 1234] = q[:, 0, 0] * np.float32(50.0)  # logit ~400 for head 0, ~+-50 for the others
