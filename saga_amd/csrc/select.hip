@@ -652,6 +652,10 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_reg_kernel(FusedS
     cb0 = WC + (base[q] >> 16) + (ex >> 16);
   };
 
+  // the kept list (key classes: in LDS in position order) or the nearer
+  // positions + the candidates (distance classes) are the softmax . V
+  // entries: the first nl from sidx / sval, then c candidates
+  int nl = k, c = 0;
   if (!near) {
     // key classes: every kept position is placed by its owner, the first
     // need equal ones by their rank among the equal ones
@@ -680,141 +684,125 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_reg_kernel(FusedS
       gidx[i] = sh.sidx[i];
       gval[i] = sh.sval[i];
     }
-    if (tid == 0) {
-      p.sel_cnt[r] = k;
-      if (p.sel_total) p.sel_total[r] = k;
-      p.pstar_out[r] = expf(key_to_f32(kth) - M) / S;
-    }
-    PV pv;
-    pv.init();
-    pv.add(k, sh.sidx, sh.sval, vbase, vrow, false, sh.red);  // (k <= LIST: the list is in LDS)
-    pv.finish(accs, v.out, v.out_dt, ooff, false);
-    return;
-  }
-
-  // distance classes: the nearer positions go to LDS at their rank among
-  // the nearer ones (with the candidates before each), the candidates in
-  // index order; the V rows of both are gathered while the candidates are
-  // ranked.  Softmax weights are exp(x - M): the row max is always kept.
-  const int c = TC;  // == the bin's count <= CAND
+  } else {
+    // distance classes: the nearer positions go to LDS at their rank among
+    // the nearer ones (with the candidates before each), the candidates in
+    // index order, where they are ranked
+    c = TC;  // == the bin's count <= CAND
+    nl = TN;  // (== k - krem) nearer positions, all kept
 #pragma unroll
-  for (int q = 0; q < CH; ++q) {
-    uint32_t mN, mC;
-    int nb0, cb0;
-    chunk_bases(q, mN, mC, nb0, cb0);
-    if (mN | mC) {
+    for (int q = 0; q < CH; ++q) {
+      uint32_t mN, mC;
+      int nb0, cb0;
+      chunk_bases(q, mN, mC, nb0, cb0);
+      if (mN | mC) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t below = (1u << j) - 1u;
-        const int nb = nb0 + __popc(mN & below), cb = cb0 + __popc(mC & below);
-        if ((mN >> j) & 1u) {
-          if (nb < LIST) {
-            sh.sidx[nb] = wbase + 256 * q + j;
-            sh.sval[nb] = chunk(q)[j];
-            sh.ncb[nb] = cb;
-          }
-        } else if ((mC >> j) & 1u) {
-          if (cb < CAND) {
-            sh.cval[cb] = chunk(q)[j];
-            sh.cidx[cb] = wbase + 256 * q + j;
-            sh.cnb[cb] = nb;
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t below = (1u << j) - 1u;
+          const int nb = nb0 + __popc(mN & below), cb = cb0 + __popc(mC & below);
+          if ((mN >> j) & 1u) {
+            if (nb < LIST) {
+              sh.sidx[nb] = wbase + 256 * q + j;
+              sh.sval[nb] = chunk(q)[j];
+              sh.ncb[nb] = cb;
+            }
+          } else if ((mC >> j) & 1u) {
+            if (cb < CAND) {
+              sh.cval[cb] = chunk(q)[j];
+              sh.cidx[cb] = wbase + 256 * q + j;
+              sh.cnb[cb] = nb;
+            }
           }
         }
       }
-    }
-  }
-  lds_sync();
-
-  // softmax . V entries: the nearer positions, then every candidate
-  const int nE = TN + c;  // TN (== k - krem) nearer positions, all kept
-  const int G = tid >> 4;
-  const char* vb = vbase + static_cast<int64_t>(tid & 15) * PV::BYTES;
-  auto entry_pos = [&](int e) { return e < TN ? sh.sidx[e] : sh.cidx[e - TN]; };
-
-  // which candidates are kept, and the k-th key (block-uniform branches)
-  if (c <= kRegRank) {
-    // pairwise ranks by (value desc, index asc), 8 threads per candidate:
-    // rank < krem is kept, rank krem - 1 is the k-th
-    const int i = tid >> 3, sub = tid & 7;
-    int rank = 0;
-    uint32_t ki = 0;
-    if (i < c) {
-      ki = f32_to_key(sh.cval[i]);
-#pragma unroll 4
-      for (int u = sub; u < c; u += 8) {
-        const uint32_t ku = f32_to_key(sh.cval[u]);
-        rank += (ku > ki || (ku == ki && u < i)) ? 1 : 0;
-      }
-    }
-    rank += __shfl_xor(rank, 1);
-    rank += __shfl_xor(rank, 2);
-    rank += __shfl_xor(rank, 4);
-    if (i < c && sub == 0) {
-      sh.cflag[i] = rank < krem ? 1 : 0;
-      if (rank == krem - 1) sh.sel_key = static_cast<int>(ki);
     }
     lds_sync();
-    kth = static_cast<uint32_t>(sh.sel_key);
-    // prefix of the flags, 8 threads per candidate
-    int before = 0;
-    if (i < c) {
+
+    // which candidates are kept, and the k-th key (block-uniform branches)
+    if (c <= kRegRank) {
+      // pairwise ranks by (value desc, index asc), 8 threads per candidate:
+      // rank < krem is kept, rank krem - 1 is the k-th
+      const int i = tid >> 3, sub = tid & 7;
+      int rank = 0;
+      uint32_t ki = 0;
+      if (i < c) {
+        ki = f32_to_key(sh.cval[i]);
 #pragma unroll 4
-      for (int u = sub; u < i; u += 8) before += sh.cflag[u];
-    }
-    before += __shfl_xor(before, 1);
-    before += __shfl_xor(before, 2);
-    before += __shfl_xor(before, 4);
-    if (i < c && sub == 0) sh.ctp[i] = before;
-    if (tid == 0) sh.ctp[c] = krem;
-  } else {
-    int nd = krem;
-    kth = radix_select_each(sh, nd, [&](auto f) {
-      for (int t = tid; t < c; t += kBlkThreads) f(sh.cval[t]);
-    });
-    // kept: above kth, or equal to it and among the first nd equal ones
-    int tflag[4] = {0, 0, 0, 0};  // candidates 4 tid .. 4 tid + 3
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int t = 4 * tid + j;
-      if (t < c) {
-        const uint32_t kt = f32_to_key(sh.cval[t]);
-        if (kt > kth) {
-          tflag[j] = 1;
-        } else if (kt == kth) {
-          int eq = 0;
-          for (int u = 0; u < t; ++u) eq += f32_to_key(sh.cval[u]) == kth ? 1 : 0;
-          tflag[j] = eq < nd ? 1 : 0;
+        for (int u = sub; u < c; u += 8) {
+          const uint32_t ku = f32_to_key(sh.cval[u]);
+          rank += (ku > ki || (ku == ki && u < i)) ? 1 : 0;
         }
-        sh.cflag[t] = tflag[j];
+      }
+      rank += __shfl_xor(rank, 1);
+      rank += __shfl_xor(rank, 2);
+      rank += __shfl_xor(rank, 4);
+      if (i < c && sub == 0) {
+        sh.cflag[i] = rank < krem ? 1 : 0;
+        if (rank == krem - 1) sh.sel_key = static_cast<int>(ki);
+      }
+      lds_sync();
+      kth = static_cast<uint32_t>(sh.sel_key);
+      // prefix of the flags, 8 threads per candidate
+      int before = 0;
+      if (i < c) {
+#pragma unroll 4
+        for (int u = sub; u < i; u += 8) before += sh.cflag[u];
+      }
+      before += __shfl_xor(before, 1);
+      before += __shfl_xor(before, 2);
+      before += __shfl_xor(before, 4);
+      if (i < c && sub == 0) sh.ctp[i] = before;
+      if (tid == 0) sh.ctp[c] = krem;
+    } else {
+      int nd = krem;
+      kth = radix_select_each(sh, nd, [&](auto f) {
+        for (int t = tid; t < c; t += kBlkThreads) f(sh.cval[t]);
+      });
+      // kept: above kth, or equal to it and among the first nd equal ones
+      int tflag[4] = {0, 0, 0, 0};  // candidates 4 tid .. 4 tid + 3
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int t = 4 * tid + j;
+        if (t < c) {
+          const uint32_t kt = f32_to_key(sh.cval[t]);
+          if (kt > kth) {
+            tflag[j] = 1;
+          } else if (kt == kth) {
+            int eq = 0;
+            for (int u = 0; u < t; ++u) eq += f32_to_key(sh.cval[u]) == kth ? 1 : 0;
+            tflag[j] = eq < nd ? 1 : 0;
+          }
+          sh.cflag[t] = tflag[j];
+        }
+      }
+      const int ts = tflag[0] + tflag[1] + tflag[2] + tflag[3];
+      const int tb = block_excl_scan4(ts, sh.scan);
+      if (4 * tid < c) {
+        sh.ctp[4 * tid] = tb;
+        if (4 * tid + 1 <= c) sh.ctp[4 * tid + 1] = tb + tflag[0];
+        if (4 * tid + 2 <= c) sh.ctp[4 * tid + 2] = tb + tflag[0] + tflag[1];
+        if (4 * tid + 3 <= c) sh.ctp[4 * tid + 3] = tb + tflag[0] + tflag[1] + tflag[2];
+        if (4 * tid + 4 <= c) sh.ctp[4 * tid + 4] = ts + tb;
       }
     }
-    const int ts = tflag[0] + tflag[1] + tflag[2] + tflag[3];
-    const int tb = block_excl_scan4(ts, sh.scan);
-    if (4 * tid < c) {
-      sh.ctp[4 * tid] = tb;
-      if (4 * tid + 1 <= c) sh.ctp[4 * tid + 1] = tb + tflag[0];
-      if (4 * tid + 2 <= c) sh.ctp[4 * tid + 2] = tb + tflag[0] + tflag[1];
-      if (4 * tid + 3 <= c) sh.ctp[4 * tid + 3] = tb + tflag[0] + tflag[1] + tflag[2];
-      if (4 * tid + 4 <= c) sh.ctp[4 * tid + 4] = ts + tb;
-    }
-  }
-  lds_sync();
+    lds_sync();
 
-  // the kept list, in position order, straight to the workspace: slot =
-  // nearer before + kept candidates before
-  for (int e = tid; e < TN; e += kBlkThreads) {
-    const int pos = e + sh.ctp[min(sh.ncb[e], c)];
-    if (pos < k) {
-      gidx[pos] = sh.sidx[e];
-      gval[pos] = sh.sval[e];
-    }
-  }
-  for (int t = tid; t < c; t += kBlkThreads) {
-    if (sh.cflag[t]) {
-      const int pos = sh.cnb[t] + sh.ctp[t];
+    // the kept list, in position order, straight to the workspace: slot =
+    // nearer before + kept candidates before
+    for (int e = tid; e < TN; e += kBlkThreads) {
+      const int pos = e + sh.ctp[min(sh.ncb[e], c)];
       if (pos < k) {
-        gidx[pos] = sh.cidx[t];
-        gval[pos] = sh.cval[t];
+        gidx[pos] = sh.sidx[e];
+        gval[pos] = sh.sval[e];
+      }
+    }
+    for (int t = tid; t < c; t += kBlkThreads) {
+      if (sh.cflag[t]) {
+        const int pos = sh.cnb[t] + sh.ctp[t];
+        if (pos < k) {
+          gidx[pos] = sh.cidx[t];
+          gval[pos] = sh.cval[t];
+        }
       }
     }
   }
@@ -824,10 +812,15 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_reg_kernel(FusedS
     p.pstar_out[r] = expf(key_to_f32(kth) - M) / S;
   }
 
-  // softmax . V over the entries: weight exp(x - M) (0 for a candidate not kept)
+  // softmax . V over the entries: weight exp(x - M) (the row max is always
+  // kept; 0 for a candidate not kept)
+  const int nE = nl + c;
+  const int G = tid >> 4;
+  const char* vb = vbase + static_cast<int64_t>(tid & 15) * PV::BYTES;
+  auto entry_pos = [&](int e) { return e < nl ? sh.sidx[e] : sh.cidx[e - nl]; };
   auto weight = [&](int e) {
-    if (e < TN) return __expf(sh.sval[e] - M);
-    return sh.cflag[e - TN] ? __expf(sh.cval[e - TN] - M) : 0.f;
+    if (e < nl) return __expf(sh.sval[e] - M);
+    return sh.cflag[e - nl] ? __expf(sh.cval[e - nl] - M) : 0.f;
   };
   PV pv;
   pv.init();
