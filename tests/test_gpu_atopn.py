@@ -320,6 +320,8 @@ K2_SHAPES = dict(K2_BASE_SHAPES, **{  # + long slice lists; lists past one LDS b
     "b1_70k": (1, 12, 1, 2, 128, 70000, 256, "bf16"),
     "b2_g1": (2, 4, 4, 2, 128, 5000, 128, "bf16"),  # one query head per key head
     "b3_g2_d64": (3, 8, 4, 4, 64, 3000, 64, "f16"),
+    "b1_4k_n512": (1, 12, 1, 2, 128, 4097, 512, "bf16"),  # one block per row, its gather split over 4
+    "b2_12k_n1024": (2, 12, 1, 2, 128, 12000, 1024, "bf16"),
 })
 
 
