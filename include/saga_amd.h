@@ -215,7 +215,8 @@ int saga_atopn_decode_noalloc(const saga_tensor* query, const saga_tensor* key, 
                               const float* softmax_threshold, saga_tensor* out, saga_stream_t stream);
 
 /* Atop-N calibration step: full softmax statistics, exact top-k
- * (k = min(top_n, L), radix select; equal values: lower index first),
+ * (k = min(top_n, L), found among the positions of its distance bin below
+ * the row max, or by a radix select; equal values: lower index first),
  * stores the k-th largest probability per row into softmax_threshold_out
  * f32 [b*q_h], output = renormalised top-k . V.
  * Replaces approx_top_n_attention_amortized_cal, attention/attention.py:173-189. */
