@@ -695,21 +695,12 @@ def test_calibration_kth_logit_paths(case):
     np.testing.assert_allclose(host(table), thr, rtol=1e-4)
 
 
-@pytest.mark.parametrize("seed", range(16))
-def test_calibration_random_shapes_exact_topk(seed):
-    """The calibration step at the seeded shapes of the fast-step test: its
-    kept list is exactly the top min(N, kv_len) of the GPU's own fp32 scores
-    (equal scores taken by lowest index), in ascending position order; the
-    stored p* and the output follow from that list in float64."""
-    b, q_h, k_h, v_h, d, L, N, dt, lens, rng = _random_case(seed)
-    print(f"calibration random seed={seed} b={b} q/k/v={q_h}/{k_h}/{v_h} d={d} L={L} N={N} {dt} kv_len={lens}",
-          flush=True)
-    (q, k, v), (qd, kd, vd) = qkv(rng, b, q_h, k_h, v_h, d, L, dt, outliers=0.01 * (seed % 2))
-    kvl = None if lens is None else torch.from_numpy(lens).cuda()
+def _check_calibration_exact_topk(b, q_h, k_h, v_h, d, L, N, dt, v, out, table, lens):
+    """The calibration's kept list is exactly the top min(N, kv_len) of the
+    GPU's own fp32 scores (equal scores taken by lowest index), in ascending
+    position order; the stored p* and the output follow from that list in
+    float64."""
     nr, cap = b * q_h, min(N, L)
-    table = torch.zeros(nr, device="cuda")
-    out = host(ops.atopn_calibrate(qd, kd, vd, N, table, kv_len=kvl, out_dtype=torch.float32)).reshape(nr, d)
-    torch.cuda.synchronize()
     views = _views(b, q_h, k_h, L, d, cap, fast=False)
     x = views["scores"]
     thr = host(table)
@@ -731,3 +722,51 @@ def test_calibration_random_shapes_exact_topk(seed):
         vv = v[i, j // (q_h // v_h), top].astype(np.float64)
         ref = (w[:, None] * vv).sum(0) / w.sum()
         assert rel_l2(out[r], ref) < tol, (r, kk)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_calibration_random_shapes_exact_topk(seed):
+    """The calibration step at the seeded shapes of the fast-step test."""
+    b, q_h, k_h, v_h, d, L, N, dt, lens, rng = _random_case(seed)
+    print(f"calibration random seed={seed} b={b} q/k/v={q_h}/{k_h}/{v_h} d={d} L={L} N={N} {dt} kv_len={lens}",
+          flush=True)
+    (q, k, v), (qd, kd, vd) = qkv(rng, b, q_h, k_h, v_h, d, L, dt, outliers=0.01 * (seed % 2))
+    kvl = None if lens is None else torch.from_numpy(lens).cuda()
+    table = torch.zeros(b * q_h, device="cuda")
+    out = host(ops.atopn_calibrate(qd, kd, vd, N, table, kv_len=kvl, out_dtype=torch.float32)).reshape(b * q_h, d)
+    torch.cuda.synchronize()
+    _check_calibration_exact_topk(b, q_h, k_h, v_h, d, L, N, dt, v, out, table, lens)
+
+
+CAL_EDGE_CASES = {  # name: L, N, d, dtype, ragged kv_len, additive -inf mask
+    "regs13_first": (36865, 300, 64, "f16", True, True),     # the first row of 13 register chunks
+    "regs13_last": (53248, 1024, 128, "bf16", False, False),
+    "regs12_lds5_first": (53249, 2048, 64, "f32", True, False),
+    "regs12_lds5_last": (69632, 512, 128, "bf16", False, True),
+    "memory_rows_n2049": (60000, 2049, 64, "bf16", False, False),  # N > 2048 past 53248: rows re-read from memory
+    "memory_rows_l69633": (69633, 256, 64, "f16", True, False),
+}
+
+
+@pytest.mark.parametrize("name", list(CAL_EDGE_CASES))
+def test_calibration_row_class_edges(name):
+    """The calibration kernels at the edges of their row classes (all in
+    registers up to 13 chunks of 4096 positions; 12 in registers + 5 in LDS
+    up to 17 with N <= 2048; beyond, the row re-read from memory), with
+    ragged kv_len and -inf masked positions inside the resident rows."""
+    L, N, d, dt, ragged, masked = CAL_EDGE_CASES[name]
+    b, q_h, k_h, v_h = 2, 4, 1, 2
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    print(f"calibration row class {name}: L={L} N={N} d={d} {dt} ragged={ragged} masked={masked}", flush=True)
+    (q, k, v), (qd, kd, vd) = qkv(rng, b, q_h, k_h, v_h, d, L, dt)
+    lens = np.array([L, int(rng.integers(L // 2, L))], dtype=np.int32) if ragged else None
+    kvl = None if lens is None else torch.from_numpy(lens).cuda()
+    mask = None
+    if masked:
+        m = np.where(rng.random((b, 1, 1, L)) < 0.1, -np.inf, 0.0).astype(np.float32)
+        mask = torch.from_numpy(m).cuda()
+    table = torch.zeros(b * q_h, device="cuda")
+    out = host(ops.atopn_calibrate(qd, kd, vd, N, table, attention_mask=mask, kv_len=kvl,
+                                   out_dtype=torch.float32)).reshape(b * q_h, d)
+    torch.cuda.synchronize()
+    _check_calibration_exact_topk(b, q_h, k_h, v_h, d, L, N, dt, v, out, table, lens)
