@@ -657,6 +657,11 @@ def main():
     def build(shape, mode):
         m = SagaDecoder(shape, B, max_len, mode=mode, top_n=args.top_n, exempt_layers=exempt if mode == "atopn" else (),
                         k2_variant=args.k2_variant)
+        # the step graphs first (they hold no prompt length), then the
+        # prompt, as a server that loads the model and then takes a request:
+        # the decode steps start right after the prefill's GPU work, not
+        # after the host-side capture
+        m.capture()
         t0 = time.perf_counter()
         if args.synthetic_kv:
             m.fill_synthetic(ctx)
@@ -664,7 +669,6 @@ def main():
             m.prefill(prompt)
         torch.cuda.synchronize()
         log(f"{mode} model: prefill {time.perf_counter() - t0:.2f}s")
-        m.capture()
         return m
 
     log(f"SAGA model ({SAGA_SHAPE.n_q}Q/{SAGA_SHAPE.n_k}K/{SAGA_SHAPE.n_v}V, Atop-N)")

@@ -115,6 +115,30 @@ def test_graph_replay_equals_eager_steps(mode):
     assert int(m.pos[0]) == 504 and int(m.kv_len[0]) == 505
 
 
+@pytest.mark.parametrize("mode", ["atopn", "dense"])
+def test_graphs_captured_before_the_prompt(mode):
+    """The step graphs hold no prompt length: captured on an empty cache
+    (bench.py captures before the prefill), they replay the steps of a
+    500-token prompt and then of a 300-token one exactly as eager steps do."""
+    m = _tiny_model(mode)
+    m.capture()
+    for T, seed in ((500, 7), (300, 8)):
+        m.prefill(torch.randint(0, 1024, (T,), generator=torch.Generator().manual_seed(seed)))
+        m.reset()
+        for i in range(4):
+            m.replay(i)
+        torch.cuda.synchronize()
+        toks_graph = m.tokens.clone()
+        k_graph = m.k_cache[:, :, :, T:T + 4].clone()
+        m.reset()
+        for i in range(4):
+            m.step(calibrate=(mode == "atopn" and i == 0))
+        torch.cuda.synchronize()
+        assert torch.equal(toks_graph, m.tokens), T
+        assert torch.equal(k_graph, m.k_cache[:, :, :, T:T + 4]), T
+        assert int(m.pos[0]) == T + 4 and int(m.kv_len[0]) == T + 5
+
+
 @pytest.mark.parametrize("batch", [2, 24])
 def test_one_decode_step_vs_float64_reference(batch):
     """One dense decode step of the harness recomputed on the host in float64:
