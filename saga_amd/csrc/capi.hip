@@ -340,6 +340,8 @@ int atopn_run(bool calibrate, const saga_tensor* query, const saga_tensor* key, 
 // length a multiple of the 32-position wave step.  The split count never
 // grows with the number of units, so the workspace bound computed for
 // k_h = 1 covers every k_h.
+constexpr int64_t kDenseHeadSplitBatch = 4;  // one key head and fewer batch rows: heads split over two units
+
 void dense_plan(int64_t units, int64_t L, int64_t* nsplit, int64_t* split_len) {
   units = std::max<int64_t>(units, 1);
   L = std::max<int64_t>(L, 1);
@@ -598,6 +600,8 @@ int saga_atopn_calibrate(const saga_tensor* query, const saga_tensor* key, const
                    kK2Auto, workspace, workspace_bytes, stream);
 }
 
+// (the head split of saga_dense_decode only lowers the split count: the plan
+// for b units bounds it)
 size_t saga_dense_workspace_bytes(int64_t b, int64_t q_h, int64_t L, int64_t d) {
   if (b < 1 || q_h < 1 || L < 1 || L >= kMaxLen || d < 1 || d > 1024 || b > ((1LL << 31) - 1) / q_h) return 0;
   int64_t ns, sl;
@@ -611,8 +615,12 @@ int saga_dense_decode(const saga_tensor* query, const saga_tensor* key, const sa
   Shape s{};
   int rc;
   if ((rc = check_qk(query, key, mask, &s)) || (rc = check_v(value, &s)) || (rc = check_out(out, s))) return rc;
+  // one key head (the merged SAGA shape) at small batch: the query heads are
+  // split over two units that read the same key head (a key-head stride of
+  // 0), which doubles the blocks of a latency-bound decode
+  const int64_t hs = (s.k_h == 1 && (s.q_h / s.k_h) % 2 == 0 && s.b < kDenseHeadSplitBatch) ? 2 : 1;
   int64_t ns, sl;
-  dense_plan(s.b * s.k_h, s.L, &ns, &sl);
+  dense_plan(s.b * s.k_h * hs, s.L, &ns, &sl);
   const size_t need = static_cast<size_t>(s.b * s.q_h * ns * (2 + s.d) * 4);
   if (ns > 1 && (!workspace || workspace_bytes < need))
     return fail(SAGA_ERR_WORKSPACE, "workspace of %zu bytes, need %zu", workspace_bytes, need);
@@ -642,6 +650,11 @@ int saga_dense_decode(const saga_tensor* query, const saga_tensor* key, const sa
   p.k_h = qp.k_h;
   p.v_h = static_cast<int32_t>(s.v_h);
   p.g = qp.g;
+  if (hs > 1) {
+    p.k_h = static_cast<int32_t>(qp.k_h * hs);
+    p.g = static_cast<int32_t>(qp.g / hs);
+    p.k_sh = 0;
+  }
   p.L = qp.L;
   p.scale = scale;
   p.out = out->data;
