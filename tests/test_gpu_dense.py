@@ -19,6 +19,10 @@ SHAPES = [  # b, q_h, k_h, v_h, d, L
     (1, 8, 8, 8, 64, 40),
     (2, 12, 2, 1, 128, 300),
     (8, 12, 2, 2, 128, 33024),
+    # one key head below batch 4: the query heads split over two units that
+    # read the same key head (each half spanning two value heads; one each)
+    (1, 12, 1, 4, 64, 5000),
+    (3, 16, 1, 2, 128, 2500),
 ]
 
 
