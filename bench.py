@@ -300,10 +300,12 @@ def c1_gpu_us(reps=20):
     return round(timed_graph(lambda i: ops.atopn_decode(q, k, v, tab, N, out=out, workspace=ws), reps), 2)
 
 
-def profile_kernels(batch, ctx, shape, top_n, launches=8, outlier_keys=0.0):
+def profile_kernels(batch, ctx, shape, top_n, launches=8, outlier_keys=0.0, cal_variant=0):
     """Kernels alone at the decode shape, for hardware-counter runs: K1
-    (qk_scores) `launches` times, the whole Atop-N fast step (after one
-    calibration) `launches` times, the dense decode at the dense-GQA
+    (qk_scores) `launches` times, the Atop-N calibration step `launches`
+    times (its kernels chosen by cal_variant: 0 by shape, 1 one block per
+    row, 2 chunk kernel + row kernel), the whole Atop-N fast step
+    `launches` times, the dense decode at the dense-GQA
     comparator's heads `launches` times, then a plain 1 GiB device-to-device
     copy 3 times, whose counters (2 GiB of known traffic per dispatch) scale
     the others'.  Inputs: N(0,1) bf16 caches of ctx + 1 positions; with
@@ -325,7 +327,8 @@ def profile_kernels(batch, ctx, shape, top_n, launches=8, outlier_keys=0.0):
     for _ in range(launches):
         ops.qk_scores(q, k, kv_len=kvl, with_partials=True)
     tab = torch.zeros(batch * shape.n_q, device="cuda")
-    ops.atopn_calibrate(q, k, v, top_n, tab, kv_len=kvl)
+    for _ in range(launches):
+        ops.atopn_calibrate(q, k, v, top_n, tab, kv_len=kvl, k2_variant=cal_variant)
     ws = torch.empty(ops.atopn_workspace_bytes(batch, shape.n_q, shape.n_k, L, d, top_n), dtype=torch.uint8,
                      device="cuda")
     for _ in range(launches):
@@ -348,7 +351,7 @@ def profile_kernels(batch, ctx, shape, top_n, launches=8, outlier_keys=0.0):
     d2 = d * 2
     qo = 2 * batch * shape.n_q * d2
     print(json.dumps({
-        "launches": launches, "batch": batch, "kv_len": L, "n_q": shape.n_q, "n_k": shape.n_k, "n_v": shape.n_v,
+        "launches": launches, "calibration_variant": cal_variant, "batch": batch, "kv_len": L, "n_q": shape.n_q, "n_k": shape.n_k, "n_v": shape.n_v,
         "head_dim": d, "top_n": top_n, "outlier_keys": outlier_keys, "rows_over_buf_k": over,
         "k1_algorithmic_bytes": batch * shape.n_k * L * d2 + batch * shape.n_q * d2,
         "atopn_call_algorithmic_bytes": batch * shape.n_k * L * d2 + vrows * d2 + qo + 4 * batch * shape.n_q,
@@ -616,6 +619,9 @@ def main():
     ap.add_argument("--profile-kernels", action="store_true",
                     help="only launch K1 (qk_scores), the whole Atop-N fast step and the dense decode at the "
                          "workload shape, then a 1 GiB device copy: for hardware-counter runs")
+    ap.add_argument("--cal-variant", type=int, choices=(0, 1, 2), default=0,
+                    help="with --profile-kernels: calibration kernels, 0 by shape (default), 1 one block per row, "
+                         "2 chunk kernel + row kernel (identical lists and p*)")
     ap.add_argument("--outlier-keys", type=float, default=0.0, metavar="FRAC",
                     help="with --profile-kernels: scale this fraction of the key rows x8 (rows overflow buf_k)")
     ap.add_argument("--summarize-counters", nargs="+", metavar="DIR",
@@ -643,7 +649,8 @@ def main():
 
     B, ctx, K, W = args.batch, args.ctx, args.steps, args.warmup
     if args.profile_kernels:
-        return profile_kernels(B, ctx, SAGA_SHAPE, args.top_n, outlier_keys=args.outlier_keys)
+        return profile_kernels(B, ctx, SAGA_SHAPE, args.top_n, outlier_keys=args.outlier_keys,
+                               cal_variant=args.cal_variant)
     if args.prefill:
         return prefill_bench(ctx, SAGA_SHAPE, no_cpu=args.no_cpu)
     if args.sweep:

@@ -226,6 +226,26 @@ int saga_atopn_calibrate(const saga_tensor* query, const saga_tensor* key,
                          saga_tensor* out, void* workspace, size_t workspace_bytes,
                          saga_stream_t stream);
 
+/* saga_atopn_calibrate with its kernels chosen per call (no counterpart in
+ * the reference; every variant keeps the same list and p* and its outputs
+ * agree to fp32 rounding, so this only serves A/B measurement and tests):
+ *   SAGA_K2_AUTO       by shape, as saga_atopn_calibrate;
+ *   SAGA_K2_ROW_BLOCK  one block per (batch, head) row;
+ *   SAGA_K2_SLICE_ROW  a chunk kernel over every (row, chunk of 4096-32768
+ *                      positions) that keeps each chunk's top-k, then a row
+ *                      kernel that selects the row's top-k among those
+ *                      lists, its V gathers split over up to 4 blocks per
+ *                      row; built for top_n <= 2048, L of at least two
+ *                      chunks and at most 32768 chunk-list entries per row
+ *                      (elsewhere one block per row); the choice of
+ *                      SAGA_K2_AUTO for rows of more than 36864 positions.
+ * Another value returns SAGA_ERR_INVALID. */
+int saga_atopn_calibrate_ex(const saga_tensor* query, const saga_tensor* key,
+                            const saga_tensor* value, const saga_tensor* mask, const int32_t* kv_len,
+                            float scale, int64_t top_n, float* softmax_threshold_out,
+                            saga_tensor* out, int32_t k2_variant, void* workspace,
+                            size_t workspace_bytes, saga_stream_t stream);
+
 /* Dense decode attention (split-L, one pass over K and V).
  * Replaces full_einsum_forward, attention/attention.py:64-85, for l_q == 1. */
 size_t saga_dense_workspace_bytes(int64_t b, int64_t q_h, int64_t L, int64_t d);

@@ -66,6 +66,8 @@ _SIGS = {
                                             ctypes.c_size_t, _P]),
     "saga_atopn_decode_noalloc": (ctypes.c_int, [_T, _T, _T, _T, _P, ctypes.c_float, _I64, _P, _T, _P]),
     "saga_atopn_calibrate": (ctypes.c_int, [_T, _T, _T, _T, _P, ctypes.c_float, _I64, _P, _T, _P, ctypes.c_size_t, _P]),
+    "saga_atopn_calibrate_ex": (ctypes.c_int, [_T, _T, _T, _T, _P, ctypes.c_float, _I64, _P, _T, ctypes.c_int32, _P,
+                                               ctypes.c_size_t, _P]),
     "saga_dense_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I64]),
     "saga_dense_decode": (ctypes.c_int, [_T, _T, _T, _T, _P, ctypes.c_float, _T, _P, ctypes.c_size_t, _P]),
     "saga_rope_kv_append": (ctypes.c_int, [_T, _I64, _I64, _I64, ctypes.c_float, _P, _P, _T, _T, _T, _P]),

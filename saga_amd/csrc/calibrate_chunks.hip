@@ -1,0 +1,841 @@
+// Calibration spread over many blocks per row: the exact top-k of each
+// chunk of a score row, then the exact top-k of the row among those lists.
+//
+// Replaces torch.topk + the renormalised gather of
+// approx_top_n_attention_amortized_cal (attention/attention.py:173-189) for
+// rows of at least two chunks, where one block per row is bound by a single
+// CU's memory draw (one CU moves about 25 GB/s: 128 KB of scores and 128 KB
+// of V rows take 10 us).
+//
+// Chunk kernel, one block per (row, chunk of C positions): the k largest
+// positions of the chunk (k = min(top_n, L); ordered by value, then lowest
+// index) in position order, into the chunk's slot of k entries.  The row's
+// top-k is a subset of the union of its chunks' top-k (fewer than k
+// positions of the row precede one of its top-k in that order, so fewer
+// than k of its chunk do), and every full chunk keeps exactly k, so a row's
+// entries are one dense list in position order.
+//
+// Row kernel, G blocks per row: each block finds the row's top-k among the
+// entries (the same distance bins and candidate ranks as the one-block
+// kernel, run over the entries instead of the positions), block 0 writes the
+// kept list and p*, and block g gathers the V rows of the g-th share of the
+// kept entries; with G > 1 the last block to finish merges the shares'
+// (sum of weights, sum of weighted V) partials in block order.
+#include <algorithm>
+
+#include "kernels.h"
+#include "select.cuh"
+
+namespace saga {
+
+constexpr int kSpreadRank = 128;      // candidates ranked pairwise; more: radix select over them
+constexpr int kChunkCand = 512;       // chunk kernel: candidates of the k-th's bin held in LDS
+constexpr int kMergeCand = 1024;      // row kernel: the same
+constexpr int kMergeList = 2048;      // row kernel: kept list in LDS (k <= 2048)
+constexpr int kMergeBlocksMax = 256;  // row kernel: one block per CU
+constexpr int kSpareBins = 32;        // histogram bins past kNearBins for positions out of range (one per bank)
+constexpr uint32_t kPadBits = 0xffffffffu;  // a NaN whose order key is 0: below every other float
+
+template <int NW, int LIST, int CAND>
+struct SpreadShared {
+  static constexpr int kList = LIST;
+  float red[2 * NW];
+  int cnt[NW];      // hist_pick's per-wave totals
+  int wtot[2][NW];  // per-wave class totals (nearer, candidates)
+  int scan[NW];     // block_excl_scan4's per-wave totals
+  int hist[kNearBins + kSpareBins];
+  int sel_bin, sel_above, sel_cnt, sel_key, last;
+  int sidx[LIST];    // row kernel: the kept list (key classes) / the nearer positions (distance classes),
+  float sval[LIST];  //   their values
+  int ncb[LIST];     //   and the candidates before each nearer position
+  float cval[CAND];  // candidates in index order: value,
+  int cidx[CAND];    // position,
+  int cnb[CAND];     // nearer positions before it,
+  int ctp[CAND + 1];  // kept candidates before it (ctp[c] = all kept)
+  int cflag[CAND];    // kept?
+};
+
+// Per-thread view of a block's share of a list: wave w holds entries
+// [256 CH w, 256 CH (w + 1)), chunk q of the wave being the 256 entries from
+// 256 CH w + 256 q, lane l holding its four from 4 l.  The index order is
+// (wave, chunk, lane, element), so an entry's rank within a class is its
+// wave's offset + its chunk's offset in the wave + a wave scan.
+template <int NW, int CH>
+struct ClassScan {
+  uint32_t msk[(CH + 3) / 4];  // per chunk 8 bits: nearer | candidates << 4
+  int base[CH];                // nearer | candidates << 16 before the lane's first element of chunk q
+  int WN, WC, TN, TC;          // nearer / candidates in the lower waves; block totals
+
+  // cls(q, j, n, c) classes element j of chunk q; lim(q) = elements of chunk
+  // q inside the list.  Ends with the wave totals published (one barrier).
+  template <class SH, class CLS, class LIM>
+  __device__ __forceinline__ void run(SH& sh, CLS cls, LIM lim) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int u = 0; u < (CH + 3) / 4; ++u) msk[u] = 0u;
+    int wN = 0, wC = 0;
+#pragma unroll
+    for (int q = 0; q < CH; ++q) {
+      uint32_t mN = 0, mC = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        bool n, c;
+        cls(q, j, n, c);
+        mN |= static_cast<uint32_t>(n) << j;
+        mC |= static_cast<uint32_t>(c) << j;
+      }
+      const int lm = lim(q);
+      const uint32_t valid = lm >= 4 ? 15u : (lm > 0 ? (1u << lm) - 1u : 0u);
+      mN &= valid;
+      mC &= valid & ~mN;
+      const int cntv = __popc(mN) | (__popc(mC) << 16);  // a wave chunk holds at most 256 of a class
+      const int inc = wave_incl_scan(cntv, lane);
+      msk[q >> 2] |= (mN | (mC << 4)) << (8 * (q & 3));
+      base[q] = (wN | (wC << 16)) + inc - cntv;  // (both halves stay below 2^16: 256 CH per wave)
+      const int tot = __builtin_amdgcn_readlane(inc, kWave - 1);
+      wN += tot & 0xffff;
+      wC += tot >> 16;
+    }
+    if (lane == 0) {
+      sh.wtot[0][w] = wN;
+      sh.wtot[1][w] = wC;
+    }
+    lds_sync();
+    WN = WC = TN = TC = 0;
+#pragma unroll
+    for (int u = 0; u < NW; ++u) {
+      const int a = sh.wtot[0][u], b = sh.wtot[1][u];
+      if (u < w) {
+        WN += a;
+        WC += b;
+      }
+      TN += a;
+      TC += b;
+    }
+  }
+
+  // chunk q's masks and the nearer / candidates before the lane's first
+  // element of it
+  __device__ __forceinline__ void chunk_bases(int q, uint32_t& mN, uint32_t& mC, int& nb0, int& cb0) const {
+    const uint32_t m8 = (msk[q >> 2] >> (8 * (q & 3))) & 0xffu;
+    mN = m8 & 15u;
+    mC = m8 >> 4;
+    nb0 = WN + (base[q] & 0xffff);
+    cb0 = WC + (base[q] >> 16);
+  }
+};
+
+// Which of the c candidates sh.cval[0..c) (index order) are among the krem
+// largest by (value desc, index asc); returns the key of the krem-th.  At
+// most 64 candidates (the usual few): every wave ranks them all, lane t
+// candidate t, into the block-uniform mask km (bit t: kept), with no LDS
+// writes or barriers.  More (c <= 4 NT): sh.cflag[t], and the kept ones
+// before t in sh.ctp[t] (sh.ctp[c] = krem).  CandKept reads either form.
+template <int NT, class SH>
+__device__ __forceinline__ uint32_t rank_candidates(SH& sh, int c, int krem, uint64_t& km) {
+  constexpr int NW = NT / kWave, TPC = NT / kSpreadRank;  // threads per candidate
+  const int tid = threadIdx.x;
+  uint32_t kth;
+  km = 0ull;
+  if (c <= kWave) {
+    const int lane = tid & 63;
+    const bool in = lane < c;
+    const uint32_t ki = in ? f32_to_key(sh.cval[lane]) : 0u;
+    int rank = 0;
+    for (int u = 0; u < c; ++u) {
+      const uint32_t ku = f32_to_key(sh.cval[u]);  // (the same address in every lane)
+      rank += (ku > ki || (ku == ki && u < lane)) ? 1 : 0;
+    }
+    km = __ballot(in && rank < krem);
+    const uint64_t kb = __ballot(in && rank == krem - 1);  // exactly one lane
+    return static_cast<uint32_t>(__shfl(static_cast<int>(ki), __builtin_ctzll(kb)));
+  }
+  if (c <= kSpreadRank) {
+    const int i = tid / TPC, sub = tid % TPC;
+    int rank = 0;
+    uint32_t ki = 0;
+    if (i < c) {
+      ki = f32_to_key(sh.cval[i]);
+#pragma unroll 4
+      for (int u = sub; u < c; u += TPC) {
+        const uint32_t ku = f32_to_key(sh.cval[u]);
+        rank += (ku > ki || (ku == ki && u < i)) ? 1 : 0;
+      }
+    }
+#pragma unroll
+    for (int o = 1; o < TPC; o <<= 1) rank += __shfl_xor(rank, o);
+    if (i < c && sub == 0) {
+      sh.cflag[i] = rank < krem ? 1 : 0;
+      if (rank == krem - 1) sh.sel_key = static_cast<int>(ki);
+    }
+    lds_sync();
+    kth = static_cast<uint32_t>(sh.sel_key);
+    int before = 0;
+    if (i < c) {
+#pragma unroll 4
+      for (int u = sub; u < i; u += TPC) before += sh.cflag[u];
+    }
+#pragma unroll
+    for (int o = 1; o < TPC; o <<= 1) before += __shfl_xor(before, o);
+    if (i < c && sub == 0) sh.ctp[i] = before;
+    if (tid == 0) sh.ctp[c] = krem;
+  } else {
+    int nd = krem;
+    kth = radix_select_each<NT>(sh, nd, [&](auto f) {
+      for (int t = tid; t < c; t += NT) f(sh.cval[t]);
+    });
+    // kept: above kth, or equal to it and among the first nd equal ones
+    int tflag[4] = {0, 0, 0, 0};  // candidates 4 tid .. 4 tid + 3
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = 4 * tid + j;
+      if (t < c) {
+        const uint32_t kt = f32_to_key(sh.cval[t]);
+        if (kt > kth) {
+          tflag[j] = 1;
+        } else if (kt == kth) {
+          int eq = 0;
+          for (int u = 0; u < t; ++u) eq += f32_to_key(sh.cval[u]) == kth ? 1 : 0;
+          tflag[j] = eq < nd ? 1 : 0;
+        }
+        sh.cflag[t] = tflag[j];
+      }
+    }
+    const int ts = tflag[0] + tflag[1] + tflag[2] + tflag[3];
+    const int tb = block_excl_scan4<NW>(ts, sh.scan);
+    if (4 * tid < c) {
+      sh.ctp[4 * tid] = tb;
+      if (4 * tid + 1 <= c) sh.ctp[4 * tid + 1] = tb + tflag[0];
+      if (4 * tid + 2 <= c) sh.ctp[4 * tid + 2] = tb + tflag[0] + tflag[1];
+      if (4 * tid + 3 <= c) sh.ctp[4 * tid + 3] = tb + tflag[0] + tflag[1] + tflag[2];
+      if (4 * tid + 4 <= c) sh.ctp[4 * tid + 4] = ts + tb;
+    }
+  }
+  lds_sync();
+  return kth;
+}
+
+// Kept flags and kept-before counts of the ranked candidates, from the mask
+// (c <= 64) or from LDS.
+template <class SH>
+struct CandKept {
+  const SH& sh;
+  int c;
+  uint64_t km;
+  __device__ __forceinline__ bool kept(int t) const { return c <= kWave ? ((km >> t) & 1ull) != 0ull : sh.cflag[t] != 0; }
+  // kept candidates among the first cb (cb <= c)
+  __device__ __forceinline__ int before(int cb) const {
+    if (c <= kWave) return __popcll(cb >= kWave ? km : (km & ((1ull << cb) - 1ull)));
+    return sh.ctp[cb];
+  }
+};
+
+// Elements past the end of a block's share (the partial last chunk of a
+// row, the entries past a row's list) are set to kPadBits: its key is 0, so
+// in key order it follows every other value (and, at the highest indices,
+// every element equal to it), and as a NaN it takes no distance bin.  The
+// selection over the padded share then equals the one over the real
+// elements (which number at least k), with no range checks per element.
+template <int CH>
+__device__ __forceinline__ void pad_past(f32x4* xr, int wbase, int n) {
+#pragma unroll
+  for (int q = 0; q < CH; ++q)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (wbase + 256 * q + j >= n) xr[q][j] = __uint_as_float(kPadBits);
+}
+
+// Every element of the share into its distance bin below M; elements out of
+// the bins' range (padding, -inf, NaN) into a spare bin, so that no lane
+// branches.  sh.hist has kNearBins + kSpareBins entries.
+template <int CH, class SH>
+__device__ __forceinline__ void near_histogram(SH& sh, const f32x4* xr, float scale, float Ms) {
+  const int spare = kNearBins + (threadIdx.x & (kSpareBins - 1));
+#pragma unroll
+  for (int q = 0; q < CH; ++q) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float dd = fmaf(-xr[q][j], scale, Ms);
+      atomicAdd(&sh.hist[dd < static_cast<float>(kNearBins) ? kNearBins - 1 - static_cast<int>(dd) : spare], 1);
+    }
+  }
+}
+
+// Entries per row of the chunk lists: rows are cs apart (a multiple of 4
+// entries, for 16-byte loads).
+__device__ __forceinline__ int64_t spread_row_stride(const FusedSelParams& p) {
+  return static_cast<int64_t>(p.nslice) * p.slice_cap / 4 * 4;
+}
+
+// ---------------------------------------------------------------------------
+// Chunk kernel: NT threads hold the chunk's C = (NT / 64) * CH * 256
+// positions in registers (CH chunks of 4 per lane, one 16-byte load each).
+template <int NT, int CH>
+__global__ void __launch_bounds__(NT, CH <= 4 ? 8 : 5) atopn_cal_chunk_kernel(FusedSelParams p) {
+  constexpr int NW = NT / kWave, C = NW * CH * 256;
+  constexpr int KEEP = C / 16;  // kept per chunk at most (k <= C / 16): staged in LDS
+  __shared__ SpreadShared<NW, KEEP, kChunkCand> sh;
+  const int r = blockIdx.x, ck = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int bi = r / p.q_h;
+  int Leff = p.L;
+  if (p.kv_len) Leff = min(Leff, max(p.kv_len[bi], 0));
+  if (ck == 0 && tid == 0) p.row_cnt[r] = 0;  // the row kernel's count of finished blocks starts at zero
+  const int base = ck * C;
+  const int nv = min(Leff - base, C);  // positions of the chunk inside the row
+  if (nv <= 0) return;
+  const int64_t cs = spread_row_stride(p);
+  int32_t* oidx = p.sl_idx + r * cs + static_cast<int64_t>(ck) * p.cap;
+  float* oval = p.sl_val + r * cs + static_cast<int64_t>(ck) * p.cap;
+  const float* x = p.scores + static_cast<int64_t>(r) * p.ld + base;
+  if (nv <= p.cap) {  // (the row's last chunk) every position is kept
+    for (int e = tid; e < nv; e += NT) {
+      oidx[e] = base + e;
+      oval[e] = x[e];
+    }
+    return;
+  }
+  const int kc = p.cap;  // < nv
+
+  const int wbase = w * (CH * 256) + 4 * lane;  // chunk q: wbase + 256 q + j
+  const int lastq = (nv + 3) / 4 * 4 - 4;       // loads past nv are clamped (and never used)
+  f32x4 xr[CH];
+#pragma unroll
+  for (int q = 0; q < CH; ++q) xr[q] = *reinterpret_cast<const f32x4*>(x + min(wbase + 256 * q, lastq));
+  for (int i = tid; i < kNearBins + kSpareBins; i += NT) sh.hist[i] = 0;
+  auto each_in = [&](auto f) {
+#pragma unroll
+    for (int q = 0; q < CH; ++q)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) f(xr[q][j]);
+  };
+  auto all4 = [](int) { return 4; };
+
+  // a NaN among the chunk's positions (before the row's last chunk is padded)
+  bool odd = false;
+  if (nv < C) {  // (block-uniform)
+#pragma unroll
+    for (int q = 0; q < CH; ++q)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) odd = odd || (wbase + 256 * q + j < nv && xr[q][j] != xr[q][j]);
+    pad_past<CH>(xr, wbase, nv);
+  } else {
+    each_in([&](float xi) { odd = odd || xi != xi; });
+  }
+  // the chunk's max and smallest finite value (one barrier, which also
+  // publishes the zeroed histogram)
+  float mx = kNegInf, mnl = INFINITY;
+  each_in([&](float xi) {
+    mx = fmaxf(mx, xi);  // (ignores NaN)
+    mnl = fminf(mnl, xi > kNegInf ? xi : INFINITY);
+  });
+  mx = wave_max(mx);
+  mnl = -wave_max(-mnl);
+  const int wodd = __ballot(odd) != 0ull ? 1 : 0;
+  if (lane == 0) {
+    sh.red[w] = mx;
+    sh.red[NW + w] = mnl;
+    sh.scan[w] = wodd;
+  }
+  lds_sync();
+  float M = sh.red[0], mn = sh.red[NW];
+  int anyodd = sh.scan[0];
+#pragma unroll
+  for (int u = 1; u < NW; ++u) {
+    M = fmaxf(M, sh.red[u]);
+    mn = fminf(mn, sh.red[NW + u]);
+    anyodd |= sh.scan[u];
+  }
+
+  // the k-th largest's distance bin below the chunk max (a NaN or a
+  // non-finite max: key classes)
+  bool near = !anyodd && M > kNegInf && M < INFINITY;  // block-uniform
+  const float scale = near_bin_scale(M, mn), Ms = M * scale;
+  int bin = -1, above = 0;
+  if (near) {
+    near_histogram<CH>(sh, xr, scale, Ms);  // (dd >= 0: every value <= M)
+    lds_sync();
+    int bcnt;
+    hist_pick<NT>(sh, kNearBins, kc, bin, above, bcnt);
+    near = bin >= 0 && bcnt <= kChunkCand;  // block-uniform
+  }
+  int krem = kc;
+  uint32_t kth = 0;
+  float wantf = 0.f;
+  if (near) {
+    krem = kc - above;
+    wantf = static_cast<float>(kNearBins - 1 - bin);
+  } else {
+    kth = radix_select_each<NT>(sh, krem, each_in);  // krem -> keys equal to kth that are kept
+  }
+  const int need = krem;
+
+  ClassScan<NW, CH> cs_;
+  if (near) {
+    const float wantf1 = wantf + 1.f;
+    // the distances again (the same bits); an opaque copy of the scale keeps
+    // the compiler from holding the histogram pass's ones in registers
+    float sc2 = scale;
+    asm volatile("" : "+v"(sc2));
+    cs_.run(
+        sh,
+        [&](int q, int j, bool& n, bool& c) {
+          const float dd = fmaf(-xr[q][j], sc2, Ms);
+          n = dd < wantf;
+          c = dd < wantf1;  // minus the nearer ones
+        },
+        all4);
+  } else {
+    cs_.run(
+        sh,
+        [&](int q, int j, bool& n, bool& c) {
+          const uint32_t key = f32_to_key(xr[q][j]);
+          n = key > kth;
+          c = key == kth;
+        },
+        all4);
+  }
+
+  if (near) {
+    // the candidates to LDS in index order, ranked there
+    const int c = cs_.TC;  // == the bin's count <= kChunkCand
+#pragma unroll
+    for (int q = 0; q < CH; ++q) {
+      uint32_t mN, mC;
+      int nb0, cb0;
+      cs_.chunk_bases(q, mN, mC, nb0, cb0);
+      if (mC) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t below = (1u << j) - 1u;
+          if ((mC >> j) & 1u) {
+            const int cb = cb0 + __popc(mC & below);
+            sh.cval[cb] = xr[q][j];
+            sh.cidx[cb] = base + wbase + 256 * q + j;
+            sh.cnb[cb] = nb0 + __popc(mN & below);
+          }
+        }
+      }
+    }
+    lds_sync();
+    uint64_t km;
+    rank_candidates<NT>(sh, c, krem, km);
+    const CandKept<decltype(sh)> ck_{sh, c, km};
+    // nearer positions by their owner: slot = nearer before + kept candidates before
+#pragma unroll
+    for (int q = 0; q < CH; ++q) {
+      uint32_t mN, mC;
+      int nb0, cb0;
+      cs_.chunk_bases(q, mN, mC, nb0, cb0);
+      if (mN) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t below = (1u << j) - 1u;
+          if ((mN >> j) & 1u) {
+            const int pos = nb0 + __popc(mN & below) + ck_.before(cb0 + __popc(mC & below));
+            sh.sidx[pos] = base + wbase + 256 * q + j;
+            sh.sval[pos] = xr[q][j];
+          }
+        }
+      }
+    }
+    for (int t = tid; t < c; t += NT) {
+      if (ck_.kept(t)) {
+        const int pos = sh.cnb[t] + ck_.before(t);
+        sh.sidx[pos] = sh.cidx[t];
+        sh.sval[pos] = sh.cval[t];
+      }
+    }
+  } else {
+    // key classes: above the k-th key, and the first `need` equal to it
+#pragma unroll
+    for (int q = 0; q < CH; ++q) {
+      uint32_t mN, mC;
+      int nb0, cb0;
+      cs_.chunk_bases(q, mN, mC, nb0, cb0);
+      if (mN | mC) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t below = (1u << j) - 1u;
+          const int cb = cb0 + __popc(mC & below);
+          if (((mN >> j) & 1u) || (((mC >> j) & 1u) && cb < need)) {
+            const int pos = nb0 + __popc(mN & below) + min(cb, need);
+            sh.sidx[pos] = base + wbase + 256 * q + j;
+            sh.sval[pos] = xr[q][j];
+          }
+        }
+      }
+    }
+  }
+  // the chunk's list, staged in LDS in position order, out in coalesced stores
+  lds_sync();
+  for (int i = tid; i < kc; i += NT) {
+    oidx[i] = sh.sidx[i];
+    oval[i] = sh.sval[i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Row kernel: NT threads hold up to CH * NT * 4 entries (value, position)
+// of the row's chunk lists; grid (rows, G).
+template <int DT, int D, int NT, int CH>
+__global__ void __launch_bounds__(NT) atopn_cal_merge_kernel(FusedSelParams p, PVParams v) {
+  constexpr int NW = NT / kWave, NG = NT / 16, LIST = kMergeList, CAND = kMergeCand;
+  __shared__ SpreadShared<NW, LIST, CAND> sh;
+  __shared__ float accs[NW * D];
+  const int r = blockIdx.x, g = blockIdx.y, G = gridDim.y;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int bi = r / p.q_h, h = r - bi * p.q_h;
+  int Leff = p.L;
+  if (p.kv_len) Leff = min(Leff, max(p.kv_len[bi], 0));
+  const float* prow_m = p.pmax + static_cast<int64_t>(r) * p.nparts;
+  const float* prow_s = p.psum + static_cast<int64_t>(r) * p.nparts;
+  const int nch = p.nparts;  // parts past kv_len hold (-inf, 0)
+  const int C = p.cal_chunk;
+  const int T = Leff / C * p.cap + min(p.cap, Leff % C);  // entries of the row's chunk lists
+  const int64_t cs = spread_row_stride(p);
+  const float* ev = p.sl_val + r * cs;
+  const int32_t* ei = p.sl_idx + r * cs;
+
+  // K1's partials first, then the entries: their loads stay in flight
+  // through the max / sum reductions
+  const float pm0 = tid < nch ? prow_m[tid] : kNegInf;
+  const float ps0 = tid < nch ? prow_s[tid] : 0.f;
+  const int wbase = w * (CH * 256) + 4 * lane;
+  const int lastq = max(0, (T + 3) / 4 * 4 - 4);
+  f32x4 xr[CH];
+  i32x4 ir[CH];
+#pragma unroll
+  for (int q = 0; q < CH; ++q) {
+    const int o = min(wbase + 256 * q, lastq);
+    xr[q] = *reinterpret_cast<const f32x4*>(ev + o);
+    ir[q] = *reinterpret_cast<const i32x4*>(ei + o);
+  }
+  for (int i = tid; i < kNearBins + kSpareBins; i += NT) sh.hist[i] = 0;
+  float mloc = pm0;
+  for (int c = tid + NT; c < nch; c += NT) mloc = fmaxf(mloc, prow_m[c]);
+  const float M = block_max<NW>(mloc, sh.red);  // (its barriers also publish the zeroed histogram)
+  float sloc = pm0 != kNegInf ? ps0 * __expf(pm0 - M) : 0.f;
+  for (int c = tid + NT; c < nch; c += NT) {
+    const float pm = prow_m[c];
+    if (pm != kNegInf) sloc += prow_s[c] * __expf(pm - M);
+  }
+  const float S = block_sum<NW>(sloc, sh.red);
+
+  const int k = min(p.cap, Leff);
+  int32_t* gidx = p.sel_idx + static_cast<int64_t>(r) * p.cap;
+  float* gval = p.sel_val + static_cast<int64_t>(r) * p.cap;
+  using PV = BlockPV<DT, D, NT>;
+  const int vh = h / (v.q_h / v.v_h);
+  const char* vbase = v.v + (bi * v.v_sb + static_cast<int64_t>(vh) * v.v_sh) * Elt<DT>::kBytes;
+  const int64_t vrow = v.v_sl * Elt<DT>::kBytes;
+  const int64_t ooff = bi * v.o_sb + static_cast<int64_t>(h) * v.o_sh;
+  if (k <= 0) {
+    if (g > 0) return;
+    if (tid == 0) {
+      p.sel_cnt[r] = 0;
+      if (p.sel_total) p.sel_total[r] = 0;
+      p.pstar_out[r] = 0.f;
+    }
+    PV pv;
+    pv.init();
+    pv.finish(accs, v.out, v.out_dt, ooff, false);  // 0 / 0: an empty row's output is NaN
+    return;
+  }
+
+  if (T < NT * 4 * CH) pad_past<CH>(xr, wbase, T);  // (block-uniform)
+  auto each_in = [&](auto f) {
+#pragma unroll
+    for (int q = 0; q < CH; ++q)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) f(xr[q][j]);
+  };
+  auto all4 = [](int) { return 4; };
+  // the smallest finite entry; a NaN entry or one above M (padding aside)
+  float mnl = INFINITY;
+  int odd = 0;
+  each_in([&](float xi) {
+    mnl = fminf(mnl, xi > kNegInf ? xi : INFINITY);
+    odd |= ((xi != xi && __float_as_uint(xi) != kPadBits) || xi > M) ? 1 : 0;
+  });
+  const float mn = -block_max<NW>(-mnl, sh.red);
+  const float scale = near_bin_scale(M, mn), Ms = M * scale;
+
+  // distance bins below the row max (a NaN, or a max that is not finite:
+  // key classes)
+  odd |= (M > kNegInf && M < INFINITY) ? 0 : 1;
+  bool near = !__syncthreads_or(odd);  // block-uniform
+  if (near) {
+    near_histogram<CH>(sh, xr, scale, Ms);
+    lds_sync();
+  }
+  int krem = k, bin = -1, above = 0;
+  if (near) {
+    int bcnt;
+    hist_pick<NT>(sh, kNearBins, k, bin, above, bcnt);
+    near = bin >= 0 && bcnt <= CAND;  // block-uniform
+  }
+  uint32_t kth = 0;
+  float wantf = 0.f;
+  if (near) {
+    krem = k - above;
+    wantf = static_cast<float>(kNearBins - 1 - bin);
+  } else {
+    krem = k;
+    kth = radix_select_each<NT>(sh, krem, each_in);
+  }
+  const int need = krem;
+
+  ClassScan<NW, CH> cs_;
+  if (near) {
+    const float wantf1 = wantf + 1.f;
+    cs_.run(
+        sh,
+        [&](int q, int j, bool& n, bool& c) {
+          const float dd = fmaf(-xr[q][j], scale, Ms);
+          n = dd < wantf;
+          c = dd < wantf1;
+        },
+        all4);
+  } else {
+    cs_.run(
+        sh,
+        [&](int q, int j, bool& n, bool& c) {
+          const uint32_t key = f32_to_key(xr[q][j]);
+          n = key > kth;
+          c = key == kth;
+        },
+        all4);
+  }
+
+  // the softmax . V entries: the first nl from sidx / sval, then c candidates
+  int nl = k, c = 0;
+  uint64_t km = 0ull;
+  if (!near) {
+#pragma unroll
+    for (int q = 0; q < CH; ++q) {
+      uint32_t mN, mC;
+      int nb0, cb0;
+      cs_.chunk_bases(q, mN, mC, nb0, cb0);
+      if (mN | mC) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t below = (1u << j) - 1u;
+          const int cb = cb0 + __popc(mC & below);
+          if (((mN >> j) & 1u) || (((mC >> j) & 1u) && cb < need)) {
+            const int pos = nb0 + __popc(mN & below) + min(cb, need);
+            sh.sidx[pos] = ir[q][j];
+            sh.sval[pos] = xr[q][j];
+          }
+        }
+      }
+    }
+    __syncthreads();
+    if (g == 0) {
+      for (int i = tid; i < k; i += NT) {  // the kept list for inspection, coalesced
+        gidx[i] = sh.sidx[i];
+        gval[i] = sh.sval[i];
+      }
+    }
+  } else {
+    c = cs_.TC;   // == the bin's count <= CAND
+    nl = cs_.TN;  // (== k - krem) nearer entries, all kept
+#pragma unroll
+    for (int q = 0; q < CH; ++q) {
+      uint32_t mN, mC;
+      int nb0, cb0;
+      cs_.chunk_bases(q, mN, mC, nb0, cb0);
+      if (mN | mC) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t below = (1u << j) - 1u;
+          const int nb = nb0 + __popc(mN & below), cb = cb0 + __popc(mC & below);
+          if ((mN >> j) & 1u) {
+            sh.sidx[nb] = ir[q][j];
+            sh.sval[nb] = xr[q][j];
+            sh.ncb[nb] = cb;
+          } else if ((mC >> j) & 1u) {
+            sh.cval[cb] = xr[q][j];
+            sh.cidx[cb] = ir[q][j];
+            sh.cnb[cb] = nb;
+          }
+        }
+      }
+    }
+    lds_sync();
+    kth = rank_candidates<NT>(sh, c, krem, km);
+    if (g == 0) {
+      const CandKept<decltype(sh)> ck_{sh, c, km};
+      // the kept list, in position order: slot = nearer before + kept candidates before
+      for (int e = tid; e < nl; e += NT) {
+        const int pos = e + ck_.before(sh.ncb[e]);
+        gidx[pos] = sh.sidx[e];
+        gval[pos] = sh.sval[e];
+      }
+      for (int t = tid; t < c; t += NT) {
+        if (ck_.kept(t)) {
+          const int pos = sh.cnb[t] + ck_.before(t);
+          gidx[pos] = sh.cidx[t];
+          gval[pos] = sh.cval[t];
+        }
+      }
+    }
+  }
+  const CandKept<decltype(sh)> ck{sh, c, km};
+  if (g == 0 && tid == 0) {
+    p.sel_cnt[r] = k;
+    if (p.sel_total) p.sel_total[r] = k;
+    p.pstar_out[r] = expf(key_to_f32(kth) - M) / S;
+  }
+
+  // this block's share of softmax . V: entries [e0, e1), weight exp(x - M)
+  // (the row max is always kept; 0 for a candidate not kept)
+  const int nE = nl + c;
+  const int e0 = static_cast<int>(static_cast<int64_t>(nE) * g / G);
+  const int e1 = static_cast<int>(static_cast<int64_t>(nE) * (g + 1) / G);
+  const int grp = tid >> 4;
+  const char* vb = vbase + static_cast<int64_t>(tid & 15) * PV::BYTES;
+  auto entry_pos = [&](int e) { return e < nl ? sh.sidx[e] : sh.cidx[e - nl]; };
+  auto weight = [&](int e) {
+    if (e < nl) return __expf(sh.sval[e] - M);
+    return ck.kept(e - nl) ? __expf(sh.cval[e - nl] - M) : 0.f;
+  };
+  PV pv;
+  pv.init();
+  pv.m = M;
+  u32x4 raw[kPVUnroll][PV::NV];
+  for (int ea = e0 + grp; ea < e1; ea += kPVUnroll * NG) {
+#pragma unroll
+    for (int u = 0; u < kPVUnroll; ++u) {
+      const int e = ea + u * NG;
+      if (e < e1) PV::load_raw(vb + static_cast<int64_t>(entry_pos(e)) * vrow, raw[u]);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // all gathers in flight before the FMAs
+#pragma unroll
+    for (int u = 0; u < kPVUnroll; ++u) {
+      const int e = ea + u * NG;
+      if (e < e1) {
+        const float wt = weight(e);
+        float f[PV::DPL];
+        PV::unpack(raw[u], f);
+#pragma unroll
+        for (int i = 0; i < PV::DPL; ++i) pv.acc[i] += wt * f[i];
+      }
+    }
+  }
+  float ls = 0.f;
+  for (int e = e0 + tid; e < e1; e += NT) ls += weight(e);
+  pv.l = block_sum<NW>(ls, sh.red);
+  if (G == 1) {
+    pv.finish(accs, v.out, v.out_dt, ooff, false);
+    return;
+  }
+  // G shares: (l, o) partials, the last block to finish adds them in block
+  // order (every share is weighted against the same max M)
+  constexpr int PW = D + 4;  // floats per partial: l, three unused, o
+  float* part = p.row_part + static_cast<int64_t>(r) * kRowSplit * PW;
+  const float og = pv.reduce(accs);  // thread i < D: dim i
+  if (tid < D) part[g * PW + 4 + tid] = og;
+  if (tid == 0) part[g * PW] = pv.l;
+  // the block's stores complete at the barrier; one agent-scope release
+  // fence (an L2 write-back) orders them before the count, and one acquire
+  // fence in the last block makes the other blocks' partials visible
+  __syncthreads();
+  if (tid == 0) {
+    __threadfence();
+    sh.last = atomicAdd(p.row_cnt + r, 1) == G - 1;
+    if (sh.last) __threadfence();
+  }
+  __syncthreads();
+  if (!sh.last) return;
+  if (tid < D) {
+    float l = 0.f, o = 0.f;
+    for (int q = 0; q < G; ++q) {
+      l += part[q * PW];
+      o += part[q * PW + 4 + tid];
+    }
+    store_from_f32(v.out, v.out_dt, ooff + tid, o / l);
+  }
+  if (tid == 0) p.row_cnt[r] = 0;  // ready for the next call
+}
+
+// ---------------------------------------------------------------------------
+// Shapes: positions per chunk C = 4096 for k <= 256, then 8192, 16384 and
+// 32768 up to k = 2048 (a chunk keeps at most 1/16 of itself); the row
+// kernel holds up to 8 * 4096 entries.
+static int spread_chunk(int64_t cap) {
+  return cap <= 256 ? 4096 : (cap <= 512 ? 8192 : (cap <= 1024 ? 16384 : 32768));
+}
+
+bool cal_spread(int64_t L, int64_t cap, int64_t nslice, int64_t slice_cap, int variant) {
+  if (variant == kK2RowBlock || cap > kMergeList || cap < 1) return false;
+  // by shape: rows past the nine-chunk register kernel (measured: 36 against
+  // 46 us at b8 x 65537, 28 against 78 at b1 x 131073; at 32769 positions
+  // one block per row is level or ahead, 25.8 against 31.2 us at b8)
+  if (variant == kK2Auto && L <= kCalSpreadAutoLen) return false;
+  const int64_t C = spread_chunk(cap);
+  if (L < 2 * C) return false;
+  const int64_t slots = (L + C - 1) / C * cap;  // chunk slots of the longest row
+  return slots <= 8 * 4096 && slots <= nslice * slice_cap / 4 * 4;
+}
+
+template <int DT, int D>
+static hipError_t launch_spread(FusedSelParams p, const PVParams& v, hipStream_t st) {
+  const int C = spread_chunk(p.cap);
+  p.cal_chunk = C;
+  const int nck = (p.L + C - 1) / C;
+  const dim3 ga(p.nrows, nck);
+  if (C == 4096)
+    hipLaunchKernelGGL((atopn_cal_chunk_kernel<256, 4>), ga, dim3(256), 0, st, p);
+  else if (C == 8192)
+    hipLaunchKernelGGL((atopn_cal_chunk_kernel<512, 4>), ga, dim3(512), 0, st, p);
+  else if (C == 16384)
+    hipLaunchKernelGGL((atopn_cal_chunk_kernel<1024, 4>), ga, dim3(1024), 0, st, p);
+  else
+    hipLaunchKernelGGL((atopn_cal_chunk_kernel<1024, 8>), ga, dim3(1024), 0, st, p);
+  // entries of the longest row: full chunks keep cap, the last min(cap, rest)
+  const int64_t tmax = static_cast<int64_t>(p.L / C) * p.cap + std::min<int64_t>(p.cap, p.L % C);
+  const int G = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(kRowSplit, kMergeBlocksMax / p.nrows)));
+  const dim3 gb(p.nrows, G);
+  // more rows than CUs: 512-thread blocks, two per CU, while their share of
+  // the entries stays in registers
+  if (static_cast<int64_t>(p.nrows) * G > kMergeBlocksMax && tmax <= 4 * 2048) {
+    const dim3 blk(512);
+    if (tmax <= 2048)
+      hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 512, 1>), gb, blk, 0, st, p, v);
+    else if (tmax <= 2 * 2048)
+      hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 512, 2>), gb, blk, 0, st, p, v);
+    else if (tmax <= 3 * 2048)
+      hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 512, 3>), gb, blk, 0, st, p, v);
+    else
+      hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 512, 4>), gb, blk, 0, st, p, v);
+    return hipGetLastError();
+  }
+  const dim3 blk(kBlkThreads);
+  if (tmax <= 4096)
+    hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 1024, 1>), gb, blk, 0, st, p, v);
+  else if (tmax <= 2 * 4096)
+    hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 1024, 2>), gb, blk, 0, st, p, v);
+  else if (tmax <= 3 * 4096)
+    hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 1024, 3>), gb, blk, 0, st, p, v);
+  else if (tmax <= 4 * 4096)
+    hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 1024, 4>), gb, blk, 0, st, p, v);
+  else if (tmax <= 6 * 4096)
+    hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 1024, 6>), gb, blk, 0, st, p, v);
+  else
+    hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 1024, 8>), gb, blk, 0, st, p, v);
+  return hipGetLastError();
+}
+
+template <int DT>
+static hipError_t launch_spread_d(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
+  return v.d == 128 ? launch_spread<DT, 128>(p, v, st) : launch_spread<DT, 64>(p, v, st);
+}
+
+hipError_t launch_calibrate_spread(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
+  if (v.v_dt == SAGA_DTYPE_BF16) return launch_spread_d<SAGA_DTYPE_BF16>(p, v, st);
+  if (v.v_dt == SAGA_DTYPE_F16) return launch_spread_d<SAGA_DTYPE_F16>(p, v, st);
+  return launch_spread_d<SAGA_DTYPE_F32>(p, v, st);
+}
+
+}  // namespace saga

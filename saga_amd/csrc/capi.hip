@@ -600,6 +600,14 @@ int saga_atopn_calibrate(const saga_tensor* query, const saga_tensor* key, const
                    kK2Auto, workspace, workspace_bytes, stream);
 }
 
+int saga_atopn_calibrate_ex(const saga_tensor* query, const saga_tensor* key, const saga_tensor* value,
+                            const saga_tensor* mask, const int32_t* kv_len, float scale, int64_t top_n,
+                            float* softmax_threshold_out, saga_tensor* out, int32_t k2_variant, void* workspace,
+                            size_t workspace_bytes, saga_stream_t stream) {
+  return atopn_run(true, query, key, value, mask, kv_len, scale, top_n, nullptr, softmax_threshold_out, out,
+                   k2_variant, workspace, workspace_bytes, stream);
+}
+
 // (the head split of saga_dense_decode only lowers the split count: the plan
 // for b units bounds it)
 size_t saga_dense_workspace_bytes(int64_t b, int64_t q_h, int64_t L, int64_t d) {

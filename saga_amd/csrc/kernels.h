@@ -105,6 +105,7 @@ struct FusedSelParams {
   int32_t* row_cnt;  // [row]
   int32_t split_min;  // rows gathering more entries than this split (set by the row kernel's launcher)
   int32_t k2_variant;  // fast step: kK2Auto / kK2RowBlock / kK2SliceRow
+  int32_t cal_chunk;   // spread calibration: positions per chunk (set by its launcher)
 };
 // calibrate: one block per row; fast step: slice kernel + per-row gather kernel
 hipError_t launch_atopn_select_pv(bool calibrate, const FusedSelParams& p, const PVParams& v, hipStream_t st);
@@ -117,6 +118,14 @@ hipError_t launch_atopn_fast(const FusedSelParams& p, const PVParams& v, hipStre
 // kernel + row kernel.  Results are identical in every variant.
 constexpr int kK2Auto = SAGA_K2_AUTO, kK2RowBlock = SAGA_K2_ROW_BLOCK, kK2SliceRow = SAGA_K2_SLICE_ROW;
 bool k2_row_block(int64_t nslice, int64_t cap, int variant);
+// Calibration spread over (row, chunk) blocks and a row kernel
+// (calibrate_chunks.hip): built for rows of at least two chunks with
+// top_n <= 2048 whose chunk lists fit the workspace's slice lists; the
+// choice of kK2Auto for rows longer than kCalSpreadAutoLen, of kK2SliceRow
+// wherever built, never of kK2RowBlock.
+constexpr int64_t kCalSpreadAutoLen = 9 * 4096;
+bool cal_spread(int64_t L, int64_t cap, int64_t nslice, int64_t slice_cap, int variant);
+hipError_t launch_calibrate_spread(const FusedSelParams& p, const PVParams& v, hipStream_t st);
 
 // API selection (threshold_topk_fast): typed rows, typed values out.
 struct ApiSelParams {

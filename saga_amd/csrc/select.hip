@@ -13,8 +13,8 @@
 // waves' total + the wave's running count + mbcnt.
 #include <type_traits>
 
-#include "block_pv.cuh"
 #include "kernels.h"
+#include "select.cuh"
 
 namespace saga {
 
@@ -38,10 +38,6 @@ __device__ __forceinline__ void scan_slots(const int* cnt, int* pre, int lane) {
   if (lane == kWave - 1) pre[kSelSlots] = incl;
 }
 
-__device__ __forceinline__ unsigned long long lanes_below(int lane) {
-  return lane == 0 ? 0ull : (~0ull >> (kWave - lane));
-}
-
 struct SelShared {
   static constexpr int kList = kListLDS;  // selection entries kept in LDS
   float red[kBlkWaves];
@@ -50,7 +46,7 @@ struct SelShared {
   int cntE[kSelSlots];
   int preE[kSelSlots + 1];
   int hist[2048];
-  int sel_bin, sel_above;
+  int sel_bin, sel_above, sel_cnt;
   int sidx[kList];
   float sval[kList];
 };
@@ -83,37 +79,6 @@ __device__ void row_pv(SH& sh, float* accs, int n, const int32_t* gidx, const fl
   pv.finish(accs, v.out, v.out_dt, bi * v.o_sb + static_cast<int64_t>(h) * v.o_sh, probs);
 }
 
-// Bin holding the krem-th largest element of sh.hist[0..nb) (bin nb - 1 holds
-// the largest) and the count in the bins above it; bin -1 if fewer than krem
-// elements are counted.  Every thread of the block calls it.
-template <class SH>
-__device__ __forceinline__ void hist_pick(SH& sh, int nb, int krem, int& bin, int& above) {
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  if (tid == 0) sh.sel_bin = -1;
-  // bins scanned from the top: thread t owns bins nb-1-2t and nb-2-2t
-  const int b0 = nb - 1 - 2 * tid, b1 = b0 - 1;
-  const int c0 = b0 >= 0 ? sh.hist[b0] : 0;
-  const int c1 = b1 >= 0 ? sh.hist[b1] : 0;
-  const int tsum = c0 + c1;
-  const int incl = wave_incl_scan(tsum, lane);
-  if (lane == kWave - 1) sh.cnt[w] = incl;
-  lds_sync();
-  int woff = 0;
-  for (int i = 0; i < w; ++i) woff += sh.cnt[i];
-  const int ex = woff + incl - tsum;
-  if (c0 > 0 && ex < krem && krem <= ex + c0) {
-    sh.sel_bin = b0;
-    sh.sel_above = ex;
-  } else if (c1 > 0 && ex + c0 < krem && krem <= ex + tsum) {
-    sh.sel_bin = b1;
-    sh.sel_above = ex + c0;
-  }
-  lds_sync();
-  bin = sh.sel_bin;
-  above = sh.sel_above;
-  lds_sync();
-}
-
 // f(x[i]) for every i < n of a score row (ld floats, 16-byte aligned, n <= ld),
 // in tiles of 16 elements per thread whose four 16-byte loads are in flight
 // together (one load per element and step would wait out a round trip each).
@@ -135,36 +100,6 @@ __device__ __forceinline__ void row_tiles(const float* x, int64_t ld, int n, F f
   }
 }
 
-// The krem-th largest of a set of keys, by a 3-pass radix select (11/11/10
-// bits of the order-preserving uint32 key) over 2048-bin LDS histograms;
-// each(f) calls f(x) for every element of the set (in the calling thread's
-// share); krem is left at the count of elements equal to it that are among
-// the krem largest.
-template <class SH, class EACH>
-__device__ __forceinline__ uint32_t radix_select_each(SH& sh, int& krem, EACH each) {
-  const int tid = threadIdx.x;
-  uint32_t prefix = 0;
-  const int shifts[3] = {21, 10, 0};
-  const int nbits[3] = {11, 11, 10};
-#pragma unroll
-  for (int pass = 0; pass < 3; ++pass) {
-    const int nb = 1 << nbits[pass];
-    const uint32_t hmask = pass == 0 ? 0u : (0xffffffffu << (shifts[pass] + nbits[pass]));
-    for (int i = tid; i < 2048; i += kBlkThreads) sh.hist[i] = 0;
-    lds_sync();
-    each([&](float xi) {
-      const uint32_t key = f32_to_key(xi);
-      if ((key & hmask) == prefix) atomicAdd(&sh.hist[(key >> shifts[pass]) & (nb - 1)], 1);
-    });
-    lds_sync();
-    int bin, above;
-    hist_pick(sh, nb, krem, bin, above);
-    prefix |= static_cast<uint32_t>(bin) << shifts[pass];
-    krem -= above;
-  }
-  return prefix;
-}
-
 // radix_select_each over the score row x (ROW) or the LDS candidates sh.sval.
 template <bool ROW, class SH>
 __device__ __forceinline__ uint32_t radix_select(SH& sh, const float* x, int64_t ld, int n, int& krem) {
@@ -176,9 +111,6 @@ __device__ __forceinline__ uint32_t radix_select(SH& sh, const float* x, int64_t
     });
   }
 }
-
-constexpr int kNearBins = 2048;      // bins of the distance below the row max
-constexpr float kNearScale = 32.0f;  // bins per unit of logit: the bins span M - 64 .. M
 
 // The krem-th largest score of the row without a radix pass over it: one
 // pass counts every position into its bin of distance (M - x) * 32 below the
@@ -218,10 +150,9 @@ template <class SH>
 __device__ __forceinline__ bool near_select(SH& sh, const float* x, int64_t ld, int Leff, float M, int& krem,
                                             uint32_t& kth) {
   const int tid = threadIdx.x;
-  int bin, above;
-  hist_pick(sh, kNearBins, krem, bin, above);
+  int bin, above, c;
+  hist_pick(sh, kNearBins, krem, bin, above, c);
   if (bin < 0) return false;
-  const int c = sh.hist[bin];
   if (c > SH::kList) return false;
   const int want = kNearBins - 1 - bin;  // distance bin of the candidates
   if (tid == 0) sh.sel_bin = 0;          // candidate count
@@ -414,7 +345,7 @@ struct RegShared {
   int wtot[2][kBlkWaves];  // per-wave class totals (nearer, candidates)
   int scan[kBlkWaves];     // per-wave totals of the taken-flag scan
   int hist[2048];
-  int sel_bin, sel_above, sel_key;
+  int sel_bin, sel_above, sel_cnt, sel_key;
   int sidx[LIST];           // the kept list (key classes) / the nearer positions (distance classes),
   float sval[LIST];         //   their values
   int ncb[LIST];            //   and the candidates before each nearer position
@@ -424,20 +355,6 @@ struct RegShared {
   int ctp[CAND + 1];        // kept candidates before it (ctp[c] = all kept)
   int cflag[CAND];          // kept?
 };
-
-// Exclusive scan over the block of four values per thread (thread t's four
-// are entries 4t..4t+3 of the sequence); returns thread t's exclusive base.
-__device__ __forceinline__ int block_excl_scan4(int tsum, int* wscan) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int incl = wave_incl_scan(tsum, lane);
-  if (lane == kWave - 1) wscan[w] = incl;
-  lds_sync();
-  int base = incl - tsum;
-#pragma unroll
-  for (int u = 0; u < kBlkWaves; ++u)
-    if (u < w) base += wscan[u];
-  return base;
-}
 
 template <int DT, int D, int CH, int LIST>
 __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_reg_kernel(FusedSelParams p, PVParams v) {
@@ -523,10 +440,7 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_reg_kernel(FusedS
     }
   };
 
-  // the bins' scale s: the largest power of two (at most 2^40) with
-  // (M - mn) * s <= 2047 for the smallest finite score mn, so that every
-  // finite position has a bin whatever the row's spread; a power of two
-  // keeps M * s exact, so the max sits at distance 0
+  // the bins' scale from the smallest finite score mn (near_bin_scale)
   float mnl = INFINITY;
 #pragma unroll
   for (int q = 0; q < CH; ++q) {
@@ -539,13 +453,7 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_reg_kernel(FusedS
     }
   }
   const float mn = -block_max<kBlkWaves>(-mnl, sh.red);
-  float scale = kNearScale;
-  const float range = M - mn;
-  if (range > 0.f && range < INFINITY) {
-    int ex;
-    frexpf(fminf(static_cast<float>(kNearBins - 1) / range, 1e30f), &ex);  // in [2^(ex-1), 2^ex)
-    scale = ldexpf(1.f, min(max(ex - 1, -100), 40));
-  }
+  const float scale = near_bin_scale(M, mn);
 
   // pass 1: distance bins (M - x) * s below the max; a NaN, or a max
   // that is not finite, sends the row to the key classes
@@ -561,8 +469,9 @@ __global__ void __launch_bounds__(kBlkThreads) atopn_calibrate_reg_kernel(FusedS
   bool near = !__syncthreads_or(odd);
   int krem = k, bin = -1, above = 0;
   if (near) {
-    hist_pick(sh, kNearBins, k, bin, above);
-    near = bin >= 0 && sh.hist[bin] <= CAND;  // block-uniform
+    int bcnt;
+    hist_pick(sh, kNearBins, k, bin, above, bcnt);
+    near = bin >= 0 && bcnt <= CAND;  // block-uniform
   }
   uint32_t kth = 0;
   float wantf = 0.f;
@@ -880,6 +789,8 @@ static hipError_t launch_calibrate_d(const FusedSelParams& p, const PVParams& v,
 
 hipError_t launch_atopn_select_pv(bool calibrate, const FusedSelParams& p, const PVParams& v, hipStream_t st) {
   if (!calibrate) return launch_atopn_fast(p, v, st);
+  // long rows: spread over (row, chunk) blocks
+  if (cal_spread(p.L, p.cap, p.nslice, p.slice_cap, p.k2_variant)) return launch_calibrate_spread(p, v, st);
   if (v.v_dt == SAGA_DTYPE_BF16) return launch_calibrate_d<SAGA_DTYPE_BF16>(p, v, st);
   if (v.v_dt == SAGA_DTYPE_F16) return launch_calibrate_d<SAGA_DTYPE_F16>(p, v, st);
   return launch_calibrate_d<SAGA_DTYPE_F32>(p, v, st);

@@ -275,10 +275,12 @@ def atopn_decode_noalloc(query, key, value, softmax_threshold, top_n, attention_
 
 
 def atopn_calibrate(query, key, value, top_n, threshold_out, attention_mask=None, scaling=None, kv_len=None,
-                    out=None, out_dtype=None, workspace=None):
+                    out=None, out_dtype=None, workspace=None, k2_variant=_lib.K2_AUTO):
     """Atop-N calibration step (attention/attention.py:173-189).
 
     threshold_out: fp32 [b*q_h], receives the k-th largest probability per row.
+    k2_variant: one block per row, or chunk kernel + row kernel (the same
+    list and p* in every variant; see saga_atopn_calibrate_ex).
     """
     dev, query, key, value, mask = _decode_prep(query, key, value, attention_mask, kv_len)
     b, q_h, _, d = query.shape
@@ -289,10 +291,10 @@ def atopn_calibrate(query, key, value, top_n, threshold_out, attention_mask=None
         out = torch.empty(b, q_h, 1, d, dtype=out_dtype or query.dtype, device=dev)
     lib = _lib.load()
     ws = _take_workspace(workspace, dev, "atopn", atopn_workspace_bytes(b, q_h, key.shape[1], L, d, top_n, True))
-    _lib.check(lib.saga_atopn_calibrate(_lib.tensor(query), _lib.tensor(key), _lib.tensor(value), _lib.tensor(mask),
-                                        _lib.ptr(_kv_len(kv_len)), _scale(query, scaling), int(top_n),
-                                        _lib.ptr(threshold_out), _lib.tensor(out), _lib.ptr(ws), ws.numel(),
-                                        _lib.stream_of(query)), "atopn_calibrate")
+    _lib.check(lib.saga_atopn_calibrate_ex(_lib.tensor(query), _lib.tensor(key), _lib.tensor(value),
+                                           _lib.tensor(mask), _lib.ptr(_kv_len(kv_len)), _scale(query, scaling),
+                                           int(top_n), _lib.ptr(threshold_out), _lib.tensor(out), int(k2_variant),
+                                           _lib.ptr(ws), ws.numel(), _lib.stream_of(query)), "atopn_calibrate")
     return out
 
 

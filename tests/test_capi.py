@@ -117,6 +117,23 @@ def test_decode_ex_checks_the_k2_variant():
     assert not hasattr(lib, "saga_set_k2_mode") and not hasattr(lib, "saga_set_fused_fast_step")
 
 
+def test_calibrate_ex_checks_the_variant():
+    """saga_atopn_calibrate_ex takes the calibration kernels per call, with
+    the same variant values and checks as saga_atopn_decode_ex."""
+    lib = _lib.load()
+    a = _good()
+
+    def call(variant, nbytes=1 << 30):
+        return lib.saga_atopn_calibrate_ex(ctypes.byref(a["q"]), ctypes.byref(a["k"]), ctypes.byref(a["v"]), None,
+                                           None, 0.125, 8, ctypes.c_void_p(0x300000), ctypes.byref(a["out"]), variant,
+                                           ctypes.c_void_p(0x200000), nbytes, None)
+
+    for bad in (-1, 3, 7):
+        assert call(bad) == -1 and "k2_variant" in _err()
+    for good in (_lib.K2_AUTO, _lib.K2_ROW_BLOCK, _lib.K2_SLICE_ROW):
+        assert call(good, nbytes=100) == -3 and "workspace" in _err()
+
+
 def test_null_descriptor_is_an_error_not_a_crash():
     lib = _lib.load()
     rc = lib.saga_atopn_decode(None, None, None, None, None, 1.0, 8, None, None, None, 0, None)

@@ -22,7 +22,7 @@ import cases
 from conftest import rel_l2, set_diff_outside_band
 from gpu_util import dev, host, qkv, round_to
 from oracle import saga_oracle as O
-from saga_amd import ops
+from saga_amd import _lib, ops
 
 pytestmark = pytest.mark.gpu
 
@@ -648,9 +648,13 @@ def test_fast_step_random_shapes_vs_oracle(seed):
             assert rel_l2(out.reshape(nr, d)[r], ref.reshape(d)) < tol, (r, cnt)
 
 
+CAL_VARIANTS = {"one_block": _lib.K2_ROW_BLOCK, "chunks": _lib.K2_SLICE_ROW}
+
+
+@pytest.mark.parametrize("variant", list(CAL_VARIANTS))
 @pytest.mark.parametrize("case", ["constant", "far_outlier", "near_constant", "gaussian", "gaussian_dup",
                                   "clustered", "clustered_dup", "long_clustered", "longest_clustered"])
-def test_calibration_kth_logit_paths(case):
+def test_calibration_kth_logit_paths(case, variant):
     """The calibration kernel finds the N-th logit among the few elements of
     its bin of distance below the max (2048 bins scaled to the row's spread:
     "near_constant" rows span ~0.01, "far_outlier" rows ~450 for head 0),
@@ -660,9 +664,13 @@ def test_calibration_kth_logit_paths(case):
     logits equal: ties taken by lowest index).  "_dup" rows repeat every key
     once, so the N-th logit is tied and the lower position must win.  Every
     path against the float64 oracle (fp32 inputs), and the kept list exactly
-    the stable top N of the GPU's scores."""
+    the stable top N of the GPU's scores.  "chunks": the same paths in the
+    chunk kernel (each chunk's top N) and in the row kernel over the chunk
+    lists (18000 positions: four full chunks of 4096 and a partial one)."""
     rng = np.random.default_rng(zlib.crc32(case.encode()))
     b, q_h, k_h, v_h, d, L, N = 2, 4, 1, 2, 64, 6000, 256
+    if variant == "chunks":
+        L = 18000
     if case == "long_clustered":
         L = 50000  # the largest all-register row class
     elif case == "longest_clustered":
@@ -681,7 +689,9 @@ def test_calibration_kth_logit_paths(case):
     if case.endswith("_dup"):
         k[:, :, L // 2:] = k[:, :, :L // 2]
     table = torch.zeros(b * q_h, device="cuda")
-    cal = host(ops.atopn_calibrate(dev(q, "f32"), dev(k, "f32"), dev(v, "f32"), N, table, out_dtype=torch.float32))
+    print(f"calibration kth path {case} {variant} L={L}", flush=True)
+    cal = host(ops.atopn_calibrate(dev(q, "f32"), dev(k, "f32"), dev(v, "f32"), N, table, out_dtype=torch.float32,
+                                   k2_variant=CAL_VARIANTS[variant]))
     torch.cuda.synchronize()
     views = _views(b, q_h, k_h, L, d, N, fast=False)
     for r in range(b * q_h):
@@ -724,16 +734,19 @@ def _check_calibration_exact_topk(b, q_h, k_h, v_h, d, L, N, dt, v, out, table, 
         assert rel_l2(out[r], ref) < tol, (r, kk)
 
 
+@pytest.mark.parametrize("variant", list(CAL_VARIANTS))
 @pytest.mark.parametrize("seed", range(16))
-def test_calibration_random_shapes_exact_topk(seed):
-    """The calibration step at the seeded shapes of the fast-step test."""
+def test_calibration_random_shapes_exact_topk(seed, variant):
+    """The calibration step at the seeded shapes of the fast-step test (the
+    chunk kernels where a row holds two chunks or more)."""
     b, q_h, k_h, v_h, d, L, N, dt, lens, rng = _random_case(seed)
-    print(f"calibration random seed={seed} b={b} q/k/v={q_h}/{k_h}/{v_h} d={d} L={L} N={N} {dt} kv_len={lens}",
-          flush=True)
+    print(f"calibration random seed={seed} {variant} b={b} q/k/v={q_h}/{k_h}/{v_h} d={d} L={L} N={N} {dt} "
+          f"kv_len={lens}", flush=True)
     (q, k, v), (qd, kd, vd) = qkv(rng, b, q_h, k_h, v_h, d, L, dt, outliers=0.01 * (seed % 2))
     kvl = None if lens is None else torch.from_numpy(lens).cuda()
     table = torch.zeros(b * q_h, device="cuda")
-    out = host(ops.atopn_calibrate(qd, kd, vd, N, table, kv_len=kvl, out_dtype=torch.float32)).reshape(b * q_h, d)
+    out = host(ops.atopn_calibrate(qd, kd, vd, N, table, kv_len=kvl, out_dtype=torch.float32,
+                                   k2_variant=CAL_VARIANTS[variant])).reshape(b * q_h, d)
     torch.cuda.synchronize()
     _check_calibration_exact_topk(b, q_h, k_h, v_h, d, L, N, dt, v, out, table, lens)
 
@@ -748,16 +761,19 @@ CAL_EDGE_CASES = {  # name: L, N, d, dtype, ragged kv_len, additive -inf mask
 }
 
 
+@pytest.mark.parametrize("variant", list(CAL_VARIANTS))
 @pytest.mark.parametrize("name", list(CAL_EDGE_CASES))
-def test_calibration_row_class_edges(name):
-    """The calibration kernels at the edges of their row classes (all in
-    registers up to 13 chunks of 4096 positions; 12 in registers + 5 in LDS
-    up to 17 with N <= 2048; beyond, the row re-read from memory), with
-    ragged kv_len and -inf masked positions inside the resident rows."""
+def test_calibration_row_class_edges(name, variant):
+    """The one-block calibration kernels at the edges of their row classes
+    (all in registers up to 13 chunks of 4096 positions; 12 in registers + 5
+    in LDS up to 17 with N <= 2048; beyond, the row re-read from memory), with
+    ragged kv_len and -inf masked positions inside the resident rows; the
+    chunk kernels on the same rows (N = 2049: one block per row)."""
     L, N, d, dt, ragged, masked = CAL_EDGE_CASES[name]
     b, q_h, k_h, v_h = 2, 4, 1, 2
     rng = np.random.default_rng(zlib.crc32(name.encode()))
-    print(f"calibration row class {name}: L={L} N={N} d={d} {dt} ragged={ragged} masked={masked}", flush=True)
+    print(f"calibration row class {name} {variant}: L={L} N={N} d={d} {dt} ragged={ragged} masked={masked}",
+          flush=True)
     (q, k, v), (qd, kd, vd) = qkv(rng, b, q_h, k_h, v_h, d, L, dt)
     lens = np.array([L, int(rng.integers(L // 2, L))], dtype=np.int32) if ragged else None
     kvl = None if lens is None else torch.from_numpy(lens).cuda()
@@ -767,6 +783,61 @@ def test_calibration_row_class_edges(name):
         mask = torch.from_numpy(m).cuda()
     table = torch.zeros(b * q_h, device="cuda")
     out = host(ops.atopn_calibrate(qd, kd, vd, N, table, attention_mask=mask, kv_len=kvl,
-                                   out_dtype=torch.float32)).reshape(b * q_h, d)
+                                   out_dtype=torch.float32, k2_variant=CAL_VARIANTS[variant])).reshape(b * q_h, d)
     torch.cuda.synchronize()
     _check_calibration_exact_topk(b, q_h, k_h, v_h, d, L, N, dt, v, out, table, lens)
+
+
+SPREAD_CASES = {  # name: b, q_h, k_h, v_h, d, L, N, dtype, kv_len, mask, keys
+    "b8_32k_n512_bf16": (8, 12, 1, 2, 128, 32769, 512, "bf16", None, False, "normal"),  # 2 blocks per row
+    "b1_20000_n1000": (1, 12, 1, 2, 128, 20000, 1000, "bf16", None, False, "normal"),   # 8192-position chunks, 4 blocks
+    "b2_40000_n2048_f16": (2, 8, 2, 4, 64, 40000, 2048, "f16", None, False, "normal"),  # 16384-position chunks
+    "ragged_masked_f32": (4, 4, 1, 2, 64, 24577, 512, "f32", [24577, 4096, 4097, 0], True, "normal"),
+    "constant_keys": (2, 4, 1, 1, 64, 20000, 300, "f32", None, False, "zero"),  # every score ties
+    "outlier_keys": (2, 6, 1, 3, 128, 30000, 700, "bf16", [30000, 17000], False, "outliers"),
+    "b4_128k_n1024": (4, 12, 1, 2, 128, 131072, 1024, "bf16", None, False, "normal"),  # 16384 entries per row
+    "b1_200k_n512": (1, 4, 1, 1, 64, 200000, 512, "bf16", None, False, "normal"),       # 25088 entries per row
+}
+
+
+@pytest.mark.parametrize("name", list(SPREAD_CASES))
+def test_chunk_calibration_matches_one_block_per_row(name):
+    """The chunk kernel + row kernel calibration against the one-block-per-row
+    kernels on the same inputs: identical kept lists, counts and stored p*
+    (bit for bit), outputs to fp32 rounding (the V sums are grouped over
+    other blocks); empty rows (kv_len 0) NaN in both.  Covers 1, 2 and 4 row
+    blocks, every chunk size, partial last chunks (kv_len one position past
+    a chunk, and a row of exactly one chunk), masked positions, all-equal
+    scores (key classes in both kernels) and outlier keys."""
+    b, q_h, k_h, v_h, d, L, N, dt, lens, masked, keys = SPREAD_CASES[name]
+    print(f"chunk calibration {name}", flush=True)
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    (q, k, v), (qd, kd, vd) = qkv(rng, b, q_h, k_h, v_h, d, L, dt, outliers=0.01 if keys == "outliers" else 0.0)
+    if keys == "zero":
+        kd.zero_()
+    kvl = None if lens is None else torch.tensor(lens, dtype=torch.int32, device="cuda")
+    mask = None
+    if masked:
+        m = np.where(rng.random((b, 1, 1, L)) < 0.1, -np.inf, 0.0).astype(np.float32)
+        mask = torch.from_numpy(m).cuda()
+    cap = min(N, L)
+    res = {}
+    for variant in ("one_block", "chunks"):
+        table = torch.zeros(b * q_h, device="cuda")
+        out = host(ops.atopn_calibrate(qd, kd, vd, N, table, attention_mask=mask, kv_len=kvl,
+                                       out_dtype=torch.float32, k2_variant=CAL_VARIANTS[variant]))
+        torch.cuda.synchronize()
+        views = _views(b, q_h, k_h, L, d, cap, fast=False)
+        res[variant] = (out.reshape(b * q_h, d), host(table), views["sel_cnt"].copy(), views["sel_idx"].copy(),
+                        views["sel_val"].copy())
+    (o1, t1, c1, i1, v1), (o2, t2, c2, i2, v2) = res["one_block"], res["chunks"]
+    np.testing.assert_array_equal(c2, c1)
+    np.testing.assert_array_equal(t2.view(np.uint32), t1.view(np.uint32))
+    for r in range(b * q_h):
+        n = int(c1[r])
+        np.testing.assert_array_equal(i2[r, :n], i1[r, :n], err_msg=f"row {r}")
+        np.testing.assert_array_equal(v2[r, :n].view(np.uint32), v1[r, :n].view(np.uint32))
+        if n == 0:
+            assert np.isnan(o1[r]).all() and np.isnan(o2[r]).all()
+        else:
+            assert rel_l2(o2[r], o1[r]) < 1e-5, (r, n)
