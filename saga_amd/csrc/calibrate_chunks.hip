@@ -268,13 +268,43 @@ __device__ __forceinline__ int64_t spread_row_stride(const FusedSelParams& p) {
 }
 
 // ---------------------------------------------------------------------------
-// Chunk kernel: NT threads hold the chunk's C = (NT / 64) * CH * 256
-// positions in registers (CH chunks of 4 per lane, one 16-byte load each).
-template <int NT, int CH>
-__global__ void __launch_bounds__(NT, CH <= 4 ? 8 : 5) atopn_cal_chunk_kernel(FusedSelParams p) {
-  constexpr int NW = NT / kWave, C = NW * CH * 256;
+// Chunk kernel: NT threads hold the chunk's C = NT * E positions in
+// registers, lane-contiguous (thread t: the E consecutive positions from
+// t * E, E / 4 16-byte loads), so a position's rank within its class is the
+// lower waves' total + the lower lanes' (one wave scan per block) + the
+// lane's own count below it.  The nearer positions are staged in LDS by
+// their rank among the nearer ones; the few kept candidates are merged in
+// when the list is written out (each output slot finds, by a binary search
+// over the kept candidates' final slots, whether it holds one).
+template <int NW, int KEEP, int CAND>
+struct ChunkShared {
+  float red[2 * NW];
+  float red2[NW];
+  int cnt[NW];   // hist_pick's per-wave totals
+  int wtot[NW];  // per-wave class totals (nearer | candidates << 16)
+  int scan[NW];  // NaN flags; block_excl_scan4's per-wave totals
+  int hist[kNearBins + kSpareBins];
+  int sel_bin, sel_above, sel_cnt, sel_key;
+  int sidx[KEEP + kWave];  // the nearer positions by rank (+ one spare slot per lane)
+  float sval[KEEP + kWave];
+  float cval[CAND];  // candidates in index order: value,
+  int cidx[CAND];    // position,
+  int cnb[CAND];     // nearer positions before it,
+  int ctp[CAND + 1];  // (more than 64 candidates: kept ones before it,
+  int cflag[CAND];    //  kept?)
+  int kf[CAND];       // kept candidates: final slot,
+  int kix[CAND];      // position,
+  float kvl[CAND];    // value
+};
+
+constexpr int chunk_waves_per_simd(int NT, int E) { return E > 16 ? 4 : (NT >= 512 ? 8 : 5); }
+
+template <int NT, int E>
+__global__ void __launch_bounds__(NT, chunk_waves_per_simd(NT, E)) atopn_cal_chunk_kernel(FusedSelParams p) {
+  constexpr int NW = NT / kWave, C = NT * E, NQ = E / 4;
   constexpr int KEEP = C / 16;  // kept per chunk at most (k <= C / 16): staged in LDS
-  __shared__ SpreadShared<NW, KEEP, kChunkCand> sh;
+  static_assert(E % 4 == 0 && E <= 32, "4 to 32 positions per lane, in 16-byte loads");
+  __shared__ ChunkShared<NW, KEEP, kChunkCand> sh;
   const int r = blockIdx.x, ck = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int bi = r / p.q_h;
@@ -297,37 +327,38 @@ __global__ void __launch_bounds__(NT, CH <= 4 ? 8 : 5) atopn_cal_chunk_kernel(Fu
   }
   const int kc = p.cap;  // < nv
 
-  const int wbase = w * (CH * 256) + 4 * lane;  // chunk q: wbase + 256 q + j
-  const int lastq = (nv + 3) / 4 * 4 - 4;       // loads past nv are clamped (and never used)
-  f32x4 xr[CH];
+  const int lp = tid * E;                   // the lane's first position in the chunk
+  const int lastq = (nv + 3) / 4 * 4 - 4;   // loads past nv are clamped (and never used)
+  f32x4 xr[NQ];
 #pragma unroll
-  for (int q = 0; q < CH; ++q) xr[q] = *reinterpret_cast<const f32x4*>(x + min(wbase + 256 * q, lastq));
+  for (int u = 0; u < NQ; ++u) xr[u] = *reinterpret_cast<const f32x4*>(x + min(lp + 4 * u, lastq));
   for (int i = tid; i < kNearBins + kSpareBins; i += NT) sh.hist[i] = 0;
   auto each_in = [&](auto f) {
 #pragma unroll
-    for (int q = 0; q < CH; ++q)
+    for (int u = 0; u < NQ; ++u)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) f(xr[q][j]);
+      for (int j = 0; j < 4; ++j) f(xr[u][j]);
   };
-  auto all4 = [](int) { return 4; };
 
-  // a NaN among the chunk's positions (before the row's last chunk is padded)
+  // a NaN among the chunk's positions, before the row's last chunk is padded
   bool odd = false;
   if (nv < C) {  // (block-uniform)
 #pragma unroll
-    for (int q = 0; q < CH; ++q)
+    for (int u = 0; u < NQ; ++u)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) odd = odd || (wbase + 256 * q + j < nv && xr[q][j] != xr[q][j]);
-    pad_past<CH>(xr, wbase, nv);
+      for (int j = 0; j < 4; ++j) {
+        odd = odd || (lp + 4 * u + j < nv && xr[u][j] != xr[u][j]);
+        if (lp + 4 * u + j >= nv) xr[u][j] = __uint_as_float(kPadBits);
+      }
   } else {
     each_in([&](float xi) { odd = odd || xi != xi; });
   }
-  // the chunk's max and smallest finite value (one barrier, which also
-  // publishes the zeroed histogram)
+  // the chunk's max and min (NaN aside; one barrier, which also publishes the
+  // zeroed histogram)
   float mx = kNegInf, mnl = INFINITY;
   each_in([&](float xi) {
-    mx = fmaxf(mx, xi);  // (ignores NaN)
-    mnl = fminf(mnl, xi > kNegInf ? xi : INFINITY);
+    mx = fmaxf(mx, xi);
+    mnl = fminf(mnl, xi);
   });
   mx = wave_max(mx);
   mnl = -wave_max(-mnl);
@@ -350,10 +381,15 @@ __global__ void __launch_bounds__(NT, CH <= 4 ? 8 : 5) atopn_cal_chunk_kernel(Fu
   // the k-th largest's distance bin below the chunk max (a NaN or a
   // non-finite max: key classes)
   bool near = !anyodd && M > kNegInf && M < INFINITY;  // block-uniform
+  if (near && !(mn > kNegInf)) {  // (block-uniform) masked positions: the smallest finite value
+    float m2 = INFINITY;
+    each_in([&](float xi) { m2 = fminf(m2, xi > kNegInf ? xi : INFINITY); });
+    mn = -block_max<NW>(-m2, sh.red2);
+  }
   const float scale = near_bin_scale(M, mn), Ms = M * scale;
   int bin = -1, above = 0;
   if (near) {
-    near_histogram<CH>(sh, xr, scale, Ms);  // (dd >= 0: every value <= M)
+    near_histogram<NQ>(sh, xr, scale, Ms);  // (dd >= 0: every value <= M)
     lds_sync();
     int bcnt;
     hist_pick<NT>(sh, kNearBins, kc, bin, above, bcnt);
@@ -370,108 +406,123 @@ __global__ void __launch_bounds__(NT, CH <= 4 ? 8 : 5) atopn_cal_chunk_kernel(Fu
   }
   const int need = krem;
 
-  ClassScan<NW, CH> cs_;
+  // classes: the lane's E-bit masks of nearer / candidate positions
+  uint32_t mN = 0u, mC = 0u;
   if (near) {
-    const float wantf1 = wantf + 1.f;
     // the distances again (the same bits); an opaque copy of the scale keeps
     // the compiler from holding the histogram pass's ones in registers
     float sc2 = scale;
     asm volatile("" : "+v"(sc2));
-    cs_.run(
-        sh,
-        [&](int q, int j, bool& n, bool& c) {
-          const float dd = fmaf(-xr[q][j], sc2, Ms);
-          n = dd < wantf;
-          c = dd < wantf1;  // minus the nearer ones
-        },
-        all4);
+    const float wantf1 = wantf + 1.f;
+#pragma unroll
+    for (int u = 0; u < NQ; ++u)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float dd = fmaf(-xr[u][j], sc2, Ms);
+        mN |= (dd < wantf ? 1u : 0u) << (4 * u + j);
+        mC |= (dd < wantf1 ? 1u : 0u) << (4 * u + j);
+      }
+    mC &= ~mN;
   } else {
-    cs_.run(
-        sh,
-        [&](int q, int j, bool& n, bool& c) {
-          const uint32_t key = f32_to_key(xr[q][j]);
-          n = key > kth;
-          c = key == kth;
-        },
-        all4);
+#pragma unroll
+    for (int u = 0; u < NQ; ++u)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t key = f32_to_key(xr[u][j]);
+        mN |= (key > kth ? 1u : 0u) << (4 * u + j);
+        mC |= (key == kth ? 1u : 0u) << (4 * u + j);
+      }
   }
+  // ranks: the lower waves' totals + the lower lanes' (one packed scan; a
+  // class of the block holds at most C = 32768 positions)
+  const int cntv = __popc(mN) | (__popc(mC) << 16);
+  const int incl = wave_incl_scan(cntv, lane);
+  if (lane == kWave - 1) sh.wtot[w] = incl;
+  lds_sync();
+  int WB = 0, TT = 0;
+#pragma unroll
+  for (int u = 0; u < NW; ++u) {
+    const int t = sh.wtot[u];
+    if (u < w) WB += t;
+    TT += t;
+  }
+  const int pre = WB + incl - cntv;
+  const int nb0 = pre & 0xffff, cb0 = pre >> 16;  // nearer / candidates before the lane's first position
 
   if (near) {
-    // the candidates to LDS in index order, ranked there
-    const int c = cs_.TC;  // == the bin's count <= kChunkCand
+    const int c = TT >> 16;  // == the bin's count <= kChunkCand
+    // the candidates (a few per chunk) to LDS in index order
+    if (__ballot(mC != 0u) != 0ull) {  // (wave-uniform)
 #pragma unroll
-    for (int q = 0; q < CH; ++q) {
-      uint32_t mN, mC;
-      int nb0, cb0;
-      cs_.chunk_bases(q, mN, mC, nb0, cb0);
-      if (mC) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t below = (1u << j) - 1u;
-          if ((mC >> j) & 1u) {
-            const int cb = cb0 + __popc(mC & below);
-            sh.cval[cb] = xr[q][j];
-            sh.cidx[cb] = base + wbase + 256 * q + j;
-            sh.cnb[cb] = nb0 + __popc(mN & below);
-          }
+      for (int i = 0; i < E; ++i) {
+        if (__ballot((mC >> i) & 1u) != 0ull && ((mC >> i) & 1u)) {
+          const uint32_t below = (1u << i) - 1u;
+          const int cb = cb0 + __popc(mC & below);
+          sh.cval[cb] = xr[i >> 2][i & 3];
+          sh.cidx[cb] = base + lp + i;
+          sh.cnb[cb] = nb0 + __popc(mN & below);
         }
       }
+    }
+    // the nearer positions by rank among the nearer ones (the lane's other
+    // positions to its spare slot)
+    int slot = nb0;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      const int n = static_cast<int>((mN >> i) & 1u);
+      const int at = n ? slot : KEEP + lane;
+      sh.sidx[at] = base + lp + i;
+      sh.sval[at] = xr[i >> 2][i & 3];
+      slot += n;
     }
     lds_sync();
     uint64_t km;
     rank_candidates<NT>(sh, c, krem, km);
     const CandKept<decltype(sh)> ck_{sh, c, km};
-    // nearer positions by their owner: slot = nearer before + kept candidates before
-#pragma unroll
-    for (int q = 0; q < CH; ++q) {
-      uint32_t mN, mC;
-      int nb0, cb0;
-      cs_.chunk_bases(q, mN, mC, nb0, cb0);
-      if (mN) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t below = (1u << j) - 1u;
-          if ((mN >> j) & 1u) {
-            const int pos = nb0 + __popc(mN & below) + ck_.before(cb0 + __popc(mC & below));
-            sh.sidx[pos] = base + wbase + 256 * q + j;
-            sh.sval[pos] = xr[q][j];
-          }
-        }
-      }
-    }
+    // the kept candidates at their final slots: nearer before + kept candidates before
     for (int t = tid; t < c; t += NT) {
       if (ck_.kept(t)) {
-        const int pos = sh.cnb[t] + ck_.before(t);
-        sh.sidx[pos] = sh.cidx[t];
-        sh.sval[pos] = sh.cval[t];
+        const int kt = ck_.before(t);
+        sh.kf[kt] = sh.cnb[t] + kt;
+        sh.kix[kt] = sh.cidx[t];
+        sh.kvl[kt] = sh.cval[t];
+      }
+    }
+    lds_sync();
+    // the chunk's list in coalesced stores: slot o holds the kept candidate
+    // whose final slot is o, else nearer position o - (kept candidates
+    // before o) (the final slots ascend)
+    for (int o = tid; o < kc; o += NT) {
+      int lo = 0, hi = krem;  // the kept candidates with final slot <= o: [0, lo)
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (sh.kf[mid] <= o) lo = mid + 1;
+        else hi = mid;
+      }
+      if (lo > 0 && sh.kf[lo - 1] == o) {
+        oidx[o] = sh.kix[lo - 1];
+        oval[o] = sh.kvl[lo - 1];
+      } else {
+        oidx[o] = sh.sidx[o - lo];
+        oval[o] = sh.sval[o - lo];
       }
     }
   } else {
     // key classes: above the k-th key, and the first `need` equal to it
 #pragma unroll
-    for (int q = 0; q < CH; ++q) {
-      uint32_t mN, mC;
-      int nb0, cb0;
-      cs_.chunk_bases(q, mN, mC, nb0, cb0);
-      if (mN | mC) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t below = (1u << j) - 1u;
-          const int cb = cb0 + __popc(mC & below);
-          if (((mN >> j) & 1u) || (((mC >> j) & 1u) && cb < need)) {
-            const int pos = nb0 + __popc(mN & below) + min(cb, need);
-            sh.sidx[pos] = base + wbase + 256 * q + j;
-            sh.sval[pos] = xr[q][j];
-          }
-        }
-      }
+    for (int i = 0; i < E; ++i) {
+      const uint32_t below = (1u << i) - 1u;
+      const int cb = cb0 + __popc(mC & below);
+      const bool kept = ((mN >> i) & 1u) || (((mC >> i) & 1u) && cb < need);
+      const int at = kept ? nb0 + __popc(mN & below) + min(cb, need) : KEEP + lane;
+      sh.sidx[at] = base + lp + i;
+      sh.sval[at] = xr[i >> 2][i & 3];
     }
-  }
-  // the chunk's list, staged in LDS in position order, out in coalesced stores
-  lds_sync();
-  for (int i = tid; i < kc; i += NT) {
-    oidx[i] = sh.sidx[i];
-    oval[i] = sh.sval[i];
+    lds_sync();
+    for (int o = tid; o < kc; o += NT) {
+      oidx[o] = sh.sidx[o];
+      oval[o] = sh.sval[o];
+    }
   }
 }
 
@@ -786,13 +837,13 @@ static hipError_t launch_spread(FusedSelParams p, const PVParams& v, hipStream_t
   const int nck = (p.L + C - 1) / C;
   const dim3 ga(p.nrows, nck);
   if (C == 4096)
-    hipLaunchKernelGGL((atopn_cal_chunk_kernel<256, 4>), ga, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((atopn_cal_chunk_kernel<256, 16>), ga, dim3(256), 0, st, p);
   else if (C == 8192)
-    hipLaunchKernelGGL((atopn_cal_chunk_kernel<512, 4>), ga, dim3(512), 0, st, p);
+    hipLaunchKernelGGL((atopn_cal_chunk_kernel<512, 16>), ga, dim3(512), 0, st, p);
   else if (C == 16384)
-    hipLaunchKernelGGL((atopn_cal_chunk_kernel<1024, 4>), ga, dim3(1024), 0, st, p);
+    hipLaunchKernelGGL((atopn_cal_chunk_kernel<1024, 16>), ga, dim3(1024), 0, st, p);
   else
-    hipLaunchKernelGGL((atopn_cal_chunk_kernel<1024, 8>), ga, dim3(1024), 0, st, p);
+    hipLaunchKernelGGL((atopn_cal_chunk_kernel<1024, 32>), ga, dim3(1024), 0, st, p);
   // entries of the longest row: full chunks keep cap, the last min(cap, rest)
   const int64_t tmax = static_cast<int64_t>(p.L / C) * p.cap + std::min<int64_t>(p.cap, p.L % C);
   const int G = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(kRowSplit, kMergeBlocksMax / p.nrows)));
