@@ -3,9 +3,9 @@
 //
 // Replaces torch.topk + the renormalised gather of
 // approx_top_n_attention_amortized_cal (attention/attention.py:173-189) for
-// rows of at least two chunks, where one block per row is bound by a single
-// CU's memory draw (one CU moves about 25 GB/s: 128 KB of scores and 128 KB
-// of V rows take 10 us).
+// rows of more than 36864 positions, where one block per row is bound by a
+// single CU's memory draw (one CU moves about 25 GB/s: 128 KB of scores and
+// 128 KB of V rows take 10 us).
 //
 // Chunk kernel, one block per (row, chunk of C positions): the k largest
 // positions of the chunk (k = min(top_n, L); ordered by value, then lowest
@@ -16,11 +16,20 @@
 // entries are one dense list in position order.
 //
 // Row kernel, G blocks per row: each block finds the row's top-k among the
-// entries (the same distance bins and candidate ranks as the one-block
-// kernel, run over the entries instead of the positions), block 0 writes the
-// kept list and p*, and block g gathers the V rows of the g-th share of the
-// kept entries; with G > 1 the last block to finish merges the shares'
-// (sum of weights, sum of weighted V) partials in block order.
+// entries (the same selection, run over the entries instead of the
+// positions), block 0 writes the kept list and p*, and block g gathers the
+// V rows of the g-th share of the kept entries; with G > 1 the last block to
+// finish merges the shares' (sum of weights, sum of weighted V) partials in
+// block order.
+//
+// The selection (block_topk): 2048 bins of the distance (M - x) * s below
+// the set's max M (s a power of two fitted to the set's spread); the bin of
+// the k-th largest splits the set into nearer entries (all kept) and that
+// bin's candidates, ranked by (value desc, position asc); a NaN, a
+// non-finite max or too many candidates (ties) take a radix select over the
+// order-preserving keys instead.  Each thread holds E consecutive entries,
+// so an entry's rank within its class is the lower waves' total + one wave
+// scan + the thread's own count below it.
 #include <algorithm>
 
 #include "kernels.h"
@@ -35,95 +44,6 @@ constexpr int kMergeList = 2048;      // row kernel: kept list in LDS (k <= 2048
 constexpr int kMergeBlocksMax = 256;  // row kernel: one block per CU
 constexpr int kSpareBins = 32;        // histogram bins past kNearBins for positions out of range (one per bank)
 constexpr uint32_t kPadBits = 0xffffffffu;  // a NaN whose order key is 0: below every other float
-
-template <int NW, int LIST, int CAND>
-struct SpreadShared {
-  static constexpr int kList = LIST;
-  float red[2 * NW];
-  int cnt[NW];      // hist_pick's per-wave totals
-  int wtot[2][NW];  // per-wave class totals (nearer, candidates)
-  int scan[NW];     // block_excl_scan4's per-wave totals
-  int hist[kNearBins + kSpareBins];
-  int sel_bin, sel_above, sel_cnt, sel_key, last;
-  int sidx[LIST];    // row kernel: the kept list (key classes) / the nearer positions (distance classes),
-  float sval[LIST];  //   their values
-  int ncb[LIST];     //   and the candidates before each nearer position
-  float cval[CAND];  // candidates in index order: value,
-  int cidx[CAND];    // position,
-  int cnb[CAND];     // nearer positions before it,
-  int ctp[CAND + 1];  // kept candidates before it (ctp[c] = all kept)
-  int cflag[CAND];    // kept?
-};
-
-// Per-thread view of a block's share of a list: wave w holds entries
-// [256 CH w, 256 CH (w + 1)), chunk q of the wave being the 256 entries from
-// 256 CH w + 256 q, lane l holding its four from 4 l.  The index order is
-// (wave, chunk, lane, element), so an entry's rank within a class is its
-// wave's offset + its chunk's offset in the wave + a wave scan.
-template <int NW, int CH>
-struct ClassScan {
-  uint32_t msk[(CH + 3) / 4];  // per chunk 8 bits: nearer | candidates << 4
-  int base[CH];                // nearer | candidates << 16 before the lane's first element of chunk q
-  int WN, WC, TN, TC;          // nearer / candidates in the lower waves; block totals
-
-  // cls(q, j, n, c) classes element j of chunk q; lim(q) = elements of chunk
-  // q inside the list.  Ends with the wave totals published (one barrier).
-  template <class SH, class CLS, class LIM>
-  __device__ __forceinline__ void run(SH& sh, CLS cls, LIM lim) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-#pragma unroll
-    for (int u = 0; u < (CH + 3) / 4; ++u) msk[u] = 0u;
-    int wN = 0, wC = 0;
-#pragma unroll
-    for (int q = 0; q < CH; ++q) {
-      uint32_t mN = 0, mC = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        bool n, c;
-        cls(q, j, n, c);
-        mN |= static_cast<uint32_t>(n) << j;
-        mC |= static_cast<uint32_t>(c) << j;
-      }
-      const int lm = lim(q);
-      const uint32_t valid = lm >= 4 ? 15u : (lm > 0 ? (1u << lm) - 1u : 0u);
-      mN &= valid;
-      mC &= valid & ~mN;
-      const int cntv = __popc(mN) | (__popc(mC) << 16);  // a wave chunk holds at most 256 of a class
-      const int inc = wave_incl_scan(cntv, lane);
-      msk[q >> 2] |= (mN | (mC << 4)) << (8 * (q & 3));
-      base[q] = (wN | (wC << 16)) + inc - cntv;  // (both halves stay below 2^16: 256 CH per wave)
-      const int tot = __builtin_amdgcn_readlane(inc, kWave - 1);
-      wN += tot & 0xffff;
-      wC += tot >> 16;
-    }
-    if (lane == 0) {
-      sh.wtot[0][w] = wN;
-      sh.wtot[1][w] = wC;
-    }
-    lds_sync();
-    WN = WC = TN = TC = 0;
-#pragma unroll
-    for (int u = 0; u < NW; ++u) {
-      const int a = sh.wtot[0][u], b = sh.wtot[1][u];
-      if (u < w) {
-        WN += a;
-        WC += b;
-      }
-      TN += a;
-      TC += b;
-    }
-  }
-
-  // chunk q's masks and the nearer / candidates before the lane's first
-  // element of it
-  __device__ __forceinline__ void chunk_bases(int q, uint32_t& mN, uint32_t& mC, int& nb0, int& cb0) const {
-    const uint32_t m8 = (msk[q >> 2] >> (8 * (q & 3))) & 0xffu;
-    mN = m8 & 15u;
-    mC = m8 >> 4;
-    nb0 = WN + (base[q] & 0xffff);
-    cb0 = WC + (base[q] >> 16);
-  }
-};
 
 // Which of the c candidates sh.cval[0..c) (index order) are among the krem
 // largest by (value desc, index asc); returns the key of the krem-th.  At
@@ -236,13 +156,13 @@ struct CandKept {
 // every element equal to it), and as a NaN it takes no distance bin.  The
 // selection over the padded share then equals the one over the real
 // elements (which number at least k), with no range checks per element.
-template <int CH>
-__device__ __forceinline__ void pad_past(f32x4* xr, int wbase, int n) {
+template <int NQ>
+__device__ __forceinline__ void pad_past(f32x4* xr, int lp, int n) {  // xr[u][j]: element lp + 4 u + j
 #pragma unroll
-  for (int q = 0; q < CH; ++q)
+  for (int u = 0; u < NQ; ++u)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      if (wbase + 256 * q + j >= n) xr[q][j] = __uint_as_float(kPadBits);
+      if (lp + 4 * u + j >= n) xr[u][j] = __uint_as_float(kPadBits);
 }
 
 // Every element of the share into its distance bin below M; elements out of
@@ -268,145 +188,73 @@ __device__ __forceinline__ int64_t spread_row_stride(const FusedSelParams& p) {
 }
 
 // ---------------------------------------------------------------------------
-// Chunk kernel: NT threads hold the chunk's C = NT * E positions in
-// registers, lane-contiguous (thread t: the E consecutive positions from
-// t * E, E / 4 16-byte loads), so a position's rank within its class is the
-// lower waves' total + the lower lanes' (one wave scan per block) + the
-// lane's own count below it.  The nearer positions are staged in LDS by
-// their rank among the nearer ones; the few kept candidates are merged in
-// when the list is written out (each output slot finds, by a binary search
-// over the kept candidates' final slots, whether it holds one).
-template <int NW, int KEEP, int CAND>
-struct ChunkShared {
+// LDS of the selection: LIST staging slots (+ one spare per lane), CAND
+// candidate slots.
+template <int NW, int LIST, int CAND>
+struct TopkShared {
+  static constexpr int kList = LIST;
   float red[2 * NW];
   float red2[NW];
-  int cnt[NW];   // hist_pick's per-wave totals
-  int wtot[NW];  // per-wave class totals (nearer | candidates << 16)
-  int scan[NW];  // NaN flags; block_excl_scan4's per-wave totals
+  int cnt[NW];     // hist_pick's per-wave totals
+  int wtot[NW];    // per-wave class totals (nearer | candidates << 16)
+  int scan[NW];    // NaN flags; block_excl_scan4's per-wave totals
   int hist[kNearBins + kSpareBins];
-  int sel_bin, sel_above, sel_cnt, sel_key;
-  int sidx[KEEP + kWave];  // the nearer positions by rank (+ one spare slot per lane)
-  float sval[KEEP + kWave];
+  int sel_bin, sel_above, sel_cnt, sel_key, last;
+  alignas(16) int sidx[LIST + kWave];    // the nearer entries' positions by rank (key classes: the kept list)
+  alignas(16) float sval[LIST + kWave];  //   and values (16-byte aligned: read back as vectors)
   float cval[CAND];  // candidates in index order: value,
   int cidx[CAND];    // position,
-  int cnb[CAND];     // nearer positions before it,
+  int cnb[CAND];     // nearer entries before it,
   int ctp[CAND + 1];  // (more than 64 candidates: kept ones before it,
   int cflag[CAND];    //  kept?)
-  int kf[CAND];       // kept candidates: final slot,
+  int kf[CAND];       // kept candidates: final slot in the list,
   int kix[CAND];      // position,
   float kvl[CAND];    // value
 };
 
-constexpr int chunk_waves_per_simd(int NT, int E) { return E > 16 ? 4 : (NT >= 512 ? 8 : 5); }
-
-template <int NT, int E>
-__global__ void __launch_bounds__(NT, chunk_waves_per_simd(NT, E)) atopn_cal_chunk_kernel(FusedSelParams p) {
-  constexpr int NW = NT / kWave, C = NT * E, NQ = E / 4;
-  constexpr int KEEP = C / 16;  // kept per chunk at most (k <= C / 16): staged in LDS
-  static_assert(E % 4 == 0 && E <= 32, "4 to 32 positions per lane, in 16-byte loads");
-  __shared__ ChunkShared<NW, KEEP, kChunkCand> sh;
-  const int r = blockIdx.x, ck = blockIdx.y;
+// The exact k largest (value desc, position asc) of a set held E per thread
+// (thread t: entries t E .. t E + E - 1 of the set, which is in position
+// order; values xr, positions pos(i) of the thread's entry i; entries past
+// the set are kPadBits), k <= the set's size <= LIST... for the nearer ones.
+// M: the set's max (every value <= M unless near is false), mn: a lower
+// bound of its finite values; near (in): M finite and no NaN.  sh.hist must
+// be zero and published.  Out, published: near mode (near true): nl nearer
+// entries in sh.sidx / sval by rank, nk kept candidates in sh.kf / kix / kvl
+// (kf ascending); key mode: the k kept entries in sh.sidx / sval in order
+// (nl = k, nk = 0).  Returns the k-th largest's key.
+template <int NT, int E, class SH, class POS>
+__device__ __forceinline__ uint32_t block_topk(SH& sh, f32x4 (&xr)[E / 4], POS pos, int k, float M, float mn,
+                                                bool& near, int& nl, int& nk) {
+  constexpr int NW = NT / kWave, NQ = E / 4, LIST = SH::kList;
+  constexpr int CAND = sizeof(sh.kf) / sizeof(int);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int bi = r / p.q_h;
-  int Leff = p.L;
-  if (p.kv_len) Leff = min(Leff, max(p.kv_len[bi], 0));
-  if (ck == 0 && tid == 0) p.row_cnt[r] = 0;  // the row kernel's count of finished blocks starts at zero
-  const int base = ck * C;
-  const int nv = min(Leff - base, C);  // positions of the chunk inside the row
-  if (nv <= 0) return;
-  const int64_t cs = spread_row_stride(p);
-  int32_t* oidx = p.sl_idx + r * cs + static_cast<int64_t>(ck) * p.cap;
-  float* oval = p.sl_val + r * cs + static_cast<int64_t>(ck) * p.cap;
-  const float* x = p.scores + static_cast<int64_t>(r) * p.ld + base;
-  if (nv <= p.cap) {  // (the row's last chunk) every position is kept
-    for (int e = tid; e < nv; e += NT) {
-      oidx[e] = base + e;
-      oval[e] = x[e];
-    }
-    return;
-  }
-  const int kc = p.cap;  // < nv
-
-  const int lp = tid * E;                   // the lane's first position in the chunk
-  const int lastq = (nv + 3) / 4 * 4 - 4;   // loads past nv are clamped (and never used)
-  f32x4 xr[NQ];
-#pragma unroll
-  for (int u = 0; u < NQ; ++u) xr[u] = *reinterpret_cast<const f32x4*>(x + min(lp + 4 * u, lastq));
-  for (int i = tid; i < kNearBins + kSpareBins; i += NT) sh.hist[i] = 0;
   auto each_in = [&](auto f) {
 #pragma unroll
     for (int u = 0; u < NQ; ++u)
 #pragma unroll
       for (int j = 0; j < 4; ++j) f(xr[u][j]);
   };
-
-  // a NaN among the chunk's positions, before the row's last chunk is padded
-  bool odd = false;
-  if (nv < C) {  // (block-uniform)
-#pragma unroll
-    for (int u = 0; u < NQ; ++u)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        odd = odd || (lp + 4 * u + j < nv && xr[u][j] != xr[u][j]);
-        if (lp + 4 * u + j >= nv) xr[u][j] = __uint_as_float(kPadBits);
-      }
-  } else {
-    each_in([&](float xi) { odd = odd || xi != xi; });
-  }
-  // the chunk's max and min (NaN aside; one barrier, which also publishes the
-  // zeroed histogram)
-  float mx = kNegInf, mnl = INFINITY;
-  each_in([&](float xi) {
-    mx = fmaxf(mx, xi);
-    mnl = fminf(mnl, xi);
-  });
-  mx = wave_max(mx);
-  mnl = -wave_max(-mnl);
-  const int wodd = __ballot(odd) != 0ull ? 1 : 0;
-  if (lane == 0) {
-    sh.red[w] = mx;
-    sh.red[NW + w] = mnl;
-    sh.scan[w] = wodd;
-  }
-  lds_sync();
-  float M = sh.red[0], mn = sh.red[NW];
-  int anyodd = sh.scan[0];
-#pragma unroll
-  for (int u = 1; u < NW; ++u) {
-    M = fmaxf(M, sh.red[u]);
-    mn = fminf(mn, sh.red[NW + u]);
-    anyodd |= sh.scan[u];
-  }
-
-  // the k-th largest's distance bin below the chunk max (a NaN or a
-  // non-finite max: key classes)
-  bool near = !anyodd && M > kNegInf && M < INFINITY;  // block-uniform
-  if (near && !(mn > kNegInf)) {  // (block-uniform) masked positions: the smallest finite value
-    float m2 = INFINITY;
-    each_in([&](float xi) { m2 = fminf(m2, xi > kNegInf ? xi : INFINITY); });
-    mn = -block_max<NW>(-m2, sh.red2);
-  }
   const float scale = near_bin_scale(M, mn), Ms = M * scale;
   int bin = -1, above = 0;
-  if (near) {
+  if (near) {  // (block-uniform)
     near_histogram<NQ>(sh, xr, scale, Ms);  // (dd >= 0: every value <= M)
     lds_sync();
     int bcnt;
-    hist_pick<NT>(sh, kNearBins, kc, bin, above, bcnt);
-    near = bin >= 0 && bcnt <= kChunkCand;  // block-uniform
+    hist_pick<NT>(sh, kNearBins, k, bin, above, bcnt);
+    near = bin >= 0 && bcnt <= CAND;  // block-uniform
   }
-  int krem = kc;
+  int krem = k;
   uint32_t kth = 0;
   float wantf = 0.f;
   if (near) {
-    krem = kc - above;
+    krem = k - above;
     wantf = static_cast<float>(kNearBins - 1 - bin);
   } else {
     kth = radix_select_each<NT>(sh, krem, each_in);  // krem -> keys equal to kth that are kept
   }
   const int need = krem;
 
-  // classes: the lane's E-bit masks of nearer / candidate positions
+  // classes: the thread's E-bit masks of nearer / candidate entries
   uint32_t mN = 0u, mC = 0u;
   if (near) {
     // the distances again (the same bits); an opaque copy of the scale keeps
@@ -434,7 +282,7 @@ __global__ void __launch_bounds__(NT, chunk_waves_per_simd(NT, E)) atopn_cal_chu
       }
   }
   // ranks: the lower waves' totals + the lower lanes' (one packed scan; a
-  // class of the block holds at most C = 32768 positions)
+  // class of the block holds at most 32768 entries)
   const int cntv = __popc(mN) | (__popc(mC) << 16);
   const int incl = wave_incl_scan(cntv, lane);
   if (lane == kWave - 1) sh.wtot[w] = incl;
@@ -447,92 +295,185 @@ __global__ void __launch_bounds__(NT, chunk_waves_per_simd(NT, E)) atopn_cal_chu
     TT += t;
   }
   const int pre = WB + incl - cntv;
-  const int nb0 = pre & 0xffff, cb0 = pre >> 16;  // nearer / candidates before the lane's first position
+  const int nb0 = pre & 0xffff, cb0 = pre >> 16;  // nearer / candidates before the thread's first entry
 
   if (near) {
-    const int c = TT >> 16;  // == the bin's count <= kChunkCand
-    // the candidates (a few per chunk) to LDS in index order
-    if (__ballot(mC != 0u) != 0ull) {  // (wave-uniform)
+    const int c = TT >> 16;  // == the bin's count <= CAND
+    nl = TT & 0xffff;        // (== k - krem)
+    nk = krem;
+    if (__ballot(mC != 0u) != 0ull) {  // (wave-uniform) the candidates to LDS in index order
 #pragma unroll
       for (int i = 0; i < E; ++i) {
         if (__ballot((mC >> i) & 1u) != 0ull && ((mC >> i) & 1u)) {
           const uint32_t below = (1u << i) - 1u;
           const int cb = cb0 + __popc(mC & below);
           sh.cval[cb] = xr[i >> 2][i & 3];
-          sh.cidx[cb] = base + lp + i;
+          sh.cidx[cb] = pos(i);
           sh.cnb[cb] = nb0 + __popc(mN & below);
         }
       }
     }
-    // the nearer positions by rank among the nearer ones (the lane's other
-    // positions to its spare slot)
-    int slot = nb0;
+    int slot = nb0;  // the nearer entries by rank (the thread's others to its lane's spare slot)
 #pragma unroll
     for (int i = 0; i < E; ++i) {
       const int n = static_cast<int>((mN >> i) & 1u);
-      const int at = n ? slot : KEEP + lane;
-      sh.sidx[at] = base + lp + i;
+      const int at = n ? slot : LIST + lane;
+      sh.sidx[at] = pos(i);
       sh.sval[at] = xr[i >> 2][i & 3];
       slot += n;
     }
     lds_sync();
     uint64_t km;
-    rank_candidates<NT>(sh, c, krem, km);
-    const CandKept<decltype(sh)> ck_{sh, c, km};
-    // the kept candidates at their final slots: nearer before + kept candidates before
-    for (int t = tid; t < c; t += NT) {
-      if (ck_.kept(t)) {
-        const int kt = ck_.before(t);
+    kth = rank_candidates<NT>(sh, c, krem, km);
+    const CandKept<SH> ck{sh, c, km};
+    for (int t = tid; t < c; t += NT) {  // the kept candidates at their final slots
+      if (ck.kept(t)) {
+        const int kt = ck.before(t);
         sh.kf[kt] = sh.cnb[t] + kt;
         sh.kix[kt] = sh.cidx[t];
         sh.kvl[kt] = sh.cval[t];
       }
     }
-    lds_sync();
-    // the chunk's list in coalesced stores: slot o holds the kept candidate
-    // whose final slot is o, else nearer position o - (kept candidates
-    // before o) (the final slots ascend)
-    for (int o = tid; o < kc; o += NT) {
-      int lo = 0, hi = krem;  // the kept candidates with final slot <= o: [0, lo)
-      while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (sh.kf[mid] <= o) lo = mid + 1;
-        else hi = mid;
-      }
-      if (lo > 0 && sh.kf[lo - 1] == o) {
-        oidx[o] = sh.kix[lo - 1];
-        oval[o] = sh.kvl[lo - 1];
-      } else {
-        oidx[o] = sh.sidx[o - lo];
-        oval[o] = sh.sval[o - lo];
-      }
-    }
   } else {
+    nl = k;
+    nk = 0;
     // key classes: above the k-th key, and the first `need` equal to it
 #pragma unroll
     for (int i = 0; i < E; ++i) {
       const uint32_t below = (1u << i) - 1u;
       const int cb = cb0 + __popc(mC & below);
       const bool kept = ((mN >> i) & 1u) || (((mC >> i) & 1u) && cb < need);
-      const int at = kept ? nb0 + __popc(mN & below) + min(cb, need) : KEEP + lane;
-      sh.sidx[at] = base + lp + i;
+      const int at = kept ? nb0 + __popc(mN & below) + min(cb, need) : LIST + lane;
+      sh.sidx[at] = pos(i);
       sh.sval[at] = xr[i >> 2][i & 3];
     }
-    lds_sync();
-    for (int o = tid; o < kc; o += NT) {
-      oidx[o] = sh.sidx[o];
-      oval[o] = sh.sval[o];
+  }
+  lds_sync();
+  return kth;
+}
+
+// The kept list of block_topk in position order, coalesced: slot o holds the
+// kept candidate whose final slot is o, else nearer entry o - (kept
+// candidates before o).
+template <int NT, class SH>
+__device__ __forceinline__ void write_list(const SH& sh, int k, int nk, int32_t* oidx, float* oval) {
+  for (int o = threadIdx.x; o < k; o += NT) {
+    int lo = 0, hi = nk;  // the kept candidates with final slot <= o: [0, lo)
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (sh.kf[mid] <= o) lo = mid + 1;
+      else hi = mid;
+    }
+    if (lo > 0 && sh.kf[lo - 1] == o) {
+      oidx[o] = sh.kix[lo - 1];
+      oval[o] = sh.kvl[lo - 1];
+    } else {
+      oidx[o] = sh.sidx[o - lo];
+      oval[o] = sh.sval[o - lo];
     }
   }
 }
 
-// ---------------------------------------------------------------------------
-// Row kernel: NT threads hold up to CH * NT * 4 entries (value, position)
-// of the row's chunk lists; grid (rows, G).
-template <int DT, int D, int NT, int CH>
+// Chunk kernel: NT threads hold the chunk's C = NT * E positions, E
+// consecutive per thread (E / 4 16-byte loads).
+constexpr int chunk_waves_per_simd(int NT, int E) { return E > 16 ? 4 : (NT >= 512 ? 8 : 5); }
+
+template <int NT, int E>
+__global__ void __launch_bounds__(NT, chunk_waves_per_simd(NT, E)) atopn_cal_chunk_kernel(FusedSelParams p) {
+  constexpr int NW = NT / kWave, C = NT * E, NQ = E / 4;
+  constexpr int KEEP = C / 16;  // kept per chunk at most (k <= C / 16)
+  static_assert(E % 4 == 0 && E <= 32, "4 to 32 positions per thread, in 16-byte loads");
+  __shared__ TopkShared<NW, KEEP, kChunkCand> sh;
+  const int r = blockIdx.x, ck = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int bi = r / p.q_h;
+  int Leff = p.L;
+  if (p.kv_len) Leff = min(Leff, max(p.kv_len[bi], 0));
+  if (ck == 0 && tid == 0) p.row_cnt[r] = 0;  // the row kernel's count of finished blocks starts at zero
+  const int base = ck * C;
+  const int nv = min(Leff - base, C);  // positions of the chunk inside the row
+  if (nv <= 0) return;
+  const int64_t cs = spread_row_stride(p);
+  int32_t* oidx = p.sl_idx + r * cs + static_cast<int64_t>(ck) * p.cap;
+  float* oval = p.sl_val + r * cs + static_cast<int64_t>(ck) * p.cap;
+  const float* x = p.scores + static_cast<int64_t>(r) * p.ld + base;
+  if (nv <= p.cap) {  // (the row's last chunk) every position is kept
+    for (int e = tid; e < nv; e += NT) {
+      oidx[e] = base + e;
+      oval[e] = x[e];
+    }
+    return;
+  }
+  const int kc = p.cap;  // < nv
+
+  const int lp = tid * E;                   // the thread's first position in the chunk
+  const int lastq = (nv + 3) / 4 * 4 - 4;   // loads past nv are clamped (and never used)
+  f32x4 xr[NQ];
+#pragma unroll
+  for (int u = 0; u < NQ; ++u) xr[u] = *reinterpret_cast<const f32x4*>(x + min(lp + 4 * u, lastq));
+  for (int i = tid; i < kNearBins + kSpareBins; i += NT) sh.hist[i] = 0;
+  auto each_in = [&](auto f) {
+#pragma unroll
+    for (int u = 0; u < NQ; ++u)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) f(xr[u][j]);
+  };
+
+  // a NaN among the chunk's positions, before the row's last chunk is padded
+  bool odd = false;
+  if (nv < C) {  // (block-uniform)
+#pragma unroll
+    for (int u = 0; u < NQ; ++u)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) odd = odd || (lp + 4 * u + j < nv && xr[u][j] != xr[u][j]);
+    pad_past<NQ>(xr, lp, nv);
+  } else {
+    each_in([&](float xi) { odd = odd || xi != xi; });
+  }
+  // the chunk's max and min (NaN aside; one barrier, which also publishes
+  // the zeroed histogram)
+  float mx = kNegInf, mnl = INFINITY;
+  each_in([&](float xi) {
+    mx = fmaxf(mx, xi);
+    mnl = fminf(mnl, xi);
+  });
+  mx = wave_max(mx);
+  mnl = -wave_max(-mnl);
+  const int wodd = __ballot(odd) != 0ull ? 1 : 0;
+  if (lane == 0) {
+    sh.red[w] = mx;
+    sh.red[NW + w] = mnl;
+    sh.scan[w] = wodd;
+  }
+  lds_sync();
+  float M = sh.red[0], mn = sh.red[NW];
+  int anyodd = sh.scan[0];
+#pragma unroll
+  for (int u = 1; u < NW; ++u) {
+    M = fmaxf(M, sh.red[u]);
+    mn = fminf(mn, sh.red[NW + u]);
+    anyodd |= sh.scan[u];
+  }
+  bool near = !anyodd && M > kNegInf && M < INFINITY;  // block-uniform
+  if (near && !(mn > kNegInf)) {  // (block-uniform) masked positions: the smallest finite value
+    float m2 = INFINITY;
+    each_in([&](float xi) { m2 = fminf(m2, xi > kNegInf ? xi : INFINITY); });
+    mn = -block_max<NW>(-m2, sh.red2);
+  }
+  int nl = 0, nk = 0;
+  block_topk<NT, E>(sh, xr, [&](int i) { return base + lp + i; }, kc, M, mn, near, nl, nk);
+  write_list<NT>(sh, kc, nk, oidx, oval);
+}
+
+// Row kernel: NT threads hold up to NT * E entries (value, position) of the
+// row's chunk lists, E consecutive per thread; grid (rows, G).  The kept
+// entries (the nearer ones by rank, then the kept candidates) are block g's
+// share of softmax . V.
+template <int DT, int D, int NT, int E>
 __global__ void __launch_bounds__(NT) atopn_cal_merge_kernel(FusedSelParams p, PVParams v) {
-  constexpr int NW = NT / kWave, NG = NT / 16, LIST = kMergeList, CAND = kMergeCand;
-  __shared__ SpreadShared<NW, LIST, CAND> sh;
+  constexpr int NW = NT / kWave, NG = NT / 16, NQ = E / 4;
+  static_assert(E % 4 == 0 && E <= 32, "4 to 32 entries per thread, in 16-byte loads");
+  __shared__ TopkShared<NW, kMergeList, kMergeCand> sh;
   __shared__ float accs[NW * D];
   const int r = blockIdx.x, g = blockIdx.y, G = gridDim.y;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -552,15 +493,15 @@ __global__ void __launch_bounds__(NT) atopn_cal_merge_kernel(FusedSelParams p, P
   // through the max / sum reductions
   const float pm0 = tid < nch ? prow_m[tid] : kNegInf;
   const float ps0 = tid < nch ? prow_s[tid] : 0.f;
-  const int wbase = w * (CH * 256) + 4 * lane;
+  const int lp = tid * E;  // the thread's first entry
   const int lastq = max(0, (T + 3) / 4 * 4 - 4);
-  f32x4 xr[CH];
-  i32x4 ir[CH];
+  f32x4 xr[NQ];
+  i32x4 ir[NQ];
 #pragma unroll
-  for (int q = 0; q < CH; ++q) {
-    const int o = min(wbase + 256 * q, lastq);
-    xr[q] = *reinterpret_cast<const f32x4*>(ev + o);
-    ir[q] = *reinterpret_cast<const i32x4*>(ei + o);
+  for (int u = 0; u < NQ; ++u) {
+    const int o = min(lp + 4 * u, lastq);
+    xr[u] = *reinterpret_cast<const f32x4*>(ev + o);
+    ir[u] = *reinterpret_cast<const i32x4*>(ei + o);
   }
   for (int i = tid; i < kNearBins + kSpareBins; i += NT) sh.hist[i] = 0;
   float mloc = pm0;
@@ -594,163 +535,61 @@ __global__ void __launch_bounds__(NT) atopn_cal_merge_kernel(FusedSelParams p, P
     return;
   }
 
-  if (T < NT * 4 * CH) pad_past<CH>(xr, wbase, T);  // (block-uniform)
-  auto each_in = [&](auto f) {
-#pragma unroll
-    for (int q = 0; q < CH; ++q)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) f(xr[q][j]);
-  };
-  auto all4 = [](int) { return 4; };
-  // the smallest finite entry; a NaN entry or one above M (padding aside)
+  if (T < NT * E) pad_past<NQ>(xr, lp, T);  // (block-uniform)
+  // the smallest entry and a NaN entry or one above M (padding aside; one barrier)
   float mnl = INFINITY;
-  int odd = 0;
-  each_in([&](float xi) {
-    mnl = fminf(mnl, xi > kNegInf ? xi : INFINITY);
-    odd |= ((xi != xi && __float_as_uint(xi) != kPadBits) || xi > M) ? 1 : 0;
-  });
-  const float mn = -block_max<NW>(-mnl, sh.red);
-  const float scale = near_bin_scale(M, mn), Ms = M * scale;
-
-  // distance bins below the row max (a NaN, or a max that is not finite:
-  // key classes)
-  odd |= (M > kNegInf && M < INFINITY) ? 0 : 1;
-  bool near = !__syncthreads_or(odd);  // block-uniform
-  if (near) {
-    near_histogram<CH>(sh, xr, scale, Ms);
-    lds_sync();
-  }
-  int krem = k, bin = -1, above = 0;
-  if (near) {
-    int bcnt;
-    hist_pick<NT>(sh, kNearBins, k, bin, above, bcnt);
-    near = bin >= 0 && bcnt <= CAND;  // block-uniform
-  }
-  uint32_t kth = 0;
-  float wantf = 0.f;
-  if (near) {
-    krem = k - above;
-    wantf = static_cast<float>(kNearBins - 1 - bin);
-  } else {
-    krem = k;
-    kth = radix_select_each<NT>(sh, krem, each_in);
-  }
-  const int need = krem;
-
-  ClassScan<NW, CH> cs_;
-  if (near) {
-    const float wantf1 = wantf + 1.f;
-    cs_.run(
-        sh,
-        [&](int q, int j, bool& n, bool& c) {
-          const float dd = fmaf(-xr[q][j], scale, Ms);
-          n = dd < wantf;
-          c = dd < wantf1;
-        },
-        all4);
-  } else {
-    cs_.run(
-        sh,
-        [&](int q, int j, bool& n, bool& c) {
-          const uint32_t key = f32_to_key(xr[q][j]);
-          n = key > kth;
-          c = key == kth;
-        },
-        all4);
-  }
-
-  // the softmax . V entries: the first nl from sidx / sval, then c candidates
-  int nl = k, c = 0;
-  uint64_t km = 0ull;
-  if (!near) {
+  bool odd = false;
 #pragma unroll
-    for (int q = 0; q < CH; ++q) {
-      uint32_t mN, mC;
-      int nb0, cb0;
-      cs_.chunk_bases(q, mN, mC, nb0, cb0);
-      if (mN | mC) {
+  for (int u = 0; u < NQ; ++u)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t below = (1u << j) - 1u;
-          const int cb = cb0 + __popc(mC & below);
-          if (((mN >> j) & 1u) || (((mC >> j) & 1u) && cb < need)) {
-            const int pos = nb0 + __popc(mN & below) + min(cb, need);
-            sh.sidx[pos] = ir[q][j];
-            sh.sval[pos] = xr[q][j];
-          }
-        }
-      }
+    for (int j = 0; j < 4; ++j) {
+      const float xi = xr[u][j];
+      mnl = fminf(mnl, xi);  // (ignores NaN)
+      odd = odd || (xi != xi && __float_as_uint(xi) != kPadBits) || xi > M;
     }
-    __syncthreads();
-    if (g == 0) {
-      for (int i = tid; i < k; i += NT) {  // the kept list for inspection, coalesced
-        gidx[i] = sh.sidx[i];
-        gval[i] = sh.sval[i];
-      }
-    }
-  } else {
-    c = cs_.TC;   // == the bin's count <= CAND
-    nl = cs_.TN;  // (== k - krem) nearer entries, all kept
+  mnl = -wave_max(-mnl);
+  const int wodd = __ballot(odd) != 0ull ? 1 : 0;
+  if (lane == 0) {
+    sh.red2[w] = mnl;
+    sh.scan[w] = wodd;
+  }
+  lds_sync();
+  float mn = sh.red2[0];
+  int anyodd = sh.scan[0];
 #pragma unroll
-    for (int q = 0; q < CH; ++q) {
-      uint32_t mN, mC;
-      int nb0, cb0;
-      cs_.chunk_bases(q, mN, mC, nb0, cb0);
-      if (mN | mC) {
+  for (int u = 1; u < NW; ++u) {
+    mn = fminf(mn, sh.red2[u]);
+    anyodd |= sh.scan[u];
+  }
+  bool near = !anyodd && M > kNegInf && M < INFINITY;  // block-uniform
+  if (near && !(mn > kNegInf)) {  // (block-uniform) masked positions: the smallest finite entry
+    float m2 = INFINITY;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t below = (1u << j) - 1u;
-          const int nb = nb0 + __popc(mN & below), cb = cb0 + __popc(mC & below);
-          if ((mN >> j) & 1u) {
-            sh.sidx[nb] = ir[q][j];
-            sh.sval[nb] = xr[q][j];
-            sh.ncb[nb] = cb;
-          } else if ((mC >> j) & 1u) {
-            sh.cval[cb] = xr[q][j];
-            sh.cidx[cb] = ir[q][j];
-            sh.cnb[cb] = nb;
-          }
-        }
-      }
-    }
-    lds_sync();
-    kth = rank_candidates<NT>(sh, c, krem, km);
-    if (g == 0) {
-      const CandKept<decltype(sh)> ck_{sh, c, km};
-      // the kept list, in position order: slot = nearer before + kept candidates before
-      for (int e = tid; e < nl; e += NT) {
-        const int pos = e + ck_.before(sh.ncb[e]);
-        gidx[pos] = sh.sidx[e];
-        gval[pos] = sh.sval[e];
-      }
-      for (int t = tid; t < c; t += NT) {
-        if (ck_.kept(t)) {
-          const int pos = sh.cnb[t] + ck_.before(t);
-          gidx[pos] = sh.cidx[t];
-          gval[pos] = sh.cval[t];
-        }
-      }
+    for (int u = 0; u < NQ; ++u)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) m2 = fminf(m2, xr[u][j] > kNegInf ? xr[u][j] : INFINITY);
+    mn = -block_max<NW>(-m2, sh.red);
+  }
+  int nl = 0, nk = 0;
+  const uint32_t kth = block_topk<NT, E>(sh, xr, [&](int i) { return ir[i >> 2][i & 3]; }, k, M, mn, near, nl, nk);
+  if (g == 0) {
+    write_list<NT>(sh, k, nk, gidx, gval);
+    if (tid == 0) {
+      p.sel_cnt[r] = k;
+      if (p.sel_total) p.sel_total[r] = k;
+      p.pstar_out[r] = expf(key_to_f32(kth) - M) / S;
     }
   }
-  const CandKept<decltype(sh)> ck{sh, c, km};
-  if (g == 0 && tid == 0) {
-    p.sel_cnt[r] = k;
-    if (p.sel_total) p.sel_total[r] = k;
-    p.pstar_out[r] = expf(key_to_f32(kth) - M) / S;
-  }
 
-  // this block's share of softmax . V: entries [e0, e1), weight exp(x - M)
-  // (the row max is always kept; 0 for a candidate not kept)
-  const int nE = nl + c;
+  // this block's share of softmax . V: kept entries [e0, e1), weight
+  // exp(x - M) (the row max is always kept)
+  const int nE = nl + nk;
   const int e0 = static_cast<int>(static_cast<int64_t>(nE) * g / G);
   const int e1 = static_cast<int>(static_cast<int64_t>(nE) * (g + 1) / G);
   const int grp = tid >> 4;
   const char* vb = vbase + static_cast<int64_t>(tid & 15) * PV::BYTES;
-  auto entry_pos = [&](int e) { return e < nl ? sh.sidx[e] : sh.cidx[e - nl]; };
-  auto weight = [&](int e) {
-    if (e < nl) return __expf(sh.sval[e] - M);
-    return ck.kept(e - nl) ? __expf(sh.cval[e - nl] - M) : 0.f;
-  };
+  auto entry_pos = [&](int e) { return e < nl ? sh.sidx[e] : sh.kix[e - nl]; };
+  auto weight = [&](int e) { return __expf((e < nl ? sh.sval[e] : sh.kvl[e - nl]) - M); };
   PV pv;
   pv.init();
   pv.m = M;
@@ -850,31 +689,31 @@ static hipError_t launch_spread(FusedSelParams p, const PVParams& v, hipStream_t
   const dim3 gb(p.nrows, G);
   // more rows than CUs: 512-thread blocks, two per CU, while their share of
   // the entries stays in registers
-  if (static_cast<int64_t>(p.nrows) * G > kMergeBlocksMax && tmax <= 4 * 2048) {
+  if (static_cast<int64_t>(p.nrows) * G > kMergeBlocksMax && tmax <= 16 * 512) {
     const dim3 blk(512);
-    if (tmax <= 2048)
-      hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 512, 1>), gb, blk, 0, st, p, v);
-    else if (tmax <= 2 * 2048)
-      hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 512, 2>), gb, blk, 0, st, p, v);
-    else if (tmax <= 3 * 2048)
-      hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 512, 3>), gb, blk, 0, st, p, v);
-    else
+    if (tmax <= 4 * 512)
       hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 512, 4>), gb, blk, 0, st, p, v);
+    else if (tmax <= 8 * 512)
+      hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 512, 8>), gb, blk, 0, st, p, v);
+    else if (tmax <= 12 * 512)
+      hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 512, 12>), gb, blk, 0, st, p, v);
+    else
+      hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 512, 16>), gb, blk, 0, st, p, v);
     return hipGetLastError();
   }
   const dim3 blk(kBlkThreads);
-  if (tmax <= 4096)
-    hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 1024, 1>), gb, blk, 0, st, p, v);
-  else if (tmax <= 2 * 4096)
-    hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 1024, 2>), gb, blk, 0, st, p, v);
-  else if (tmax <= 3 * 4096)
-    hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 1024, 3>), gb, blk, 0, st, p, v);
-  else if (tmax <= 4 * 4096)
+  if (tmax <= 4 * 1024)
     hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 1024, 4>), gb, blk, 0, st, p, v);
-  else if (tmax <= 6 * 4096)
-    hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 1024, 6>), gb, blk, 0, st, p, v);
-  else
+  else if (tmax <= 8 * 1024)
     hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 1024, 8>), gb, blk, 0, st, p, v);
+  else if (tmax <= 12 * 1024)
+    hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 1024, 12>), gb, blk, 0, st, p, v);
+  else if (tmax <= 16 * 1024)
+    hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 1024, 16>), gb, blk, 0, st, p, v);
+  else if (tmax <= 24 * 1024)
+    hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 1024, 24>), gb, blk, 0, st, p, v);
+  else
+    hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 1024, 32>), gb, blk, 0, st, p, v);
   return hipGetLastError();
 }
 
