@@ -657,12 +657,15 @@ static int spread_chunk(int64_t cap) {
   return cap <= 256 ? 4096 : (cap <= 512 ? 8192 : (cap <= 1024 ? 16384 : 32768));
 }
 
-bool cal_spread(int64_t L, int64_t cap, int64_t nslice, int64_t slice_cap, int variant) {
+bool cal_spread(int64_t L, int64_t cap, int64_t nslice, int64_t slice_cap, int variant, int64_t nrows) {
   if (variant == kK2RowBlock || cap > kMergeList || cap < 1) return false;
-  // by shape: rows past the nine-chunk register kernel (measured: 36 against
-  // 46 us at b8 x 65537, 28 against 78 at b1 x 131073; at 32769 positions
-  // one block per row is level or ahead, 25.8 against 31.2 us at b8)
-  if (variant == kK2Auto && L <= kCalSpreadAutoLen) return false;
+  // by shape: rows past the nine-chunk register kernel (measured: 33 against
+  // 47 us at b8 x 65537, 24 against 78 at b1 x 131073; at 32769 positions
+  // one block per row is ahead at b8, 26.3 against 28.0 us), and from 16384
+  // positions when the rows are few (at most 24: 21.4 against 23.3 us at
+  // b1 x 16385, 22.0 against 25.4 at b2 x 32769, level at b4)
+  if (variant == kK2Auto && L <= kCalSpreadAutoLen && !(L >= kCalSpreadFewRowsLen && nrows <= kCalSpreadFewRows))
+    return false;
   const int64_t C = spread_chunk(cap);
   if (L < 2 * C) return false;
   const int64_t slots = (L + C - 1) / C * cap;  // chunk slots of the longest row

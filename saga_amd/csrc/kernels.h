@@ -121,10 +121,13 @@ bool k2_row_block(int64_t nslice, int64_t cap, int variant);
 // Calibration spread over (row, chunk) blocks and a row kernel
 // (calibrate_chunks.hip): built for rows of at least two chunks with
 // top_n <= 2048 whose chunk lists fit the workspace's slice lists; the
-// choice of kK2Auto for rows longer than kCalSpreadAutoLen, of kK2SliceRow
-// wherever built, never of kK2RowBlock.
+// choice of kK2Auto for rows longer than kCalSpreadAutoLen, or of at least
+// kCalSpreadFewRowsLen positions when there are at most kCalSpreadFewRows
+// rows; of kK2SliceRow wherever built; never of kK2RowBlock.
 constexpr int64_t kCalSpreadAutoLen = 9 * 4096;
-bool cal_spread(int64_t L, int64_t cap, int64_t nslice, int64_t slice_cap, int variant);
+constexpr int64_t kCalSpreadFewRowsLen = 16384;
+constexpr int64_t kCalSpreadFewRows = 24;
+bool cal_spread(int64_t L, int64_t cap, int64_t nslice, int64_t slice_cap, int variant, int64_t nrows);
 hipError_t launch_calibrate_spread(const FusedSelParams& p, const PVParams& v, hipStream_t st);
 
 // API selection (threshold_topk_fast): typed rows, typed values out.

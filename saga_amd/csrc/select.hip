@@ -790,7 +790,7 @@ static hipError_t launch_calibrate_d(const FusedSelParams& p, const PVParams& v,
 hipError_t launch_atopn_select_pv(bool calibrate, const FusedSelParams& p, const PVParams& v, hipStream_t st) {
   if (!calibrate) return launch_atopn_fast(p, v, st);
   // long rows: spread over (row, chunk) blocks
-  if (cal_spread(p.L, p.cap, p.nslice, p.slice_cap, p.k2_variant)) return launch_calibrate_spread(p, v, st);
+  if (cal_spread(p.L, p.cap, p.nslice, p.slice_cap, p.k2_variant, p.nrows)) return launch_calibrate_spread(p, v, st);
   if (v.v_dt == SAGA_DTYPE_BF16) return launch_calibrate_d<SAGA_DTYPE_BF16>(p, v, st);
   if (v.v_dt == SAGA_DTYPE_F16) return launch_calibrate_d<SAGA_DTYPE_F16>(p, v, st);
   return launch_calibrate_d<SAGA_DTYPE_F32>(p, v, st);
