@@ -797,6 +797,13 @@ SPREAD_CASES = {  # name: b, q_h, k_h, v_h, d, L, N, dtype, kv_len, mask, keys
     "outlier_keys": (2, 6, 1, 3, 128, 30000, 700, "bf16", [30000, 17000], False, "outliers"),
     "b4_128k_n1024": (4, 12, 1, 2, 128, 131072, 1024, "bf16", None, False, "normal"),  # 16384 entries per row
     "b1_200k_n512": (1, 4, 1, 1, 64, 200000, 512, "bf16", None, False, "normal"),       # 25088 entries per row
+    # kv_len at the 8192-position chunk boundaries (the last chunk empty, one position, one short)
+    "chunk_edges_n512": (5, 4, 1, 2, 64, 40000, 512, "bf16", [8191, 8192, 8193, 16384, 24577], False, "normal"),
+    "top1_n1": (2, 4, 1, 1, 64, 9000, 1, "f32", [9000, 8193], False, "normal"),       # 4096-position chunks
+    "n2048_chunks32k": (1, 4, 1, 2, 128, 70000, 2048, "bf16", None, False, "normal"),  # 32768 positions per thread block
+    "nan_scores": (2, 4, 1, 2, 64, 20000, 300, "f32", None, False, "nan"),             # key classes in both kernels
+    "mostly_masked": (2, 4, 1, 2, 64, 40000, 700, "f32", None, True, "masked90"),      # finite min past -inf
+    "fewer_finite_than_n": (2, 4, 1, 2, 64, 20000, 512, "f32", None, True, "masked_all_but_100"),  # -inf ties kept by index
 }
 
 
@@ -808,17 +815,25 @@ def test_chunk_calibration_matches_one_block_per_row(name):
     other blocks); empty rows (kv_len 0) NaN in both.  Covers 1, 2 and 4 row
     blocks, every chunk size, partial last chunks (kv_len one position past
     a chunk, and a row of exactly one chunk), masked positions, all-equal
-    scores (key classes in both kernels) and outlier keys."""
+    scores (key classes in both kernels) and outlier keys; kv_len at chunk
+    boundaries, top-1, 32768-position chunks, NaN scores, mostly masked rows
+    and rows with fewer finite scores than N (-inf ties taken by index)."""
     b, q_h, k_h, v_h, d, L, N, dt, lens, masked, keys = SPREAD_CASES[name]
     print(f"chunk calibration {name}", flush=True)
     rng = np.random.default_rng(zlib.crc32(name.encode()))
     (q, k, v), (qd, kd, vd) = qkv(rng, b, q_h, k_h, v_h, d, L, dt, outliers=0.01 if keys == "outliers" else 0.0)
     if keys == "zero":
         kd.zero_()
+    if keys == "nan":  # a few key rows of NaN: NaN scores in every head of those positions
+        kd[:, :, rng.choice(L, 7, replace=False)] = float("nan")
     kvl = None if lens is None else torch.tensor(lens, dtype=torch.int32, device="cuda")
     mask = None
     if masked:
-        m = np.where(rng.random((b, 1, 1, L)) < 0.1, -np.inf, 0.0).astype(np.float32)
+        frac = {"masked90": 0.9}.get(keys, 0.1)
+        m = np.where(rng.random((b, 1, 1, L)) < frac, -np.inf, 0.0).astype(np.float32)
+        if keys == "masked_all_but_100":
+            m[:] = -np.inf
+            m[..., rng.choice(L, 100, replace=False)] = 0.0
         mask = torch.from_numpy(m).cuda()
     cap = min(N, L)
     res = {}
@@ -840,4 +855,7 @@ def test_chunk_calibration_matches_one_block_per_row(name):
         if n == 0:
             assert np.isnan(o1[r]).all() and np.isnan(o2[r]).all()
         else:
-            assert rel_l2(o2[r], o1[r]) < 1e-5, (r, n)
+            fin = np.isfinite(o1[r])  # (a kept NaN score makes the row NaN in both)
+            np.testing.assert_array_equal(np.isfinite(o2[r]), fin)
+            if fin.any():
+                assert rel_l2(o2[r][fin], o1[r][fin]) < 1e-5, (r, n)
