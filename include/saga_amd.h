@@ -239,7 +239,7 @@ int saga_atopn_calibrate(const saga_tensor* query, const saga_tensor* key,
  *                      chunks and at most 32768 chunk-list entries per row
  *                      (elsewhere one block per row); the choice of
  *                      SAGA_K2_AUTO for rows of more than 36864 positions,
- *                      and of 16384 or more when b * q_h <= 24.
+ *                      and of 16384 or more when b * q_h <= 24 or > 256.
  * Another value returns SAGA_ERR_INVALID. */
 int saga_atopn_calibrate_ex(const saga_tensor* query, const saga_tensor* key,
                             const saga_tensor* value, const saga_tensor* mask, const int32_t* kv_len,

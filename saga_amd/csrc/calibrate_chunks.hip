@@ -31,6 +31,7 @@
 // so an entry's rank within its class is the lower waves' total + one wave
 // scan + the thread's own count below it.
 #include <algorithm>
+#include <type_traits>
 
 #include "kernels.h"
 #include "select.cuh"
@@ -227,6 +228,12 @@ __device__ __forceinline__ uint32_t block_topk(SH& sh, f32x4 (&xr)[E / 4], POS p
                                                 bool& near, int& nl, int& nk) {
   constexpr int NW = NT / kWave, NQ = E / 4, LIST = SH::kList;
   constexpr int CAND = sizeof(sh.kf) / sizeof(int);
+  static_assert(E % 4 == 0 && E <= 64 && NT * E < 65536, "class counts are packed in 16 bits");
+  using MT = typename std::conditional<(E > 32), uint64_t, uint32_t>::type;  // one bit per entry of the thread
+  auto popc = [](MT m) -> int {
+    if constexpr (sizeof(MT) == 8) return __popcll(m);
+    else return __popc(m);
+  };
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   auto each_in = [&](auto f) {
 #pragma unroll
@@ -255,7 +262,7 @@ __device__ __forceinline__ uint32_t block_topk(SH& sh, f32x4 (&xr)[E / 4], POS p
   const int need = krem;
 
   // classes: the thread's E-bit masks of nearer / candidate entries
-  uint32_t mN = 0u, mC = 0u;
+  MT mN = 0, mC = 0;
   if (near) {
     // the distances again (the same bits); an opaque copy of the scale keeps
     // the compiler from holding the histogram pass's ones in registers
@@ -267,8 +274,8 @@ __device__ __forceinline__ uint32_t block_topk(SH& sh, f32x4 (&xr)[E / 4], POS p
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float dd = fmaf(-xr[u][j], sc2, Ms);
-        mN |= (dd < wantf ? 1u : 0u) << (4 * u + j);
-        mC |= (dd < wantf1 ? 1u : 0u) << (4 * u + j);
+        mN |= MT(dd < wantf ? 1 : 0) << (4 * u + j);
+        mC |= MT(dd < wantf1 ? 1 : 0) << (4 * u + j);
       }
     mC &= ~mN;
   } else {
@@ -277,13 +284,13 @@ __device__ __forceinline__ uint32_t block_topk(SH& sh, f32x4 (&xr)[E / 4], POS p
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint32_t key = f32_to_key(xr[u][j]);
-        mN |= (key > kth ? 1u : 0u) << (4 * u + j);
-        mC |= (key == kth ? 1u : 0u) << (4 * u + j);
+        mN |= MT(key > kth ? 1 : 0) << (4 * u + j);
+        mC |= MT(key == kth ? 1 : 0) << (4 * u + j);
       }
   }
   // ranks: the lower waves' totals + the lower lanes' (one packed scan; a
   // class of the block holds at most 32768 entries)
-  const int cntv = __popc(mN) | (__popc(mC) << 16);
+  const int cntv = popc(mN) | (popc(mC) << 16);
   const int incl = wave_incl_scan(cntv, lane);
   if (lane == kWave - 1) sh.wtot[w] = incl;
   lds_sync();
@@ -301,22 +308,22 @@ __device__ __forceinline__ uint32_t block_topk(SH& sh, f32x4 (&xr)[E / 4], POS p
     const int c = TT >> 16;  // == the bin's count <= CAND
     nl = TT & 0xffff;        // (== k - krem)
     nk = krem;
-    if (__ballot(mC != 0u) != 0ull) {  // (wave-uniform) the candidates to LDS in index order
+    if (__ballot(mC != 0) != 0ull) {  // (wave-uniform) the candidates to LDS in index order
 #pragma unroll
       for (int i = 0; i < E; ++i) {
-        if (__ballot((mC >> i) & 1u) != 0ull && ((mC >> i) & 1u)) {
-          const uint32_t below = (1u << i) - 1u;
-          const int cb = cb0 + __popc(mC & below);
+        if (__ballot((mC >> i) & 1) != 0ull && ((mC >> i) & 1)) {
+          const MT below = (MT(1) << i) - 1;
+          const int cb = cb0 + popc(mC & below);
           sh.cval[cb] = xr[i >> 2][i & 3];
           sh.cidx[cb] = pos(i);
-          sh.cnb[cb] = nb0 + __popc(mN & below);
+          sh.cnb[cb] = nb0 + popc(mN & below);
         }
       }
     }
     int slot = nb0;  // the nearer entries by rank (the thread's others to its lane's spare slot)
 #pragma unroll
     for (int i = 0; i < E; ++i) {
-      const int n = static_cast<int>((mN >> i) & 1u);
+      const int n = static_cast<int>((mN >> i) & 1);
       const int at = n ? slot : LIST + lane;
       sh.sidx[at] = pos(i);
       sh.sval[at] = xr[i >> 2][i & 3];
@@ -340,10 +347,10 @@ __device__ __forceinline__ uint32_t block_topk(SH& sh, f32x4 (&xr)[E / 4], POS p
     // key classes: above the k-th key, and the first `need` equal to it
 #pragma unroll
     for (int i = 0; i < E; ++i) {
-      const uint32_t below = (1u << i) - 1u;
-      const int cb = cb0 + __popc(mC & below);
-      const bool kept = ((mN >> i) & 1u) || (((mC >> i) & 1u) && cb < need);
-      const int at = kept ? nb0 + __popc(mN & below) + min(cb, need) : LIST + lane;
+      const MT below = (MT(1) << i) - 1;
+      const int cb = cb0 + popc(mC & below);
+      const bool kept = ((mN >> i) & 1) || (((mC >> i) & 1) && cb < need);
+      const int at = kept ? nb0 + popc(mN & below) + min(cb, need) : LIST + lane;
       sh.sidx[at] = pos(i);
       sh.sval[at] = xr[i >> 2][i & 3];
     }
@@ -465,16 +472,24 @@ __global__ void __launch_bounds__(NT, chunk_waves_per_simd(NT, E)) atopn_cal_chu
   write_list<NT>(sh, kc, nk, oidx, oval);
 }
 
-// Row kernel: NT threads hold up to NT * E entries (value, position) of the
-// row's chunk lists, E consecutive per thread; grid (rows, G).  The kept
-// entries (the nearer ones by rank, then the kept candidates) are block g's
-// share of softmax . V.
-template <int DT, int D, int NT, int E>
-__global__ void __launch_bounds__(NT) atopn_cal_merge_kernel(FusedSelParams p, PVParams v) {
+// Row body: NT threads hold up to NT * E entries (value, position), E
+// consecutive per thread: LISTS, of the row's chunk lists (grid (rows, G));
+// else the row's scores themselves, positions implicit (one block per row,
+// G = 1).  The kept entries (the nearer ones by rank, then the kept
+// candidates) are block g's share of softmax . V.
+template <int NW, int D>
+struct RowShared {
+  TopkShared<NW, kMergeList, kMergeCand> t;
+  float accs[NW * D];
+};
+
+template <int DT, int D, int NT, int E, bool LISTS>
+__device__ __forceinline__ void cal_row_body(const FusedSelParams& p, const PVParams& v,
+                                             RowShared<NT / kWave, D>& shr) {
   constexpr int NW = NT / kWave, NG = NT / 16, NQ = E / 4;
-  static_assert(E % 4 == 0 && E <= 32, "4 to 32 entries per thread, in 16-byte loads");
-  __shared__ TopkShared<NW, kMergeList, kMergeCand> sh;
-  __shared__ float accs[NW * D];
+  static_assert(E % 4 == 0 && E <= 64, "4 to 64 entries per thread, in 16-byte loads");
+  auto& sh = shr.t;
+  float* accs = shr.accs;
   const int r = blockIdx.x, g = blockIdx.y, G = gridDim.y;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int bi = r / p.q_h, h = r - bi * p.q_h;
@@ -483,11 +498,16 @@ __global__ void __launch_bounds__(NT) atopn_cal_merge_kernel(FusedSelParams p, P
   const float* prow_m = p.pmax + static_cast<int64_t>(r) * p.nparts;
   const float* prow_s = p.psum + static_cast<int64_t>(r) * p.nparts;
   const int nch = p.nparts;  // parts past kv_len hold (-inf, 0)
-  const int C = p.cal_chunk;
-  const int T = Leff / C * p.cap + min(p.cap, Leff % C);  // entries of the row's chunk lists
-  const int64_t cs = spread_row_stride(p);
-  const float* ev = p.sl_val + r * cs;
-  const int32_t* ei = p.sl_idx + r * cs;
+  int T = Leff;  // entries: the row's positions, or
+  const float* ev = p.scores + static_cast<int64_t>(r) * p.ld;
+  const int32_t* ei = nullptr;
+  if constexpr (LISTS) {  // the entries of its chunk lists
+    const int C = p.cal_chunk;
+    T = Leff / C * p.cap + min(p.cap, Leff % C);
+    const int64_t cs = spread_row_stride(p);
+    ev = p.sl_val + r * cs;
+    ei = p.sl_idx + r * cs;
+  }
 
   // K1's partials first, then the entries: their loads stay in flight
   // through the max / sum reductions
@@ -496,12 +516,12 @@ __global__ void __launch_bounds__(NT) atopn_cal_merge_kernel(FusedSelParams p, P
   const int lp = tid * E;  // the thread's first entry
   const int lastq = max(0, (T + 3) / 4 * 4 - 4);
   f32x4 xr[NQ];
-  i32x4 ir[NQ];
+  i32x4 ir[LISTS ? NQ : 1];
 #pragma unroll
   for (int u = 0; u < NQ; ++u) {
     const int o = min(lp + 4 * u, lastq);
     xr[u] = *reinterpret_cast<const f32x4*>(ev + o);
-    ir[u] = *reinterpret_cast<const i32x4*>(ei + o);
+    if constexpr (LISTS) ir[u] = *reinterpret_cast<const i32x4*>(ei + o);
   }
   for (int i = tid; i < kNearBins + kSpareBins; i += NT) sh.hist[i] = 0;
   float mloc = pm0;
@@ -571,7 +591,8 @@ __global__ void __launch_bounds__(NT) atopn_cal_merge_kernel(FusedSelParams p, P
     mn = -block_max<NW>(-m2, sh.red);
   }
   int nl = 0, nk = 0;
-  const uint32_t kth = block_topk<NT, E>(sh, xr, [&](int i) { return ir[i >> 2][i & 3]; }, k, M, mn, near, nl, nk);
+  const uint32_t kth = block_topk<NT, E>(
+      sh, xr, [&](int i) { return LISTS ? ir[LISTS ? i >> 2 : 0][i & 3] : lp + i; }, k, M, mn, near, nl, nk);
   if (g == 0) {
     write_list<NT>(sh, k, nk, gidx, gval);
     if (tid == 0) {
@@ -649,6 +670,20 @@ __global__ void __launch_bounds__(NT) atopn_cal_merge_kernel(FusedSelParams p, P
   if (tid == 0) p.row_cnt[r] = 0;  // ready for the next call
 }
 
+template <int DT, int D, int NT, int E>
+__global__ void __launch_bounds__(NT) atopn_cal_merge_kernel(FusedSelParams p, PVParams v) {
+  __shared__ RowShared<NT / kWave, D> sh;
+  cal_row_body<DT, D, NT, E, true>(p, v, sh);
+}
+
+// One block per row over the row's scores (rows of at most 1024 * 24
+// positions, k <= 2048).
+template <int DT, int D, int E>
+__global__ void __launch_bounds__(kBlkThreads) atopn_cal_row_kernel(FusedSelParams p, PVParams v) {
+  __shared__ RowShared<kBlkWaves, D> sh;
+  cal_row_body<DT, D, kBlkThreads, E, false>(p, v, sh);
+}
+
 // ---------------------------------------------------------------------------
 // Shapes: positions per chunk C = 4096 for k <= 256, then 8192, 16384 and
 // 32768 up to k = 2048 (a chunk keeps at most 1/16 of itself); the row
@@ -663,9 +698,11 @@ bool cal_spread(int64_t L, int64_t cap, int64_t nslice, int64_t slice_cap, int v
   // 47 us at b8 x 65537, 24 against 78 at b1 x 131073; at 32769 positions
   // one block per row is ahead at b8, 26.3 against 28.0 us), and from 16384
   // positions when the rows are few (at most 24: 21.4 against 23.3 us at
-  // b1 x 16385, 22.0 against 25.4 at b2 x 32769, level at b4)
-  if (variant == kK2Auto && L <= kCalSpreadAutoLen && !(L >= kCalSpreadFewRowsLen && nrows <= kCalSpreadFewRows))
-    return false;
+  // b1 x 16385, 22.0 against 25.4 at b2 x 32769, level at b4) or more than
+  // the CUs (29.4 against 36.8 us at b24 x 16385, 37.9 against 56.0 at
+  // b32 x 24577; one block per row ahead at b16 x 16385, 19.2 against 25.0)
+  const bool by_rows = nrows <= kCalSpreadFewRows || nrows > kCalSpreadManyRows;
+  if (variant == kK2Auto && L <= kCalSpreadAutoLen && !(L >= kCalSpreadFewRowsLen && by_rows)) return false;
   const int64_t C = spread_chunk(cap);
   if (L < 2 * C) return false;
   const int64_t slots = (L + C - 1) / C * cap;  // chunk slots of the longest row
@@ -723,6 +760,31 @@ static hipError_t launch_spread(FusedSelParams p, const PVParams& v, hipStream_t
 template <int DT>
 static hipError_t launch_spread_d(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
   return v.d == 128 ? launch_spread<DT, 128>(p, v, st) : launch_spread<DT, 64>(p, v, st);
+}
+
+bool cal_row_block(int64_t L, int64_t cap) { return cap >= 1 && cap <= kMergeList && L <= kCalRowBlockLen; }
+
+template <int DT, int D>
+static hipError_t launch_row_block(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
+  const dim3 grid(p.nrows), blk(kBlkThreads);
+  if (p.L <= 8 * 1024)
+    hipLaunchKernelGGL((atopn_cal_row_kernel<DT, D, 8>), grid, blk, 0, st, p, v);
+  else if (p.L <= 16 * 1024)
+    hipLaunchKernelGGL((atopn_cal_row_kernel<DT, D, 16>), grid, blk, 0, st, p, v);
+  else
+    hipLaunchKernelGGL((atopn_cal_row_kernel<DT, D, 24>), grid, blk, 0, st, p, v);
+  return hipGetLastError();
+}
+
+template <int DT>
+static hipError_t launch_row_block_d(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
+  return v.d == 128 ? launch_row_block<DT, 128>(p, v, st) : launch_row_block<DT, 64>(p, v, st);
+}
+
+hipError_t launch_calibrate_row_block(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
+  if (v.v_dt == SAGA_DTYPE_BF16) return launch_row_block_d<SAGA_DTYPE_BF16>(p, v, st);
+  if (v.v_dt == SAGA_DTYPE_F16) return launch_row_block_d<SAGA_DTYPE_F16>(p, v, st);
+  return launch_row_block_d<SAGA_DTYPE_F32>(p, v, st);
 }
 
 hipError_t launch_calibrate_spread(const FusedSelParams& p, const PVParams& v, hipStream_t st) {

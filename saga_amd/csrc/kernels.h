@@ -123,12 +123,21 @@ bool k2_row_block(int64_t nslice, int64_t cap, int variant);
 // top_n <= 2048 whose chunk lists fit the workspace's slice lists; the
 // choice of kK2Auto for rows longer than kCalSpreadAutoLen, or of at least
 // kCalSpreadFewRowsLen positions when there are at most kCalSpreadFewRows
-// rows; of kK2SliceRow wherever built; never of kK2RowBlock.
+// rows or more than kCalSpreadManyRows (one block per row then takes more
+// than one round of the CUs); of kK2SliceRow wherever built; never of
+// kK2RowBlock.
 constexpr int64_t kCalSpreadAutoLen = 9 * 4096;
 constexpr int64_t kCalSpreadFewRowsLen = 16384;
 constexpr int64_t kCalSpreadFewRows = 24;
+constexpr int64_t kCalSpreadManyRows = 256;
 bool cal_spread(int64_t L, int64_t cap, int64_t nslice, int64_t slice_cap, int variant, int64_t nrows);
 hipError_t launch_calibrate_spread(const FusedSelParams& p, const PVParams& v, hipStream_t st);
+// One block per row on the same selection, rows of up to kCalRowBlockLen
+// positions and k <= 2048 (the other rows: the older one-block kernels,
+// which measured as fast as it from 24577 to 36864 positions).
+constexpr int64_t kCalRowBlockLen = 24 * 1024;
+bool cal_row_block(int64_t L, int64_t cap);
+hipError_t launch_calibrate_row_block(const FusedSelParams& p, const PVParams& v, hipStream_t st);
 
 // API selection (threshold_topk_fast): typed rows, typed values out.
 struct ApiSelParams {

@@ -37,7 +37,9 @@ __device__ __forceinline__ void hist_pick(SH& sh, int nb, int krem, int& bin, in
   if (lane == kWave - 1) sh.cnt[w] = incl;
   lds_sync();
   int ex = incl - tsum;
-  for (int i = 0; i < w; ++i) ex += sh.cnt[i];
+#pragma unroll
+  for (int i = 0; i < NT / kWave; ++i)  // (all reads in flight together)
+    if (i < w) ex += sh.cnt[i];
 #pragma unroll
   for (int i = 0; i < BPT; ++i) {
     if (c[i] > 0 && ex < krem && krem <= ex + c[i]) {

@@ -791,6 +791,7 @@ hipError_t launch_atopn_select_pv(bool calibrate, const FusedSelParams& p, const
   if (!calibrate) return launch_atopn_fast(p, v, st);
   // long rows: spread over (row, chunk) blocks
   if (cal_spread(p.L, p.cap, p.nslice, p.slice_cap, p.k2_variant, p.nrows)) return launch_calibrate_spread(p, v, st);
+  if (cal_row_block(p.L, p.cap)) return launch_calibrate_row_block(p, v, st);
   if (v.v_dt == SAGA_DTYPE_BF16) return launch_calibrate_d<SAGA_DTYPE_BF16>(p, v, st);
   if (v.v_dt == SAGA_DTYPE_F16) return launch_calibrate_d<SAGA_DTYPE_F16>(p, v, st);
   return launch_calibrate_d<SAGA_DTYPE_F32>(p, v, st);
