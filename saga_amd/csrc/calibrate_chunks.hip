@@ -1,11 +1,14 @@
 // Calibration spread over many blocks per row: the exact top-k of each
-// chunk of a score row, then the exact top-k of the row among those lists.
+// chunk of a score row, then the exact top-k of the row among those lists;
+// and the same selection with one block per row over a short row's scores.
 //
 // Replaces torch.topk + the renormalised gather of
-// approx_top_n_attention_amortized_cal (attention/attention.py:173-189) for
-// rows of more than 36864 positions, where one block per row is bound by a
-// single CU's memory draw (one CU moves about 25 GB/s: 128 KB of scores and
-// 128 KB of V rows take 10 us).
+// approx_top_n_attention_amortized_cal (attention/attention.py:173-189):
+// spread over chunks for rows of more than 36864 positions (and from 16384
+// when the rows are few or outnumber the CUs), where one block per row is
+// bound by a single CU's memory draw (one CU moves about 25 GB/s: 128 KB of
+// scores and 128 KB of V rows take 10 us); one block per row (the row
+// kernel's body over the scores themselves) for rows of up to 24576.
 //
 // Chunk kernel, one block per (row, chunk of C positions): the k largest
 // positions of the chunk (k = min(top_n, L); ordered by value, then lowest

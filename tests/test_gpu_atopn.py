@@ -800,6 +800,8 @@ SPREAD_CASES = {  # name: b, q_h, k_h, v_h, d, L, N, dtype, kv_len, mask, keys
     "b1_20000_n1000": (1, 12, 1, 2, 128, 20000, 1000, "bf16", None, False, "normal"),   # 8192-position chunks, 4 blocks
     "b2_40000_n2048_f16": (2, 8, 2, 4, 64, 40000, 2048, "f16", None, False, "normal"),  # 16384-position chunks
     "ragged_masked_f32": (4, 4, 1, 2, 64, 24577, 512, "f32", [24577, 4096, 4097, 0], True, "normal"),
+    # one block per row on the shared selection (<= 24576 positions), an empty row among them
+    "ragged_masked_20000_f32": (4, 4, 1, 2, 64, 20000, 512, "f32", [20000, 4096, 4097, 0], True, "normal"),
     "constant_keys": (2, 4, 1, 1, 64, 20000, 300, "f32", None, False, "zero"),  # every score ties
     "outlier_keys": (2, 6, 1, 3, 128, 30000, 700, "bf16", [30000, 17000], False, "outliers"),
     "b4_128k_n1024": (4, 12, 1, 2, 128, 131072, 1024, "bf16", None, False, "normal"),  # 16384 entries per row
