@@ -169,6 +169,17 @@ __device__ __forceinline__ void pad_past(f32x4* xr, int lp, int n) {  // xr[u][j
       if (lp + 4 * u + j >= n) xr[u][j] = __uint_as_float(kPadBits);
 }
 
+// The same for the quad-interleaved share (xr[u][j]: element wbase + 256 u +
+// 4 lane + j).
+template <int NQ>
+__device__ __forceinline__ void pad_past_qi(f32x4* xr, int wbase, int lane, int n) {
+#pragma unroll
+  for (int u = 0; u < NQ; ++u)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (wbase + kWave * 4 * u + 4 * lane + j >= n) xr[u][j] = __uint_as_float(kPadBits);
+}
+
 // Every element of the share into its distance bin below M; elements out of
 // the bins' range (padding, -inf, NaN) into a spare bin, so that no lane
 // branches.  sh.hist has kNearBins + kSpareBins entries.
@@ -218,15 +229,18 @@ struct TopkShared {
 
 // The exact k largest (value desc, position asc) of a set held E per thread
 // (thread t: entries t E .. t E + E - 1 of the set, which is in position
-// order; values xr, positions pos(i) of the thread's entry i; entries past
-// the set are kPadBits), k <= the set's size <= LIST... for the nearer ones.
+// order; QI: wave w holds entries [64 E w, 64 E (w + 1)), its quad u the 256
+// entries from 64 E w + 256 u, lane l entries 4 l .. 4 l + 3 of each quad,
+// so that every 16-byte load of a wave reads 1 KB in a row; values xr,
+// positions pos(i) of the thread's entry i = 4 u + j; entries past the set
+// are kPadBits), k <= the set's size <= LIST... for the nearer ones.
 // M: the set's max (every value <= M unless near is false), mn: a lower
 // bound of its finite values; near (in): M finite and no NaN.  sh.hist must
 // be zero and published.  Out, published: near mode (near true): nl nearer
 // entries in sh.sidx / sval by rank, nk kept candidates in sh.kf / kix / kvl
 // (kf ascending); key mode: the k kept entries in sh.sidx / sval in order
 // (nl = k, nk = 0).  Returns the k-th largest's key.
-template <int NT, int E, class SH, class POS>
+template <int NT, int E, bool QI = false, class SH, class POS>
 __device__ __forceinline__ uint32_t block_topk(SH& sh, f32x4 (&xr)[E / 4], POS pos, int k, float M, float mn,
                                                 bool& near, int& nl, int& nk) {
   constexpr int NW = NT / kWave, NQ = E / 4, LIST = SH::kList;
@@ -291,10 +305,26 @@ __device__ __forceinline__ uint32_t block_topk(SH& sh, f32x4 (&xr)[E / 4], POS p
         mC |= MT(key == kth ? 1 : 0) << (4 * u + j);
       }
   }
-  // ranks: the lower waves' totals + the lower lanes' (one packed scan; a
-  // class of the block holds at most 32768 entries)
+  // ranks: the lower waves' totals + the lower lanes' (one packed scan, nearer
+  // | candidates << 16; a class of the block holds fewer than 65536
+  // entries); QI: one scan per quad, whose wave totals precede the next quad
   const int cntv = popc(mN) | (popc(mC) << 16);
-  const int incl = wave_incl_scan(cntv, lane);
+  int qpre[QI ? NQ : 1];  // QI: entries of the wave before the lane's entries of quad u (packed)
+  int incl = 0;
+  if constexpr (QI) {
+    int run = 0;  // (wave-uniform)
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      const int c = __popc(static_cast<uint32_t>(mN >> (4 * u)) & 15u) |
+                    (__popc(static_cast<uint32_t>(mC >> (4 * u)) & 15u) << 16);
+      const int inc = wave_incl_scan(c, lane);
+      qpre[u] = run + inc - c;
+      run += __builtin_amdgcn_readlane(inc, kWave - 1);
+    }
+    incl = run;
+  } else {
+    incl = wave_incl_scan(cntv, lane);
+  }
   if (lane == kWave - 1) sh.wtot[w] = incl;
   lds_sync();
   int WB = 0, TT = 0;
@@ -306,6 +336,15 @@ __device__ __forceinline__ uint32_t block_topk(SH& sh, f32x4 (&xr)[E / 4], POS p
   }
   const int pre = WB + incl - cntv;
   const int nb0 = pre & 0xffff, cb0 = pre >> 16;  // nearer / candidates before the thread's first entry
+  // QI: nearer / candidates before entry i of the thread, in set order
+  auto before_n = [&](int i) -> int {
+    return ((WB + qpre[QI ? i >> 2 : 0]) & 0xffff) +
+           __popc(static_cast<uint32_t>(mN >> (i & ~3)) & ((1u << (i & 3)) - 1u));
+  };
+  auto before_c = [&](int i) -> int {
+    return ((WB + qpre[QI ? i >> 2 : 0]) >> 16) +
+           __popc(static_cast<uint32_t>(mC >> (i & ~3)) & ((1u << (i & 3)) - 1u));
+  };
 
   if (near) {
     const int c = TT >> 16;  // == the bin's count <= CAND
@@ -316,16 +355,17 @@ __device__ __forceinline__ uint32_t block_topk(SH& sh, f32x4 (&xr)[E / 4], POS p
       for (int i = 0; i < E; ++i) {
         if (__ballot((mC >> i) & 1) != 0ull && ((mC >> i) & 1)) {
           const MT below = (MT(1) << i) - 1;
-          const int cb = cb0 + popc(mC & below);
+          const int cb = QI ? before_c(i) : cb0 + popc(mC & below);
           sh.cval[cb] = xr[i >> 2][i & 3];
           sh.cidx[cb] = pos(i);
-          sh.cnb[cb] = nb0 + popc(mN & below);
+          sh.cnb[cb] = QI ? before_n(i) : nb0 + popc(mN & below);
         }
       }
     }
     int slot = nb0;  // the nearer entries by rank (the thread's others to its lane's spare slot)
 #pragma unroll
     for (int i = 0; i < E; ++i) {
+      if (QI && (i & 3) == 0) slot = before_n(i);
       const int n = static_cast<int>((mN >> i) & 1);
       const int at = n ? slot : LIST + lane;
       sh.sidx[at] = pos(i);
@@ -351,9 +391,9 @@ __device__ __forceinline__ uint32_t block_topk(SH& sh, f32x4 (&xr)[E / 4], POS p
 #pragma unroll
     for (int i = 0; i < E; ++i) {
       const MT below = (MT(1) << i) - 1;
-      const int cb = cb0 + popc(mC & below);
+      const int cb = QI ? before_c(i) : cb0 + popc(mC & below);
       const bool kept = ((mN >> i) & 1) || (((mC >> i) & 1) && cb < need);
-      const int at = kept ? nb0 + popc(mN & below) + min(cb, need) : LIST + lane;
+      const int at = kept ? (QI ? before_n(i) : nb0 + popc(mN & below)) + min(cb, need) : LIST + lane;
       sh.sidx[at] = pos(i);
       sh.sval[at] = xr[i >> 2][i & 3];
     }
@@ -516,13 +556,19 @@ __device__ __forceinline__ void cal_row_body(const FusedSelParams& p, const PVPa
   // through the max / sum reductions
   const float pm0 = tid < nch ? prow_m[tid] : kNegInf;
   const float ps0 = tid < nch ? prow_s[tid] : 0.f;
-  const int lp = tid * E;  // the thread's first entry
+  // the entries: E consecutive per thread from the chunk lists; the score
+  // row quad-interleaved (wave w: entries [wbase, wbase + 64 E), quad u the
+  // 256 from wbase + 256 u, lane l 4 of each), every load 1 KB in a row
+  constexpr bool QI = !LISTS;
+  const int lp = tid * E;  // the thread's first entry (E consecutive)
+  const int wbase = w * kWave * E;
+  auto entry = [&](int u) { return QI ? wbase + kWave * 4 * u + 4 * lane : lp + 4 * u; };
   const int lastq = max(0, (T + 3) / 4 * 4 - 4);
   f32x4 xr[NQ];
   i32x4 ir[LISTS ? NQ : 1];
 #pragma unroll
   for (int u = 0; u < NQ; ++u) {
-    const int o = min(lp + 4 * u, lastq);
+    const int o = min(entry(u), lastq);
     xr[u] = *reinterpret_cast<const f32x4*>(ev + o);
     if constexpr (LISTS) ir[u] = *reinterpret_cast<const i32x4*>(ei + o);
   }
@@ -558,7 +604,10 @@ __device__ __forceinline__ void cal_row_body(const FusedSelParams& p, const PVPa
     return;
   }
 
-  if (T < NT * E) pad_past<NQ>(xr, lp, T);  // (block-uniform)
+  if (T < NT * E) {  // (block-uniform)
+    if constexpr (QI) pad_past_qi<NQ>(xr, wbase, lane, T);
+    else pad_past<NQ>(xr, lp, T);
+  }
   // the smallest entry and a NaN entry or one above M (padding aside; one barrier)
   float mnl = INFINITY;
   bool odd = false;
@@ -594,8 +643,9 @@ __device__ __forceinline__ void cal_row_body(const FusedSelParams& p, const PVPa
     mn = -block_max<NW>(-m2, sh.red);
   }
   int nl = 0, nk = 0;
-  const uint32_t kth = block_topk<NT, E>(
-      sh, xr, [&](int i) { return LISTS ? ir[LISTS ? i >> 2 : 0][i & 3] : lp + i; }, k, M, mn, near, nl, nk);
+  const uint32_t kth = block_topk<NT, E, QI>(
+      sh, xr, [&](int i) { return LISTS ? ir[LISTS ? i >> 2 : 0][i & 3] : entry(i >> 2) + (i & 3); }, k, M, mn, near,
+      nl, nk);
   if (g == 0) {
     write_list<NT>(sh, k, nk, gidx, gval);
     if (tid == 0) {
@@ -679,7 +729,7 @@ __global__ void __launch_bounds__(NT) atopn_cal_merge_kernel(FusedSelParams p, P
   cal_row_body<DT, D, NT, E, true>(p, v, sh);
 }
 
-// One block per row over the row's scores (rows of at most 1024 * 24
+// One block per row over the row's scores (rows of at most 1024 * 36
 // positions, k <= 2048).
 template <int DT, int D, int E>
 __global__ void __launch_bounds__(kBlkThreads) atopn_cal_row_kernel(FusedSelParams p, PVParams v) {
@@ -774,8 +824,10 @@ static hipError_t launch_row_block(const FusedSelParams& p, const PVParams& v, h
     hipLaunchKernelGGL((atopn_cal_row_kernel<DT, D, 8>), grid, blk, 0, st, p, v);
   else if (p.L <= 16 * 1024)
     hipLaunchKernelGGL((atopn_cal_row_kernel<DT, D, 16>), grid, blk, 0, st, p, v);
-  else
+  else if (p.L <= 24 * 1024)
     hipLaunchKernelGGL((atopn_cal_row_kernel<DT, D, 24>), grid, blk, 0, st, p, v);
+  else
+    hipLaunchKernelGGL((atopn_cal_row_kernel<DT, D, 36>), grid, blk, 0, st, p, v);
   return hipGetLastError();
 }
 

@@ -133,9 +133,8 @@ constexpr int64_t kCalSpreadManyRows = 256;
 bool cal_spread(int64_t L, int64_t cap, int64_t nslice, int64_t slice_cap, int variant, int64_t nrows);
 hipError_t launch_calibrate_spread(const FusedSelParams& p, const PVParams& v, hipStream_t st);
 // One block per row on the same selection, rows of up to kCalRowBlockLen
-// positions and k <= 2048 (the other rows: the older one-block kernels,
-// which measured as fast as it from 24577 to 36864 positions).
-constexpr int64_t kCalRowBlockLen = 24 * 1024;
+// positions and k <= 2048 (the other rows: the older one-block kernels).
+constexpr int64_t kCalRowBlockLen = 36 * 1024;
 bool cal_row_block(int64_t L, int64_t cap);
 hipError_t launch_calibrate_row_block(const FusedSelParams& p, const PVParams& v, hipStream_t st);
 

@@ -755,8 +755,9 @@ CAL_EDGE_CASES = {  # name: L, N, d, dtype, ragged kv_len, additive -inf mask
     "row8_last": (8192, 256, 64, "f32", True, True),         # 8 positions per thread of the shared selection
     "row16_first": (8193, 2048, 128, "bf16", False, False),  # 16 per thread, the largest N it takes
     "row24_last": (24576, 1000, 64, "f16", True, False),     # 24 per thread
+    "row36_first": (24577, 512, 128, "bf16", True, False),   # 36 per thread
+    "row36_last": (36864, 2048, 64, "f32", True, True),
     "row_n2049": (20000, 2049, 64, "bf16", False, True),     # N > 2048: the register kernel
-    "regs9_first": (24577, 512, 128, "bf16", True, False),   # the first row of the register kernel
     "regs13_first": (36865, 300, 64, "f16", True, True),     # the first row of 13 register chunks
     "regs13_last": (53248, 1024, 128, "bf16", False, False),
     "regs12_lds5_first": (53249, 2048, 64, "f32", True, False),
@@ -770,8 +771,8 @@ CAL_EDGE_CASES = {  # name: L, N, d, dtype, ragged kv_len, additive -inf mask
 @pytest.mark.parametrize("name", list(CAL_EDGE_CASES))
 def test_calibration_row_class_edges(name, variant):
     """The one-block calibration kernels at the edges of their row classes
-    (the shared selection with 8, 16 or 24 positions per thread up to 24576
-    positions and N <= 2048; beyond, the row in registers up to 13 chunks of
+    (the shared selection with 8, 16, 24 or 36 positions per thread up to
+    36864 positions and N <= 2048; beyond, the row in registers up to 13 chunks of
     4096 positions; 12 in registers + 5
     in LDS up to 17 with N <= 2048; beyond, the row re-read from memory), with
     ragged kv_len and -inf masked positions inside the resident rows; the
@@ -800,7 +801,7 @@ SPREAD_CASES = {  # name: b, q_h, k_h, v_h, d, L, N, dtype, kv_len, mask, keys
     "b1_20000_n1000": (1, 12, 1, 2, 128, 20000, 1000, "bf16", None, False, "normal"),   # 8192-position chunks, 4 blocks
     "b2_40000_n2048_f16": (2, 8, 2, 4, 64, 40000, 2048, "f16", None, False, "normal"),  # 16384-position chunks
     "ragged_masked_f32": (4, 4, 1, 2, 64, 24577, 512, "f32", [24577, 4096, 4097, 0], True, "normal"),
-    # one block per row on the shared selection (<= 24576 positions), an empty row among them
+    # one block per row on the shared selection (<= 36864 positions), an empty row among them
     "ragged_masked_20000_f32": (4, 4, 1, 2, 64, 20000, 512, "f32", [20000, 4096, 4097, 0], True, "normal"),
     "constant_keys": (2, 4, 1, 1, 64, 20000, 300, "f32", None, False, "zero"),  # every score ties
     "outlier_keys": (2, 6, 1, 3, 128, 30000, 700, "bf16", [30000, 17000], False, "outliers"),
