@@ -32,7 +32,9 @@
 // non-finite max or too many candidates (ties) take a radix select over the
 // order-preserving keys instead.  Each thread holds E consecutive entries,
 // so an entry's rank within its class is the lower waves' total + one wave
-// scan + the thread's own count below it.
+// scan + the thread's own count below it; or, for one block per row, each
+// wave holds 64 E consecutive entries quad-interleaved (every 16-byte load
+// of the wave reads 1 KB in a row), and a rank takes one wave scan per quad.
 #include <algorithm>
 #include <type_traits>
 
