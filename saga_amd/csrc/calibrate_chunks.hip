@@ -18,12 +18,9 @@
 // than k of its chunk do), and every full chunk keeps exactly k, so a row's
 // entries are one dense list in position order.
 //
-// Row kernel, G blocks per row: each block finds the row's top-k among the
-// entries (the same selection, run over the entries instead of the
-// positions), block 0 writes the kept list and p*, and block g gathers the
-// V rows of the g-th share of the kept entries; with G > 1 the last block to
-// finish merges the shares' (sum of weights, sum of weighted V) partials in
-// block order.
+// Row kernel, one block per row: the row's top-k among the entries (the
+// same selection, run over the entries instead of the positions), the kept
+// list, p* and softmax . V over the kept entries.
 //
 // The selection (block_topk): 2048 bins of the distance (M - x) * s below
 // the set's max M (s a power of two fitted to the set's spread); the bin of
@@ -441,7 +438,6 @@ __global__ void __launch_bounds__(NT, chunk_waves_per_simd(NT, E)) atopn_cal_chu
   const int bi = r / p.q_h;
   int Leff = p.L;
   if (p.kv_len) Leff = min(Leff, max(p.kv_len[bi], 0));
-  if (ck == 0 && tid == 0) p.row_cnt[r] = 0;  // the row kernel's count of finished blocks starts at zero
   const int base = ck * C;
   const int nv = min(Leff - base, C);  // positions of the chunk inside the row
   if (nv <= 0) return;
@@ -517,11 +513,10 @@ __global__ void __launch_bounds__(NT, chunk_waves_per_simd(NT, E)) atopn_cal_chu
   write_list<NT>(sh, kc, nk, oidx, oval);
 }
 
-// Row body: NT threads hold up to NT * E entries (value, position), E
-// consecutive per thread: LISTS, of the row's chunk lists (grid (rows, G));
-// else the row's scores themselves, positions implicit (one block per row,
-// G = 1).  The kept entries (the nearer ones by rank, then the kept
-// candidates) are block g's share of softmax . V.
+// Row body, one block per row: NT threads hold up to NT * E entries (value,
+// position), E per thread: LISTS, of the row's chunk lists; else the row's
+// scores themselves, positions implicit.  The kept entries (the nearer ones
+// by rank, then the kept candidates) are the row's softmax . V.
 template <int NW, int D>
 struct RowShared {
   TopkShared<NW, kMergeList, kMergeCand> t;
@@ -535,7 +530,7 @@ __device__ __forceinline__ void cal_row_body(const FusedSelParams& p, const PVPa
   static_assert(E % 4 == 0 && E <= 64, "4 to 64 entries per thread, in 16-byte loads");
   auto& sh = shr.t;
   float* accs = shr.accs;
-  const int r = blockIdx.x, g = blockIdx.y, G = gridDim.y;
+  const int r = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int bi = r / p.q_h, h = r - bi * p.q_h;
   int Leff = p.L;
@@ -594,7 +589,6 @@ __device__ __forceinline__ void cal_row_body(const FusedSelParams& p, const PVPa
   const int64_t vrow = v.v_sl * Elt<DT>::kBytes;
   const int64_t ooff = bi * v.o_sb + static_cast<int64_t>(h) * v.o_sh;
   if (k <= 0) {
-    if (g > 0) return;
     if (tid == 0) {
       p.sel_cnt[r] = 0;
       if (p.sel_total) p.sel_total[r] = 0;
@@ -648,20 +642,19 @@ __device__ __forceinline__ void cal_row_body(const FusedSelParams& p, const PVPa
   const uint32_t kth = block_topk<NT, E, QI>(
       sh, xr, [&](int i) { return LISTS ? ir[LISTS ? i >> 2 : 0][i & 3] : entry(i >> 2) + (i & 3); }, k, M, mn, near,
       nl, nk);
-  if (g == 0) {
-    write_list<NT>(sh, k, nk, gidx, gval);
-    if (tid == 0) {
-      p.sel_cnt[r] = k;
-      if (p.sel_total) p.sel_total[r] = k;
-      p.pstar_out[r] = expf(key_to_f32(kth) - M) / S;
-    }
+  write_list<NT>(sh, k, nk, gidx, gval);
+  if (tid == 0) {
+    p.sel_cnt[r] = k;
+    if (p.sel_total) p.sel_total[r] = k;
+    p.pstar_out[r] = expf(key_to_f32(kth) - M) / S;
   }
 
-  // this block's share of softmax . V: kept entries [e0, e1), weight
-  // exp(x - M) (the row max is always kept)
-  const int nE = nl + nk;
-  const int e0 = static_cast<int>(static_cast<int64_t>(nE) * g / G);
-  const int e1 = static_cast<int>(static_cast<int64_t>(nE) * (g + 1) / G);
+  // softmax . V over the kept entries [0, nl + nk), weight exp(x - M) (the
+  // row max is always kept).  One block gathers the row's V rows: splitting
+  // them over several blocks per row (each repeating the selection, the last
+  // one adding the shares after an agent-scope fence) measured slower
+  // wherever it applied (b8 x 32769: 17.4 against 12.6 us)
+  const int e0 = 0, e1 = nl + nk;
   const int grp = tid >> 4;
   const char* vb = vbase + static_cast<int64_t>(tid & 15) * PV::BYTES;
   auto entry_pos = [&](int e) { return e < nl ? sh.sidx[e] : sh.kix[e - nl]; };
@@ -692,37 +685,7 @@ __device__ __forceinline__ void cal_row_body(const FusedSelParams& p, const PVPa
   float ls = 0.f;
   for (int e = e0 + tid; e < e1; e += NT) ls += weight(e);
   pv.l = block_sum<NW>(ls, sh.red);
-  if (G == 1) {
-    pv.finish(accs, v.out, v.out_dt, ooff, false);
-    return;
-  }
-  // G shares: (l, o) partials, the last block to finish adds them in block
-  // order (every share is weighted against the same max M)
-  constexpr int PW = D + 4;  // floats per partial: l, three unused, o
-  float* part = p.row_part + static_cast<int64_t>(r) * kRowSplit * PW;
-  const float og = pv.reduce(accs);  // thread i < D: dim i
-  if (tid < D) part[g * PW + 4 + tid] = og;
-  if (tid == 0) part[g * PW] = pv.l;
-  // the block's stores complete at the barrier; one agent-scope release
-  // fence (an L2 write-back) orders them before the count, and one acquire
-  // fence in the last block makes the other blocks' partials visible
-  __syncthreads();
-  if (tid == 0) {
-    __threadfence();
-    sh.last = atomicAdd(p.row_cnt + r, 1) == G - 1;
-    if (sh.last) __threadfence();
-  }
-  __syncthreads();
-  if (!sh.last) return;
-  if (tid < D) {
-    float l = 0.f, o = 0.f;
-    for (int q = 0; q < G; ++q) {
-      l += part[q * PW];
-      o += part[q * PW + 4 + tid];
-    }
-    store_from_f32(v.out, v.out_dt, ooff + tid, o / l);
-  }
-  if (tid == 0) p.row_cnt[r] = 0;  // ready for the next call
+  pv.finish(accs, v.out, v.out_dt, ooff, false);
 }
 
 template <int DT, int D, int NT, int E>
@@ -780,11 +743,10 @@ static hipError_t launch_spread(FusedSelParams p, const PVParams& v, hipStream_t
     hipLaunchKernelGGL((atopn_cal_chunk_kernel<1024, 32>), ga, dim3(1024), 0, st, p);
   // entries of the longest row: full chunks keep cap, the last min(cap, rest)
   const int64_t tmax = static_cast<int64_t>(p.L / C) * p.cap + std::min<int64_t>(p.cap, p.L % C);
-  const int G = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(kRowSplit, kMergeBlocksMax / p.nrows)));
-  const dim3 gb(p.nrows, G);
+  const dim3 gb(p.nrows);
   // more rows than CUs: 512-thread blocks, two per CU, while their share of
   // the entries stays in registers
-  if (static_cast<int64_t>(p.nrows) * G > kMergeBlocksMax && tmax <= 16 * 512) {
+  if (p.nrows > kMergeBlocksMax && tmax <= 16 * 512) {
     const dim3 blk(512);
     if (tmax <= 4 * 512)
       hipLaunchKernelGGL((atopn_cal_merge_kernel<DT, D, 512, 4>), gb, blk, 0, st, p, v);
