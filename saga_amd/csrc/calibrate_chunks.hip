@@ -44,7 +44,7 @@ constexpr int kSpreadRank = 128;      // candidates ranked pairwise; more: radix
 constexpr int kChunkCand = 512;       // chunk kernel: candidates of the k-th's bin held in LDS
 constexpr int kMergeCand = 1024;      // row kernel: the same
 constexpr int kMergeList = 2048;      // row kernel: kept list in LDS (k <= 2048)
-constexpr int kMergeBlocksMax = 256;  // row kernel: one block per CU
+constexpr int kMergeBlocksMax = 256;  // row kernel: past this many rows, 512-thread blocks (two per CU)
 constexpr int kSpareBins = 32;        // histogram bins past kNearBins for positions out of range (one per bank)
 constexpr uint32_t kPadBits = 0xffffffffu;  // a NaN whose order key is 0: below every other float
 
@@ -712,13 +712,13 @@ static int spread_chunk(int64_t cap) {
 
 bool cal_spread(int64_t L, int64_t cap, int64_t nslice, int64_t slice_cap, int variant, int64_t nrows) {
   if (variant == kK2RowBlock || cap > kMergeList || cap < 1) return false;
-  // by shape: rows past the nine-chunk register kernel (measured: 33 against
-  // 47 us at b8 x 65537, 24 against 78 at b1 x 131073; at 32769 positions
-  // one block per row is ahead at b8, 26.3 against 28.0 us), and from 16384
-  // positions when the rows are few (at most 24: 21.4 against 23.3 us at
-  // b1 x 16385, 22.0 against 25.4 at b2 x 32769, level at b4) or more than
-  // the CUs (29.4 against 36.8 us at b24 x 16385, 37.9 against 56.0 at
-  // b32 x 24577; one block per row ahead at b16 x 16385, 19.2 against 25.0)
+  // by shape: rows past one block per row's 36864 positions (measured: 27.1
+  // against 43.9 us at b8 x 65537, 23.2 against 77.9 at b1 x 131073; at
+  // 32769 positions one block per row is ahead at b8, 21.7 against 22.7 us),
+  // and from 16384 positions when the rows are few (at most 24: 19.1-19.8
+  // against 20.7-21.8 us at b1 x 32769) or more than the CUs (29.8 against
+  // 36.7 us at b32 x 16385, 41.4 against 49.7 at b32 x 32769; one block per
+  // row ahead at b16 x 16385, 19.1 against 24.2)
   const bool by_rows = nrows <= kCalSpreadFewRows || nrows > kCalSpreadManyRows;
   if (variant == kK2Auto && L <= kCalSpreadAutoLen && !(L >= kCalSpreadFewRowsLen && by_rows)) return false;
   const int64_t C = spread_chunk(cap);
