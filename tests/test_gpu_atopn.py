@@ -126,8 +126,8 @@ def test_against_reference_golden(name, golden):
                 flips += len(set(sel) ^ set(sel_ref))
         ok = ~np.isnan(o_ref)
         # the reference's own output, whatever the near-tie flips (a flipped
-        # entry's weight is about p*): the north star's 1e-3 always, fp32's
-        # 1e-5 when both kept the same sets
+        # entry's weight is about p*): the path's stated relative-L2 bound of
+        # 1e-3 always, fp32's 1e-5 when both kept the same sets
         print(f"  golden {name} {tag}: flips={flips}", flush=True)
         assert rel_l2(out[ok], o_ref[ok]) < 1e-3, (tag, flips)
         if flips == 0 and not bf:
