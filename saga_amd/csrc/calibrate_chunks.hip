@@ -783,15 +783,22 @@ bool cal_row_block(int64_t L, int64_t cap) { return cap >= 1 && cap <= kMergeLis
 
 template <int DT, int D>
 static hipError_t launch_row_block(const FusedSelParams& p, const PVParams& v, hipStream_t st) {
+  // the fewest whole quads per wave that hold the row: a context of a power
+  // of two plus the decoded tokens (8193, 16385, 32769) takes one more quad,
+  // not the next power of two's share
   const dim3 grid(p.nrows), blk(kBlkThreads);
-  if (p.L <= 8 * 1024)
-    hipLaunchKernelGGL((atopn_cal_row_kernel<DT, D, 8>), grid, blk, 0, st, p, v);
-  else if (p.L <= 16 * 1024)
-    hipLaunchKernelGGL((atopn_cal_row_kernel<DT, D, 16>), grid, blk, 0, st, p, v);
-  else if (p.L <= 24 * 1024)
-    hipLaunchKernelGGL((atopn_cal_row_kernel<DT, D, 24>), grid, blk, 0, st, p, v);
-  else
-    hipLaunchKernelGGL((atopn_cal_row_kernel<DT, D, 36>), grid, blk, 0, st, p, v);
+  switch ((p.L + 4095) / 4096) {
+    case 0:
+    case 1:
+    case 2: hipLaunchKernelGGL((atopn_cal_row_kernel<DT, D, 8>), grid, blk, 0, st, p, v); break;
+    case 3: hipLaunchKernelGGL((atopn_cal_row_kernel<DT, D, 12>), grid, blk, 0, st, p, v); break;
+    case 4: hipLaunchKernelGGL((atopn_cal_row_kernel<DT, D, 16>), grid, blk, 0, st, p, v); break;
+    case 5: hipLaunchKernelGGL((atopn_cal_row_kernel<DT, D, 20>), grid, blk, 0, st, p, v); break;
+    case 6: hipLaunchKernelGGL((atopn_cal_row_kernel<DT, D, 24>), grid, blk, 0, st, p, v); break;
+    case 7: hipLaunchKernelGGL((atopn_cal_row_kernel<DT, D, 28>), grid, blk, 0, st, p, v); break;
+    case 8: hipLaunchKernelGGL((atopn_cal_row_kernel<DT, D, 32>), grid, blk, 0, st, p, v); break;
+    default: hipLaunchKernelGGL((atopn_cal_row_kernel<DT, D, 36>), grid, blk, 0, st, p, v); break;
+  }
   return hipGetLastError();
 }
 

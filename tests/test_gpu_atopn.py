@@ -753,10 +753,10 @@ def test_calibration_random_shapes_exact_topk(seed, variant):
 
 CAL_EDGE_CASES = {  # name: L, N, d, dtype, ragged kv_len, additive -inf mask
     "row8_last": (8192, 256, 64, "f32", True, True),         # 8 positions per thread of the shared selection
-    "row16_first": (8193, 2048, 128, "bf16", False, False),  # 16 per thread, the largest N it takes
+    "row16_first": (8193, 2048, 128, "bf16", False, False),  # 12 per thread, the largest N it takes
     "row24_last": (24576, 1000, 64, "f16", True, False),     # 24 per thread
-    "row36_first": (24577, 512, 128, "bf16", True, False),   # 36 per thread
-    "row36_last": (36864, 2048, 64, "f32", True, True),
+    "row36_first": (24577, 512, 128, "bf16", True, False),   # 28 per thread
+    "row36_last": (36864, 2048, 64, "f32", True, True),      # 36 per thread
     "row_n2049": (20000, 2049, 64, "bf16", False, True),     # N > 2048: the register kernel
     "regs13_first": (36865, 300, 64, "f16", True, True),     # the first row of 13 register chunks
     "regs13_last": (53248, 1024, 128, "bf16", False, False),
@@ -771,7 +771,7 @@ CAL_EDGE_CASES = {  # name: L, N, d, dtype, ragged kv_len, additive -inf mask
 @pytest.mark.parametrize("name", list(CAL_EDGE_CASES))
 def test_calibration_row_class_edges(name, variant):
     """The one-block calibration kernels at the edges of their row classes
-    (the shared selection with 8, 16, 24 or 36 positions per thread up to
+    (the shared selection with 8 to 36 positions per thread, a multiple of 4, up to
     36864 positions and N <= 2048; beyond, the row in registers up to 13 chunks of
     4096 positions; 12 in registers + 5
     in LDS up to 17 with N <= 2048; beyond, the row re-read from memory), with
